@@ -1,0 +1,313 @@
+/*
+ * spar_hip.h — the C ABI of Spar's MI355X (gfx950) device backend.
+ *
+ * This header is the drop-in boundary that replaces Spar's CUDA launcher ABI
+ * (src/backend/cuda_kernels.hpp:1-135) and the device runtime that core/storage
+ * and core/tensor call (src/backend/cuda_runtime.cppm:14-36).  It is plain C:
+ * raw pointers, 64-bit counts and integer tags, no C++ or torch types, so the
+ * C++ host layer (or a ctypes/FFI binding) includes it in a global module
+ * fragment exactly as src/backend/cuda_ops.cppm:1-5 includes cuda_kernels.hpp.
+ *
+ * Conventions shared by every entry point:
+ *   - Status: {code, hip_error}.  code 0 = success, 1 = invalid argument
+ *     (rejected on the host before any device API call), 2 = HIP runtime error
+ *     (hip_error holds the hipError_t value).  Same meaning as SparCudaStatus
+ *     (cuda_kernels.hpp:41-44, cuda_kernels.cu:12-22).
+ *   - count == 0 returns success without touching the device, as the reference
+ *     launchers do (e.g. cuda_kernels.cu:718-720).
+ *   - Every launch is enqueued on the backend's single stream for `device`
+ *     and returns without waiting.  Work is stream-ordered; host<->device
+ *     copies and spar_hip_synchronize() are the synchronisation points.  The
+ *     reference instead synchronised after every launch (cuda_kernels.cu:39-49).
+ *   - Device pointers come from spar_hip_allocate (or any allocation visible to
+ *     the device); element pointers must be aligned to their element size.
+ *   - Strides and offsets are in elements, never bytes.
+ *   - Geometry (extents/strides, rank <= SPAR_HIP_MAX_RANK) is passed to the
+ *     kernels by value; no launcher allocates metadata on the device
+ *     (the reference cudaMalloc'd it per call: cuda_kernels.cu:1165-1190).
+ */
+#ifndef SPAR_HIP_H
+#define SPAR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPAR_HIP_MAX_RANK 8
+
+/* Element types; values equal SparCudaDType (cuda_kernels.hpp:10-15). */
+enum SparHipDType {
+  SPAR_HIP_FLOAT32 = 0,
+  SPAR_HIP_FLOAT64 = 1,
+  SPAR_HIP_INT32 = 2,
+  SPAR_HIP_INT64 = 3,
+};
+
+/* Binary operations.  0-3 equal SparCudaBinaryOp (cuda_kernels.hpp:17-22).
+ * 4-9 are comparisons, which the reference does not have: they write 1 or 0
+ * in the input dtype (there is no Bool dtype, src/core/dtype.cppm:8-13) and
+ * follow IEEE-754 ordered comparison, so NaN compares unequal to everything. */
+enum SparHipBinaryOp {
+  SPAR_HIP_ADD = 0,
+  SPAR_HIP_SUBTRACT = 1,
+  SPAR_HIP_MULTIPLY = 2,
+  SPAR_HIP_DIVIDE = 3,
+  SPAR_HIP_EQUAL = 4,
+  SPAR_HIP_NOT_EQUAL = 5,
+  SPAR_HIP_LESS = 6,
+  SPAR_HIP_LESS_EQUAL = 7,
+  SPAR_HIP_GREATER = 8,
+  SPAR_HIP_GREATER_EQUAL = 9,
+};
+
+/* Unary operations.  0-7 equal SparCudaUnaryOp (cuda_kernels.hpp:24-33).
+ * TANH and GELU are additions: gelu(x) = 0.5 * x * erfc(-x * (1/sqrt(2))),
+ * evaluated in double precision and rounded once to the element type. */
+enum SparHipUnaryOp {
+  SPAR_HIP_NEGATE = 0,
+  SPAR_HIP_SQUARE = 1,
+  SPAR_HIP_RECIPROCAL = 2,
+  SPAR_HIP_EXP = 3,
+  SPAR_HIP_LOG = 4,
+  SPAR_HIP_SQRT = 5,
+  SPAR_HIP_SIGMOID = 6,
+  SPAR_HIP_SILU = 7,
+  SPAR_HIP_TANH = 8,
+  SPAR_HIP_GELU = 9,
+};
+
+/* Reductions.  0-2 equal SparCudaReductionOp (cuda_kernels.hpp:35-39).
+ * ARGMAX writes int64 indices.  MAX and ARGMAX share one rule: a NaN wins
+ * (the first NaN in logical order), otherwise the first element equal to the
+ * maximum wins, so max(-0.0, +0.0) is -0.0 when -0.0 comes first — the result
+ * of the reference's sequential `value > result` scan (reduction.cpp:44-60). */
+enum SparHipReductionOp {
+  SPAR_HIP_SUM = 0,
+  SPAR_HIP_MEAN = 1,
+  SPAR_HIP_MAX = 2,
+  SPAR_HIP_ARGMAX = 3,
+};
+
+/* Replaces struct SparCudaStatus (cuda_kernels.hpp:41-44). */
+struct SparHipStatus {
+  int code;
+  int hip_error;
+};
+
+/* Allocator statistics for one device (no reference counterpart: the
+ * reference called cudaMalloc/cudaFree per tensor, cuda_runtime.cppm:121-159). */
+struct SparHipMemoryStats {
+  uint64_t bytes_in_use;      /* bytes handed out and not yet returned      */
+  uint64_t bytes_cached;      /* bytes held in free lists for reuse          */
+  uint64_t bytes_reserved;    /* bytes obtained from hipMalloc in total      */
+  uint64_t device_allocations;/* number of hipMalloc calls made              */
+  uint64_t cache_hits;        /* allocations served from a free list         */
+};
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Number of visible HIP devices (replaces the cudaGetDeviceCount check in
+ * spar::detail::cuda::validate_device, cuda_runtime.cppm:109-120). */
+struct SparHipStatus spar_hip_device_count(int* count);
+
+/* Caching device allocator: size-classed free lists over hipMalloc, reuse is
+ * stream-ordered on the backend's single stream.  Replaces cuda::allocate /
+ * cuda::deallocate (cuda_runtime.cppm:121-159).  bytes == 0 yields NULL. */
+struct SparHipStatus spar_hip_allocate(void** pointer, uint64_t bytes, int device);
+struct SparHipStatus spar_hip_deallocate(void* pointer, int device);
+/* Synchronises the device and returns every cached block to the driver. */
+struct SparHipStatus spar_hip_empty_cache(int device);
+struct SparHipStatus spar_hip_memory_stats(struct SparHipMemoryStats* stats, int device);
+
+/* Zero-fill of device bytes with a fill kernel (cuda::zero,
+ * cuda_runtime.cppm:161-174, used cudaMemset). */
+struct SparHipStatus spar_hip_zero(void* destination, uint64_t bytes, int device);
+
+/* Copies (cuda_runtime.cppm:176-237).  Host<->device copies return after the
+ * copy has completed (the host buffer may be reused at once); device-to-device
+ * copies are stream-ordered.  Cross-device copies use hipMemcpyPeerAsync. */
+struct SparHipStatus spar_hip_copy_host_to_device(void* destination, const void* source,
+                                                  uint64_t bytes, int device);
+struct SparHipStatus spar_hip_copy_device_to_host(void* destination, const void* source,
+                                                  uint64_t bytes, int device);
+struct SparHipStatus spar_hip_copy_device_to_device(void* destination, int destination_device,
+                                                    const void* source, int source_device,
+                                                    uint64_t bytes);
+
+/* Waits for all work enqueued on the backend's stream for `device`. */
+struct SparHipStatus spar_hip_synchronize(int device);
+/* Returns the backend's hipStream_t for `device` (for interoperation). */
+struct SparHipStatus spar_hip_stream(void** stream, int device);
+
+/* Event timing on the backend's stream (no reference counterpart; Spar has no
+ * tracing).  Elapsed time is in milliseconds between two recorded events. */
+struct SparHipStatus spar_hip_event_create(void** event);
+struct SparHipStatus spar_hip_event_destroy(void* event);
+struct SparHipStatus spar_hip_event_record(void* event, int device);
+struct SparHipStatus spar_hip_event_elapsed(float* milliseconds, void* start, void* stop);
+
+/* Replaces spar_cuda_error_string (cuda_kernels.hpp:129). */
+const char* spar_hip_error_string(int hip_error);
+
+/* ------------------------------------------------ contiguous elementwise */
+
+/* output[i] = left[i] op right[i] over `count` contiguous elements.
+ * Replaces spar_cuda_launch_binary (cuda_kernels.hpp:46-47); comparisons
+ * (ops 4-9) are additions. */
+struct SparHipStatus spar_hip_launch_binary(void* output, const void* left, const void* right,
+                                            uint64_t count, int dtype, int operation, int device);
+
+/* output[i] = input[i] op (T)scalar.  For float32 the double scalar is
+ * rounded to float before the operation, as the CPU path does
+ * (src/ops/scalar.cpp:40-47).  Replaces spar_cuda_launch_scalar
+ * (cuda_kernels.hpp:48-49). */
+struct SparHipStatus spar_hip_launch_scalar(void* output, const void* input, uint64_t count,
+                                            int dtype, int operation, double scalar, int device);
+
+/* output[i] = op(input[i]).  Replaces spar_cuda_launch_unary
+ * (cuda_kernels.hpp:50-51); TANH and GELU are additions. */
+struct SparHipStatus spar_hip_launch_unary(void* output, const void* input, uint64_t count,
+                                           int dtype, int operation, int device);
+
+/* output[i] = scalar[0] / (T)divisor with scalar a device pointer to one
+ * element.  Used by sum backward (divisor 1) and mean backward (divisor n).
+ * Replaces spar_cuda_launch_fill_from_scalar (cuda_kernels.hpp:85-87), whose
+ * `scale` argument multiplied by a rounded reciprocal; the divisor form
+ * reproduces the CPU path's `g / (float)n` (src/ops/reduction.cpp:263-277). */
+struct SparHipStatus spar_hip_launch_fill_from_scalar(void* output, const void* scalar,
+                                                      uint64_t count, int dtype, double divisor,
+                                                      int device);
+
+/* output[i] = (T)value for a host value (ones/full on the device,
+ * src/core/tensor.cppm:168-178 staged these through the host). */
+struct SparHipStatus spar_hip_launch_fill(void* output, uint64_t count, int dtype, double value,
+                                          int device);
+
+/* destination[i] += source[i].  Replaces spar_cuda_launch_add_in_place
+ * (cuda_kernels.hpp:88-89). */
+struct SparHipStatus spar_hip_launch_add_in_place(void* destination, const void* source,
+                                                  uint64_t count, int dtype, int device);
+
+/* ------------------------------------------------------- strided layouts */
+
+/* Materialises a strided view (rank, extents, strides, storage_offset) into a
+ * contiguous row-major destination.  element_size is 4 or 8.  Same arguments
+ * as spar_cuda_launch_strided_copy (cuda_kernels.hpp:90-94); rank must be
+ * <= SPAR_HIP_MAX_RANK. */
+struct SparHipStatus spar_hip_launch_strided_copy(void* destination, const void* source,
+                                                  uint64_t rank, const uint64_t* extents,
+                                                  const uint64_t* strides,
+                                                  uint64_t storage_offset, uint64_t count,
+                                                  uint64_t element_size, int device);
+
+/* Binary op over the broadcast shape `extents` (rank dims) without
+ * materialising either operand: each operand is read through its own strides
+ * (0 on broadcast axes) and storage offset; output is contiguous row-major.
+ * Replaces the expand().contiguous() + binary chain of the reference
+ * (src/ops/elementwise.cpp:26-31). */
+struct SparHipStatus spar_hip_launch_strided_binary(void* output, const void* left,
+                                                    const uint64_t* left_strides,
+                                                    uint64_t left_offset, const void* right,
+                                                    const uint64_t* right_strides,
+                                                    uint64_t right_offset, uint64_t rank,
+                                                    const uint64_t* extents, int dtype,
+                                                    int operation, int device);
+
+/* ------------------------------------------------------------ reductions */
+
+/* Full reduction of `count` contiguous elements to one element (ARGMAX: one
+ * int64).  Replaces spar_cuda_launch_reduction (cuda_kernels.hpp:52-53).  A
+ * grid of partial reductions is combined by a second pass in a fixed order,
+ * so results are deterministic.  MEAN/MAX/ARGMAX reject count == 0. */
+struct SparHipStatus spar_hip_launch_reduction(void* output, const void* input, uint64_t count,
+                                               int dtype, int operation, int device);
+
+/* Reduces each of `row_count` contiguous rows of `reduction_count` elements.
+ * Replaces spar_cuda_launch_row_reduction (cuda_kernels.hpp:54-56), which
+ * accepted SUM/MEAN only; MAX and ARGMAX (int64 output) are additions. */
+struct SparHipStatus spar_hip_launch_row_reduction(void* output, const void* input,
+                                                   uint64_t row_count, uint64_t reduction_count,
+                                                   int dtype, int operation, int device);
+
+/* Axis reduction of a strided view without materialising it.  The input view
+ * is (rank, extents, strides, storage_offset); reduced_mask bit k set means
+ * axis k is reduced.  The output is the contiguous tensor of the kept axes in
+ * order (keepdim only changes the shape, not the layout).  MEAN divides the
+ * sum by (T)(product of the reduced extents).  ARGMAX writes int64 indices
+ * into the flattened reduced sub-space (row-major over the reduced axes).
+ * Replaces the permute().contiguous() + row_reduction chain
+ * (src/ops/reduction.cpp:167-185). */
+struct SparHipStatus spar_hip_launch_axis_reduction(void* output, const void* input,
+                                                    uint64_t rank, const uint64_t* extents,
+                                                    const uint64_t* strides,
+                                                    uint64_t storage_offset,
+                                                    uint32_t reduced_mask, int dtype,
+                                                    int operation, int device);
+
+/* Sums a contiguous gradient of shape gradient_extents over its broadcast
+ * axes into the contiguous original shape (right-aligned numpy rules).  The
+ * destination is overwritten (the reference required a zeroed destination and
+ * used atomicAdd, cuda_kernels.cu:287-311; this is deterministic).  Same
+ * arguments as spar_cuda_launch_broadcast_reduce (cuda_kernels.hpp:95-98). */
+struct SparHipStatus spar_hip_launch_broadcast_reduce(
+    void* destination, const void* gradient, uint64_t gradient_rank,
+    const uint64_t* gradient_extents, uint64_t original_rank, const uint64_t* original_extents,
+    const uint64_t* original_strides, uint64_t count, int dtype, int device);
+
+/* Fused broadcast_reduce of a product: destination = reduce_to_original(
+ * gradient * factor) where gradient and factor are contiguous with
+ * gradient_extents.  Each product is rounded to T before it is summed, exactly
+ * like multiply() followed by reduce_gradient_to_shape() in the multiply
+ * backward rule (src/ops/elementwise.cpp:159-166), but in one HBM pass. */
+struct SparHipStatus spar_hip_launch_multiply_reduce(
+    void* destination, const void* gradient, const void* factor, uint64_t gradient_rank,
+    const uint64_t* gradient_extents, uint64_t original_rank, const uint64_t* original_extents,
+    uint64_t count, int dtype, int device);
+
+/* --------------------------------------------------------------- softmax */
+
+/* Softmax (logarithmic = 0) or log-softmax (1) over slices (outer, axis,
+ * inner) of a contiguous input, with the reference's special cases: a slice
+ * with NaN or with only -inf becomes all NaN; k > 0 entries of +inf share the
+ * mass (1/k, log: -log k) and the rest are 0 (log: -inf).  undefined_slices
+ * (int32, outer*inner) is set to 1 for those slices.  Replaces
+ * spar_cuda_launch_probability_forward (cuda_kernels.hpp:57-60). */
+struct SparHipStatus spar_hip_launch_probability_forward(void* output, int32_t* undefined_slices,
+                                                         const void* input, uint64_t outer,
+                                                         uint64_t axis_extent, uint64_t inner,
+                                                         int dtype, int logarithmic, int device);
+
+/* Backward of the above: softmax dx = y * (g - sum(g*y)); log-softmax
+ * dx = g - exp(lp) * sum(g); undefined slices become NaN.  Replaces
+ * spar_cuda_launch_probability_backward (cuda_kernels.hpp:61-63). */
+struct SparHipStatus spar_hip_launch_probability_backward(
+    void* output, const void* gradient, const void* saved_output, const int32_t* undefined_slices,
+    uint64_t outer, uint64_t axis_extent, uint64_t inner, int dtype, int logarithmic, int device);
+
+/* ------------------------------------------------------ random generation */
+
+/* Fills `count` contiguous elements with Spar's SplitMix64 stream for `seed`
+ * (src/core/random.cpp:22-38): element i uses draw i of Random(seed).
+ * UNIFORM: low + (high-low) * uniform (random.cpp:40-80).  The device result is
+ * bit-identical to the host generator for float32 and float64. */
+struct SparHipStatus spar_hip_random_uniform(void* output, uint64_t count, int dtype,
+                                             uint64_t seed, double low, double high, int device);
+
+/* Normal samples by the Box-Muller transform on uniform_double draws (the
+ * reference has no normal sampler): pair k uses draws 2k and 2k+1,
+ * r = sqrt(-2 log(1 - u0)), element 2k = mean + stddev * r * cos(2 pi u1),
+ * element 2k+1 = mean + stddev * r * sin(2 pi u1), computed in double and
+ * rounded to T.  Same definition as the host spar::random_normal; the device
+ * log/sin/cos may differ from the host libm in the last bit of the double,
+ * so values can differ from the host generator by one float32 ulp. */
+struct SparHipStatus spar_hip_random_normal(void* output, uint64_t count, int dtype,
+                                            uint64_t seed, double mean, double stddev,
+                                            int device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPAR_HIP_H */

@@ -1,0 +1,195 @@
+// Shared device-side and launcher-side helpers for the gfx950 backend.
+//
+// Every .hip translation unit of the backend includes this header.  It holds
+// the status convention (mirrors src/backend/cuda_kernels.cu:12-22), the
+// per-device stream/launch bookkeeping, geometry structs passed to kernels by
+// value, fast 32-bit division by invariant integers, and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "spar_hip.h"
+
+namespace spar_hip {
+
+constexpr int kMaxRank = SPAR_HIP_MAX_RANK;
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ status
+
+inline SparHipStatus ok() { return {0, static_cast<int>(hipSuccess)}; }
+inline SparHipStatus invalid() { return {1, static_cast<int>(hipErrorInvalidValue)}; }
+inline SparHipStatus runtime(hipError_t error) { return {2, static_cast<int>(error)}; }
+
+inline bool valid_float_dtype(int dtype) {
+  return dtype == SPAR_HIP_FLOAT32 || dtype == SPAR_HIP_FLOAT64;
+}
+
+// --------------------------------------------------------- device context
+
+// Per-device state owned by the runtime TU (runtime.hip).  Launchers call
+// `enter(device)` which makes `device` current for the calling thread,
+// creates its stream on first use, and restores the previous device when the
+// returned guard goes out of scope.
+struct DeviceGuard {
+  int previous = -1;
+  bool changed = false;
+  hipStream_t stream = nullptr;
+  hipError_t error = hipSuccess;
+  int multiprocessors = 256;
+  ~DeviceGuard();
+};
+
+// Fills `guard`; returns hipSuccess or the failing HIP error.
+hipError_t enter(int device, DeviceGuard& guard);
+
+// Checks hipGetLastError after a launch and converts it to a status.
+SparHipStatus finish(const DeviceGuard& guard);
+
+// Temporary device memory from the caching allocator, for kernel scratch.
+// Freed blocks return to the free list immediately; since every launch is on
+// the same stream, a later reuse is ordered after the kernel that used it.
+hipError_t scratch_allocate(void** pointer, uint64_t bytes, int device);
+void scratch_release(void* pointer, int device);
+
+// ------------------------------------------------------------- geometry
+
+// Fast unsigned division by an invariant divisor, following Granlund &
+// Montgomery, "Division by Invariant Integers using Multiplication" (PLDI
+// 1994): with s = ceil(log2 d) and magic = floor(2^32 (2^s - d) / d) + 1,
+// q = (mulhi(n, magic) + n) >> s for 1 <= d <= 2^31 - 1 and n < 2^31.
+// Launchers use it only when every dividend is below 2^31.
+struct FastDiv {
+  uint32_t divisor;
+  uint32_t magic;
+  uint32_t shift;
+
+  __host__ __device__ void init(uint32_t d) {
+    divisor = d;
+    uint32_t s = 0;
+    while (s < 32 && (uint64_t{1} << s) < d) ++s;
+    shift = s;
+    const uint64_t numerator = (uint64_t{1} << 32) * ((uint64_t{1} << s) - d);
+    magic = static_cast<uint32_t>(numerator / d + 1);
+  }
+
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint64_t hi = __umulhi(n, magic);
+    return static_cast<uint32_t>((hi + n) >> shift);
+  }
+};
+
+// Largest element count for which 32-bit index arithmetic is used.
+constexpr uint64_t kIndex32Limit = (uint64_t{1} << 31) - 1;
+
+// A strided operand of up to kMaxRank coalesced dimensions, passed by value.
+struct StridedGeometry {
+  int rank;
+  uint64_t extents[kMaxRank];
+  uint64_t strides[kMaxRank];
+  uint64_t offset;
+};
+
+// --------------------------------------------------------- wave reductions
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T value) {
+#pragma unroll
+  for (int lane_mask = kWave / 2; lane_mask > 0; lane_mask >>= 1) {
+    value += __shfl_xor(value, lane_mask, kWave);
+  }
+  return value;
+}
+
+// (value, index) pair under Spar's max rule: NaN beats everything (smaller
+// index first among NaNs), otherwise the larger value wins and equal values
+// keep the smaller index, so the result is the first occurrence of the
+// maximum in logical order.
+template <typename T>
+struct ArgMax {
+  T value;
+  int64_t index;
+};
+
+template <typename T>
+__device__ __forceinline__ bool argmax_better(T value, int64_t index, T best, int64_t best_index) {
+  const bool nan_v = value != value;
+  const bool nan_b = best != best;
+  if (nan_v || nan_b) {
+    if (nan_v && nan_b) return index < best_index;
+    return nan_v;
+  }
+  if (value > best) return true;
+  if (value == best) return index < best_index;
+  return false;
+}
+
+template <typename T>
+__device__ __forceinline__ void argmax_update(ArgMax<T>& best, T value, int64_t index) {
+  if (argmax_better(value, index, best.value, best.index)) {
+    best.value = value;
+    best.index = index;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ ArgMax<T> wave_argmax(ArgMax<T> best) {
+#pragma unroll
+  for (int lane_mask = kWave / 2; lane_mask > 0; lane_mask >>= 1) {
+    const T other_value = __shfl_xor(best.value, lane_mask, kWave);
+    const int64_t other_index = __shfl_xor(best.index, lane_mask, kWave);
+    argmax_update(best, other_value, other_index);
+  }
+  return best;
+}
+
+// Identity element for the argmax reduction: loses to every real element.
+template <typename T>
+__device__ __forceinline__ ArgMax<T> argmax_identity() {
+  return ArgMax<T>{-__builtin_huge_valf(), INT64_MAX};
+}
+
+template <>
+__device__ __forceinline__ ArgMax<double> argmax_identity<double>() {
+  return ArgMax<double>{-__builtin_huge_val(), INT64_MAX};
+}
+
+// --------------------------------------------------------------- vectors
+
+template <typename T> struct Vec16;
+template <> struct Vec16<float> { using type = float4; static constexpr int width = 4; };
+template <> struct Vec16<double> { using type = double2; static constexpr int width = 2; };
+
+template <typename T>
+__device__ __forceinline__ T vec_get(const typename Vec16<T>::type& v, int i);
+template <>
+__device__ __forceinline__ float vec_get<float>(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+template <>
+__device__ __forceinline__ double vec_get<double>(const double2& v, int i) {
+  return i == 0 ? v.x : v.y;
+}
+
+template <typename T>
+__device__ __forceinline__ void vec_set(typename Vec16<T>::type& v, int i, T x);
+template <>
+__device__ __forceinline__ void vec_set<float>(float4& v, int i, float x) {
+  if (i == 0) v.x = x; else if (i == 1) v.y = x; else if (i == 2) v.z = x; else v.w = x;
+}
+template <>
+__device__ __forceinline__ void vec_set<double>(double2& v, int i, double x) {
+  if (i == 0) v.x = x; else v.y = x;
+}
+
+inline bool aligned16(const void* pointer) {
+  return (reinterpret_cast<uintptr_t>(pointer) & 15U) == 0;
+}
+
+inline uint32_t ceil_div_u32(uint64_t a, uint64_t b) {
+  return static_cast<uint32_t>((a + b - 1) / b);
+}
+
+}  // namespace spar_hip

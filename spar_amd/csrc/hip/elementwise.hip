@@ -1,0 +1,420 @@
+// Contiguous elementwise kernels: binary, compare, scalar, unary, fills,
+// gradient accumulation and the seeded generators.
+//
+// Replaces kernels K1-K3, K9, K10 of src/backend/cuda_kernels.cu (:113-191,
+// :249-266).  Design for CDNA4: each 256-thread workgroup streams one tile of
+// 256 x UNROLL 16-byte vectors per operand, issuing every load of the tile
+// before the first store so that UNROLL independent 128-bit loads per lane
+// are in flight; the tiles are laid out so consecutive lanes touch
+// consecutive 16-byte words (fully coalesced 1 KiB per wave per load).  The
+// grid has one workgroup per tile (tens of thousands at the benchmark shapes,
+// far more than the 256 CUs), and a tile loop keeps launches within the grid
+// limit for any size.  Pointers that are not 16-byte aligned take a scalar
+// grid-stride kernel.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace spar_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
+
+template <typename T, typename F>
+__global__ void __launch_bounds__(kThreads)
+    map1_vec_kernel(T* out, const T* in, uint64_t count, F f) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  const uint64_t vectors = count / W;
+  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  const V* in_v = reinterpret_cast<const V*>(in);
+  V* out_v = reinterpret_cast<V*>(out);
+  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < vectors;
+       base += static_cast<uint64_t>(gridDim.x) * tile) {
+    V r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      if (i < vectors) r[u] = in_v[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      if (i < vectors) {
+        V o;
+#pragma unroll
+        for (int k = 0; k < W; ++k) vec_set<T>(o, k, f(vec_get<T>(r[u], k)));
+        out_v[i] = o;
+      }
+    }
+  }
+  if (blockIdx.x == 0) {
+    const uint64_t i = vectors * W + threadIdx.x;
+    if (i < count) out[i] = f(in[i]);
+  }
+}
+
+template <typename T, typename F>
+__global__ void __launch_bounds__(kThreads)
+    map2_vec_kernel(T* out, const T* a, const T* b, uint64_t count, F f) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  const uint64_t vectors = count / W;
+  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  const V* a_v = reinterpret_cast<const V*>(a);
+  const V* b_v = reinterpret_cast<const V*>(b);
+  V* out_v = reinterpret_cast<V*>(out);
+  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < vectors;
+       base += static_cast<uint64_t>(gridDim.x) * tile) {
+    V ra[kUnroll];
+    V rb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      if (i < vectors) {
+        ra[u] = a_v[i];
+        rb[u] = b_v[i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      if (i < vectors) {
+        V o;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          vec_set<T>(o, k, f(vec_get<T>(ra[u], k), vec_get<T>(rb[u], k)));
+        }
+        out_v[i] = o;
+      }
+    }
+  }
+  if (blockIdx.x == 0) {
+    const uint64_t i = vectors * W + threadIdx.x;
+    if (i < count) out[i] = f(a[i], b[i]);
+  }
+}
+
+template <typename T, typename F>
+__global__ void __launch_bounds__(kThreads)
+    map1_scalar_kernel(T* out, const T* in, uint64_t count, F f) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += stride) {
+    out[i] = f(in[i]);
+  }
+}
+
+template <typename T, typename F>
+__global__ void __launch_bounds__(kThreads)
+    map2_scalar_kernel(T* out, const T* a, const T* b, uint64_t count, F f) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += stride) {
+    out[i] = f(a[i], b[i]);
+  }
+}
+
+uint32_t vector_grid(uint64_t count, int width) {
+  const uint64_t vectors = count / static_cast<uint64_t>(width);
+  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  uint64_t blocks = (vectors + tile - 1) / tile;
+  if (blocks == 0) blocks = 1;
+  if (blocks > kMaxGrid) blocks = kMaxGrid;
+  return static_cast<uint32_t>(blocks);
+}
+
+uint32_t scalar_grid(uint64_t count, const DeviceGuard& guard) {
+  uint64_t blocks = (count + kThreads - 1) / kThreads;
+  const uint64_t cap = static_cast<uint64_t>(guard.multiprocessors) * 16;
+  if (blocks > cap) blocks = cap;
+  if (blocks == 0) blocks = 1;
+  return static_cast<uint32_t>(blocks);
+}
+
+template <typename T, typename F>
+void launch_map1(T* out, const T* in, uint64_t count, F f, const DeviceGuard& guard) {
+  if (aligned16(out) && aligned16(in)) {
+    map1_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
+        out, in, count, f);
+  } else {
+    map1_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        out, in, count, f);
+  }
+}
+
+template <typename T, typename F>
+void launch_map2(T* out, const T* a, const T* b, uint64_t count, F f, const DeviceGuard& guard) {
+  if (aligned16(out) && aligned16(a) && aligned16(b)) {
+    map2_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
+        out, a, b, count, f);
+  } else {
+    map2_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        out, a, b, count, f);
+  }
+}
+
+// Writes a constant; the input pointer of map1 is the output itself and is
+// never read through.
+template <typename T>
+struct ConstantOp {
+  T value;
+  __device__ __forceinline__ T operator()(T) const { return value; }
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    fill_from_scalar_kernel(T* out, const T* scalar, uint64_t count, T divisor, bool divide) {
+  const T value = divide ? scalar[0] / divisor : scalar[0];
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += stride) {
+    out[i] = value;
+  }
+}
+
+// SplitMix64 draw `index` (0-based) of Random(seed): the generator adds the
+// golden-ratio increment before mixing (src/core/random.cpp:22-28), so draw i
+// mixes seed + (i + 1) * increment.
+__device__ __forceinline__ uint64_t splitmix_draw(uint64_t seed, uint64_t index) {
+  uint64_t value = seed + (index + 1) * 0x9E3779B97F4A7C15ULL;
+  value = (value ^ (value >> 30U)) * 0xBF58476D1CE4E5B9ULL;
+  value = (value ^ (value >> 27U)) * 0x94D049BB133111EBULL;
+  return value ^ (value >> 31U);
+}
+
+__device__ __forceinline__ double uniform_double_draw(uint64_t seed, uint64_t index) {
+  return static_cast<double>(splitmix_draw(seed, index) >> 11U) / 9007199254740992.0;
+}
+
+__global__ void __launch_bounds__(kThreads)
+    uniform_f32_kernel(float* out, uint64_t count, uint64_t seed, float low, float width) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += stride) {
+    const float u = static_cast<float>(splitmix_draw(seed, i) >> 40U) / 16777216.0F;
+    out[i] = low + width * u;
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+    uniform_f64_kernel(double* out, uint64_t count, uint64_t seed, double low, double width) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += stride) {
+    out[i] = low + width * uniform_double_draw(seed, i);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    normal_kernel(T* out, uint64_t count, uint64_t seed, double mean, double stddev) {
+  const uint64_t pairs = (count + 1) / 2;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  const double two_pi = 6.283185307179586476925286766559;
+  for (uint64_t k = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; k < pairs;
+       k += stride) {
+    const double u0 = uniform_double_draw(seed, 2 * k);
+    const double u1 = uniform_double_draw(seed, 2 * k + 1);
+    const double radius = sqrt(-2.0 * log(1.0 - u0));
+    const double angle = two_pi * u1;
+    out[2 * k] = static_cast<T>(mean + stddev * (radius * cos(angle)));
+    if (2 * k + 1 < count) out[2 * k + 1] = static_cast<T>(mean + stddev * (radius * sin(angle)));
+  }
+}
+
+}  // namespace
+}  // namespace spar_hip
+
+using namespace spar_hip;
+
+extern "C" SparHipStatus spar_hip_launch_binary(void* output, const void* left, const void* right,
+                                                uint64_t count, int dtype, int operation,
+                                                int device) {
+  if (!valid_float_dtype(dtype) || operation < SPAR_HIP_ADD ||
+      operation > SPAR_HIP_GREATER_EQUAL ||
+      (count != 0 && (output == nullptr || left == nullptr || right == nullptr))) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  dispatch_binary(operation, [&](auto op) {
+    if (dtype == SPAR_HIP_FLOAT32) {
+      launch_map2(static_cast<float*>(output), static_cast<const float*>(left),
+                  static_cast<const float*>(right), count, op, guard);
+    } else {
+      launch_map2(static_cast<double*>(output), static_cast<const double*>(left),
+                  static_cast<const double*>(right), count, op, guard);
+    }
+  });
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_scalar(void* output, const void* input, uint64_t count,
+                                                int dtype, int operation, double scalar,
+                                                int device) {
+  if (!valid_float_dtype(dtype) || operation < SPAR_HIP_ADD || operation > SPAR_HIP_DIVIDE ||
+      (count != 0 && (output == nullptr || input == nullptr))) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  dispatch_binary(operation, [&](auto op) {
+    using Op = decltype(op);
+    if (dtype == SPAR_HIP_FLOAT32) {
+      launch_map1(static_cast<float*>(output), static_cast<const float*>(input), count,
+                  BindRight<Op, float>{op, static_cast<float>(scalar)}, guard);
+    } else {
+      launch_map1(static_cast<double*>(output), static_cast<const double*>(input), count,
+                  BindRight<Op, double>{op, scalar}, guard);
+    }
+  });
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_unary(void* output, const void* input, uint64_t count,
+                                               int dtype, int operation, int device) {
+  if (!valid_float_dtype(dtype) || operation < SPAR_HIP_NEGATE || operation > SPAR_HIP_GELU ||
+      (count != 0 && (output == nullptr || input == nullptr))) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  dispatch_unary(operation, [&](auto op) {
+    if (dtype == SPAR_HIP_FLOAT32) {
+      launch_map1(static_cast<float*>(output), static_cast<const float*>(input), count, op, guard);
+    } else {
+      launch_map1(static_cast<double*>(output), static_cast<const double*>(input), count, op,
+                  guard);
+    }
+  });
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_fill_from_scalar(void* output, const void* scalar,
+                                                          uint64_t count, int dtype,
+                                                          double divisor, int device) {
+  if (!valid_float_dtype(dtype) || scalar == nullptr || (count != 0 && output == nullptr) ||
+      !(divisor > 0.0)) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const bool divide = divisor != 1.0;
+  if (dtype == SPAR_HIP_FLOAT32) {
+    fill_from_scalar_kernel<float><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        static_cast<float*>(output), static_cast<const float*>(scalar), count,
+        static_cast<float>(divisor), divide);
+  } else {
+    fill_from_scalar_kernel<double><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        static_cast<double*>(output), static_cast<const double*>(scalar), count, divisor, divide);
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_fill(void* output, uint64_t count, int dtype,
+                                              double value, int device) {
+  if (!valid_float_dtype(dtype) && dtype != SPAR_HIP_INT32 && dtype != SPAR_HIP_INT64) {
+    return invalid();
+  }
+  if (count != 0 && output == nullptr) return invalid();
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  switch (dtype) {
+    case SPAR_HIP_FLOAT32: {
+      float* out = static_cast<float*>(output);
+      launch_map1(out, static_cast<const float*>(out), count,
+                  ConstantOp<float>{static_cast<float>(value)}, guard);
+      break;
+    }
+    case SPAR_HIP_FLOAT64: {
+      double* out = static_cast<double*>(output);
+      launch_map1(out, static_cast<const double*>(out), count, ConstantOp<double>{value}, guard);
+      break;
+    }
+    case SPAR_HIP_INT32: {
+      int32_t* out = static_cast<int32_t*>(output);
+      map1_scalar_kernel<int32_t, ConstantOp<int32_t>>
+          <<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+              out, out, count, ConstantOp<int32_t>{static_cast<int32_t>(value)});
+      break;
+    }
+    default: {
+      int64_t* out = static_cast<int64_t*>(output);
+      map1_scalar_kernel<int64_t, ConstantOp<int64_t>>
+          <<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+              out, out, count, ConstantOp<int64_t>{static_cast<int64_t>(value)});
+      break;
+    }
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_add_in_place(void* destination, const void* source,
+                                                      uint64_t count, int dtype, int device) {
+  if (!valid_float_dtype(dtype) || (count != 0 && (destination == nullptr || source == nullptr))) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (dtype == SPAR_HIP_FLOAT32) {
+    float* dst = static_cast<float*>(destination);
+    launch_map2(dst, static_cast<const float*>(dst), static_cast<const float*>(source), count,
+                AddOp{}, guard);
+  } else {
+    double* dst = static_cast<double*>(destination);
+    launch_map2(dst, static_cast<const double*>(dst), static_cast<const double*>(source), count,
+                AddOp{}, guard);
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_random_uniform(void* output, uint64_t count, int dtype,
+                                                 uint64_t seed, double low, double high,
+                                                 int device) {
+  if (!valid_float_dtype(dtype) || !(low < high) || (count != 0 && output == nullptr)) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (dtype == SPAR_HIP_FLOAT32) {
+    // random.cpp:59-63: low and width are rounded to float once.
+    uniform_f32_kernel<<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        static_cast<float*>(output), count, seed, static_cast<float>(low),
+        static_cast<float>(high - low));
+  } else {
+    uniform_f64_kernel<<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        static_cast<double*>(output), count, seed, low, high - low);
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_random_normal(void* output, uint64_t count, int dtype,
+                                                uint64_t seed, double mean, double stddev,
+                                                int device) {
+  if (!valid_float_dtype(dtype) || !(stddev >= 0.0) || (count != 0 && output == nullptr)) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const uint64_t pairs = (count + 1) / 2;
+  if (dtype == SPAR_HIP_FLOAT32) {
+    normal_kernel<float><<<scalar_grid(pairs, guard), kThreads, 0, guard.stream>>>(
+        static_cast<float*>(output), count, seed, mean, stddev);
+  } else {
+    normal_kernel<double><<<scalar_grid(pairs, guard), kThreads, 0, guard.stream>>>(
+        static_cast<double*>(output), count, seed, mean, stddev);
+  }
+  return finish(guard);
+}

@@ -1,0 +1,780 @@
+// Reductions: full, row (reduced axis contiguous), column (kept axis
+// contiguous, reduced axis strided), generic; broadcast-gradient sums and the
+// fused product-sum used by the multiply backward rule.
+//
+// Replaces K4-K6 and K12 of the reference (src/backend/cuda_kernels.cu:193-247,
+// :287-311, :457-480) and the permute().contiguous() staging of
+// src/ops/reduction.cpp:167-185 and src/core/tensor.cpp:604-623.
+//
+// CDNA4 design:
+//   * row reduction: a 256-thread workgroup per row segment, 128-bit loads,
+//     per-lane accumulation, wave64 butterfly (DPP/ds_swizzle via __shfl_xor)
+//     and one LDS exchange across the 4 waves.  Long rows with few outputs
+//     (a full reduction is one row) are split over many workgroups and
+//     finished by a second, fixed-order pass (deterministic, no atomics);
+//   * column reduction: lanes own 4 adjacent output columns (one float4),
+//     rows are split across workgroups so that 8192 columns still fill 256
+//     CUs; partials [outer, splits, inner] are combined in split order;
+//   * argmax/max carry (value, index) pairs with the rule "NaN first, then
+//     larger value, then smaller index", which reproduces the first-occurrence
+//     result of a sequential scan bit for bit (including -0.0 vs +0.0).
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "layout.hpp"
+
+namespace spar_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
+
+enum class Kind { Sum, Max };
+
+// Accumulator: a running sum, or a (value, index) pair for max/argmax.
+template <typename T, Kind K> struct Acc;
+
+template <typename T> struct Acc<T, Kind::Sum> {
+  T value;
+  __device__ __forceinline__ void init() { value = T(0); }
+  __device__ __forceinline__ void add(T x, int64_t) { value += x; }
+  __device__ __forceinline__ void merge(const Acc& other) { value += other.value; }
+  __device__ __forceinline__ void wave_reduce() { value = wave_sum(value); }
+};
+
+template <typename T> struct Acc<T, Kind::Max> {
+  ArgMax<T> best;
+  __device__ __forceinline__ void init() { best = argmax_identity<T>(); }
+  __device__ __forceinline__ void add(T x, int64_t index) { argmax_update(best, x, index); }
+  __device__ __forceinline__ void merge(const Acc& other) {
+    argmax_update(best, other.best.value, other.best.index);
+  }
+  __device__ __forceinline__ void wave_reduce() { best = wave_argmax(best); }
+};
+
+// Reads one element: the input itself, or the product of two inputs that
+// share strides (each product rounded to T, as multiply() would store it).
+template <typename T, int NIN>
+__device__ __forceinline__ T load_value(const T* a, const T* b, uint64_t offset) {
+  if constexpr (NIN == 1) {
+    return a[offset];
+  } else {
+    return a[offset] * b[offset];
+  }
+}
+
+template <typename T, int NIN>
+__device__ __forceinline__ typename Vec16<T>::type load_vector(const T* a, const T* b,
+                                                               uint64_t offset) {
+  using V = typename Vec16<T>::type;
+  V va = *reinterpret_cast<const V*>(a + offset);
+  if constexpr (NIN == 2) {
+    const V vb = *reinterpret_cast<const V*>(b + offset);
+#pragma unroll
+    for (int k = 0; k < Vec16<T>::width; ++k) {
+      vec_set<T>(va, k, vec_get<T>(va, k) * vec_get<T>(vb, k));
+    }
+  }
+  return va;
+}
+
+// Block-wide combine of per-thread accumulators; every thread gets the result.
+template <typename T, Kind K>
+__device__ __forceinline__ Acc<T, K> block_reduce(Acc<T, K> acc) {
+  __shared__ Acc<T, K> lds[kWaves];
+  acc.wave_reduce();
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  __syncthreads();
+  if (lane == 0) lds[wave] = acc;
+  __syncthreads();
+  Acc<T, K> total = lds[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) total.merge(lds[w]);
+  return total;
+}
+
+// Where a reduction writes: final outputs, or partials for a second pass.
+template <typename T>
+struct Sink {
+  T* values;            // final values (Sum/Mean/Max) or partial values
+  int64_t* indices;     // argmax output or partial indices (may be null)
+  int operation;        // SPAR_HIP_SUM / MEAN / MAX / ARGMAX
+  T mean_divisor;       // (T)count for MEAN
+  int partial;          // 1: write raw partials (values + indices)
+};
+
+template <typename T, Kind K>
+__device__ __forceinline__ void sink_write(const Sink<T>& sink, uint64_t slot, const Acc<T, K>& acc) {
+  if constexpr (K == Kind::Sum) {
+    T v = acc.value;
+    if (!sink.partial && sink.operation == SPAR_HIP_MEAN) v = v / sink.mean_divisor;
+    sink.values[slot] = v;
+  } else {
+    if (sink.partial) {
+      sink.values[slot] = acc.best.value;
+      sink.indices[slot] = acc.best.index;
+    } else if (sink.operation == SPAR_HIP_ARGMAX) {
+      sink.indices[slot] = acc.best.index;
+    } else {
+      sink.values[slot] = acc.best.value;
+    }
+  }
+}
+
+// Row offsets: the kept axes (innermost first) with their strides.
+struct RowMap {
+  int rank;
+  FastDiv divisors[kMaxRank];
+  uint64_t extents[kMaxRank];
+  uint64_t strides[kMaxRank];
+  uint64_t offset;
+  int index32;
+};
+
+__device__ __forceinline__ uint64_t row_offset(const RowMap& map, uint64_t row) {
+  uint64_t off = map.offset;
+  if (map.index32) {
+    uint32_t rem = static_cast<uint32_t>(row);
+#pragma unroll
+    for (int k = 0; k < kMaxRank; ++k) {
+      if (k < map.rank) {
+        const uint32_t q = map.divisors[k].div(rem);
+        off += static_cast<uint64_t>(rem - q * map.divisors[k].divisor) * map.strides[k];
+        rem = q;
+      }
+    }
+  } else {
+    uint64_t rem = row;
+    for (int k = 0; k < map.rank; ++k) {
+      const uint64_t q = rem / map.extents[k];
+      off += (rem - q * map.extents[k]) * map.strides[k];
+      rem = q;
+    }
+  }
+  return off;
+}
+
+// --------------------------------------------------------------- row kernel
+
+// Block b reduces segment (b % splits) of row (b / splits); the reduced axis
+// is contiguous (stride 1) with length n.  VEC: 16-byte loads (row starts and
+// segment length aligned to the vector width).
+template <typename T, Kind K, int NIN, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+    row_kernel(const T* a, const T* b, uint64_t rows, uint64_t n, uint64_t splits,
+               uint64_t segment, RowMap map, Sink<T> sink) {
+  constexpr int W = Vec16<T>::width;
+  for (uint64_t block = blockIdx.x; block < rows * splits; block += gridDim.x) {
+    const uint64_t row = block / splits;
+    const uint64_t split = block - row * splits;
+    const uint64_t begin = split * segment;
+    const uint64_t end = begin + segment < n ? begin + segment : n;
+    const uint64_t base = row_offset(map, row);
+    Acc<T, K> acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u].init();
+    if constexpr (VEC) {
+      const uint64_t step = static_cast<uint64_t>(kThreads) * W;
+      uint64_t i = begin + static_cast<uint64_t>(threadIdx.x) * W;
+      for (; i + 3 * step < end; i += 4 * step) {
+        typename Vec16<T>::type v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = load_vector<T, NIN>(a, b, base + i + u * step);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) {
+            acc[u].add(vec_get<T>(v[u], k), static_cast<int64_t>(i + u * step + k));
+          }
+        }
+      }
+      for (; i < end; i += step) {
+        const auto v = load_vector<T, NIN>(a, b, base + i);
+#pragma unroll
+        for (int k = 0; k < W; ++k) acc[0].add(vec_get<T>(v, k), static_cast<int64_t>(i + k));
+      }
+    } else {
+      for (uint64_t i = begin + threadIdx.x; i < end; i += kThreads) {
+        acc[0].add(load_value<T, NIN>(a, b, base + i), static_cast<int64_t>(i));
+      }
+    }
+    acc[0].merge(acc[1]);
+    acc[2].merge(acc[3]);
+    acc[0].merge(acc[2]);
+    const Acc<T, K> total = block_reduce<T, K>(acc[0]);
+    if (threadIdx.x == 0) sink_write<T, K>(sink, block, total);
+  }
+}
+
+// Second pass after row splits: one block per output reduces its `parts`
+// consecutive partials with a fixed tree.
+template <typename T, Kind K>
+__global__ void __launch_bounds__(kThreads)
+    combine_rows_kernel(const T* part_values, const int64_t* part_indices, uint64_t outputs,
+                        uint64_t parts, Sink<T> sink) {
+  for (uint64_t o = blockIdx.x; o < outputs; o += gridDim.x) {
+    Acc<T, K> acc;
+    acc.init();
+    for (uint64_t s = threadIdx.x; s < parts; s += kThreads) {
+      Acc<T, K> other;
+      if constexpr (K == Kind::Sum) {
+        other.value = part_values[o * parts + s];
+      } else {
+        other.best.value = part_values[o * parts + s];
+        other.best.index = part_indices[o * parts + s];
+      }
+      acc.merge(other);
+    }
+    const Acc<T, K> total = block_reduce<T, K>(acc);
+    if (threadIdx.x == 0) sink_write<T, K>(sink, o, total);
+  }
+}
+
+// ------------------------------------------------------------ column kernel
+
+// Input element (o, r, i) at map-offset(o) + r * reduced_stride + i, with
+// inner axis contiguous.  Lanes own W (VEC) or 1 adjacent columns; block b
+// covers column block cb, split s, outer o.
+template <typename T, Kind K, int NIN, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+    column_kernel(const T* a, const T* b, uint64_t outer, uint64_t n, uint64_t reduced_stride,
+                  uint64_t inner, uint64_t column_blocks, uint64_t splits, uint64_t segment,
+                  RowMap map, Sink<T> sink) {
+  constexpr int W = VEC ? Vec16<T>::width : 1;
+  const uint64_t total_blocks = outer * splits * column_blocks;
+  for (uint64_t block = blockIdx.x; block < total_blocks; block += gridDim.x) {
+    const uint64_t cb = block % column_blocks;
+    const uint64_t rest = block / column_blocks;
+    const uint64_t split = rest % splits;
+    const uint64_t o = rest / splits;
+    const uint64_t column = (cb * kThreads + threadIdx.x) * W;
+    if (column >= inner) continue;
+    const uint64_t begin = split * segment;
+    const uint64_t end = begin + segment < n ? begin + segment : n;
+    const uint64_t base = row_offset(map, o) + column;
+    Acc<T, K> acc[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) acc[k].init();
+    uint64_t r = begin;
+    if constexpr (VEC) {
+      for (; r + 3 < end; r += 4) {
+        typename Vec16<T>::type v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v[u], k), static_cast<int64_t>(r + u));
+        }
+      }
+      for (; r < end; ++r) {
+        const auto v = load_vector<T, NIN>(a, b, base + r * reduced_stride);
+#pragma unroll
+        for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v, k), static_cast<int64_t>(r));
+      }
+    } else {
+      for (; r < end; ++r) {
+        acc[0].add(load_value<T, NIN>(a, b, base + r * reduced_stride), static_cast<int64_t>(r));
+      }
+    }
+    // Output slot: final [outer, inner]; partial [outer, splits, inner].
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      if (column + k < inner) {
+        const uint64_t slot = sink.partial ? (o * splits + split) * inner + column + k
+                                           : o * inner + column + k;
+        sink_write<T, K>(sink, slot, acc[k]);
+      }
+    }
+  }
+}
+
+// Second pass after column splits: one thread per (outer, inner) output sums
+// its splits in order.
+template <typename T, Kind K>
+__global__ void __launch_bounds__(kThreads)
+    combine_columns_kernel(const T* part_values, const int64_t* part_indices, uint64_t outer,
+                           uint64_t splits, uint64_t inner, Sink<T> sink) {
+  const uint64_t outputs = outer * inner;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < outputs;
+       idx += stride) {
+    const uint64_t o = idx / inner;
+    const uint64_t i = idx - o * inner;
+    Acc<T, K> acc;
+    acc.init();
+    for (uint64_t s = 0; s < splits; ++s) {
+      const uint64_t slot = (o * splits + s) * inner + i;
+      Acc<T, K> other;
+      if constexpr (K == Kind::Sum) {
+        other.value = part_values[slot];
+      } else {
+        other.best.value = part_values[slot];
+        other.best.index = part_indices[slot];
+      }
+      acc.merge(other);
+    }
+    sink_write<T, K>(sink, idx, acc);
+  }
+}
+
+// ----------------------------------------------------------- generic kernel
+
+// One wave per output; lanes stride over the flattened reduced sub-space and
+// decode its coordinates (reduced axes, innermost first).
+struct ReducedMap {
+  int rank;
+  uint64_t extents[kMaxRank];
+  uint64_t strides[kMaxRank];
+  uint64_t count;
+};
+
+template <typename T, Kind K, int NIN>
+__global__ void __launch_bounds__(kThreads)
+    generic_kernel(const T* a, const T* b, uint64_t outputs, RowMap map, ReducedMap red,
+                   Sink<T> sink) {
+  const uint64_t wave = (static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x) / kWave;
+  const int lane = threadIdx.x % kWave;
+  const uint64_t waves = static_cast<uint64_t>(gridDim.x) * kWaves;
+  for (uint64_t o = wave; o < outputs; o += waves) {
+    const uint64_t base = row_offset(map, o);
+    Acc<T, K> acc;
+    acc.init();
+    for (uint64_t j = lane; j < red.count; j += kWave) {
+      uint64_t rem = j;
+      uint64_t off = base;
+      for (int k = 0; k < red.rank; ++k) {
+        const uint64_t q = rem / red.extents[k];
+        off += (rem - q * red.extents[k]) * red.strides[k];
+        rem = q;
+      }
+      acc.add(load_value<T, NIN>(a, b, off), static_cast<int64_t>(j));
+    }
+    acc.wave_reduce();
+    if (lane == 0) sink_write<T, K>(sink, o, acc);
+  }
+}
+
+// ------------------------------------------------------------------ planner
+
+// A reduction over a permuted, coalesced view: kept axes (output order) and
+// reduced axes (flattened-index order), each innermost last.
+struct Plan {
+  int kept_rank = 0;
+  uint64_t kept_extents[kMaxRank];
+  uint64_t kept_strides[kMaxRank];
+  int red_rank = 0;
+  uint64_t red_extents[kMaxRank];
+  uint64_t red_strides[kMaxRank];
+  uint64_t offset = 0;
+  uint64_t outputs = 1;
+  uint64_t reduced = 1;
+};
+
+// Merges neighbours in a list of (extent, stride) axes (row-major order) and
+// drops extent-1 axes.
+void coalesce_list(int& rank, uint64_t* extents, uint64_t* strides) {
+  int out = 0;
+  for (int axis = 0; axis < rank; ++axis) {
+    if (extents[axis] == 1) continue;
+    if (out > 0 && strides[out - 1] == strides[axis] * extents[axis]) {
+      extents[out - 1] *= extents[axis];
+      strides[out - 1] = strides[axis];
+      continue;
+    }
+    extents[out] = extents[axis];
+    strides[out] = strides[axis];
+    ++out;
+  }
+  rank = out;
+}
+
+RowMap make_row_map(const Plan& plan, int kept_axes_used) {
+  // kept axes [0, kept_axes_used) in output order; innermost first in the map
+  RowMap map{};
+  map.rank = kept_axes_used;
+  map.offset = plan.offset;
+  uint64_t rows = 1;
+  for (int k = 0; k < kept_axes_used; ++k) {
+    const int axis = kept_axes_used - 1 - k;
+    map.extents[k] = plan.kept_extents[axis];
+    map.strides[k] = plan.kept_strides[axis];
+    rows *= plan.kept_extents[axis];
+  }
+  map.index32 = rows <= kIndex32Limit;
+  for (int k = 0; k < map.rank; ++k) {
+    map.divisors[k].init(static_cast<uint32_t>(map.index32 ? map.extents[k] : 1));
+  }
+  return map;
+}
+
+uint32_t grid_for(uint64_t blocks) {
+  if (blocks == 0) blocks = 1;
+  return static_cast<uint32_t>(blocks > kMaxGrid ? kMaxGrid : blocks);
+}
+
+template <typename T, Kind K, int NIN>
+hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int operation,
+                    int device, const DeviceGuard& guard) {
+  constexpr int W = Vec16<T>::width;
+  Sink<T> sink{};
+  sink.operation = operation;
+  sink.mean_divisor = static_cast<T>(plan.reduced);
+  const bool argmax = operation == SPAR_HIP_ARGMAX;
+  const int cus = guard.multiprocessors;
+  const uint64_t target_blocks = static_cast<uint64_t>(cus) * 4;
+
+  auto final_sink = [&]() {
+    Sink<T> s = sink;
+    s.partial = 0;
+    s.values = argmax ? nullptr : static_cast<T*>(output);
+    s.indices = argmax ? static_cast<int64_t*>(output) : nullptr;
+    return s;
+  };
+
+  // Scratch for partial results (values, plus indices for max/argmax).
+  auto with_partials = [&](uint64_t slots, auto&& body) -> hipError_t {
+    void* values = nullptr;
+    void* indices = nullptr;
+    hipError_t error = scratch_allocate(&values, slots * sizeof(T), device);
+    if (error != hipSuccess) return error;
+    if constexpr (K == Kind::Max) {
+      error = scratch_allocate(&indices, slots * sizeof(int64_t), device);
+      if (error != hipSuccess) {
+        scratch_release(values, device);
+        return error;
+      }
+    }
+    Sink<T> partial = sink;
+    partial.partial = 1;
+    partial.values = static_cast<T*>(values);
+    partial.indices = static_cast<int64_t*>(indices);
+    body(partial);
+    scratch_release(values, device);
+    scratch_release(indices, device);
+    return hipSuccess;
+  };
+
+  const bool row_case = plan.red_rank == 1 && plan.red_strides[0] == 1;
+  const bool column_case = !row_case && plan.red_rank == 1 && plan.kept_rank >= 1 &&
+                           plan.kept_strides[plan.kept_rank - 1] == 1;
+
+  if (plan.red_rank == 0) {
+    // Nothing is reduced (all reduced extents are 1): a reduction of one
+    // element per output.
+    Plan single = plan;
+    single.red_rank = 1;
+    single.red_extents[0] = 1;
+    single.red_strides[0] = 1;
+    return run_plan<T, K, NIN>(single, a, b, output, operation, device, guard);
+  }
+
+  if (row_case) {
+    const uint64_t rows = plan.outputs;
+    const uint64_t n = plan.red_extents[0];
+    const RowMap map = make_row_map(plan, plan.kept_rank);
+    bool vec = n % W == 0 && plan.offset % W == 0 && aligned16(a) && (NIN == 1 || aligned16(b));
+    for (int k = 0; k < plan.kept_rank; ++k) {
+      if (plan.kept_strides[k] % W != 0) vec = false;
+    }
+    // Split long rows when there are too few rows to fill the device.
+    uint64_t splits = 1;
+    const uint64_t min_segment = static_cast<uint64_t>(kThreads) * W * 8;
+    if (rows < target_blocks && n >= 2 * min_segment) {
+      splits = (target_blocks + rows - 1) / rows;
+      const uint64_t max_splits = n / min_segment;
+      if (splits > max_splits) splits = max_splits;
+      if (splits < 1) splits = 1;
+    }
+    uint64_t segment = (n + splits - 1) / splits;
+    if (vec) segment = (segment + W - 1) / W * W;
+    splits = (n + segment - 1) / segment;
+    auto launch = [&](const Sink<T>& s) {
+      if (vec) {
+        row_kernel<T, K, NIN, true><<<grid_for(rows * splits), kThreads, 0, guard.stream>>>(
+            a, b, rows, n, splits, segment, map, s);
+      } else {
+        row_kernel<T, K, NIN, false><<<grid_for(rows * splits), kThreads, 0, guard.stream>>>(
+            a, b, rows, n, splits, segment, map, s);
+      }
+    };
+    if (splits == 1) {
+      launch(final_sink());
+      return hipSuccess;
+    }
+    return with_partials(rows * splits, [&](const Sink<T>& partial) {
+      launch(partial);
+      combine_rows_kernel<T, K><<<grid_for(rows), kThreads, 0, guard.stream>>>(
+          partial.values, partial.indices, rows, splits, final_sink());
+    });
+  }
+
+  if (column_case) {
+    const uint64_t inner = plan.kept_extents[plan.kept_rank - 1];
+    const uint64_t outer = plan.outputs / inner;
+    const uint64_t n = plan.red_extents[0];
+    const uint64_t reduced_stride = plan.red_strides[0];
+    const RowMap map = make_row_map(plan, plan.kept_rank - 1);
+    bool vec = inner % W == 0 && plan.offset % W == 0 && reduced_stride % W == 0 &&
+               aligned16(a) && (NIN == 1 || aligned16(b));
+    for (int k = 0; k < plan.kept_rank - 1; ++k) {
+      if (plan.kept_strides[k] % W != 0) vec = false;
+    }
+    const uint64_t lanes_per_block = static_cast<uint64_t>(kThreads) * (vec ? W : 1);
+    const uint64_t column_blocks = (inner + lanes_per_block - 1) / lanes_per_block;
+    const uint64_t base_blocks = outer * column_blocks;
+    uint64_t splits = 1;
+    const uint64_t min_rows = 32;
+    if (base_blocks < target_blocks && n >= 2 * min_rows) {
+      splits = (target_blocks + base_blocks - 1) / base_blocks;
+      if (splits > n / min_rows) splits = n / min_rows;
+      if (splits < 1) splits = 1;
+    }
+    const uint64_t segment = (n + splits - 1) / splits;
+    splits = (n + segment - 1) / segment;
+    auto launch = [&](const Sink<T>& s) {
+      const uint32_t grid = grid_for(outer * splits * column_blocks);
+      if (vec) {
+        column_kernel<T, K, NIN, true><<<grid, kThreads, 0, guard.stream>>>(
+            a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
+      } else {
+        column_kernel<T, K, NIN, false><<<grid, kThreads, 0, guard.stream>>>(
+            a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
+      }
+    };
+    if (splits == 1) {
+      launch(final_sink());
+      return hipSuccess;
+    }
+    return with_partials(outer * splits * inner, [&](const Sink<T>& partial) {
+      launch(partial);
+      combine_columns_kernel<T, K>
+          <<<grid_for((outer * inner + kThreads - 1) / kThreads), kThreads, 0, guard.stream>>>(
+              partial.values, partial.indices, outer, splits, inner, final_sink());
+    });
+  }
+
+  // Generic: one wave per output.
+  const RowMap map = make_row_map(plan, plan.kept_rank);
+  ReducedMap red{};
+  red.rank = plan.red_rank;
+  red.count = plan.reduced;
+  for (int k = 0; k < plan.red_rank; ++k) {
+    red.extents[k] = plan.red_extents[plan.red_rank - 1 - k];
+    red.strides[k] = plan.red_strides[plan.red_rank - 1 - k];
+  }
+  generic_kernel<T, K, NIN><<<grid_for((plan.outputs + kWaves - 1) / kWaves), kThreads, 0,
+                              guard.stream>>>(a, b, plan.outputs, map, red, final_sink());
+  return hipSuccess;
+}
+
+template <typename T, int NIN>
+hipError_t dispatch_plan(const Plan& plan, const void* a, const void* b, void* output,
+                         int operation, int device, const DeviceGuard& guard) {
+  const T* ta = static_cast<const T*>(a);
+  const T* tb = static_cast<const T*>(b);
+  if (operation == SPAR_HIP_SUM || operation == SPAR_HIP_MEAN) {
+    return run_plan<T, Kind::Sum, NIN>(plan, ta, tb, output, operation, device, guard);
+  }
+  return run_plan<T, Kind::Max, NIN>(plan, ta, tb, output, operation, device, guard);
+}
+
+// Builds a plan from a view and a reduced-axis mask.
+Plan make_plan(uint64_t rank, const uint64_t* extents, const uint64_t* strides, uint64_t offset,
+               uint32_t mask) {
+  Plan plan;
+  plan.offset = offset;
+  for (uint64_t axis = 0; axis < rank; ++axis) {
+    if ((mask >> axis) & 1U) {
+      plan.red_extents[plan.red_rank] = extents[axis];
+      plan.red_strides[plan.red_rank] = strides[axis];
+      ++plan.red_rank;
+      plan.reduced *= extents[axis];
+    } else {
+      plan.kept_extents[plan.kept_rank] = extents[axis];
+      plan.kept_strides[plan.kept_rank] = strides[axis];
+      ++plan.kept_rank;
+      plan.outputs *= extents[axis];
+    }
+  }
+  coalesce_list(plan.kept_rank, plan.kept_extents, plan.kept_strides);
+  coalesce_list(plan.red_rank, plan.red_extents, plan.red_strides);
+  return plan;
+}
+
+SparHipStatus execute(const Plan& plan, const void* a, const void* b, int nin, void* output,
+                      int dtype, int operation, int device) {
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  hipError_t error;
+  if (dtype == SPAR_HIP_FLOAT32) {
+    error = nin == 1 ? dispatch_plan<float, 1>(plan, a, b, output, operation, device, guard)
+                     : dispatch_plan<float, 2>(plan, a, b, output, operation, device, guard);
+  } else {
+    error = nin == 1 ? dispatch_plan<double, 1>(plan, a, b, output, operation, device, guard)
+                     : dispatch_plan<double, 2>(plan, a, b, output, operation, device, guard);
+  }
+  if (error != hipSuccess) return runtime(error);
+  return finish(guard);
+}
+
+bool valid_reduction(int operation) {
+  return operation >= SPAR_HIP_SUM && operation <= SPAR_HIP_ARGMAX;
+}
+
+// Gradient view + mask for reducing a contiguous gradient to a right-aligned
+// original shape: leading axes and axes where the original extent is 1 (and
+// the gradient's is not) are reduced.
+bool broadcast_plan(Plan& plan, uint64_t gradient_rank, const uint64_t* gradient_extents,
+                    uint64_t original_rank, const uint64_t* original_extents) {
+  if (gradient_rank > kMaxRank || original_rank > gradient_rank) return false;
+  uint64_t strides[kMaxRank];
+  uint64_t running = 1;
+  for (uint64_t axis = gradient_rank; axis > 0; --axis) {
+    strides[axis - 1] = running;
+    running *= gradient_extents[axis - 1];
+  }
+  const uint64_t leading = gradient_rank - original_rank;
+  uint32_t mask = 0;
+  for (uint64_t axis = 0; axis < gradient_rank; ++axis) {
+    if (axis < leading) {
+      mask |= 1U << axis;
+      continue;
+    }
+    const uint64_t original = original_extents[axis - leading];
+    if (original == gradient_extents[axis]) continue;
+    if (original != 1) return false;
+    mask |= 1U << axis;
+  }
+  plan = make_plan(gradient_rank, gradient_extents, strides, 0, mask);
+  return true;
+}
+
+}  // namespace
+}  // namespace spar_hip
+
+using namespace spar_hip;
+
+extern "C" SparHipStatus spar_hip_launch_reduction(void* output, const void* input, uint64_t count,
+                                                   int dtype, int operation, int device) {
+  if (!valid_float_dtype(dtype) || !valid_reduction(operation) || output == nullptr ||
+      (count != 0 && input == nullptr) || (operation != SPAR_HIP_SUM && count == 0)) {
+    return invalid();
+  }
+  if (count == 0) {
+    // sum of nothing is 0 (reduction.cpp:21-30)
+    const uint64_t bytes = dtype == SPAR_HIP_FLOAT32 ? 4 : 8;
+    return spar_hip_zero(output, bytes, device);
+  }
+  uint64_t extents[1] = {count};
+  uint64_t strides[1] = {1};
+  const Plan plan = make_plan(1, extents, strides, 0, 1U);
+  return execute(plan, input, nullptr, 1, output, dtype, operation, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_row_reduction(void* output, const void* input,
+                                                       uint64_t row_count,
+                                                       uint64_t reduction_count, int dtype,
+                                                       int operation, int device) {
+  if (!valid_float_dtype(dtype) || !valid_reduction(operation) ||
+      (row_count != 0 && output == nullptr) ||
+      (row_count != 0 && reduction_count != 0 && input == nullptr) ||
+      (operation != SPAR_HIP_SUM && reduction_count == 0)) {
+    return invalid();
+  }
+  if (row_count == 0) return ok();
+  if (reduction_count == 0) {
+    const uint64_t bytes = row_count * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8);
+    return spar_hip_zero(output, bytes, device);
+  }
+  uint64_t extents[2] = {row_count, reduction_count};
+  uint64_t strides[2] = {reduction_count, 1};
+  const Plan plan = make_plan(2, extents, strides, 0, 2U);
+  return execute(plan, input, nullptr, 1, output, dtype, operation, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_axis_reduction(void* output, const void* input,
+                                                        uint64_t rank, const uint64_t* extents,
+                                                        const uint64_t* strides,
+                                                        uint64_t storage_offset,
+                                                        uint32_t reduced_mask, int dtype,
+                                                        int operation, int device) {
+  if (!valid_float_dtype(dtype) || !valid_reduction(operation) || rank > kMaxRank ||
+      (rank != 0 && (extents == nullptr || strides == nullptr)) ||
+      (rank < 32 && (reduced_mask >> rank) != 0)) {
+    return invalid();
+  }
+  uint64_t outputs = 1;
+  uint64_t reduced = 1;
+  for (uint64_t axis = 0; axis < rank; ++axis) {
+    if ((reduced_mask >> axis) & 1U) {
+      reduced *= extents[axis];
+    } else {
+      outputs *= extents[axis];
+    }
+  }
+  if (outputs == 0) return ok();
+  if (output == nullptr) return invalid();
+  if (reduced == 0) {
+    if (operation != SPAR_HIP_SUM) return invalid();
+    return spar_hip_zero(output, outputs * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8), device);
+  }
+  if (input == nullptr) return invalid();
+  const Plan plan = make_plan(rank, extents, strides, storage_offset, reduced_mask);
+  return execute(plan, input, nullptr, 1, output, dtype, operation, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_broadcast_reduce(
+    void* destination, const void* gradient, uint64_t gradient_rank,
+    const uint64_t* gradient_extents, uint64_t original_rank, const uint64_t* original_extents,
+    const uint64_t* original_strides, uint64_t count, int dtype, int device) {
+  (void)original_strides;  // the destination is always contiguous
+  if (!valid_float_dtype(dtype) || original_rank > gradient_rank ||
+      gradient_rank > kMaxRank || (count != 0 && (destination == nullptr || gradient == nullptr)) ||
+      (gradient_rank != 0 && gradient_extents == nullptr) ||
+      (original_rank != 0 && original_extents == nullptr)) {
+    return invalid();
+  }
+  uint64_t product = 1;
+  for (uint64_t axis = 0; axis < gradient_rank; ++axis) product *= gradient_extents[axis];
+  if (product != count) return invalid();
+  uint64_t original_count = 1;
+  for (uint64_t axis = 0; axis < original_rank; ++axis) original_count *= original_extents[axis];
+  if (count == 0) {
+    if (original_count == 0 || destination == nullptr) return ok();
+    return spar_hip_zero(destination, original_count * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8), device);
+  }
+  Plan plan;
+  if (!broadcast_plan(plan, gradient_rank, gradient_extents, original_rank, original_extents)) {
+    return invalid();
+  }
+  return execute(plan, gradient, nullptr, 1, destination, dtype, SPAR_HIP_SUM, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_multiply_reduce(
+    void* destination, const void* gradient, const void* factor, uint64_t gradient_rank,
+    const uint64_t* gradient_extents, uint64_t original_rank, const uint64_t* original_extents,
+    uint64_t count, int dtype, int device) {
+  if (!valid_float_dtype(dtype) || original_rank > gradient_rank || gradient_rank > kMaxRank ||
+      (count != 0 && (destination == nullptr || gradient == nullptr || factor == nullptr)) ||
+      (gradient_rank != 0 && gradient_extents == nullptr) ||
+      (original_rank != 0 && original_extents == nullptr)) {
+    return invalid();
+  }
+  uint64_t product = 1;
+  for (uint64_t axis = 0; axis < gradient_rank; ++axis) product *= gradient_extents[axis];
+  if (product != count) return invalid();
+  uint64_t original_count = 1;
+  for (uint64_t axis = 0; axis < original_rank; ++axis) original_count *= original_extents[axis];
+  if (count == 0) {
+    if (original_count == 0 || destination == nullptr) return ok();
+    return spar_hip_zero(destination, original_count * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8), device);
+  }
+  Plan plan;
+  if (!broadcast_plan(plan, gradient_rank, gradient_extents, original_rank, original_extents)) {
+    return invalid();
+  }
+  return execute(plan, gradient, factor, 2, destination, dtype, SPAR_HIP_SUM, device);
+}

@@ -1,0 +1,446 @@
+// Strided layouts: materialising views (strided copy) and binary operations
+// over broadcast/strided operands without materialising them.
+//
+// Replaces K11 strided_copy_kernel and the expand().contiguous() + K1 chain
+// of the reference (src/backend/cuda_kernels.cu:268-285, :1145-1191;
+// src/ops/elementwise.cpp:26-31).  Geometry is coalesced on the host and
+// passed by value (no per-call device metadata).  Three kernels:
+//   * row-vector: the innermost (coalesced) axis is contiguous or broadcast
+//     for every operand and a multiple of the 16-byte vector width - e.g. a
+//     bias [C] or a scale [B,1,C] against x [B,T,C]; 128-bit loads/stores,
+//     broadcast operands are re-read from cache, not HBM;
+//   * tiled: an operand is contiguous along an outer axis only (a transposed
+//     view); 64x64 tiles are staged through LDS so both the operand reads and
+//     the output writes are coalesced;
+//   * generic: per-element index decode with invariant-divisor division.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "layout.hpp"
+#include "ops.hpp"
+
+namespace spar_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
+
+struct CopyOp {
+  template <typename T> __device__ __forceinline__ T operator()(T x) const { return x; }
+};
+
+// ------------------------------------------------------------ generic path
+
+template <int NOPS, bool kIndex32>
+__device__ __forceinline__ void decode(uint64_t e, const KernelGeometry& g, uint64_t (&off)[2]) {
+  off[0] = g.offsets[0];
+  off[1] = g.offsets[1];
+  if constexpr (kIndex32) {
+    uint32_t rem = static_cast<uint32_t>(e);
+#pragma unroll
+    for (int k = 0; k < kMaxRank; ++k) {
+      if (k < g.rank) {
+        const uint32_t q = g.divisors[k].div(rem);
+        const uint32_t c = rem - q * g.divisors[k].divisor;
+        rem = q;
+        off[0] += static_cast<uint64_t>(c) * g.strides[0][k];
+        if constexpr (NOPS == 2) off[1] += static_cast<uint64_t>(c) * g.strides[1][k];
+      }
+    }
+  } else {
+    uint64_t rem = e;
+#pragma unroll
+    for (int k = 0; k < kMaxRank; ++k) {
+      if (k < g.rank) {
+        const uint64_t q = rem / g.extents[k];
+        const uint64_t c = rem - q * g.extents[k];
+        rem = q;
+        off[0] += c * g.strides[0][k];
+        if constexpr (NOPS == 2) off[1] += c * g.strides[1][k];
+      }
+    }
+  }
+}
+
+template <typename T, int NOPS, bool kIndex32, typename F>
+__global__ void __launch_bounds__(kThreads)
+    generic_kernel(T* out, const T* a, const T* b, uint64_t count, KernelGeometry g, F f) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; e < count;
+       e += stride) {
+    uint64_t off[2];
+    decode<NOPS, kIndex32>(e, g, off);
+    if constexpr (NOPS == 1) {
+      out[e] = f(a[off[0]]);
+    } else {
+      out[e] = f(a[off[0]], b[off[1]]);
+    }
+  }
+}
+
+// -------------------------------------------------------- row-vector path
+
+// The innermost axis has extent `inner` (a multiple of W); each operand's
+// inner stride is 0 (broadcast) or 1 (contiguous).  Rows are decoded from the
+// outer axes of `g` (g.rank - 1 axes, innermost first starting at index 1).
+struct RowGeometry {
+  KernelGeometry g;        // full coalesced geometry (axis 0 = innermost)
+  FastDiv groups_per_row;  // inner / W
+  int inner_unit[2];       // 1 if the operand is contiguous along the inner axis
+};
+
+template <typename T, int NOPS, typename F>
+__global__ void __launch_bounds__(kThreads)
+    row_vector_kernel(T* out, const T* a, const T* b, uint64_t groups, RowGeometry rg, F f) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  const KernelGeometry& g = rg.g;
+  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  V* out_v = reinterpret_cast<V*>(out);
+  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < groups;
+       base += static_cast<uint64_t>(gridDim.x) * tile) {
+    V ra[kUnroll];
+    V rb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint64_t group = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      if (group < groups) {
+        const uint32_t row = rg.groups_per_row.div(static_cast<uint32_t>(group));
+        const uint32_t column = (static_cast<uint32_t>(group) - row * rg.groups_per_row.divisor) * W;
+        uint64_t off0 = g.offsets[0];
+        uint64_t off1 = g.offsets[1];
+        uint32_t rem = row;
+#pragma unroll
+        for (int k = 1; k < kMaxRank; ++k) {
+          if (k < g.rank) {
+            const uint32_t q = g.divisors[k].div(rem);
+            const uint32_t c = rem - q * g.divisors[k].divisor;
+            rem = q;
+            off0 += static_cast<uint64_t>(c) * g.strides[0][k];
+            if constexpr (NOPS == 2) off1 += static_cast<uint64_t>(c) * g.strides[1][k];
+          }
+        }
+        if (rg.inner_unit[0]) {
+          ra[u] = *reinterpret_cast<const V*>(a + off0 + column);
+        } else {
+          const T s = a[off0];
+#pragma unroll
+          for (int k = 0; k < W; ++k) vec_set<T>(ra[u], k, s);
+        }
+        if constexpr (NOPS == 2) {
+          if (rg.inner_unit[1]) {
+            rb[u] = *reinterpret_cast<const V*>(b + off1 + column);
+          } else {
+            const T s = b[off1];
+#pragma unroll
+            for (int k = 0; k < W; ++k) vec_set<T>(rb[u], k, s);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint64_t group = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      if (group < groups) {
+        V o;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          if constexpr (NOPS == 1) {
+            vec_set<T>(o, k, f(vec_get<T>(ra[u], k)));
+          } else {
+            vec_set<T>(o, k, f(vec_get<T>(ra[u], k), vec_get<T>(rb[u], k)));
+          }
+        }
+        out_v[group] = o;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- tiled path
+
+// Output axes p (an outer axis) and q (the innermost axis) are tiled; the
+// remaining axes form the batch.  Operands flagged `staged` are contiguous
+// along p and are read p-fastest into LDS; others are read q-fastest.
+struct TileGeometry {
+  uint64_t extent_p, extent_q;
+  uint64_t out_stride_p;          // output (contiguous) stride of axis p
+  uint64_t stride_p[2], stride_q[2];
+  int staged[2];
+  int batch_rank;
+  uint64_t batch_extents[kMaxRank];  // innermost first
+  uint64_t batch_out_strides[kMaxRank];
+  uint64_t batch_strides[2][kMaxRank];
+  uint64_t offsets[2];
+  uint64_t tiles_p, tiles_q;
+};
+
+template <typename T, int NOPS, int TILE, typename F>
+__global__ void __launch_bounds__(kThreads)
+    tiled_kernel(T* out, const T* a, const T* b, uint64_t tile_count, TileGeometry tg, F f) {
+  __shared__ T tile[NOPS][TILE][TILE + 1];
+  constexpr int kRowsPerPass = kThreads / TILE;
+  const int tx = threadIdx.x % TILE;
+  const int ty = threadIdx.x / TILE;
+  const T* operands[2] = {a, b};
+  for (uint64_t block = blockIdx.x; block < tile_count; block += gridDim.x) {
+    uint64_t rem = block;
+    const uint64_t tq = rem % tg.tiles_q;
+    rem /= tg.tiles_q;
+    const uint64_t tp = rem % tg.tiles_p;
+    rem /= tg.tiles_p;
+    uint64_t out_base = 0;
+    uint64_t base[2] = {tg.offsets[0], tg.offsets[1]};
+    for (int k = 0; k < tg.batch_rank; ++k) {
+      const uint64_t c = rem % tg.batch_extents[k];
+      rem /= tg.batch_extents[k];
+      out_base += c * tg.batch_out_strides[k];
+      base[0] += c * tg.batch_strides[0][k];
+      base[1] += c * tg.batch_strides[1][k];
+    }
+    const uint64_t p0 = tp * TILE;
+    const uint64_t q0 = tq * TILE;
+#pragma unroll
+    for (int op = 0; op < NOPS; ++op) {
+      if (tg.staged[op]) {
+        for (int j = ty; j < TILE; j += kRowsPerPass) {
+          const uint64_t p = p0 + tx;
+          const uint64_t q = q0 + j;
+          if (p < tg.extent_p && q < tg.extent_q) {
+            tile[op][j][tx] = operands[op][base[op] + p * tg.stride_p[op] + q * tg.stride_q[op]];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int j = ty; j < TILE; j += kRowsPerPass) {
+      const uint64_t p = p0 + j;
+      const uint64_t q = q0 + tx;
+      if (p < tg.extent_p && q < tg.extent_q) {
+        T v[2];
+#pragma unroll
+        for (int op = 0; op < NOPS; ++op) {
+          v[op] = tg.staged[op]
+                      ? tile[op][tx][j]
+                      : operands[op][base[op] + p * tg.stride_p[op] + q * tg.stride_q[op]];
+        }
+        T result;
+        if constexpr (NOPS == 1) {
+          result = f(v[0]);
+        } else {
+          result = f(v[0], v[1]);
+        }
+        out[out_base + p * tg.out_stride_p + q] = result;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- dispatch
+
+uint32_t capped_grid(uint64_t work, uint64_t per_block) {
+  uint64_t blocks = (work + per_block - 1) / per_block;
+  if (blocks == 0) blocks = 1;
+  if (blocks > kMaxGrid) blocks = kMaxGrid;
+  return static_cast<uint32_t>(blocks);
+}
+
+// Chooses and launches the kernel for a coalesced view; out is contiguous.
+template <typename T, int NOPS, typename F>
+void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
+                 const DeviceGuard& guard) {
+  constexpr int W = Vec16<T>::width;
+  const uint64_t count = view_numel(view);
+  const int last = view.rank - 1;
+  const uint64_t inner = view.extents[last];
+
+  bool index32 = count <= kIndex32Limit;
+  for (int op = 0; op < NOPS; ++op) {
+    if (view_span(view, op) > kIndex32Limit) {
+      // offsets stay 64-bit in every kernel; only coordinates need 32 bits
+    }
+  }
+
+  // Row-vector path.
+  bool row_ok = index32 && inner % W == 0 && aligned16(out);
+  int inner_unit[2] = {0, 0};
+  for (int op = 0; op < NOPS && row_ok; ++op) {
+    const uint64_t s = view.strides[op][last];
+    const T* base = op == 0 ? a : b;
+    if (s == 1) {
+      inner_unit[op] = 1;
+      if (!aligned16(base) || view.offsets[op] % W != 0) row_ok = false;
+      for (int axis = 0; axis < last; ++axis) {
+        if (view.strides[op][axis] % W != 0) row_ok = false;
+      }
+    } else if (s != 0) {
+      row_ok = false;
+    }
+  }
+  if (row_ok) {
+    RowGeometry rg{};
+    rg.g = kernel_geometry(view);
+    rg.groups_per_row.init(static_cast<uint32_t>(inner / W));
+    rg.inner_unit[0] = inner_unit[0];
+    rg.inner_unit[1] = inner_unit[1];
+    const uint64_t groups = count / W;
+    row_vector_kernel<T, NOPS, F>
+        <<<capped_grid(groups, static_cast<uint64_t>(kThreads) * kUnroll), kThreads, 0,
+           guard.stream>>>(out, a, b, groups, rg, f);
+    return;
+  }
+
+  // Tiled path: some operand is strided along q but contiguous along an
+  // outer axis p.
+  if (view.rank >= 2) {
+    int p_axis = -1;
+    for (int op = 0; op < NOPS && p_axis < 0; ++op) {
+      const uint64_t sq = view.strides[op][last];
+      if (sq == 0 || sq == 1) continue;
+      for (int axis = last - 1; axis >= 0; --axis) {
+        if (view.strides[op][axis] == 1) {
+          p_axis = axis;
+          break;
+        }
+      }
+    }
+    if (p_axis >= 0) {
+      constexpr int TILE = sizeof(T) == 4 ? 64 : 32;
+      TileGeometry tg{};
+      tg.extent_p = view.extents[p_axis];
+      tg.extent_q = inner;
+      uint64_t out_strides[kMaxRank];
+      uint64_t running = 1;
+      for (int axis = view.rank - 1; axis >= 0; --axis) {
+        out_strides[axis] = running;
+        running *= view.extents[axis];
+      }
+      tg.out_stride_p = out_strides[p_axis];
+      for (int op = 0; op < NOPS; ++op) {
+        tg.stride_p[op] = view.strides[op][p_axis];
+        tg.stride_q[op] = view.strides[op][last];
+        tg.staged[op] = (tg.stride_p[op] == 1 && tg.stride_q[op] != 1 && tg.stride_q[op] != 0);
+        tg.offsets[op] = view.offsets[op];
+      }
+      tg.batch_rank = 0;
+      uint64_t batch_count = 1;
+      for (int axis = view.rank - 1; axis >= 0; --axis) {
+        if (axis == p_axis || axis == last) continue;
+        const int k = tg.batch_rank++;
+        tg.batch_extents[k] = view.extents[axis];
+        tg.batch_out_strides[k] = out_strides[axis];
+        for (int op = 0; op < NOPS; ++op) tg.batch_strides[op][k] = view.strides[op][axis];
+        batch_count *= view.extents[axis];
+      }
+      tg.tiles_p = (tg.extent_p + TILE - 1) / TILE;
+      tg.tiles_q = (tg.extent_q + TILE - 1) / TILE;
+      const uint64_t tiles = tg.tiles_p * tg.tiles_q * batch_count;
+      tiled_kernel<T, NOPS, TILE, F><<<capped_grid(tiles, 1), kThreads, 0, guard.stream>>>(
+          out, a, b, tiles, tg, f);
+      return;
+    }
+  }
+
+  // Generic path.
+  const KernelGeometry g = kernel_geometry(view);
+  uint64_t blocks = (count + kThreads - 1) / kThreads;
+  const uint64_t cap = static_cast<uint64_t>(guard.multiprocessors) * 32;
+  if (blocks > cap) blocks = cap;
+  if (blocks == 0) blocks = 1;
+  if (index32) {
+    generic_kernel<T, NOPS, true, F><<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(
+        out, a, b, count, g, f);
+  } else {
+    generic_kernel<T, NOPS, false, F>
+        <<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(out, a, b, count, g, f);
+  }
+}
+
+template <typename T>
+void launch_copy(void* destination, const void* source, const MultiView& view,
+                 const DeviceGuard& guard) {
+  launch_view<T, 1>(static_cast<T*>(destination), static_cast<const T*>(source),
+                    static_cast<const T*>(nullptr), view, CopyOp{}, guard);
+}
+
+}  // namespace
+}  // namespace spar_hip
+
+using namespace spar_hip;
+
+extern "C" SparHipStatus spar_hip_launch_strided_copy(void* destination, const void* source,
+                                                      uint64_t rank, const uint64_t* extents,
+                                                      const uint64_t* strides,
+                                                      uint64_t storage_offset, uint64_t count,
+                                                      uint64_t element_size, int device) {
+  if ((element_size != 4U && element_size != 8U) ||
+      (count != 0 && (destination == nullptr || source == nullptr)) ||
+      (rank != 0 && (extents == nullptr || strides == nullptr)) || rank > kMaxRank) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  MultiView view;
+  view.rank = static_cast<int>(rank);
+  view.operands = 1;
+  uint64_t product = 1;
+  for (uint64_t axis = 0; axis < rank; ++axis) {
+    view.extents[axis] = extents[axis];
+    view.strides[0][axis] = strides[axis];
+    product *= extents[axis];
+  }
+  view.offsets[0] = storage_offset;
+  if (product != count) return invalid();
+  coalesce(view);
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  // The payload is moved as 4- or 8-byte words (float / double bit patterns).
+  if (element_size == 4U) {
+    launch_copy<float>(destination, source, view, guard);
+  } else {
+    launch_copy<double>(destination, source, view, guard);
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_strided_binary(void* output, const void* left,
+                                                        const uint64_t* left_strides,
+                                                        uint64_t left_offset, const void* right,
+                                                        const uint64_t* right_strides,
+                                                        uint64_t right_offset, uint64_t rank,
+                                                        const uint64_t* extents, int dtype,
+                                                        int operation, int device) {
+  if (!valid_float_dtype(dtype) || operation < SPAR_HIP_ADD ||
+      operation > SPAR_HIP_GREATER_EQUAL || rank > kMaxRank ||
+      (rank != 0 && (extents == nullptr || left_strides == nullptr || right_strides == nullptr))) {
+    return invalid();
+  }
+  MultiView view;
+  view.rank = static_cast<int>(rank);
+  view.operands = 2;
+  uint64_t count = 1;
+  for (uint64_t axis = 0; axis < rank; ++axis) {
+    view.extents[axis] = extents[axis];
+    view.strides[0][axis] = left_strides[axis];
+    view.strides[1][axis] = right_strides[axis];
+    count *= extents[axis];
+  }
+  view.offsets[0] = left_offset;
+  view.offsets[1] = right_offset;
+  if (count == 0) return ok();
+  if (output == nullptr || left == nullptr || right == nullptr) return invalid();
+  coalesce(view);
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  dispatch_binary(operation, [&](auto op) {
+    if (dtype == SPAR_HIP_FLOAT32) {
+      launch_view<float, 2>(static_cast<float*>(output), static_cast<const float*>(left),
+                            static_cast<const float*>(right), view, op, guard);
+    } else {
+      launch_view<double, 2>(static_cast<double*>(output), static_cast<const double*>(left),
+                             static_cast<const double*>(right), view, op, guard);
+    }
+  });
+  return finish(guard);
+}

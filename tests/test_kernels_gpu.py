@@ -1,0 +1,535 @@
+"""Kernel-level parity: every C-ABI launcher against the oracle.
+
+Inputs are seeded and identical on both sides (host bytes copied to the
+device).  Tolerance classes are defined in tests/helpers.py.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import ops as ref
+from tests.helpers import (assert_bitexact, assert_red, assert_ulp, special_values)
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = np.float32, np.float64
+DTYPES = [F32, F64]
+
+
+def tag(dtype):
+    return 0 if np.dtype(dtype) == np.float32 else 1
+
+
+# Device buffers stay alive until the test ends: a buffer freed early would
+# return its block to the caching allocator and the next upload could reuse it.
+_alive = []
+
+
+@pytest.fixture(autouse=True)
+def _release_buffers():
+    yield
+    _alive.clear()
+
+
+def dev(hip, array):
+    buffer = hip.DeviceBuffer.from_numpy(np.ascontiguousarray(array))
+    _alive.append(buffer)
+    return buffer
+
+
+def out_buf(hip, shape, dtype):
+    n = int(np.prod(shape, dtype=np.int64))
+    buffer = hip.DeviceBuffer(max(n, 1) * np.dtype(dtype).itemsize)
+    _alive.append(buffer)
+    return buffer
+
+
+def inputs(seed, n, dtype, with_specials=True):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(n).astype(dtype)
+    if with_specials and n >= 64:
+        sp = special_values(dtype)
+        x[: sp.size] = sp
+        rng.shuffle(x)
+    return x
+
+
+# ------------------------------------------------------------ elementwise
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 3, 4, 7, 1000, 4096, 65537, 1 << 20])
+@pytest.mark.parametrize("op", list(ref.BINARY))
+def test_binary_contiguous_bitexact(hip, dtype, n, op):
+    a = inputs(1, n, dtype)
+    b = inputs(2, n, dtype)
+    out = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_launch_binary", out.ptr, dev(hip, a).ptr, dev(hip, b).ptr, n, tag(dtype),
+             hip.BINARY_OPS[op], 0)
+    assert_bitexact(out.to_numpy(dtype, (n,)), ref.binary(a, b, op), f"{op} n={n}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", ["add", "subtract", "multiply", "divide"])
+@pytest.mark.parametrize("value", [0.1, -3.0, 1e-3, 2.5e38, 0.0])
+def test_scalar_bitexact(hip, dtype, op, value):
+    n = 10007
+    a = inputs(3, n, dtype)
+    out = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_launch_scalar", out.ptr, dev(hip, a).ptr, n, tag(dtype),
+             hip.BINARY_OPS[op], value, 0)
+    assert_bitexact(out.to_numpy(dtype, (n,)), ref.scalar(a, op, value), f"{op} {value}")
+
+
+EXACT_UNARY = ["negate", "square", "reciprocal", "sqrt"]
+TRANSCENDENTAL = ["exp", "log", "sigmoid", "silu", "tanh", "gelu"]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", EXACT_UNARY + TRANSCENDENTAL)
+def test_unary(hip, dtype, op):
+    n = 200003
+    with np.errstate(over="ignore"):
+        a = inputs(4, n, dtype) * dtype(4)
+    if op in ("log", "sqrt"):
+        a = np.abs(a)
+        a[:5] = [0.0, -0.0, -1.0, np.inf, np.nan]
+    out = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_launch_unary", out.ptr, dev(hip, a).ptr, n, tag(dtype), hip.UNARY_OPS[op], 0)
+    got = out.to_numpy(dtype, (n,))
+    want = ref.unary(a, op)
+    if op in EXACT_UNARY:
+        assert_bitexact(got, want, op)
+    else:
+        # float32: <= 2 ulp.  float64 composites (sigmoid/silu/gelu) chain two
+        # libm results with no wider type to evaluate in: <= 4 ulp.
+        composite = op in ("sigmoid", "silu", "gelu")
+        assert_ulp(got, want, 4 if (dtype == F64 and composite) else 2, op)
+
+
+def test_exp_clipped_config_range(hip):
+    # exp over N(0,1) clipped to [-10, 10], the elementwise benchmark input
+    x = np.clip(np.random.default_rng(5).standard_normal(1 << 20), -10, 10).astype(F32)
+    out = out_buf(hip, x.shape, F32)
+    hip.call("spar_hip_launch_unary", out.ptr, dev(hip, x).ptr, x.size, 0, hip.EXP, 0)
+    assert_ulp(out.to_numpy(F32, x.shape), ref.unary(x, "exp"), 2, "exp")
+
+
+def test_unaligned_pointers_take_scalar_path(hip):
+    n = 4099
+    a = inputs(6, n + 1, F32)
+    b = inputs(7, n + 1, F32)
+    da, db = dev(hip, a), dev(hip, b)
+    out = out_buf(hip, (n + 1,), F32)
+    # offset every pointer by one element (4 bytes): not 16-byte aligned
+    hip.call("spar_hip_launch_binary", out.address(4), da.address(4), db.address(4), n, 0,
+             hip.ADD, 0)
+    got = out.to_numpy(F32, (n + 1,))[1:]
+    assert_bitexact(got, ref.binary(a[1:], b[1:], "add"), "unaligned add")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fill_add_in_place_zero(hip, dtype):
+    n = 12345
+    d = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_launch_fill", d.ptr, n, tag(dtype), 1.0, 0)
+    assert np.all(d.to_numpy(dtype, (n,)) == 1)
+    src = inputs(8, n, dtype, with_specials=False)
+    want = np.ones(n, dtype)
+    ref.add_in_place(want, src)
+    hip.call("spar_hip_launch_add_in_place", d.ptr, dev(hip, src).ptr, n, tag(dtype), 0)
+    assert_bitexact(d.to_numpy(dtype, (n,)), want, "add_in_place")
+    hip.call("spar_hip_zero", d.ptr, n * np.dtype(dtype).itemsize, 0)
+    assert np.all(d.to_numpy(dtype, (n,)) == 0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("divisor", [1.0, 3.0, 4096.0, 67108864.0])
+def test_fill_from_scalar_divides_like_cpu(hip, dtype, divisor):
+    g = np.array([0.7], dtype)
+    n = 1000
+    out = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_launch_fill_from_scalar", out.ptr, dev(hip, g).ptr, n, tag(dtype), divisor, 0)
+    # mean backward on the CPU: g / (T)n (ops/reduction.cpp:263-277)
+    want = np.full(n, g[0] / dtype(divisor), dtype)
+    assert_bitexact(out.to_numpy(dtype, (n,)), want, "fill_from_scalar")
+
+
+# --------------------------------------------------------------- layouts
+
+def strided_copy(hip, base, view, dtype):
+    """Runs spar_hip_launch_strided_copy on `view`, a numpy view of `base`."""
+    item = base.itemsize
+    offset = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // item
+    strides = [s // item for s in view.strides]
+    db = dev(hip, base)
+    out = out_buf(hip, view.shape, dtype)
+    hip.call("spar_hip_launch_strided_copy", out.ptr, db.ptr, view.ndim, hip.u64_array(view.shape),
+             hip.u64_array(strides), offset, view.size, item, 0)
+    return out.to_numpy(dtype, view.shape)
+
+
+def views_of(base2d):
+    yield "transpose", base2d.T
+    yield "slice", base2d[3:, 5:-2]
+    yield "slice_step", base2d[1::2, ::3]
+    yield "column", base2d[:, 7:8]
+    yield "transpose_slice", base2d[2:-1, 4:].T
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_strided_copy_views(hip, dtype):
+    base = inputs(9, 300 * 517, dtype).reshape(300, 517)
+    for name, view in views_of(base):
+        assert_bitexact(strided_copy(hip, base, view, dtype), ref.strided_copy(view), name)
+    base3 = inputs(10, 6 * 70 * 33, dtype).reshape(6, 70, 33)
+    for perm in [(0, 2, 1), (2, 1, 0), (1, 0, 2), (2, 0, 1)]:
+        view = base3.transpose(perm)
+        assert_bitexact(strided_copy(hip, base3, view, dtype), ref.strided_copy(view), str(perm))
+    bias = inputs(11, 33, dtype)
+    expanded = np.broadcast_to(bias, (5, 7, 33))
+    assert_bitexact(strided_copy(hip, bias, expanded, dtype), ref.strided_copy(expanded), "expand")
+
+
+def strided_binary(hip, left_base, left_view, right_base, right_view, op, dtype):
+    shape = np.broadcast_shapes(left_view.shape, right_view.shape)
+    lv = np.broadcast_to(left_view, shape)
+    rv = np.broadcast_to(right_view, shape)
+    item = np.dtype(dtype).itemsize
+
+    def geometry(base, view):
+        offset = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // item
+        return [s // item for s in view.strides], offset
+
+    ls, lo = geometry(left_base, lv)
+    rs, ro = geometry(right_base, rv)
+    dl, dr = dev(hip, left_base), dev(hip, right_base)
+    out = out_buf(hip, shape, dtype)
+    hip.call("spar_hip_launch_strided_binary", out.ptr, dl.ptr, hip.u64_array(ls), lo, dr.ptr,
+             hip.u64_array(rs), ro, len(shape), hip.u64_array(shape), tag(dtype),
+             hip.BINARY_OPS[op], 0)
+    return out.to_numpy(dtype, shape), ref.binary(lv, rv, op)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", ["add", "subtract", "multiply", "divide", "less"])
+def test_strided_binary_broadcasts(hip, dtype, op):
+    x = inputs(12, 4 * 64 * 96, dtype).reshape(4, 64, 96)
+    bias = inputs(13, 96, dtype)
+    scale = inputs(14, 4 * 96, dtype).reshape(4, 1, 96)
+    column = inputs(15, 4 * 64, dtype).reshape(4, 64, 1)
+    one = inputs(16, 1, dtype)
+    for name, rb, rv in [("bias", bias, bias), ("scale", scale, scale), ("column", column, column),
+                         ("scalar", one, one)]:
+        got, want = strided_binary(hip, x, x, rb, rv, op, dtype)
+        assert_bitexact(got, want, f"x {op} {name}")
+        got, want = strided_binary(hip, rb, rv, x, x, op, dtype)
+        assert_bitexact(got, want, f"{name} {op} x")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_strided_binary_views(hip, dtype):
+    base = inputs(17, 200 * 130, dtype).reshape(200, 130)
+    other = inputs(18, 130 * 200, dtype).reshape(130, 200)
+    mu = inputs(19, 130, dtype).reshape(130, 1)
+    cases = [
+        ("transpose-contig", base, base.T, other, other),
+        ("contig-transpose", other, other, base, base.T),
+        ("transpose-column", base, base.T, mu, mu),
+        ("slice-slice", base, base[10:140, 3:103], base, base[50:180, 20:120]),
+    ]
+    for name, lb, lv, rb, rv in cases:
+        got, want = strided_binary(hip, lb, lv, rb, rv, "subtract", dtype)
+        assert_bitexact(got, want, name)
+
+
+def test_strided_binary_odd_inner_extent(hip):
+    # inner extent not a multiple of 4: row-vector path must not be taken
+    x = inputs(20, 33 * 37, F32).reshape(33, 37)
+    bias = inputs(21, 37, F32)
+    got, want = strided_binary(hip, x, x, bias, bias, "add", F32)
+    assert_bitexact(got, want, "odd inner")
+
+
+# ------------------------------------------------------------ reductions
+
+def axis_reduce(hip, base, view, axes, op, dtype):
+    item = np.dtype(dtype).itemsize
+    offset = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // item
+    strides = [s // item for s in view.strides]
+    mask = 0
+    for a in axes:
+        mask |= 1 << a
+    kept = [d for i, d in enumerate(view.shape) if i not in axes]
+    out_dtype = np.int64 if op == "argmax" else dtype
+    out = out_buf(hip, kept, out_dtype)
+    opcode = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}[op]
+    hip.call("spar_hip_launch_axis_reduction", out.ptr, dev(hip, base).ptr, view.ndim,
+             hip.u64_array(view.shape), hip.u64_array(strides), offset, mask, tag(dtype), opcode, 0)
+    return out.to_numpy(out_dtype, kept)
+
+
+def check_axis(hip, base, view, axes, dtype, name):
+    n = int(np.prod([view.shape[a] for a in axes]))
+    s = ref.axis_sum(view, axes)
+    norm = np.sqrt(ref.axis_sum((view.astype(np.float64) ** 2), axes))
+    assert_red(axis_reduce(hip, base, view, axes, "sum", dtype), s, n, norm, f"{name} sum")
+    mean_ref = ref.scalar(s, "divide", float(n)).reshape(s.shape) if s.ndim else s / dtype(n)
+    assert_red(axis_reduce(hip, base, view, axes, "mean", dtype), mean_ref, n, norm / n,
+               f"{name} mean")
+    mx, am = ref.axis_max(view, axes)
+    assert_bitexact(axis_reduce(hip, base, view, axes, "max", dtype), mx, f"{name} max")
+    assert_bitexact(axis_reduce(hip, base, view, axes, "argmax", dtype), am, f"{name} argmax")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_axis_reductions_2d(hip, dtype):
+    base = inputs(22, 512 * 1536, dtype, with_specials=False).reshape(512, 1536)
+    for axes in ([0], [1], [0, 1]):
+        check_axis(hip, base, base, axes, dtype, f"contig {axes}")
+        check_axis(hip, base, base.T, axes, dtype, f"transposed {axes}")
+    sliced = base[7:300, 8:1032]
+    for axes in ([0], [1]):
+        check_axis(hip, base, sliced, axes, dtype, f"sliced {axes}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_axis_reductions_3d(hip, dtype):
+    base = inputs(23, 6 * 40 * 260, dtype, with_specials=False).reshape(6, 40, 260)
+    for axes in ([0], [1], [2], [0, 1], [0, 2], [1, 2], [0, 1, 2]):
+        check_axis(hip, base, base, axes, dtype, f"3d {axes}")
+    perm = base.transpose(2, 0, 1)
+    for axes in ([0], [2], [1, 2]):
+        check_axis(hip, base, perm, axes, dtype, f"3d perm {axes}")
+
+
+def test_max_argmax_ties_nan_signed_zero(hip):
+    rows = np.array([
+        [1.0, 3.0, 3.0, 2.0],
+        [-0.0, 0.0, -1.0, 0.0],
+        [0.0, -0.0, -0.0, -2.0],
+        [1.0, np.nan, 5.0, np.nan],
+        [-np.inf, -np.inf, -np.inf, -np.inf],
+        [np.inf, 1.0, np.inf, 0.0],
+    ], dtype=F32)
+    got = axis_reduce(hip, rows, rows, [1], "max", F32)
+    want, want_idx = ref.axis_max(rows, [1])
+    assert_bitexact(got, want, "max ties")
+    assert_bitexact(axis_reduce(hip, rows, rows, [1], "argmax", F32), want_idx, "argmax ties")
+    assert list(want_idx) == [1, 0, 0, 1, 0, 0]
+    assert np.signbit(got[1]) and not np.signbit(got[2])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 5, 1000, 1 << 16, 3 * (1 << 18) + 7])
+def test_full_reduction(hip, dtype, n):
+    x = (np.random.default_rng(24).random(n) * 2 - 1).astype(dtype)
+    dx = dev(hip, x)
+    out = out_buf(hip, (1,), np.int64)
+    norm = float(np.sqrt(np.sum(x.astype(np.float64) ** 2)))
+    for op, code in [("sum", hip.SUM), ("mean", hip.MEAN)]:
+        hip.call("spar_hip_launch_reduction", out.ptr, dx.ptr, n, tag(dtype), code, 0)
+        got = out.to_numpy(dtype, (1,))[0]
+        want = ref.full_reduce(x, op)
+        assert_red(got, want, n, norm / (n if op == "mean" else 1), f"full {op}")
+    hip.call("spar_hip_launch_reduction", out.ptr, dx.ptr, n, tag(dtype), hip.MAX, 0)
+    assert_bitexact(out.to_numpy(dtype, (1,)), np.array([ref.full_reduce(x, "max")]), "full max")
+    hip.call("spar_hip_launch_reduction", out.ptr, dx.ptr, n, tag(dtype), hip.ARGMAX, 0)
+    assert out.to_numpy(np.int64, (1,))[0] == int(np.argmax(x))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_row_reduction(hip, dtype):
+    rows, cols = 77, 3000
+    x = inputs(25, rows * cols, dtype, with_specials=False).reshape(rows, cols)
+    out = out_buf(hip, (rows,), np.int64)
+    dx = dev(hip, x)
+    hip.call("spar_hip_launch_row_reduction", out.ptr, dx.ptr, rows, cols, tag(dtype), hip.SUM, 0)
+    norm = np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=1))
+    assert_red(out.to_numpy(dtype, (rows,)), ref.axis_sum(x, [1]), cols, norm, "row sum")
+    hip.call("spar_hip_launch_row_reduction", out.ptr, dx.ptr, rows, cols, tag(dtype), hip.ARGMAX, 0)
+    assert_bitexact(out.to_numpy(np.int64, (rows,)), ref.axis_max(x, [1])[1], "row argmax")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("gshape,oshape", [
+    ((4, 64, 96), (96,)), ((4, 64, 96), (4, 1, 96)), ((4, 64, 96), (64, 1)),
+    ((4, 64, 96), (1, 64, 96)), ((4, 64, 96), (4, 64, 96)), ((4, 64, 96), ()),
+    ((3, 1, 5), (1, 5)), ((2048, 36), (36,)),
+])
+def test_broadcast_reduce_and_product(hip, dtype, gshape, oshape):
+    g = inputs(26, int(np.prod(gshape)), dtype, with_specials=False).reshape(gshape)
+    f = inputs(27, int(np.prod(gshape)), dtype, with_specials=False).reshape(gshape)
+    out = out_buf(hip, oshape, dtype)
+    n = max(int(np.prod(gshape)) // max(int(np.prod(oshape)), 1), 1)
+    want = ref.reduce_gradient(g, oshape)
+    norm = np.sqrt(ref.reduce_gradient(g.astype(np.float64) ** 2, oshape))
+    hip.call("spar_hip_launch_broadcast_reduce", out.ptr, dev(hip, g).ptr, len(gshape),
+             hip.u64_array(gshape), len(oshape), hip.u64_array(oshape), hip.u64_array([0] * 8),
+             g.size, tag(dtype), 0)
+    assert_red(out.to_numpy(dtype, oshape), want, n, norm, f"reduce {gshape}->{oshape}")
+    # multiply backward: reduce_gradient_to_shape(multiply(g, f)) in one pass
+    product = ref.binary(g, f, "multiply")
+    want = ref.reduce_gradient(product, oshape)
+    norm = np.sqrt(ref.reduce_gradient(product.astype(np.float64) ** 2, oshape))
+    hip.call("spar_hip_launch_multiply_reduce", out.ptr, dev(hip, g).ptr, dev(hip, f).ptr,
+             len(gshape), hip.u64_array(gshape), len(oshape), hip.u64_array(oshape), g.size,
+             tag(dtype), 0)
+    assert_red(out.to_numpy(dtype, oshape), want, n, norm, f"multiply_reduce {gshape}->{oshape}")
+
+
+# --------------------------------------------------------------- softmax
+
+def softmax_device(hip, x, outer, extent, inner, log, dtype):
+    out = out_buf(hip, x.shape, dtype)
+    undefined = out_buf(hip, (outer * inner,), np.int32)
+    hip.call("spar_hip_launch_probability_forward", out.ptr, undefined.ptr, dev(hip, x).ptr, outer,
+             extent, inner, tag(dtype), int(log), 0)
+    return out.to_numpy(dtype, x.shape), undefined.to_numpy(np.int32, (outer * inner,))
+
+
+def softmax_tolerance_check(got, want, extent, dtype, what):
+    """p = e / S: exp within 2 ulp, S within red(extent), one more rounding:
+    |dp| <= (4 eps + 1e-6 sqrt(extent)) |p| (+ tiny for underflowed p)."""
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
+    eps = np.finfo(dtype).eps
+    bound = (4 * eps + 1e-6 * np.sqrt(extent)) * np.abs(want) + np.finfo(dtype).tiny
+    ok = gn | (got == want) | (np.abs(got.astype(np.float64) - want) <= bound)
+    assert ok.all(), f"{what}: {(~ok).sum()} elements out of tolerance"
+
+
+def log_softmax_tolerance_check(got, want, extent, dtype, what):
+    """lp = (x - m) - log S: x - m is exact on both sides; log S differs by
+    S's relative difference (red) plus log's rounding; one final rounding:
+    |dlp| <= 1e-6 sqrt(extent) + 4 eps (|lp| + log(extent) + 1)."""
+    eps = np.finfo(dtype).eps
+    finite = np.isfinite(want)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), what
+    assert np.array_equal(got[~finite & ~np.isnan(want)], want[~finite & ~np.isnan(want)]), what
+    err = np.abs(got[finite].astype(np.float64) - want[finite])
+    bound = 1e-6 * np.sqrt(extent) + 4 * eps * (np.abs(want[finite]) + np.log(extent) + 1)
+    assert np.all(err <= bound), f"{what}: max err {err.max()}"
+
+
+def softmax_backward_bound(g, y, extent, dtype, log):
+    """softmax: dx = y (g - dot), |d dot| <= red(extent) with scale ||g||_2
+    (|y| <= 1), so |d dx| <= 1e-6 sqrt(n) ||g|| |y| + 4 eps (|dx| + |y| (|g| + max|g|)).
+    log-softmax: dx = g - exp(lp) s, |d s| <= 1e-6 sqrt(n) max(|s|, ||g||),
+    exp within 2 ulp: |d dx| <= e (1e-6 sqrt(n) max(|s|, ||g||) + 3 eps |s|) + 4 eps (|dx| + |g|)."""
+    eps = np.finfo(dtype).eps
+    g64 = g.astype(np.float64)
+    norm = np.sqrt(np.sum(g64 ** 2, axis=-1, keepdims=True))
+    if not log:
+        dot = np.sum(g64 * y, axis=-1, keepdims=True)
+        dx = y * (g64 - dot)
+        bound = 1e-6 * np.sqrt(extent) * norm * np.abs(y) + 4 * eps * (
+            np.abs(dx) + np.abs(y) * (np.abs(g64) + np.abs(g64).max(axis=-1, keepdims=True)))
+    else:
+        e = np.exp(y.astype(np.float64))
+        total = np.sum(g64, axis=-1, keepdims=True)
+        dx = g64 - e * total
+        bound = e * (1e-6 * np.sqrt(extent) * np.maximum(np.abs(total), norm)
+                     + 3 * eps * np.abs(total)) + 4 * eps * (np.abs(dx) + np.abs(g64))
+    return bound + np.finfo(dtype).tiny
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,extent", [(3, 1), (5, 7), (64, 1000), (16, 1024), (8, 4096),
+                                         (4, 8192), (4, 12000), (2, 16384), (2, 32768),
+                                         (2, 32770), (1, 40000)])
+def test_softmax_rows(hip, dtype, rows, extent):
+    x = (inputs(28, rows * extent, dtype, with_specials=False) * dtype(np.sqrt(2))).reshape(rows, extent)
+    got, und = softmax_device(hip, x, rows, extent, 1, False, dtype)
+    want, und_ref = ref.softmax_axis(x, 1)
+    softmax_tolerance_check(got, want, extent, dtype, f"softmax {rows}x{extent}")
+    assert np.array_equal(und, und_ref.astype(np.int32))
+    lgot, _ = softmax_device(hip, x, rows, extent, 1, True, dtype)
+    lwant, _ = ref.log_softmax(x, 1)
+    log_softmax_tolerance_check(lgot, lwant, extent, dtype, f"log_softmax {rows}x{extent}")
+
+    g = inputs(29, rows * extent, dtype, with_specials=False).reshape(rows, extent)
+    dund = dev(hip, und_ref.astype(np.int32))
+    for log, saved, back in [(False, want, ref.softmax_axis_backward(g, want, und_ref, 1)),
+                             (True, lwant, ref.log_softmax_backward(g, lwant, und_ref, 1))]:
+        out = out_buf(hip, x.shape, dtype)
+        hip.call("spar_hip_launch_probability_backward", out.ptr, dev(hip, g).ptr,
+                 dev(hip, saved).ptr, dund.ptr, rows, extent, 1, tag(dtype), int(log), 0)
+        got_b = out.to_numpy(dtype, x.shape)
+        err = np.abs(got_b.astype(np.float64) - back)
+        bound = softmax_backward_bound(g, saved, extent, dtype, log)
+        assert np.all(err <= bound), f"backward log={log} worst {(err / bound).max()}x bound"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_softmax_special_slices(hip, dtype):
+    inf, nan = np.inf, np.nan
+    x = np.array([
+        [1.0, 2.0, 3.0, 4.0],
+        [nan, 1.0, 2.0, 3.0],
+        [-inf, -inf, -inf, -inf],
+        [inf, 1.0, inf, -inf],
+        [inf, 0.0, 0.0, 0.0],
+        [-inf, 0.0, -inf, 1.0],
+        [-0.0, 0.0, -inf, -inf],
+    ], dtype=dtype)
+    rows, extent = x.shape
+    for log in (False, True):
+        got, und = softmax_device(hip, x, rows, extent, 1, log, dtype)
+        want, und_ref = (ref.log_softmax(x, 1) if log else ref.softmax_axis(x, 1))
+        assert np.array_equal(und, und_ref.astype(np.int32))
+        assert_ulp(got, want, 2, f"special log={log}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape,axis", [((6, 50, 33), 1), ((40, 9), 0), ((3, 4, 5, 6), 2)])
+def test_softmax_inner_axis(hip, dtype, shape, axis):
+    x = inputs(30, int(np.prod(shape)), dtype, with_specials=False).reshape(shape)
+    outer = int(np.prod(shape[:axis]))
+    inner = int(np.prod(shape[axis + 1:]))
+    got, und = softmax_device(hip, x, outer, shape[axis], inner, False, dtype)
+    want, und_ref = ref.softmax_axis(x, axis)
+    softmax_tolerance_check(got, want, shape[axis], dtype, "inner-axis softmax")
+    g = inputs(31, x.size, dtype, with_specials=False).reshape(shape)
+    back = ref.softmax_axis_backward(g, want, und_ref, axis)
+    out = out_buf(hip, shape, dtype)
+    hip.call("spar_hip_launch_probability_backward", out.ptr, dev(hip, g).ptr, dev(hip, want).ptr,
+             dev(hip, und_ref.astype(np.int32)).ptr, outer, shape[axis], inner, tag(dtype), 0, 0)
+    err = np.abs(out.to_numpy(dtype, shape).astype(np.float64) - back)
+    g_axis_last = np.moveaxis(g, axis, -1)
+    y_axis_last = np.moveaxis(want, axis, -1)
+    bound = np.moveaxis(softmax_backward_bound(g_axis_last, y_axis_last, shape[axis], dtype, False),
+                        -1, axis)
+    assert np.all(err <= bound)
+
+
+# ---------------------------------------------------------------- random
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_random_uniform_matches_host_generator(hip, dtype):
+    n = 100001
+    out = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_random_uniform", out.ptr, n, tag(dtype), 1234, -1.0, 1.0, 0)
+    want = ref.Random(1234).uniform((n,), dtype, -1.0, 1.0)
+    assert_bitexact(out.to_numpy(dtype, (n,)), want, "uniform")
+
+
+def test_random_normal_close_to_host_generator(hip):
+    n = 100001
+    out = out_buf(hip, (n,), F32)
+    hip.call("spar_hip_random_normal", out.ptr, n, 0, 99, 0.0, 2.0, 0)
+    want = ref.Random(99).normal((n,), F32, 0.0, 2.0)
+    assert_ulp(out.to_numpy(F32, (n,)), want, 1, "normal")
+
+
+# ----------------------------------------------------------- error paths
+
+def test_status_codes_on_device(hip):
+    st = hip.status_of("spar_hip_launch_binary", None, None, None, 0, 0, 0, 0)
+    assert st.code == 0  # count 0: success without touching the device
+    st = hip.status_of("spar_hip_launch_binary", None, None, None, 5, 0, 0, 0)
+    assert st.code == 1
+    st = hip.status_of("spar_hip_launch_unary", None, None, 0, 0, 0, 999)
+    assert st.code == 0
+    st = hip.status_of("spar_hip_synchronize", 999)
+    assert st.code == 2
