@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Benchmark of the fp32 elementwise / broadcast / reduction path on one MI355X.
+
+Default workload (one "step" = one pass of the hot path over one batch):
+broadcast binary ops on x[32,1024,4096] fp32 ~ N(0,1) with bias[4096] ~
+U(-0.1,0.1) and scale[32,1,4096] ~ U(0.5,1.5), forward and backward:
+    y1 = x + bias                     (broadcast binary)
+    y2 = x * scale                    (broadcast binary)
+    dbias  = sum_{B,T} G              (broadcast-gradient reduction)
+    dscale = sum_T G * x              (fused product reduction)
+    dx     = G * scale                (broadcast binary)
+with upstream gradient G ~ N(0,1).  Every op runs through the backend's C ABI
+(the entry points the Tensor layer calls) with inputs resident in HBM.
+
+`value` is the step's algorithmic HBM bytes (each distinct input byte read
+once, each output byte written once, broadcast operands at their stored size)
+divided by the measured time, in GB/s (1e9 B/s).  One JSON line is printed.
+`--suite` additionally measures every op of the five benchmark configurations
+and prints one JSON line per op.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E peak, 8 TB/s
+METRIC = "achieved HBM GB/s (% of MI355X peak) for fp32 elementwise/broadcast/reduce ops"
+
+B, T, C = 32, 1024, 4096
+SEEDS = {"x": 11, "bias": 12, "scale": 13, "G": 14}
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--suite", action="store_true", help="also measure every config op")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--profile-loop", type=int, default=0,
+                   help="run only N steps of the workload (for rocprofv3) and exit")
+    return p.parse_args()
+
+
+class Workload:
+    """Device buffers and launchers of the broadcast workload."""
+
+    def __init__(self, hip, batch=B):
+        self.hip = hip
+        self.batch = batch
+        n = batch * T * C
+        self.n = n
+        f = 4
+        self.x = hip.DeviceBuffer(n * f)
+        self.G = hip.DeviceBuffer(n * f)
+        self.bias = hip.DeviceBuffer(C * f)
+        self.scale = hip.DeviceBuffer(batch * C * f)
+        self.y1 = hip.DeviceBuffer(n * f)
+        self.y2 = hip.DeviceBuffer(n * f)
+        self.dx = hip.DeviceBuffer(n * f)
+        self.dbias = hip.DeviceBuffer(C * f)
+        self.dscale = hip.DeviceBuffer(batch * C * f)
+        hip.call("spar_hip_random_normal", self.x.ptr, n, hip.FLOAT32, SEEDS["x"], 0.0, 1.0, 0)
+        hip.call("spar_hip_random_normal", self.G.ptr, n, hip.FLOAT32, SEEDS["G"], 0.0, 1.0, 0)
+        hip.call("spar_hip_random_uniform", self.bias.ptr, C, hip.FLOAT32, SEEDS["bias"], -0.1, 0.1, 0)
+        hip.call("spar_hip_random_uniform", self.scale.ptr, batch * C, hip.FLOAT32, SEEDS["scale"],
+                 0.5, 1.5, 0)
+        u = hip.u64_array
+        self.shape3 = u([batch, T, C])
+        self.x_strides = u([T * C, C, 1])
+        self.bias_strides = u([0, 0, 1])
+        self.scale_strides = u([C, 0, 1])
+        self.bias_shape = u([C])
+        self.scale_shape = u([batch, 1, C])
+        self.zero8 = u([0] * 8)
+        hip.synchronize()
+
+    # algorithmic bytes of each op
+    def op_bytes(self):
+        n, f = self.n, 4
+        return {
+            "x+bias": 2 * n * f + C * f,
+            "x*scale": 2 * n * f + self.batch * C * f,
+            "dbias=sum_BT(G)": n * f + C * f,
+            "dscale=sum_T(G*x)": 2 * n * f + self.batch * C * f,
+            "dx=G*scale": 2 * n * f + self.batch * C * f,
+        }
+
+    def ops(self):
+        hip = self.hip
+        call = hip.call
+        F = hip.FLOAT32
+        return [
+            ("x+bias", "broadcast_binary", lambda: call(
+                "spar_hip_launch_strided_binary", self.y1.ptr, self.x.ptr, self.x_strides, 0,
+                self.bias.ptr, self.bias_strides, 0, 3, self.shape3, F, hip.ADD, 0)),
+            ("x*scale", "broadcast_binary", lambda: call(
+                "spar_hip_launch_strided_binary", self.y2.ptr, self.x.ptr, self.x_strides, 0,
+                self.scale.ptr, self.scale_strides, 0, 3, self.shape3, F, hip.MULTIPLY, 0)),
+            ("dbias=sum_BT(G)", "column_reduction", lambda: call(
+                "spar_hip_launch_broadcast_reduce", self.dbias.ptr, self.G.ptr, 3, self.shape3, 1,
+                self.bias_shape, self.zero8, self.n, F, 0)),
+            ("dscale=sum_T(G*x)", "column_reduction", lambda: call(
+                "spar_hip_launch_multiply_reduce", self.dscale.ptr, self.G.ptr, self.x.ptr, 3,
+                self.shape3, 3, self.scale_shape, self.n, F, 0)),
+            ("dx=G*scale", "broadcast_binary", lambda: call(
+                "spar_hip_launch_strided_binary", self.dx.ptr, self.G.ptr, self.x_strides, 0,
+                self.scale.ptr, self.scale_strides, 0, 3, self.shape3, F, hip.MULTIPLY, 0)),
+        ]
+
+    def step(self):
+        for _, _, launch in self.ops():
+            launch()
+
+
+def time_ops(hip, ops, reps=20, warmup=3):
+    """Median and mean event time (ms) of each op, each launch bracketed by
+    HIP events recorded on the backend's stream."""
+    for _ in range(warmup):
+        for _, _, launch in ops:
+            launch()
+    hip.synchronize()
+    times = {name: [] for name, _, _ in ops}
+    start, stop = hip.Event(), hip.Event()
+    for _ in range(reps):
+        for name, _, launch in ops:
+            start.record()
+            launch()
+            stop.record()
+            times[name].append(start.elapsed_ms(stop))
+    return times
+
+
+def cpu_baseline(hip, work: Workload, sample_batch=16, repeats=3):
+    """The oracle (a 1-thread C restatement of Spar's CPU loops) on the first
+    `sample_batch` batch rows of the same device inputs."""
+    import oracle.ops as O
+
+    rows = sample_batch * T * C
+    x = work.x.to_numpy(np.float32, (B, T, C))[:sample_batch].copy()
+    G = work.G.to_numpy(np.float32, (B, T, C))[:sample_batch].copy()
+    bias = work.bias.to_numpy(np.float32, (C,))
+    scale = work.scale.to_numpy(np.float32, (B, 1, C))[:sample_batch].copy()
+    sample = Workload.__new__(Workload)
+    sample.n, sample.batch = rows, sample_batch
+    nbytes = Workload.op_bytes(sample)
+    ops = [
+        ("x+bias", lambda: O.binary(x, bias, "add")),
+        ("x*scale", lambda: O.binary(x, scale, "multiply")),
+        ("dbias=sum_BT(G)", lambda: O.reduce_gradient(G, (C,))),
+        ("dscale=sum_T(G*x)", lambda: O.reduce_gradient(O.binary(G, x, "multiply"), (sample_batch, 1, C))),
+        ("dx=G*scale", lambda: O.binary(G, scale, "multiply")),
+    ]
+    per_rep = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        for _, fn in ops:
+            fn()
+        per_rep.append(time.perf_counter() - t0)
+    seconds = statistics.median(per_rep)
+    total = sum(nbytes.values())
+    return {
+        "value": round(total / seconds / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"the same five ops on the first {sample_batch} of {B} batch rows "
+                   f"(x[{sample_batch},{T},{C}]), oracle C loops compiled -O2 -ffp-contract=off, "
+                   f"median of {repeats} runs of {sum(per_rep) / repeats:.2f} s; host "
+                   f"{os.cpu_count()} logical CPUs, 1 thread used"),
+        "seconds_per_step_sample": round(seconds, 4),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); this backend's "
+              "benchmark is a single-device measurement", file=sys.stderr)
+        sys.exit(2)
+    from spar_amd import hip
+
+    hip.load()
+    if hip.device_count() < 1:
+        print("no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+
+    work = Workload(hip)
+    if args.profile_loop:
+        for _ in range(args.profile_loop):
+            work.step()
+        hip.synchronize()
+        print(json.dumps({"profile_loop_steps": args.profile_loop}))
+        return
+
+    nbytes = work.op_bytes()
+    step_bytes = sum(nbytes.values())
+    for _ in range(args.warmup):
+        work.step()
+    hip.synchronize()
+
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        work.step()
+    stop.record()
+    hip.synchronize()
+    wall = time.perf_counter() - wall0
+    elapsed_ms = start.elapsed_ms(stop)
+    ms_per_step = elapsed_ms / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # per-kernel event timing (same stream as the launches)
+    ops = work.ops()
+    times = time_ops(hip, ops)
+    per_op = {}
+    kernel_time = {}
+    kernel_bytes = {}
+    for name, kernel, _ in ops:
+        mean_ms = statistics.mean(times[name])
+        gbps = nbytes[name] / (mean_ms * 1e-3) / 1e9
+        per_op[name] = {"kernel": kernel, "ms": round(mean_ms, 5), "GB/s": round(gbps, 1),
+                        "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": nbytes[name]}
+        kernel_time[kernel] = kernel_time.get(kernel, 0.0) + mean_ms
+        kernel_bytes[kernel] = kernel_bytes.get(kernel, 0) + nbytes[name]
+    dominant = max(kernel_time, key=kernel_time.get)
+    launches = sum(1 for _, k, _ in ops if k == dominant)
+    achieved = kernel_bytes[dominant] / (kernel_time[dominant] * 1e-3) / 1e9
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    traffic = None
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get(dominant)
+    roofline = {
+        "bound": "hbm",
+        "kernel": dominant,
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "traffic": traffic,
+        "bytes_per_launch": kernel_bytes[dominant] // launches,
+        "avg_launch_ms": round(kernel_time[dominant] / launches, 5),
+    }
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (device SplitMix64 generator, seeds %s)" % SEEDS,
+        "config": {
+            "workload": "broadcast binary fp32: x[32,1024,4096]+bias[4096], x*scale[32,1,4096]; "
+                        "backward dbias=sum_BT(G), dscale=sum_T(G*x), dx=G*scale",
+            "elements": work.n,
+            "step_bytes": step_bytes,
+            "parallelism": "single device",
+        },
+        "frac_of_peak": round(value / HBM_PEAK_GBPS, 4),
+        "elements_per_s": round(5 * work.n / (ms_per_step * 1e-3), 1),
+        "wall_s": round(wall, 4),
+        "per_op": per_op,
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(hip, work)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

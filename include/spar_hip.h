@@ -64,7 +64,9 @@ enum SparHipBinaryOp {
 
 /* Unary operations.  0-7 equal SparCudaUnaryOp (cuda_kernels.hpp:24-33).
  * TANH and GELU are additions: gelu(x) = 0.5 * x * erfc(-x * (1/sqrt(2))),
- * evaluated in double precision and rounded once to the element type. */
+ * evaluated in double precision and rounded once to the element type.
+ * GELU_DERIVATIVE (used by the gelu backward rule) is
+ * 0.5 * erfc(-x / sqrt(2)) + x * exp(-x*x/2) / sqrt(2 pi), evaluated the same way. */
 enum SparHipUnaryOp {
   SPAR_HIP_NEGATE = 0,
   SPAR_HIP_SQUARE = 1,
@@ -76,6 +78,7 @@ enum SparHipUnaryOp {
   SPAR_HIP_SILU = 7,
   SPAR_HIP_TANH = 8,
   SPAR_HIP_GELU = 9,
+  SPAR_HIP_GELU_DERIVATIVE = 10,
 };
 
 /* Reductions.  0-2 equal SparCudaReductionOp (cuda_kernels.hpp:35-39).
@@ -201,6 +204,17 @@ struct SparHipStatus spar_hip_launch_strided_copy(void* destination, const void*
                                                   const uint64_t* strides,
                                                   uint64_t storage_offset, uint64_t count,
                                                   uint64_t element_size, int device);
+
+/* Scatter: writes the contiguous `source` (rank, extents) into the strided
+ * destination view (destination base, strides, storage_offset).  Used for
+ * gradients of narrowed views and value copies into views (the reference's
+ * copy_tensor_values, src/core/tensor.cpp:514-537, needed a contiguous
+ * destination). */
+struct SparHipStatus spar_hip_launch_strided_assign(void* destination, uint64_t rank,
+                                                    const uint64_t* extents,
+                                                    const uint64_t* strides,
+                                                    uint64_t storage_offset, const void* source,
+                                                    uint64_t element_size, int device);
 
 /* Binary op over the broadcast shape `extents` (rank dims) without
  * materialising either operand: each operand is read through its own strides

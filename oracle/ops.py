@@ -16,7 +16,7 @@ from . import fn, lib, ptr, u64
 BINARY = {"add": 0, "subtract": 1, "multiply": 2, "divide": 3, "equal": 4, "not_equal": 5,
           "less": 6, "less_equal": 7, "greater": 8, "greater_equal": 9}
 UNARY = {"negate": 0, "square": 1, "reciprocal": 2, "exp": 3, "log": 4, "sqrt": 5,
-         "sigmoid": 6, "silu": 7, "tanh": 8, "gelu": 9}
+         "sigmoid": 6, "silu": 7, "tanh": 8, "gelu": 9, "gelu_derivative": 10}
 
 
 def _view(array: np.ndarray):

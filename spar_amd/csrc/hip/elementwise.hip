@@ -279,7 +279,7 @@ extern "C" SparHipStatus spar_hip_launch_scalar(void* output, const void* input,
 
 extern "C" SparHipStatus spar_hip_launch_unary(void* output, const void* input, uint64_t count,
                                                int dtype, int operation, int device) {
-  if (!valid_float_dtype(dtype) || operation < SPAR_HIP_NEGATE || operation > SPAR_HIP_GELU ||
+  if (!valid_float_dtype(dtype) || operation < SPAR_HIP_NEGATE || operation > SPAR_HIP_GELU_DERIVATIVE ||
       (count != 0 && (output == nullptr || input == nullptr))) {
     return invalid();
   }

@@ -150,6 +150,22 @@ struct GeluOp {
   __device__ __forceinline__ double operator()(double x) const { return gelu_double(x); }
 };
 
+// gelu'(x) = Phi(x) + x phi(x) = 0.5 erfc(-x/sqrt 2) + x exp(-x^2/2)/sqrt(2 pi),
+// in double precision, rounded once.
+__device__ __forceinline__ double gelu_derivative_double(double x) {
+  const double cdf = 0.5 * erfc(-x * 0.70710678118654752440);
+  const double pdf = exp(-0.5 * (x * x)) * 0.39894228040143267794;
+  return cdf + x * pdf;
+}
+struct GeluDerivativeOp {
+  __device__ __forceinline__ float operator()(float x) const {
+    return static_cast<float>(gelu_derivative_double(static_cast<double>(x)));
+  }
+  __device__ __forceinline__ double operator()(double x) const {
+    return gelu_derivative_double(x);
+  }
+};
+
 template <typename Body>
 inline bool dispatch_unary(int operation, Body&& body) {
   switch (operation) {
@@ -163,6 +179,7 @@ inline bool dispatch_unary(int operation, Body&& body) {
     case SPAR_HIP_SILU: body(SiluOp{}); return true;
     case SPAR_HIP_TANH: body(TanhOp{}); return true;
     case SPAR_HIP_GELU: body(GeluOp{}); return true;
+    case SPAR_HIP_GELU_DERIVATIVE: body(GeluDerivativeOp{}); return true;
     default: return false;
   }
 }

@@ -444,3 +444,74 @@ extern "C" SparHipStatus spar_hip_launch_strided_binary(void* output, const void
   });
   return finish(guard);
 }
+
+namespace spar_hip {
+namespace {
+
+// Scatter of a contiguous source into a strided destination view: element e
+// of the source goes to the destination offset decoded from e.
+template <typename T, bool kIndex32>
+__global__ void __launch_bounds__(kThreads)
+    scatter_kernel(T* destination, const T* source, uint64_t count, KernelGeometry g) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; e < count;
+       e += stride) {
+    uint64_t off[2];
+    decode<1, kIndex32>(e, g, off);
+    destination[off[0]] = source[e];
+  }
+}
+
+template <typename T>
+void launch_scatter(void* destination, const void* source, const MultiView& view,
+                    const DeviceGuard& guard) {
+  const uint64_t count = view_numel(view);
+  const KernelGeometry g = kernel_geometry(view);
+  uint64_t blocks = (count + kThreads - 1) / kThreads;
+  const uint64_t cap = static_cast<uint64_t>(guard.multiprocessors) * 32;
+  if (blocks > cap) blocks = cap;
+  if (blocks == 0) blocks = 1;
+  if (count <= kIndex32Limit) {
+    scatter_kernel<T, true><<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(
+        static_cast<T*>(destination), static_cast<const T*>(source), count, g);
+  } else {
+    scatter_kernel<T, false><<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(
+        static_cast<T*>(destination), static_cast<const T*>(source), count, g);
+  }
+}
+
+}  // namespace
+}  // namespace spar_hip
+
+extern "C" SparHipStatus spar_hip_launch_strided_assign(void* destination, uint64_t rank,
+                                                        const uint64_t* extents,
+                                                        const uint64_t* strides,
+                                                        uint64_t storage_offset,
+                                                        const void* source,
+                                                        uint64_t element_size, int device) {
+  if ((element_size != 4U && element_size != 8U) || rank > kMaxRank ||
+      (rank != 0 && (extents == nullptr || strides == nullptr))) {
+    return invalid();
+  }
+  MultiView view;
+  view.rank = static_cast<int>(rank);
+  view.operands = 1;
+  uint64_t count = 1;
+  for (uint64_t axis = 0; axis < rank; ++axis) {
+    view.extents[axis] = extents[axis];
+    view.strides[0][axis] = strides[axis];
+    count *= extents[axis];
+  }
+  view.offsets[0] = storage_offset;
+  if (count == 0) return ok();
+  if (destination == nullptr || source == nullptr) return invalid();
+  coalesce(view);
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (element_size == 4U) {
+    launch_scatter<float>(destination, source, view, guard);
+  } else {
+    launch_scatter<double>(destination, source, view, guard);
+  }
+  return finish(guard);
+}

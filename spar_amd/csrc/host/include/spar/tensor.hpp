@@ -1,0 +1,233 @@
+// spar::Tensor for the HIP device backend.
+//
+// Mirrors the reference's spar.tensor module (src/core/tensor.cppm:22-218,
+// src/core/tensor.cpp:26-632, src/autograd/autograd.cpp:43-265): a typed,
+// shaped, strided view over reference-counted Storage with reverse-mode
+// autograd.  Storage is host memory (Device::cpu()) or HBM of an MI355X
+// (Device::hip(i)) obtained from the backend's caching allocator.  Every
+// arithmetic op runs on the HIP device; CPU tensors are host buffers for
+// construction, typed access and transfers.
+#pragma once
+
+#include <algorithm>
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <initializer_list>
+#include <memory>
+#include <optional>
+#include <span>
+#include <stdexcept>
+#include <string_view>
+#include <vector>
+
+#include "spar/core.hpp"
+
+namespace spar {
+class Tensor;
+}
+
+namespace spar::detail {
+
+struct AutogradAccess;
+struct AutogradMeta;
+struct HipTensorAccess;
+
+/// Ref-counted allocation (src/core/storage.cppm:10-33): host bytes, or a
+/// device block from the backend's caching allocator.
+class Storage final {
+ public:
+  Storage(std::size_t nbytes, Device device);
+  Storage(const Storage&) = delete;
+  Storage& operator=(const Storage&) = delete;
+  ~Storage() noexcept;
+
+  [[nodiscard]] std::byte* host_data();
+  [[nodiscard]] const std::byte* host_data() const;
+  [[nodiscard]] void* hip_data();
+  [[nodiscard]] const void* hip_data() const;
+  [[nodiscard]] Device device() const noexcept;
+  [[nodiscard]] std::size_t nbytes() const noexcept;
+  void swap_payload(Storage& other) noexcept;
+
+ private:
+  std::size_t nbytes_;
+  Device device_;
+  std::unique_ptr<std::byte[]> host_data_;
+  void* hip_data_;
+};
+
+}  // namespace spar::detail
+
+namespace spar {
+
+/// A typed, shaped, strided view over reference-counted Storage.
+/// Copies and metadata-only views share Storage; `clone()` copies.
+class Tensor {
+ public:
+  /// allocates contiguous row-major storage without initialising it.
+  Tensor(Shape shape, DType dtype, Device device = Device::cpu());
+  Tensor(const Tensor&) = default;
+  Tensor& operator=(const Tensor&) = default;
+  Tensor(Tensor&& other) noexcept;
+  Tensor& operator=(Tensor&& other) noexcept;
+  ~Tensor();
+
+  void swap(Tensor& other) noexcept;
+
+  [[nodiscard]] std::size_t rank() const noexcept;
+  [[nodiscard]] const Shape& shape() const noexcept;
+  [[nodiscard]] std::span<const Shape::stride_type> strides() const noexcept;
+  [[nodiscard]] std::size_t storage_offset() const noexcept;
+  [[nodiscard]] std::size_t numel() const noexcept;
+  [[nodiscard]] DType dtype() const noexcept;
+  [[nodiscard]] Device device() const noexcept;
+  /// logical tensor bytes, not the size of the shared allocation.
+  [[nodiscard]] std::size_t nbytes() const noexcept;
+  [[nodiscard]] bool is_contiguous() const noexcept;
+
+  [[nodiscard]] bool requires_grad() const noexcept;
+  [[nodiscard]] bool is_leaf() const noexcept;
+  [[nodiscard]] bool has_grad() const noexcept;
+  void set_requires_grad(bool enabled = true);
+  [[nodiscard]] Tensor grad() const;
+  void zero_grad();
+  /// first-order reverse-mode differentiation from a one-element loss.
+  void backward();
+  [[nodiscard]] Tensor detach() const;
+  /// transfers logical values; a same-Device transfer preserves identity.
+  [[nodiscard]] Tensor to(Device target) const;
+
+  [[nodiscard]] Tensor clone() const;
+  [[nodiscard]] Tensor contiguous() const;
+  [[nodiscard]] Tensor reshape(Shape new_shape) const;
+  [[nodiscard]] Tensor transpose(std::size_t axis_a, std::size_t axis_b) const;
+  [[nodiscard]] Tensor permute(std::span<const std::size_t> axes) const;
+  [[nodiscard]] Tensor permute(std::initializer_list<std::size_t> axes) const;
+  [[nodiscard]] Tensor expand(Shape target_shape) const;
+  /// metadata-only view of `length` entries of `axis` starting at `start`
+  /// (no reference counterpart; needed for offset sub-block views).
+  [[nodiscard]] Tensor narrow(std::size_t axis, std::size_t start, std::size_t length) const;
+
+  template <typename T> [[nodiscard]] std::span<T> span() & {
+    if (requires_grad()) {
+      throw std::logic_error{
+          "Mutable tensor access requires a non-grad Tensor identity; detach explicitly first"};
+    }
+    validate_access<T>();
+    if (numel() == 0) return {};
+    return {reinterpret_cast<T*>(mutable_host_data()) + storage_offset_, numel()};
+  }
+
+  template <typename T> [[nodiscard]] std::span<const T> span() const& {
+    validate_access<T>();
+    if (numel() == 0) return {};
+    return {reinterpret_cast<const T*>(host_data()) + storage_offset_, numel()};
+  }
+
+  template <typename T> std::span<T> span() && = delete;
+  template <typename T> std::span<const T> span() const&& = delete;
+
+  template <typename T> void fill(T value) & {
+    auto values{span<T>()};
+    std::fill(values.begin(), values.end(), value);
+  }
+
+ private:
+  friend struct detail::AutogradAccess;
+  friend struct detail::HipTensorAccess;
+  friend Tensor zeros(Shape shape, DType dtype, Device device);
+  friend Tensor full_value(Shape shape, DType dtype, double value, Device device);
+
+  Tensor(std::shared_ptr<detail::Storage> storage, DType dtype, Shape shape,
+         std::vector<Shape::stride_type> strides, std::size_t storage_offset);
+
+  void initialize_autograd();
+  void reset_to_empty() noexcept;
+  void validate_view_bounds() const;
+
+  [[nodiscard]] static std::size_t checked_nbytes(std::size_t numel, DType dtype);
+  [[nodiscard]] std::size_t checked_storage_byte_offset() const;
+  [[nodiscard]] Tensor materialize_values(Device target) const;
+  [[nodiscard]] std::byte* mutable_host_data();
+  [[nodiscard]] const std::byte* host_data() const;
+
+  template <typename T> void validate_access() const {
+    if (!device().is_cpu()) throw std::logic_error{"Tensor span requires CPU Storage"};
+    if (dtype_of<T>() != dtype_) {
+      throw std::invalid_argument{"Typed tensor access does not match the tensor dtype"};
+    }
+    if (!is_contiguous()) throw std::invalid_argument{"Tensor span requires a contiguous tensor"};
+  }
+
+  std::shared_ptr<detail::Storage> storage_;
+  DType dtype_;
+  Shape shape_;
+  std::vector<Shape::stride_type> strides_;
+  std::size_t storage_offset_;
+  std::size_t nbytes_;
+  std::shared_ptr<detail::AutogradMeta> autograd_;
+};
+
+void swap(Tensor& left, Tensor& right) noexcept;
+
+/// contiguous tensor of zeros (tensor.cpp:429-450).
+[[nodiscard]] Tensor zeros(Shape shape, DType dtype, Device device = Device::cpu());
+/// contiguous tensor of ones (tensor.cpp:452-481).
+[[nodiscard]] Tensor ones(Shape shape, DType dtype, Device device = Device::cpu());
+/// contiguous tensor filled with `value` converted to `dtype`.
+[[nodiscard]] Tensor full_value(Shape shape, DType dtype, double value,
+                                Device device = Device::cpu());
+
+/// contiguous tensor filled with `value`, dtype inferred from T
+/// (tensor.cppm:167-178); device tensors are filled by a device kernel.
+template <typename T>
+[[nodiscard]] Tensor full(Shape shape, T value, Device device = Device::cpu()) {
+  if (device.is_cpu()) {
+    Tensor tensor{std::move(shape), dtype_of<T>(), device};
+    tensor.template fill<T>(value);
+    return tensor;
+  }
+  return full_value(std::move(shape), dtype_of<T>(), static_cast<double>(value), device);
+}
+
+/// copies host values into a new CPU tensor of `shape`.
+template <typename T>
+[[nodiscard]] Tensor from_values(Shape shape, std::span<const T> values) {
+  Tensor tensor{std::move(shape), dtype_of<T>(), Device::cpu()};
+  if (values.size() != tensor.numel()) {
+    throw std::invalid_argument{"from_values needs exactly one value per element"};
+  }
+  auto out{tensor.template span<T>()};
+  std::copy(values.begin(), values.end(), out.begin());
+  return tensor;
+}
+
+}  // namespace spar
+
+namespace spar::detail {
+
+/// Raw device pointers of contiguous HIP tensors (tensor.cpp:487-506).
+struct HipTensorAccess final {
+  [[nodiscard]] static void* mutable_data(Tensor& tensor);
+  [[nodiscard]] static const void* data(const Tensor& tensor);
+  /// base pointer of the tensor's storage (views index from it).
+  [[nodiscard]] static const void* storage_base(const Tensor& tensor);
+};
+
+[[nodiscard]] Shape broadcast_shape(const Shape& left, const Shape& right);
+void validate_same_device(const Tensor& left, const Tensor& right, std::string_view operation);
+/// every arithmetic op of this backend runs on a HIP device.
+void require_hip(const Tensor& tensor, std::string_view operation);
+void copy_tensor_values(Tensor& destination, const Tensor& source);
+void swap_storage_payloads(Tensor& original, Tensor& staged) noexcept;
+[[nodiscard]] Tensor reduce_gradient_to_shape(const Tensor& gradient, const Shape& original_shape);
+
+using BackwardFunction = std::function<std::vector<Tensor>(const Tensor&)>;
+
+void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
+                      BackwardFunction backward);
+void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward);
+[[nodiscard]] bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept;
+
+}  // namespace spar::detail

@@ -1,0 +1,253 @@
+// Python binding of the host library (spar_amd._spar) for tests, benchmarks
+// and Python users.  It exposes the same names as the C++ API; exceptions map
+// to Python as: std::invalid_argument -> ValueError, std::out_of_range ->
+// IndexError, std::overflow_error -> OverflowError, other std::logic_error ->
+// spar_amd._spar.LogicError, std::runtime_error -> RuntimeError.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstring>
+
+#include "spar/spar.hpp"
+
+namespace py = pybind11;
+using spar::Device;
+using spar::DType;
+using spar::Shape;
+using spar::Tensor;
+
+namespace {
+
+Shape to_shape(const std::vector<std::int64_t>& dims) { return Shape{dims}; }
+
+py::tuple shape_tuple(const Shape& shape) {
+  py::tuple t(shape.rank());
+  for (std::size_t i = 0; i < shape.rank(); ++i) t[i] = shape[i];
+  return t;
+}
+
+py::dtype numpy_dtype(DType dtype) {
+  switch (dtype) {
+    case DType::Float32: return py::dtype::of<float>();
+    case DType::Float64: return py::dtype::of<double>();
+    case DType::Int32: return py::dtype::of<std::int32_t>();
+    case DType::Int64: return py::dtype::of<std::int64_t>();
+  }
+  throw std::logic_error{"unknown dtype"};
+}
+
+template <typename T>
+Tensor tensor_from(py::array_t<T, py::array::c_style | py::array::forcecast> array) {
+  std::vector<std::int64_t> dims(array.shape(), array.shape() + array.ndim());
+  const auto* begin = array.data();
+  return spar::from_values<T>(Shape{dims}, std::span<const T>{begin, static_cast<std::size_t>(array.size())});
+}
+
+Tensor from_numpy(py::array array) {
+  const auto kind = array.dtype().kind();
+  const auto size = array.dtype().itemsize();
+  if (kind == 'f' && size == 4) return tensor_from<float>(array);
+  if (kind == 'f' && size == 8) return tensor_from<double>(array);
+  if (kind == 'i' && size == 4) return tensor_from<std::int32_t>(array);
+  if (kind == 'i' && size == 8) return tensor_from<std::int64_t>(array);
+  throw std::invalid_argument{"from_numpy supports float32, float64, int32 and int64 arrays"};
+}
+
+// Copies a CPU tensor's logical values into a new numpy array.
+py::array to_numpy(const Tensor& tensor) {
+  if (!tensor.device().is_cpu()) {
+    throw std::logic_error{"numpy() requires a CPU tensor; call to(Device.cpu()) first"};
+  }
+  const Tensor contiguous{tensor.detach().contiguous()};
+  std::vector<py::ssize_t> dims(contiguous.shape().dimensions().begin(),
+                                contiguous.shape().dimensions().end());
+  py::array out(numpy_dtype(contiguous.dtype()), dims);
+  if (contiguous.nbytes() == 0) return out;
+  switch (contiguous.dtype()) {
+    case DType::Float32:
+      std::memcpy(out.mutable_data(), contiguous.span<float>().data(), contiguous.nbytes());
+      break;
+    case DType::Float64:
+      std::memcpy(out.mutable_data(), contiguous.span<double>().data(), contiguous.nbytes());
+      break;
+    case DType::Int32:
+      std::memcpy(out.mutable_data(), contiguous.span<std::int32_t>().data(), contiguous.nbytes());
+      break;
+    case DType::Int64:
+      std::memcpy(out.mutable_data(), contiguous.span<std::int64_t>().data(), contiguous.nbytes());
+      break;
+  }
+  return out;
+}
+
+std::vector<std::size_t> axes_of(py::object axes) {
+  if (py::isinstance<py::int_>(axes)) return {axes.cast<std::size_t>()};
+  return axes.cast<std::vector<std::size_t>>();
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_spar, m) {
+  m.doc() = "Spar tensor/ops API on the MI355X HIP backend";
+
+  static py::exception<std::logic_error> logic_error(m, "LogicError", PyExc_RuntimeError);
+  py::register_exception_translator([](std::exception_ptr p) {
+    try {
+      if (p) std::rethrow_exception(p);
+    } catch (const std::invalid_argument& e) {
+      PyErr_SetString(PyExc_ValueError, e.what());
+    } catch (const std::out_of_range& e) {
+      PyErr_SetString(PyExc_IndexError, e.what());
+    } catch (const std::overflow_error& e) {
+      PyErr_SetString(PyExc_OverflowError, e.what());
+    } catch (const std::logic_error& e) {
+      logic_error(e.what());
+    }
+  });
+
+  py::enum_<DType>(m, "DType")
+      .value("float32", DType::Float32)
+      .value("float64", DType::Float64)
+      .value("int32", DType::Int32)
+      .value("int64", DType::Int64);
+
+  py::class_<Device>(m, "Device")
+      .def_static("cpu", &Device::cpu)
+      .def_static("hip", &Device::hip, py::arg("index") = 0)
+      .def_property_readonly("index", &Device::index)
+      .def_property_readonly("is_cpu", &Device::is_cpu)
+      .def_property_readonly("is_hip", &Device::is_hip)
+      .def("__eq__", [](const Device& a, const Device& b) { return a == b; })
+      .def("__repr__", &Device::to_string);
+
+  py::class_<Tensor>(m, "Tensor")
+      .def(py::init([](const std::vector<std::int64_t>& shape, DType dtype, Device device) {
+             return Tensor{to_shape(shape), dtype, device};
+           }),
+           py::arg("shape"), py::arg("dtype"), py::arg("device") = Device::cpu())
+      .def_static("from_numpy", &from_numpy)
+      .def("numpy", &to_numpy)
+      .def_property_readonly("shape", [](const Tensor& t) { return shape_tuple(t.shape()); })
+      .def_property_readonly("strides", [](const Tensor& t) {
+        return std::vector<std::size_t>(t.strides().begin(), t.strides().end());
+      })
+      .def_property_readonly("storage_offset", &Tensor::storage_offset)
+      .def_property_readonly("dtype", &Tensor::dtype)
+      .def_property_readonly("device", &Tensor::device)
+      .def_property_readonly("numel", &Tensor::numel)
+      .def_property_readonly("nbytes", &Tensor::nbytes)
+      .def_property_readonly("rank", &Tensor::rank)
+      .def("is_contiguous", &Tensor::is_contiguous)
+      .def_property_readonly("requires_grad", &Tensor::requires_grad)
+      .def_property_readonly("is_leaf", &Tensor::is_leaf)
+      .def_property_readonly("has_grad", &Tensor::has_grad)
+      .def("set_requires_grad", &Tensor::set_requires_grad, py::arg("enabled") = true)
+      .def("grad", &Tensor::grad)
+      .def("zero_grad", &Tensor::zero_grad)
+      .def("backward", &Tensor::backward, py::call_guard<py::gil_scoped_release>())
+      .def("detach", &Tensor::detach)
+      .def("to", &Tensor::to)
+      .def("clone", &Tensor::clone)
+      .def("contiguous", &Tensor::contiguous)
+      .def("reshape", [](const Tensor& t, const std::vector<std::int64_t>& s) { return t.reshape(to_shape(s)); })
+      .def("transpose", &Tensor::transpose)
+      .def("permute", [](const Tensor& t, const std::vector<std::size_t>& axes) {
+        return t.permute(std::span<const std::size_t>{axes.data(), axes.size()});
+      })
+      .def("expand", [](const Tensor& t, const std::vector<std::int64_t>& s) { return t.expand(to_shape(s)); })
+      .def("narrow", &Tensor::narrow);
+
+  py::class_<spar::Random>(m, "Random")
+      .def(py::init<std::uint64_t>())
+      .def_property("state", &spar::Random::state, &spar::Random::set_state)
+      .def("next_u64", &spar::Random::next_u64)
+      .def("uniform_float", &spar::Random::uniform_float)
+      .def("uniform_double", &spar::Random::uniform_double);
+
+  m.def("random_uniform",
+        [](const std::vector<std::int64_t>& shape, DType dtype, spar::Random& random, double low,
+           double high, Device device) {
+          return spar::random_uniform(to_shape(shape), dtype, random, low, high, device);
+        },
+        py::arg("shape"), py::arg("dtype"), py::arg("random"), py::arg("low") = 0.0,
+        py::arg("high") = 1.0, py::arg("device") = Device::cpu());
+  m.def("random_normal",
+        [](const std::vector<std::int64_t>& shape, DType dtype, spar::Random& random, double mean,
+           double stddev, Device device) {
+          return spar::random_normal(to_shape(shape), dtype, random, mean, stddev, device);
+        },
+        py::arg("shape"), py::arg("dtype"), py::arg("random"), py::arg("mean") = 0.0,
+        py::arg("stddev") = 1.0, py::arg("device") = Device::cpu());
+
+  m.def("zeros", [](const std::vector<std::int64_t>& s, DType d, Device dev) { return spar::zeros(to_shape(s), d, dev); },
+        py::arg("shape"), py::arg("dtype"), py::arg("device") = Device::cpu());
+  m.def("ones", [](const std::vector<std::int64_t>& s, DType d, Device dev) { return spar::ones(to_shape(s), d, dev); },
+        py::arg("shape"), py::arg("dtype"), py::arg("device") = Device::cpu());
+  m.def("full", [](const std::vector<std::int64_t>& s, double v, DType d, Device dev) {
+          return spar::full_value(to_shape(s), d, v, dev);
+        },
+        py::arg("shape"), py::arg("value"), py::arg("dtype"), py::arg("device") = Device::cpu());
+
+#define SPAR_BINARY(name) m.def(#name, &spar::name, py::call_guard<py::gil_scoped_release>());
+  SPAR_BINARY(add)
+  SPAR_BINARY(subtract)
+  SPAR_BINARY(multiply)
+  SPAR_BINARY(divide)
+  SPAR_BINARY(equal)
+  SPAR_BINARY(not_equal)
+  SPAR_BINARY(less)
+  SPAR_BINARY(less_equal)
+  SPAR_BINARY(greater)
+  SPAR_BINARY(greater_equal)
+  SPAR_BINARY(add_scalar)
+  SPAR_BINARY(subtract_scalar)
+  SPAR_BINARY(multiply_scalar)
+  SPAR_BINARY(divide_scalar)
+  SPAR_BINARY(negate)
+  SPAR_BINARY(square)
+  SPAR_BINARY(reciprocal)
+  SPAR_BINARY(exp)
+  SPAR_BINARY(log)
+  SPAR_BINARY(sqrt)
+  SPAR_BINARY(sigmoid)
+  SPAR_BINARY(silu)
+  SPAR_BINARY(tanh)
+  SPAR_BINARY(gelu)
+  SPAR_BINARY(reduce_max)
+#undef SPAR_BINARY
+
+  m.def("sum", [](const Tensor& x, py::object axes, bool keepdim) {
+          if (axes.is_none()) return spar::sum(x);
+          const auto a = axes_of(axes);
+          return spar::sum(x, std::span<const std::size_t>{a.data(), a.size()}, keepdim);
+        },
+        py::arg("input"), py::arg("axes") = py::none(), py::arg("keepdim") = false);
+  m.def("mean", [](const Tensor& x, py::object axes, bool keepdim) {
+          if (axes.is_none()) return spar::mean(x);
+          const auto a = axes_of(axes);
+          return spar::mean(x, std::span<const std::size_t>{a.data(), a.size()}, keepdim);
+        },
+        py::arg("input"), py::arg("axes") = py::none(), py::arg("keepdim") = false);
+  m.def("max", &spar::max, py::arg("input"), py::arg("axis"), py::arg("keepdim") = false);
+  m.def("argmax", &spar::argmax, py::arg("input"), py::arg("axis"), py::arg("keepdim") = false);
+  m.def("softmax", [](const Tensor& x, py::object axis) {
+          return axis.is_none() ? spar::softmax(x) : spar::softmax(x, axis.cast<std::size_t>());
+        },
+        py::arg("input"), py::arg("axis") = py::none());
+  m.def("log_softmax", [](const Tensor& x, py::object axis) {
+          return axis.is_none() ? spar::log_softmax(x) : spar::log_softmax(x, axis.cast<std::size_t>());
+        },
+        py::arg("input"), py::arg("axis") = py::none());
+  m.def("reduce_gradient_to_shape", [](const Tensor& g, const std::vector<std::int64_t>& s) {
+    return spar::detail::reduce_gradient_to_shape(g, to_shape(s));
+  });
+  m.def("broadcast_shape", [](const std::vector<std::int64_t>& a, const std::vector<std::int64_t>& b) {
+    return shape_tuple(spar::detail::broadcast_shape(to_shape(a), to_shape(b)));
+  });
+  m.def("copy_values", [](Tensor& destination, const Tensor& source) {
+    spar::detail::copy_tensor_values(destination, source);
+  });
+  m.def("synchronize", &spar::synchronize, py::arg("device") = Device::hip(0));
+  m.def("hip_device_count", &spar::hip_device_count);
+}

@@ -18,7 +18,7 @@ _LIB_PATH = Path(__file__).resolve().parent / "lib" / "libspar_hip.so"
 FLOAT32, FLOAT64, INT32, INT64 = 0, 1, 2, 3
 ADD, SUBTRACT, MULTIPLY, DIVIDE = 0, 1, 2, 3
 EQUAL, NOT_EQUAL, LESS, LESS_EQUAL, GREATER, GREATER_EQUAL = 4, 5, 6, 7, 8, 9
-NEGATE, SQUARE, RECIPROCAL, EXP, LOG, SQRT, SIGMOID, SILU, TANH, GELU = range(10)
+NEGATE, SQUARE, RECIPROCAL, EXP, LOG, SQRT, SIGMOID, SILU, TANH, GELU, GELU_DERIVATIVE = range(11)
 SUM, MEAN, MAX, ARGMAX = 0, 1, 2, 3
 MAX_RANK = 8
 
@@ -27,7 +27,7 @@ BINARY_OPS = {"add": ADD, "subtract": SUBTRACT, "multiply": MULTIPLY, "divide": 
               "greater": GREATER, "greater_equal": GREATER_EQUAL}
 UNARY_OPS = {"negate": NEGATE, "square": SQUARE, "reciprocal": RECIPROCAL, "exp": EXP,
              "log": LOG, "sqrt": SQRT, "sigmoid": SIGMOID, "silu": SILU, "tanh": TANH,
-             "gelu": GELU}
+             "gelu": GELU, "gelu_derivative": GELU_DERIVATIVE}
 
 _DTYPE_TAGS = {np.dtype(np.float32): FLOAT32, np.dtype(np.float64): FLOAT64,
                np.dtype(np.int32): INT32, np.dtype(np.int64): INT64}
@@ -81,6 +81,7 @@ SIGNATURES = {
     "spar_hip_launch_fill": [_P, _U64, _I, _D, _I],
     "spar_hip_launch_add_in_place": [_P, _P, _U64, _I, _I],
     "spar_hip_launch_strided_copy": [_P, _P, _U64, _U64P, _U64P, _U64, _U64, _U64, _I],
+    "spar_hip_launch_strided_assign": [_P, _U64, _U64P, _U64P, _U64, _P, _U64, _I],
     "spar_hip_launch_strided_binary": [_P, _P, _U64P, _U64, _P, _U64P, _U64, _U64, _U64P, _I, _I,
                                        _I],
     "spar_hip_launch_reduction": [_P, _P, _U64, _I, _I, _I],

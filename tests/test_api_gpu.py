@@ -1,0 +1,406 @@
+"""Public tensor/ops API on HIP tensors against the oracle's restatement of
+Spar's CPU path (oracle.reference), including autograd.
+
+Parity classes (tests/helpers.py): elementwise, broadcast, layout, compare,
+argmax and max are bit-exact; transcendentals <= 2 ulp (float32);
+reductions red(N).  Gradients that pass only through elementwise ops are
+bit-exact; gradients that pass through a reduction are compared with the
+red bound of that reduction.
+"""
+import numpy as np
+import pytest
+
+import oracle.reference as R
+from oracle import ops as C
+from tests.helpers import assert_bitexact, assert_red, assert_ulp
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+@pytest.fixture(scope="module")
+def sp():
+    from spar_amd import spar
+
+    if spar.hip_device_count() < 1:
+        pytest.fail("no HIP device visible to a gpu-marked test")
+    return spar
+
+
+def hip_tensor(sp, array, requires_grad=False):
+    t = sp.Tensor.from_numpy(np.ascontiguousarray(array)).to(sp.Device.hip(0))
+    if requires_grad:
+        t.set_requires_grad(True)
+    return t
+
+
+def host(sp, tensor):
+    return tensor.to(sp.Device.cpu()).numpy()
+
+
+def normal(seed, shape, scale=1.0, dtype=F32):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(dtype)
+
+
+# ------------------------------------------------------------ transfers
+
+def test_round_trip_and_views(sp):
+    x = normal(1, (37, 53))
+    t = hip_tensor(sp, x)
+    assert t.device == sp.Device.hip(0)
+    assert_bitexact(host(sp, t), x, "round trip")
+    assert_bitexact(host(sp, t.transpose(0, 1)), x.T.copy(), "transpose to host")
+    assert_bitexact(host(sp, t.narrow(0, 3, 20).narrow(1, 5, 40)), x[3:23, 5:45].copy(), "narrow")
+    assert_bitexact(host(sp, t.transpose(0, 1).contiguous()), x.T.copy(), "contiguous")
+    cpu_view = sp.Tensor.from_numpy(x).transpose(0, 1)
+    assert_bitexact(host(sp, cpu_view.to(sp.Device.hip(0))), x.T.copy(), "host view upload")
+    e = hip_tensor(sp, x[0]).expand([4, 53])
+    assert e.strides == [0, 1]
+    assert_bitexact(host(sp, e), np.broadcast_to(x[0], (4, 53)).copy(), "expand")
+
+
+def test_factories_on_device(sp):
+    dev = sp.Device.hip(0)
+    assert np.all(host(sp, sp.zeros([5, 7], sp.DType.float32, dev)) == 0)
+    assert np.all(host(sp, sp.ones([5, 7], sp.DType.float64, dev)) == 1)
+    assert np.all(host(sp, sp.full([3], 2.5, sp.DType.float32, dev)) == 2.5)
+    assert np.all(host(sp, sp.full([3], 7, sp.DType.int64, dev)) == 7)
+
+
+def test_random_uniform_device_matches_host(sp):
+    r_host, r_dev = sp.Random(5), sp.Random(5)
+    a = sp.random_uniform([1000], sp.DType.float32, r_host, -2.0, 3.0)
+    b = sp.random_uniform([1000], sp.DType.float32, r_dev, -2.0, 3.0, sp.Device.hip(0))
+    assert_bitexact(host(sp, b), a.numpy(), "device uniform")
+    assert r_host.state == r_dev.state
+    ref = C.Random(5).uniform((1000,), F32, -2.0, 3.0)
+    assert_bitexact(a.numpy(), ref, "host uniform vs oracle")
+
+
+# ----------------------------------------------------------- elementwise
+
+BINARY = ["add", "subtract", "multiply", "divide"]
+COMPARE = ["equal", "not_equal", "less", "less_equal", "greater", "greater_equal"]
+
+
+@pytest.mark.parametrize("op", BINARY + COMPARE)
+@pytest.mark.parametrize("shapes", [((6, 8, 12), (12,)), ((6, 8, 12), (6, 1, 12)),
+                                    ((6, 1, 12), (1, 8, 1)), ((5,), (5,)), ((), (3, 4))])
+def test_binary_broadcast_api(sp, op, shapes):
+    a = normal(2, shapes[0])
+    b = normal(3, shapes[1])
+    if op in COMPARE:
+        b = np.where(np.random.default_rng(9).random(b.shape) < 0.3,
+                     np.broadcast_to(a.reshape(-1)[0], b.shape), b).astype(F32)
+    got = host(sp, getattr(sp, op)(hip_tensor(sp, a), hip_tensor(sp, b)))
+    want = C.binary(a, b, op)
+    assert_bitexact(got, want, op)
+
+
+def test_binary_on_views(sp):
+    base = normal(4, (64, 96))
+    other = normal(5, (96, 64))
+    tb, to = hip_tensor(sp, base), hip_tensor(sp, other)
+    got = host(sp, sp.subtract(tb.transpose(0, 1), to))
+    assert_bitexact(got, C.binary(base.T, other, "subtract"), "transposed left")
+    got = host(sp, sp.multiply(tb.narrow(0, 10, 30), tb.narrow(0, 20, 30)))
+    assert_bitexact(got, C.binary(base[10:40], base[20:50], "multiply"), "narrowed")
+
+
+def test_binary_errors(sp):
+    a = hip_tensor(sp, normal(1, (3, 4)))
+    b = hip_tensor(sp, normal(1, (5, 4)))
+    with pytest.raises(ValueError):
+        sp.add(a, b)
+    with pytest.raises(ValueError):
+        sp.add(a, hip_tensor(sp, normal(1, (3, 4), dtype=np.float64)))
+    with pytest.raises(ValueError):
+        sp.add(a, sp.Tensor.from_numpy(normal(1, (3, 4))))
+    with pytest.raises(ValueError):
+        sp.add(hip_tensor(sp, np.arange(4, dtype=np.int64)), hip_tensor(sp, np.arange(4, dtype=np.int64)))
+    x = hip_tensor(sp, normal(1, (3, 4)), requires_grad=True)
+    with pytest.raises(sp.LogicError):
+        sp.less(x, a)
+
+
+@pytest.mark.parametrize("op,value", [("add_scalar", 0.1), ("subtract_scalar", 3.0),
+                                      ("multiply_scalar", -1.5), ("divide_scalar", 7.0)])
+def test_scalar_api(sp, op, value):
+    x = normal(6, (33, 7))
+    got = host(sp, getattr(sp, op)(hip_tensor(sp, x), value))
+    assert_bitexact(got, C.scalar(x, op.split("_")[0], value), op)
+
+
+def test_scalar_errors(sp):
+    x = hip_tensor(sp, normal(6, (4, 5)))
+    with pytest.raises(OverflowError):
+        sp.add_scalar(x, 1e39)
+    with pytest.raises(ValueError):
+        sp.add_scalar(x.transpose(0, 1), 1.0)
+    sp.add_scalar(x, float("inf"))  # non-finite scalars are allowed
+
+
+@pytest.mark.parametrize("op", ["negate", "square", "reciprocal", "exp", "log", "sqrt", "sigmoid",
+                                "silu", "tanh", "gelu"])
+def test_unary_api(sp, op):
+    x = normal(7, (257, 31), 3.0)
+    if op in ("log", "sqrt"):
+        x = np.abs(x) + F32(1e-3)
+    got = host(sp, getattr(sp, op)(hip_tensor(sp, x)))
+    want = C.unary(x, op)
+    if op in ("negate", "square", "reciprocal", "sqrt"):
+        assert_bitexact(got, want, op)
+    else:
+        assert_ulp(got, want, 2, op)
+    with pytest.raises(ValueError):
+        getattr(sp, op)(hip_tensor(sp, x).transpose(0, 1))
+
+
+# ------------------------------------------------------------ reductions
+
+def red_norm(x, axes):
+    return np.sqrt(C.axis_sum(x.astype(np.float64) ** 2, axes))
+
+
+@pytest.mark.parametrize("axes,keepdim", [((0,), False), ((1,), True), ((0, 2), False),
+                                          ((1, 2), True), ((0, 1, 2), False)])
+def test_sum_mean_axes(sp, axes, keepdim):
+    x = normal(8, (12, 40, 66))
+    t = hip_tensor(sp, x)
+    n = int(np.prod([x.shape[a] for a in axes]))
+    s = sp.sum(t, list(axes), keepdim)
+    expect_shape = tuple(1 if (i in axes) else d for i, d in enumerate(x.shape) if keepdim or i not in axes)
+    assert s.shape == expect_shape
+    assert_red(host(sp, s).reshape(-1), C.axis_sum(x, axes).reshape(-1), n,
+               red_norm(x, axes).reshape(-1), "sum")
+    m = sp.mean(t, list(axes), keepdim)
+    want = C.scalar(C.axis_sum(x, axes).reshape(-1), "divide", float(n))
+    assert_red(host(sp, m).reshape(-1), want, n, red_norm(x, axes).reshape(-1) / n, "mean")
+
+
+def test_full_reductions_and_views(sp):
+    x = normal(9, (300, 257))
+    t = hip_tensor(sp, x)
+    norm = float(np.sqrt(np.sum(x.astype(np.float64) ** 2)))
+    assert_red(host(sp, sp.sum(t)), C.full_reduce(x, "sum"), x.size, norm, "sum")
+    assert_red(host(sp, sp.mean(t)), C.full_reduce(x, "mean"), x.size, norm / x.size, "mean")
+    assert_bitexact(host(sp, sp.reduce_max(t)), np.array(C.full_reduce(x, "max")), "reduce_max")
+    tt = t.transpose(0, 1)
+    assert_red(host(sp, sp.sum(tt)), C.full_reduce(x.T, "sum"), x.size, norm, "sum of view")
+    assert_red(host(sp, sp.sum(tt, 0)), C.axis_sum(x.T, [0]), 257, red_norm(x.T, [0]), "axis of view")
+
+
+def test_max_argmax_api(sp):
+    x = normal(10, (20, 33))
+    x[3, 5] = x[3, 9] = 50.0
+    x[7, 2] = np.nan
+    t = hip_tensor(sp, x)
+    for axis in (0, 1):
+        values, indices = C.axis_max(x, [axis])
+        assert_bitexact(host(sp, sp.max(t, axis)), values, "max")
+        got = sp.argmax(t, axis, True)
+        assert got.dtype == sp.DType.int64
+        assert_bitexact(host(sp, got).reshape(-1), indices, "argmax")
+    with pytest.raises(sp.LogicError):
+        sp.reduce_max(hip_tensor(sp, x, requires_grad=True))
+
+
+def test_reduction_errors(sp):
+    t = hip_tensor(sp, normal(1, (3, 4)))
+    with pytest.raises(ValueError):
+        sp.sum(t, [])
+    with pytest.raises(IndexError):
+        sp.sum(t, [2])
+    with pytest.raises(ValueError):
+        sp.sum(t, [1, 1])
+    with pytest.raises(ValueError):
+        sp.mean(hip_tensor(sp, np.zeros((0, 3), F32)))
+    with pytest.raises(ValueError):
+        sp.reduce_max(hip_tensor(sp, np.zeros((0,), F32)))
+    assert host(sp, sp.sum(hip_tensor(sp, np.zeros((0, 3), F32)), [0])).tolist() == [0, 0, 0]
+
+
+# --------------------------------------------------------------- softmax
+
+@pytest.mark.parametrize("axis", [None, 0, 1])
+def test_softmax_api(sp, axis):
+    x = normal(11, (24, 50), np.sqrt(2))
+    t = hip_tensor(sp, x)
+    got = host(sp, sp.softmax(t, axis))
+    want = C.softmax_full(x) if axis is None else C.softmax_axis(x, axis)[0]
+    n = x.size if axis is None else x.shape[axis]
+    bound = (4 * np.finfo(F32).eps + 1e-6 * np.sqrt(n)) * np.abs(want) + np.finfo(F32).tiny
+    assert np.all(np.abs(got.astype(np.float64) - want) <= bound)
+    lgot = host(sp, sp.log_softmax(t, axis))
+    lwant = C.log_softmax(x, axis)[0]
+    err = np.abs(lgot.astype(np.float64) - lwant)
+    assert np.all(err <= 1e-6 * np.sqrt(n) + 4 * np.finfo(F32).eps * (np.abs(lwant) + np.log(n) + 1))
+
+
+def test_softmax_errors(sp):
+    t = hip_tensor(sp, normal(1, (3, 4)))
+    with pytest.raises(IndexError):
+        sp.softmax(t, 2)
+    with pytest.raises(ValueError):
+        sp.softmax(hip_tensor(sp, np.zeros((0, 4), F32)), 1)
+    with pytest.raises(ValueError):
+        sp.softmax(t.transpose(0, 1))
+    with pytest.raises(IndexError):
+        sp.log_softmax(t, 5)
+
+
+# -------------------------------------------------------------- autograd
+
+def run_both(sp, build, arrays):
+    """Runs `build(lib, tensors)` on the device and on the oracle; returns the
+    losses and leaf gradients of both."""
+    dev = [hip_tensor(sp, a, requires_grad=True) for a in arrays]
+    ref = [R.RTensor.of(a, requires_grad=True) for a in arrays]
+    loss_d = build(sp, dev)
+    loss_r = build(R, ref)
+    loss_d.backward()
+    loss_r.backward()
+    return (host(sp, loss_d), loss_r.numpy(), [host(sp, t.grad()) for t in dev],
+            [r.grad().numpy() for r in ref])
+
+
+def weighted_sum(lib, y, weight):
+    return lib.sum(lib.multiply(y, weight))
+
+
+def test_autograd_elementwise_chain_bitexact_grads(sp):
+    # loss = sum(((a*b - a/b) + a) * w): gradients pass through elementwise
+    # ops and one full sum, whose backward is a broadcast fill (exact).
+    a = normal(12, (16, 24))
+    b = np.abs(normal(13, (16, 24))) + F32(0.5)
+    w = normal(14, (16, 24))
+
+    def build(lib, t):
+        y = lib.add(lib.subtract(lib.multiply(t[0], t[1]), lib.divide(t[0], t[1])), t[0])
+        return weighted_sum(lib, y, t[2])
+
+    loss_d, loss_r, grads_d, grads_r = run_both(sp, build, [a, b, w])
+    assert_red(loss_d, loss_r, a.size, np.sqrt(np.sum(a.astype(np.float64) ** 2)) * 4, "loss")
+    for i, (gd, gr) in enumerate(zip(grads_d, grads_r)):
+        assert_bitexact(gd, gr, f"grad {i}")
+
+
+def test_autograd_unary_chain(sp):
+    x = normal(15, (8, 32))
+    w = normal(16, (8, 32))
+    for name in ["negate", "square", "exp", "sigmoid", "silu", "tanh", "gelu"]:
+        def build(lib, t, name=name):
+            return weighted_sum(lib, getattr(lib, name)(t[0]), t[1])
+
+        _, _, grads_d, grads_r = run_both(sp, build, [x, w])
+        # The backward rules reuse the forward value (y within 2 ulp); rules
+        # such as 1 - y*y cancel, so the bound is absolute in |w| as well as
+        # relative: |d grad| <= 8 eps (|grad| + |w|).
+        eps = np.finfo(F32).eps
+        err = np.abs(grads_d[0].astype(np.float64) - grads_r[0])
+        assert np.all(err <= 8 * eps * (np.abs(grads_r[0]) + np.abs(w))), f"{name} grad"
+        assert_ulp(grads_d[1], grads_r[1], 2, f"{name} weight grad")
+
+
+def test_autograd_broadcast_reduction_grads(sp):
+    # C2 structure at small size: y = x*scale + bias, loss = sum(y*G)
+    B, T, Cn = 4, 64, 96
+    x = normal(17, (B, T, Cn))
+    bias = np.random.default_rng(18).uniform(-0.1, 0.1, Cn).astype(F32)
+    scale = np.random.default_rng(19).uniform(0.5, 1.5, (B, 1, Cn)).astype(F32)
+    G = normal(20, (B, T, Cn))
+
+    def build(lib, t):
+        return weighted_sum(lib, lib.add(lib.multiply(t[0], t[1]), t[2]), t[3])
+
+    _, _, gd, gr = run_both(sp, build, [x, scale, bias, G])
+    assert_bitexact(gd[0], gr[0], "dx = G*scale")
+    prod = C.binary(G, x, "multiply")
+    assert_red(gd[1], gr[1], T, np.sqrt(C.reduce_gradient(prod.astype(np.float64) ** 2, scale.shape)),
+               "dscale")
+    assert_red(gd[2], gr[2], B * T, np.sqrt(C.reduce_gradient(G.astype(np.float64) ** 2, bias.shape)),
+               "dbias")
+
+
+def test_autograd_reuse_accumulates_in_order(sp):
+    # x feeds three ops: contributions accumulate in the engine's order
+    x = normal(21, (10, 10))
+    w = normal(22, (10, 10))
+
+    def build(lib, t):
+        y = lib.add(lib.multiply(t[0], t[0]), lib.multiply_scalar(t[0], 3.0))
+        return weighted_sum(lib, y, t[1])
+
+    _, _, gd, gr = run_both(sp, build, [x, w])
+    assert_bitexact(gd[0], gr[0], "reused x")
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("log", [False, True])
+def test_autograd_softmax(sp, axis, log):
+    x = normal(23, (12, 40), np.sqrt(2))
+    w = normal(24, (12, 40))
+
+    def build(lib, t):
+        y = lib.log_softmax(t[0], axis) if log else lib.softmax(t[0], axis)
+        return weighted_sum(lib, y, t[1])
+
+    _, _, gd, gr = run_both(sp, build, [x, w])
+    n = x.shape[axis]
+    scale = np.sqrt(np.sum(w.astype(np.float64) ** 2, axis=axis, keepdims=True))
+    err = np.abs(gd[0].astype(np.float64) - gr[0])
+    assert np.all(err <= 1e-6 * np.sqrt(n) * scale + 8 * np.finfo(F32).eps * (np.abs(gr[0]) + np.abs(w)))
+
+
+def layer_norm(lib, x, gamma, beta, G):
+    # mu = mean(x,1,keepdim); xc = x - mu; var = mean(square(xc),1,keepdim)
+    # xhat = xc / sqrt(var + 1e-5); y = xhat*gamma + beta; loss = sum(y*G)
+    mu = lib.mean(x, [1], True) if lib is not R else R.mean(x, [1], True)
+    xc = lib.subtract(x, mu)
+    var = lib.mean(lib.square(xc), [1], True) if lib is not R else R.mean(R.square(xc), [1], True)
+    xhat = lib.divide(xc, lib.sqrt(lib.add_scalar(var, 1e-5)))
+    y = lib.add(lib.multiply(xhat, gamma), beta)
+    return weighted_sum(lib, y, G)
+
+
+@pytest.mark.parametrize("view", ["transpose", "narrow"])
+def test_autograd_layernorm_chain_on_views(sp, view):
+    rows, cols = 48, 80
+    if view == "transpose":
+        base = normal(25, (cols, rows))
+    else:
+        base = normal(25, (rows + 7, cols + 9))
+    gamma = np.random.default_rng(26).uniform(0.5, 1.5, cols).astype(F32)
+    beta = np.random.default_rng(27).uniform(-0.1, 0.1, cols).astype(F32)
+    G = normal(28, (rows, cols))
+
+    def build(lib, t):
+        x = t[0].transpose(0, 1) if view == "transpose" else t[0].narrow(0, 3, rows).narrow(1, 4, cols)
+        return layer_norm(lib, x, t[1], t[2], t[3])
+
+    loss_d, loss_r, gd, gr = run_both(sp, build, [base, gamma, beta, G])
+    assert_red(loss_d, loss_r, rows * cols, np.sqrt(np.sum(G.astype(np.float64) ** 2)) * 2, "loss")
+    # every gradient passes through row means (n = cols) and the final sum
+    for i, name in enumerate(["x", "gamma", "beta"]):
+        scale = np.max(np.abs(gr[i])) + 1e-30
+        err = np.max(np.abs(gd[i].astype(np.float64) - gr[i]))
+        assert err <= 1e-6 * np.sqrt(rows * cols) * scale * 8, f"{name}: {err} vs scale {scale}"
+
+
+def test_autograd_api_errors(sp):
+    x = hip_tensor(sp, normal(1, (3,)), requires_grad=True)
+    y = sp.multiply(x, x)
+    with pytest.raises(ValueError):
+        y.backward()  # not one element
+    loss = sp.sum(y)
+    loss.backward()
+    g1 = host(sp, x.grad())
+    sp.sum(sp.multiply(x, x)).backward()
+    assert_bitexact(host(sp, x.grad()), g1 + g1, "second backward accumulates")
+    x.zero_grad()
+    assert not x.has_grad
+    with pytest.raises(ValueError):
+        y.grad()
+    with pytest.raises(ValueError):
+        hip_tensor(sp, np.arange(3, dtype=np.int64)).set_requires_grad(True)

@@ -1,0 +1,150 @@
+"""Host-side logic of the C++ Tensor layer that runs without a GPU: shapes,
+devices, views and their metadata, broadcast rules, error types, CPU tensor
+transfers, and the rule that arithmetic needs a HIP tensor (no CPU path)."""
+import numpy as np
+import pytest
+
+from spar_amd import spar
+import oracle.reference as R
+from oracle import ops as O
+
+
+def cpu(array):
+    return spar.Tensor.from_numpy(np.ascontiguousarray(array))
+
+
+def test_shape_and_strides():
+    t = spar.Tensor([2, 3, 4], spar.DType.float32)
+    assert t.shape == (2, 3, 4) and t.strides == [12, 4, 1] and t.numel == 24 and t.nbytes == 96
+    assert spar.Tensor([], spar.DType.float64).numel == 1
+    assert spar.Tensor([3, 0], spar.DType.float32).numel == 0
+    with pytest.raises(ValueError):
+        spar.Tensor([-1], spar.DType.float32)
+
+
+def test_views_match_numpy_metadata():
+    x = np.arange(60, dtype=np.float32).reshape(3, 4, 5)
+    t = cpu(x)
+    cases = [
+        (t.transpose(0, 2), x.transpose(2, 1, 0)),
+        (t.permute([1, 2, 0]), x.transpose(1, 2, 0)),
+        (t.narrow(1, 1, 2), x[:, 1:3]),
+        (t.narrow(2, 2, 3).transpose(0, 1), x[:, :, 2:5].transpose(1, 0, 2)),
+        (cpu(x[0, 0]).expand([2, 5]), np.broadcast_to(x[0, 0], (2, 5))),
+        (t.reshape([12, 5]), x.reshape(12, 5)),
+    ]
+    for view, ref in cases:
+        assert view.shape == ref.shape
+        assert view.strides == [s // 4 for s in ref.strides]
+        np.testing.assert_array_equal(view.numpy(), ref)
+        assert view.is_contiguous() == ref.flags["C_CONTIGUOUS"] or ref.size <= 1
+
+
+def test_is_contiguous_ignores_extent_one_axes():
+    t = cpu(np.zeros((4, 1, 3), np.float32))
+    assert t.transpose(0, 1).is_contiguous()  # core/tensor.cpp:113-128
+    assert not cpu(np.zeros((4, 3), np.float32)).transpose(0, 1).is_contiguous()
+
+
+def test_view_errors():
+    t = cpu(np.zeros((3, 4), np.float32))
+    with pytest.raises(IndexError):
+        t.transpose(0, 2)
+    with pytest.raises(ValueError):
+        t.permute([0, 0])
+    with pytest.raises(IndexError):
+        t.permute([0, 3])
+    with pytest.raises(ValueError):
+        t.expand([4])
+    with pytest.raises(ValueError):
+        t.expand([2, 4])
+    with pytest.raises(ValueError):
+        t.transpose(0, 1).reshape([12])
+    with pytest.raises(ValueError):
+        t.reshape([5])
+    with pytest.raises(IndexError):
+        t.narrow(1, 3, 2)
+
+
+@pytest.mark.parametrize("a,b", [((3, 1), (1, 4)), ((5, 1, 7), (6, 1)), ((), (2, 3)), ((4,), (4,))])
+def test_broadcast_shape_matches_oracle_and_numpy(a, b):
+    assert spar.broadcast_shape(list(a), list(b)) == R.broadcast_shape(a, b) == \
+        np.broadcast_shapes(a, b)
+
+
+def test_broadcast_shape_error():
+    with pytest.raises(ValueError):
+        spar.broadcast_shape([3, 2], [4, 2])
+
+
+def test_random_matches_oracle():
+    r = spar.Random(2024)
+    o = O.Random(2024)
+    assert [r.next_u64() for _ in range(5)] == [o.next_u64() for _ in range(5)]
+    a = spar.random_uniform([1000], spar.DType.float32, spar.Random(3), -1.0, 1.0).numpy()
+    np.testing.assert_array_equal(a, O.Random(3).uniform((1000,), np.float32, -1.0, 1.0))
+    n = spar.random_normal([1001], spar.DType.float64, spar.Random(4), 0.0, 2.0).numpy()
+    np.testing.assert_array_equal(n, O.Random(4).normal((1001,), np.float64, 0.0, 2.0))
+    with pytest.raises(ValueError):
+        spar.random_uniform([3], spar.DType.float32, spar.Random(1), 1.0, 1.0)
+    with pytest.raises(ValueError):
+        spar.random_uniform([3], spar.DType.int32, spar.Random(1))
+
+
+def test_arithmetic_requires_hip_tensors():
+    t = cpu(np.ones((2, 2), np.float32))
+    for fn in (lambda: spar.add(t, t), lambda: spar.exp(t), lambda: spar.sum(t),
+               lambda: spar.softmax(t, 1), lambda: spar.multiply_scalar(t, 2.0),
+               lambda: spar.max(t, 0)):
+        with pytest.raises(RuntimeError, match="requires a HIP tensor"):
+            fn()
+
+
+def test_validation_precedes_device_check():
+    t = cpu(np.ones((2, 2), np.float32))
+    with pytest.raises(OverflowError):
+        spar.add_scalar(t, 1e39)
+    with pytest.raises(ValueError):
+        spar.exp(t.transpose(0, 1))
+    with pytest.raises(IndexError):
+        spar.sum(t, [3])
+    with pytest.raises(ValueError):
+        spar.mean(cpu(np.zeros((0,), np.float32)))
+
+
+def test_autograd_flags_on_cpu_tensors():
+    t = cpu(np.ones(3, np.float32))
+    assert not t.requires_grad and t.is_leaf and not t.has_grad
+    t.set_requires_grad(True)
+    assert t.requires_grad
+    with pytest.raises(spar.LogicError):
+        t.grad()
+    with pytest.raises(ValueError):
+        cpu(np.ones(3, np.int64)).set_requires_grad(True)
+    with pytest.raises(ValueError):
+        t.backward()  # three elements
+    d = t.detach()
+    assert not d.requires_grad
+
+
+def test_cpu_transfers_and_factories():
+    x = np.random.default_rng(0).standard_normal((5, 6)).astype(np.float32)
+    t = cpu(x)
+    np.testing.assert_array_equal(t.to(spar.Device.cpu()).numpy(), x)
+    np.testing.assert_array_equal(t.transpose(0, 1).contiguous().numpy(), x.T)
+    np.testing.assert_array_equal(spar.zeros([2, 3], spar.DType.int32).numpy(), np.zeros((2, 3)))
+    np.testing.assert_array_equal(spar.full([2], 1.5, spar.DType.float64).numpy(), [1.5, 1.5])
+    with pytest.raises(ValueError):
+        spar.Tensor([2], spar.DType.float32, spar.Device.hip(0)) if spar.hip_device_count() == 0 \
+            else (_ for _ in ()).throw(ValueError())
+    with pytest.raises(ValueError):
+        spar.Device.hip(-1)
+
+
+def test_oracle_reference_autograd_runs_on_cpu():
+    # the restated engine on a small graph: d/dx sum(x*x + 3x) = 2x + 3
+    x = np.arange(6, dtype=np.float32).reshape(2, 3)
+    t = R.RTensor.of(x, requires_grad=True)
+    loss = R.sum(R.add(R.multiply(t, t), R.multiply_scalar(t, 3.0)))
+    loss.backward()
+    np.testing.assert_array_equal(t.grad().numpy(), 2 * x + 3)
