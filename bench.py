@@ -198,10 +198,14 @@ def main():
 
     work = Workload(hip)
     if args.profile_loop:
+        # Workload steps, then one plain contiguous copy of x (512 MiB read,
+        # 512 MiB written) whose counters calibrate bytes per counter unit.
         for _ in range(args.profile_loop):
             work.step()
+        hip.call("spar_hip_launch_strided_copy", work.y1.ptr, work.x.ptr, 1, hip.u64_array([work.n]),
+                 hip.u64_array([1]), 0, work.n, 4, 0)
         hip.synchronize()
-        print(json.dumps({"profile_loop_steps": args.profile_loop}))
+        print(json.dumps({"profile_loop_steps": args.profile_loop, "copy_bytes": work.n * 4}))
         return
 
     nbytes = work.op_bytes()
@@ -284,6 +288,124 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(hip, work)
     print(json.dumps(result), flush=True)
+    if args.suite:
+        del work
+        run_suite(hip)
+
+
+# ----------------------------------------------------------------- suite
+
+def run_suite(hip, reps=10):
+    """Times every op of the five benchmark configurations (one JSON line per
+    op).  The 256 MB Infinity Cache is flushed before each timed launch by
+    reading a 512 MiB scratch buffer (a read leaves no dirty lines whose
+    write-back would overlap the timed kernel) outside the timed region."""
+    F = hip.FLOAT32
+    u = hip.u64_array
+    flush = hip.DeviceBuffer(512 << 20)
+    hip.call("spar_hip_zero", flush.ptr, flush.nbytes, 0)
+    flush_sink = hip.DeviceBuffer(8)
+    start, stop = hip.Event(), hip.Event()
+
+    def measure(config, name, nbytes, launch, elements):
+        launch()
+        hip.synchronize()
+        samples = []
+        for _ in range(reps):
+            hip.call("spar_hip_launch_reduction", flush_sink.ptr, flush.ptr, flush.nbytes // 4, F,
+                     hip.SUM, 0)
+            start.record()
+            launch()
+            stop.record()
+            samples.append(start.elapsed_ms(stop))
+        ms = statistics.median(samples)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"suite": config, "op": name, "ms": round(ms, 5), "GB/s": round(gbps, 1),
+                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": nbytes,
+                          "elements_per_s": round(elements / (ms * 1e-3), 1)}), flush=True)
+
+    def normal(n, seed, std=1.0):
+        buf = hip.DeviceBuffer(n * 4)
+        hip.call("spar_hip_random_normal", buf.ptr, n, F, seed, 0.0, std, 0)
+        return buf
+
+    def uniform(n, seed, low, high):
+        buf = hip.DeviceBuffer(n * 4)
+        hip.call("spar_hip_random_uniform", buf.ptr, n, F, seed, low, high, 0)
+        return buf
+
+    # C1: contiguous elementwise on [4096, 4096]
+    n = 4096 * 4096
+    a, b, out = normal(n, 1), normal(n, 2), hip.DeviceBuffer(n * 4)
+    clipped = hip.DeviceBuffer(n * 4)
+    hip.call("spar_hip_launch_scalar", clipped.ptr, a.ptr, n, F, hip.ADD, 0.0, 0)
+    for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
+        measure("C1", name, 12 * n, lambda op=op: hip.call(
+            "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0), n)
+    measure("C1", "gelu(a)", 8 * n, lambda: hip.call(
+        "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0), n)
+    measure("C1", "exp(a)", 8 * n, lambda: hip.call(
+        "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0), n)
+    del a, b, out, clipped
+
+    # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
+    R = 8192
+    n = R * R
+    x = normal(n, 3)
+    out = hip.DeviceBuffer(R * 8)
+    codes = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}
+    for axis in (1, 0):
+        for name, code in codes.items():
+            out_bytes = R * (8 if name == "argmax" else 4)
+            measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, lambda code=code, axis=axis: hip.call(
+                "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
+                1 << axis, F, code, 0), n)
+    del x
+    n = 1 << 28
+    v = uniform(n, 4, -1.0, 1.0)
+    for name in ("sum", "mean", "max"):
+        measure("C3", f"full {name} 2^28", 4 * n + 4, lambda name=name: hip.call(
+            "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0), n)
+    del v, out
+
+    # C4: row softmax / log-softmax on [8192, 32768]
+    rows, V = 8192, 32768
+    n = rows * V
+    logits = normal(n, 5, np.sqrt(2.0))
+    grad = normal(n, 6)
+    probs = hip.DeviceBuffer(n * 4)
+    dx = hip.DeviceBuffer(n * 4)
+    undefined = hip.DeviceBuffer(rows * 4)
+    for log in (0, 1):
+        label = "log_softmax" if log else "softmax"
+        measure("C4", f"{label} forward", 8 * n + 4 * rows, lambda log=log: hip.call(
+            "spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows, V, 1,
+            F, log, 0), n)
+        measure("C4", f"{label} backward", 12 * n + 4 * rows, lambda log=log: hip.call(
+            "spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
+            rows, V, 1, F, log, 0), n)
+    del logits, grad, probs, dx, undefined
+
+    # C5: LayerNorm-chain ops on a transposed view ([8192,4096] base viewed as
+    # [4096,8192]) and on a sliced [4096,8192] block of a [4608,9216] base.
+    rows, cols = 4096, 8192
+    n = rows * cols
+    base_t = normal(8192 * 4096, 7)
+    base_s = normal(4608 * 9216, 8)
+    mu = hip.DeviceBuffer(rows * 4)
+    out = hip.DeviceBuffer(n * 4)
+    offset = 256 * 9216 + 512
+    views = {"transposed": (base_t, [1, 4096], 0), "sliced": (base_s, [9216, 1], offset)}
+    for label, (base, strides, off) in views.items():
+        measure("C5", f"mean(x,1) {label}", 4 * n + 4 * rows, lambda base=base, strides=strides, off=off: hip.call(
+            "spar_hip_launch_axis_reduction", mu.ptr, base.ptr, 2, u([rows, cols]), u(strides), off,
+            2, F, hip.MEAN, 0), n)
+        measure("C5", f"x-mu {label}", 8 * n + 4 * rows, lambda base=base, strides=strides, off=off: hip.call(
+            "spar_hip_launch_strided_binary", out.ptr, base.ptr, u(strides), off, mu.ptr, u([1, 0]), 0,
+            2, u([rows, cols]), F, hip.SUBTRACT, 0), n)
+        measure("C5", f"contiguous() {label}", 8 * n, lambda base=base, strides=strides, off=off: hip.call(
+            "spar_hip_launch_strided_copy", out.ptr, base.ptr, 2, u([rows, cols]), u(strides), off, n, 4,
+            0), n)
 
 
 if __name__ == "__main__":

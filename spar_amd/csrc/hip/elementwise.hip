@@ -19,8 +19,11 @@
 namespace spar_hip {
 namespace {
 
+// One 16-byte vector per lane per tile and one tile per workgroup: on MI355X
+// this beats deeper per-lane unrolling for streaming kernels (many short
+// workgroups keep every CU's memory pipeline full until the end of the grid).
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;
 constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
 
 template <typename T, typename F>
@@ -38,7 +41,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
-      if (i < vectors) r[u] = in_v[i];
+      if (i < vectors) r[u] = stream_load(in_v + i);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -75,8 +78,8 @@ __global__ void __launch_bounds__(kThreads)
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
       if (i < vectors) {
-        ra[u] = a_v[i];
-        rb[u] = b_v[i];
+        ra[u] = stream_load(a_v + i);
+        rb[u] = stream_load(b_v + i);
       }
     }
 #pragma unroll

@@ -68,9 +68,9 @@ template <typename T, int NIN>
 __device__ __forceinline__ typename Vec16<T>::type load_vector(const T* a, const T* b,
                                                                uint64_t offset) {
   using V = typename Vec16<T>::type;
-  V va = *reinterpret_cast<const V*>(a + offset);
+  V va = stream_load(reinterpret_cast<const V*>(a + offset));
   if constexpr (NIN == 2) {
-    const V vb = *reinterpret_cast<const V*>(b + offset);
+    const V vb = stream_load(reinterpret_cast<const V*>(b + offset));
 #pragma unroll
     for (int k = 0; k < Vec16<T>::width; ++k) {
       vec_set<T>(va, k, vec_get<T>(va, k) * vec_get<T>(vb, k));
@@ -234,89 +234,124 @@ __global__ void __launch_bounds__(kThreads)
 
 // ------------------------------------------------------------ column kernel
 
-// Input element (o, r, i) at map-offset(o) + r * reduced_stride + i, with
-// inner axis contiguous.  Lanes own W (VEC) or 1 adjacent columns; block b
-// covers column block cb, split s, outer o.
+// Input element (o, r, i) at map-offset(o) + r * reduced_stride + i, with the
+// inner axis contiguous.  A block owns 64 * W adjacent columns (each lane W
+// of them, one 16-byte load per row when VEC); its four waves walk the rows
+// of the block's segment interleaved (wave w takes rows w, w+4, ...), so a
+// wave reads 1 KiB contiguous per row.  The four wave partials are combined
+// through LDS in wave order.  Block b covers column block cb, split s, outer o.
 template <typename T, Kind K, int NIN, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     column_kernel(const T* a, const T* b, uint64_t outer, uint64_t n, uint64_t reduced_stride,
                   uint64_t inner, uint64_t column_blocks, uint64_t splits, uint64_t segment,
                   RowMap map, Sink<T> sink) {
   constexpr int W = VEC ? Vec16<T>::width : 1;
+  __shared__ Acc<T, K> lds[kWaves][kWave * W];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
   const uint64_t total_blocks = outer * splits * column_blocks;
   for (uint64_t block = blockIdx.x; block < total_blocks; block += gridDim.x) {
     const uint64_t cb = block % column_blocks;
     const uint64_t rest = block / column_blocks;
     const uint64_t split = rest % splits;
     const uint64_t o = rest / splits;
-    const uint64_t column = (cb * kThreads + threadIdx.x) * W;
-    if (column >= inner) continue;
+    const uint64_t column = (cb * kWave + lane) * W;
     const uint64_t begin = split * segment;
     const uint64_t end = begin + segment < n ? begin + segment : n;
-    const uint64_t base = row_offset(map, o) + column;
     Acc<T, K> acc[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) acc[k].init();
-    uint64_t r = begin;
-    if constexpr (VEC) {
-      for (; r + 3 < end; r += 4) {
-        typename Vec16<T>::type v[4];
+    if (column < inner) {
+      const uint64_t base = row_offset(map, o) + column;
+      uint64_t r = begin + wave;
+      if constexpr (VEC) {
+        for (; r + 3 * kWaves < end; r += 4 * kWaves) {
+          typename Vec16<T>::type v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride);
+          for (int u = 0; u < 4; ++u) {
+            v[u] = load_vector<T, NIN>(a, b, base + (r + u * kWaves) * reduced_stride);
+          }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < 4; ++u) {
 #pragma unroll
-          for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v[u], k), static_cast<int64_t>(r + u));
+            for (int k = 0; k < W; ++k) {
+              acc[k].add(vec_get<T>(v[u], k), static_cast<int64_t>(r + u * kWaves));
+            }
+          }
+        }
+        for (; r < end; r += kWaves) {
+          const auto v = load_vector<T, NIN>(a, b, base + r * reduced_stride);
+#pragma unroll
+          for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v, k), static_cast<int64_t>(r));
+        }
+      } else {
+        for (; r < end; r += kWaves) {
+          acc[0].add(load_value<T, NIN>(a, b, base + r * reduced_stride), static_cast<int64_t>(r));
         }
       }
-      for (; r < end; ++r) {
-        const auto v = load_vector<T, NIN>(a, b, base + r * reduced_stride);
-#pragma unroll
-        for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v, k), static_cast<int64_t>(r));
-      }
-    } else {
-      for (; r < end; ++r) {
-        acc[0].add(load_value<T, NIN>(a, b, base + r * reduced_stride), static_cast<int64_t>(r));
-      }
     }
-    // Output slot: final [outer, inner]; partial [outer, splits, inner].
+    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < W; ++k) {
-      if (column + k < inner) {
-        const uint64_t slot = sink.partial ? (o * splits + split) * inner + column + k
-                                           : o * inner + column + k;
-        sink_write<T, K>(sink, slot, acc[k]);
+    for (int k = 0; k < W; ++k) lds[wave][lane * W + k] = acc[k];
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        if (column + k < inner) {
+          Acc<T, K> total = lds[0][lane * W + k];
+#pragma unroll
+          for (int w = 1; w < kWaves; ++w) total.merge(lds[w][lane * W + k]);
+          // Output slot: final [outer, inner]; partial [outer, splits, inner].
+          const uint64_t slot = sink.partial ? (o * splits + split) * inner + column + k
+                                             : o * inner + column + k;
+          sink_write<T, K>(sink, slot, total);
+        }
       }
     }
   }
 }
 
-// Second pass after column splits: one thread per (outer, inner) output sums
-// its splits in order.
+// Second pass after column splits: a 1024-lane block owns 64 columns of one
+// outer index; wave w sums splits w, w+16, ... and the 16 wave partials are
+// combined in wave order, so the result is deterministic.
+constexpr int kCombineThreads = 1024;
+constexpr int kCombineWaves = kCombineThreads / kWave;
+
 template <typename T, Kind K>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kCombineThreads)
     combine_columns_kernel(const T* part_values, const int64_t* part_indices, uint64_t outer,
                            uint64_t splits, uint64_t inner, Sink<T> sink) {
-  const uint64_t outputs = outer * inner;
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
-  for (uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < outputs;
-       idx += stride) {
-    const uint64_t o = idx / inner;
-    const uint64_t i = idx - o * inner;
+  __shared__ Acc<T, K> lds[kCombineWaves][kWave];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const uint64_t groups = (inner + kWave - 1) / kWave;
+  for (uint64_t block = blockIdx.x; block < outer * groups; block += gridDim.x) {
+    const uint64_t o = block / groups;
+    const uint64_t i = (block - o * groups) * kWave + lane;
     Acc<T, K> acc;
     acc.init();
-    for (uint64_t s = 0; s < splits; ++s) {
-      const uint64_t slot = (o * splits + s) * inner + i;
-      Acc<T, K> other;
-      if constexpr (K == Kind::Sum) {
-        other.value = part_values[slot];
-      } else {
-        other.best.value = part_values[slot];
-        other.best.index = part_indices[slot];
+    if (i < inner) {
+      for (uint64_t s = wave; s < splits; s += kCombineWaves) {
+        const uint64_t slot = (o * splits + s) * inner + i;
+        Acc<T, K> other;
+        if constexpr (K == Kind::Sum) {
+          other.value = part_values[slot];
+        } else {
+          other.best.value = part_values[slot];
+          other.best.index = part_indices[slot];
+        }
+        acc.merge(other);
       }
-      acc.merge(other);
     }
-    sink_write<T, K>(sink, idx, acc);
+    __syncthreads();
+    lds[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && i < inner) {
+      Acc<T, K> total = lds[0][lane];
+#pragma unroll
+      for (int w = 1; w < kCombineWaves; ++w) total.merge(lds[w][lane]);
+      sink_write<T, K>(sink, o * inner + i, total);
+    }
   }
 }
 
@@ -424,7 +459,7 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
   sink.mean_divisor = static_cast<T>(plan.reduced);
   const bool argmax = operation == SPAR_HIP_ARGMAX;
   const int cus = guard.multiprocessors;
-  const uint64_t target_blocks = static_cast<uint64_t>(cus) * 4;
+  const uint64_t target_blocks = static_cast<uint64_t>(cus) * 8;
 
   auto final_sink = [&]() {
     Sink<T> s = sink;
@@ -522,13 +557,15 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     for (int k = 0; k < plan.kept_rank - 1; ++k) {
       if (plan.kept_strides[k] % W != 0) vec = false;
     }
-    const uint64_t lanes_per_block = static_cast<uint64_t>(kThreads) * (vec ? W : 1);
-    const uint64_t column_blocks = (inner + lanes_per_block - 1) / lanes_per_block;
+    const uint64_t columns_per_block = static_cast<uint64_t>(kWave) * (vec ? W : 1);
+    const uint64_t column_blocks = (inner + columns_per_block - 1) / columns_per_block;
     const uint64_t base_blocks = outer * column_blocks;
+    // Enough blocks for ~8 per CU, each wave still walking >= 16 rows.
     uint64_t splits = 1;
-    const uint64_t min_rows = 32;
-    if (base_blocks < target_blocks && n >= 2 * min_rows) {
-      splits = (target_blocks + base_blocks - 1) / base_blocks;
+    const uint64_t min_rows = 16 * kWaves;
+    const uint64_t wanted_blocks = static_cast<uint64_t>(cus) * 8;
+    if (base_blocks < wanted_blocks && n >= 2 * min_rows) {
+      splits = (wanted_blocks + base_blocks - 1) / base_blocks;
       if (splits > n / min_rows) splits = n / min_rows;
       if (splits < 1) splits = 1;
     }
@@ -551,7 +588,7 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     return with_partials(outer * splits * inner, [&](const Sink<T>& partial) {
       launch(partial);
       combine_columns_kernel<T, K>
-          <<<grid_for((outer * inner + kThreads - 1) / kThreads), kThreads, 0, guard.stream>>>(
+          <<<grid_for(outer * ((inner + kWave - 1) / kWave)), kCombineThreads, 0, guard.stream>>>(
               partial.values, partial.indices, outer, splits, inner, final_sink());
     });
   }

@@ -155,7 +155,7 @@ __device__ __forceinline__ void load_row(T (&x)[E], const T* row, uint64_t n) {
     for (int v = 0; v < E / W; ++v) {
       const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
       if (FULL || col < n) {
-        const V value = *reinterpret_cast<const V*>(row + col);
+        const V value = stream_load(reinterpret_cast<const V*>(row + col));
 #pragma unroll
         for (int k = 0; k < W; ++k) x[v * W + k] = vec_get<T>(value, k);
       }

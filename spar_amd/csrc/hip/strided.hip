@@ -23,7 +23,7 @@ namespace spar_hip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;  // one 16-byte group per lane per tile (see elementwise.hip)
 constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
 
 struct CopyOp {
@@ -88,6 +88,7 @@ struct RowGeometry {
   KernelGeometry g;        // full coalesced geometry (axis 0 = innermost)
   FastDiv groups_per_row;  // inner / W
   int inner_unit[2];       // 1 if the operand is contiguous along the inner axis
+  int reused[2];           // 1 if the operand is broadcast (read many times: keep it cached)
 };
 
 template <typename T, int NOPS, typename F>
@@ -122,7 +123,8 @@ __global__ void __launch_bounds__(kThreads)
           }
         }
         if (rg.inner_unit[0]) {
-          ra[u] = *reinterpret_cast<const V*>(a + off0 + column);
+          const V* p = reinterpret_cast<const V*>(a + off0 + column);
+          ra[u] = rg.reused[0] ? *p : stream_load(p);
         } else {
           const T s = a[off0];
 #pragma unroll
@@ -130,7 +132,8 @@ __global__ void __launch_bounds__(kThreads)
         }
         if constexpr (NOPS == 2) {
           if (rg.inner_unit[1]) {
-            rb[u] = *reinterpret_cast<const V*>(b + off1 + column);
+            const V* p = reinterpret_cast<const V*>(b + off1 + column);
+            rb[u] = rg.reused[1] ? *p : stream_load(p);
           } else {
             const T s = b[off1];
 #pragma unroll
@@ -285,6 +288,12 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
     rg.groups_per_row.init(static_cast<uint32_t>(inner / W));
     rg.inner_unit[0] = inner_unit[0];
     rg.inner_unit[1] = inner_unit[1];
+    for (int op = 0; op < NOPS; ++op) {
+      rg.reused[op] = 0;
+      for (int axis = 0; axis < view.rank; ++axis) {
+        if (view.strides[op][axis] == 0 && view.extents[axis] > 1) rg.reused[op] = 1;
+      }
+    }
     const uint64_t groups = count / W;
     row_vector_kernel<T, NOPS, F>
         <<<capped_grid(groups, static_cast<uint64_t>(kThreads) * kUnroll), kThreads, 0,
