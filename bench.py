@@ -297,9 +297,11 @@ def main():
 
 def run_suite(hip, reps=10):
     """Times every op of the five benchmark configurations (one JSON line per
-    op).  The 256 MB Infinity Cache is flushed before each timed launch by
-    reading a 512 MiB scratch buffer (a read leaves no dirty lines whose
-    write-back would overlap the timed kernel) outside the timed region."""
+    op).  Before each timed launch, outside the timed region, a 512 MiB
+    scratch buffer is read with ordinary cached loads (spar_hip_touch): that
+    evicts the 256 MB Infinity Cache and writes back the previous launch's
+    dirty lines, whose write-back would otherwise land inside the timed
+    kernel."""
     F = hip.FLOAT32
     u = hip.u64_array
     flush = hip.DeviceBuffer(512 << 20)
@@ -312,8 +314,7 @@ def run_suite(hip, reps=10):
         hip.synchronize()
         samples = []
         for _ in range(reps):
-            hip.call("spar_hip_launch_reduction", flush_sink.ptr, flush.ptr, flush.nbytes // 4, F,
-                     hip.SUM, 0)
+            hip.call("spar_hip_touch", flush.ptr, flush.nbytes, flush_sink.ptr, 0)
             start.record()
             launch()
             stop.record()

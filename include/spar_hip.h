@@ -128,6 +128,13 @@ struct SparHipStatus spar_hip_memory_stats(struct SparHipMemoryStats* stats, int
  * cuda_runtime.cppm:161-174, used cudaMemset). */
 struct SparHipStatus spar_hip_zero(void* destination, uint64_t bytes, int device);
 
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) with ordinary cached
+ * loads; `sink` (4 bytes, may be NULL) is never written for real data.
+ * Benchmarks call it on a buffer larger than the L2 and Infinity Cache to
+ * evict and write back cached lines before a timed launch.  No reference
+ * counterpart (Spar has no benchmarking support). */
+struct SparHipStatus spar_hip_touch(const void* buffer, uint64_t bytes, void* sink, int device);
+
 /* Copies (cuda_runtime.cppm:176-237).  Host<->device copies return after the
  * copy has completed (the host buffer may be reused at once); device-to-device
  * copies are stream-ordered.  Cross-device copies use hipMemcpyPeerAsync. */

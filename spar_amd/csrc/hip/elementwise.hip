@@ -28,7 +28,7 @@ constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
 
 template <typename T, typename F>
 __global__ void __launch_bounds__(kThreads)
-    map1_vec_kernel(T* out, const T* in, uint64_t count, F f) {
+    map1_vec_kernel(T* out, const T* in, uint64_t count, F f, bool stream_out) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
@@ -50,7 +50,11 @@ __global__ void __launch_bounds__(kThreads)
         V o;
 #pragma unroll
         for (int k = 0; k < W; ++k) vec_set<T>(o, k, f(vec_get<T>(r[u], k)));
-        out_v[i] = o;
+        if (stream_out) {
+          stream_store(out_v + i, o);
+        } else {
+          out_v[i] = o;
+        }
       }
     }
   }
@@ -62,7 +66,7 @@ __global__ void __launch_bounds__(kThreads)
 
 template <typename T, typename F>
 __global__ void __launch_bounds__(kThreads)
-    map2_vec_kernel(T* out, const T* a, const T* b, uint64_t count, F f) {
+    map2_vec_kernel(T* out, const T* a, const T* b, uint64_t count, F f, bool stream_out) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
@@ -91,7 +95,11 @@ __global__ void __launch_bounds__(kThreads)
         for (int k = 0; k < W; ++k) {
           vec_set<T>(o, k, f(vec_get<T>(ra[u], k), vec_get<T>(rb[u], k)));
         }
-        out_v[i] = o;
+        if (stream_out) {
+          stream_store(out_v + i, o);
+        } else {
+          out_v[i] = o;
+        }
       }
     }
   }
@@ -142,7 +150,7 @@ template <typename T, typename F>
 void launch_map1(T* out, const T* in, uint64_t count, F f, const DeviceGuard& guard) {
   if (aligned16(out) && aligned16(in)) {
     map1_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
-        out, in, count, f);
+        out, in, count, f, stream_output(count * sizeof(T)));
   } else {
     map1_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         out, in, count, f);
@@ -153,29 +161,71 @@ template <typename T, typename F>
 void launch_map2(T* out, const T* a, const T* b, uint64_t count, F f, const DeviceGuard& guard) {
   if (aligned16(out) && aligned16(a) && aligned16(b)) {
     map2_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
-        out, a, b, count, f);
+        out, a, b, count, f, stream_output(count * sizeof(T)));
   } else {
     map2_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         out, a, b, count, f);
   }
 }
 
-// Writes a constant; the input pointer of map1 is the output itself and is
-// never read through.
+
+// Writes one value to every element.  The value is scalar[0] when a scalar
+// is given, else `value`; with `divide` it is then divided by `divisor` in T
+// (the mean backward's g / (T)n).  The vector form stores 16 bytes per lane
+// over the aligned body and needs a 16-byte aligned output.
 template <typename T>
-struct ConstantOp {
-  T value;
-  __device__ __forceinline__ T operator()(T) const { return value; }
-};
+__device__ __forceinline__ T fill_value(const T* scalar, T value, T divisor, bool divide) {
+  const T v = scalar != nullptr ? scalar[0] : value;
+  return divide ? v / divisor : v;
+}
 
 template <typename T>
 __global__ void __launch_bounds__(kThreads)
-    fill_from_scalar_kernel(T* out, const T* scalar, uint64_t count, T divisor, bool divide) {
-  const T value = divide ? scalar[0] / divisor : scalar[0];
+    fill_vec_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide,
+                    bool stream_out) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  const T v = fill_value(scalar, value, divisor, divide);
+  V o;
+#pragma unroll
+  for (int k = 0; k < W; ++k) vec_set<T>(o, k, v);
+  const uint64_t vectors = count / W;
+  V* out_v = reinterpret_cast<V*>(out);
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors;
+       i += stride) {
+    if (stream_out) {
+      stream_store(out_v + i, o);
+    } else {
+      out_v[i] = o;
+    }
+  }
+  if (blockIdx.x == 0) {
+    const uint64_t i = vectors * W + threadIdx.x;
+    if (i < count) out[i] = v;
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    fill_scalar_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide) {
+  const T v = fill_value(scalar, value, divisor, divide);
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
        i += stride) {
-    out[i] = value;
+    out[i] = v;
+  }
+}
+
+template <typename T>
+void launch_fill_values(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide,
+                        const DeviceGuard& guard) {
+  if (aligned16(out)) {
+    fill_vec_kernel<T><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
+        out, count, scalar, value, divisor, divide, stream_output(count * sizeof(T)));
+  } else {
+    fill_scalar_kernel<T><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
+        out, count, scalar, value, divisor, divide);
   }
 }
 
@@ -312,12 +362,11 @@ extern "C" SparHipStatus spar_hip_launch_fill_from_scalar(void* output, const vo
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
   const bool divide = divisor != 1.0;
   if (dtype == SPAR_HIP_FLOAT32) {
-    fill_from_scalar_kernel<float><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
-        static_cast<float*>(output), static_cast<const float*>(scalar), count,
-        static_cast<float>(divisor), divide);
+    launch_fill_values(static_cast<float*>(output), count, static_cast<const float*>(scalar), 0.0F,
+                       static_cast<float>(divisor), divide, guard);
   } else {
-    fill_from_scalar_kernel<double><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
-        static_cast<double*>(output), static_cast<const double*>(scalar), count, divisor, divide);
+    launch_fill_values(static_cast<double*>(output), count, static_cast<const double*>(scalar),
+                       0.0, divisor, divide, guard);
   }
   return finish(guard);
 }
@@ -332,31 +381,22 @@ extern "C" SparHipStatus spar_hip_launch_fill(void* output, uint64_t count, int 
   DeviceGuard guard;
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
   switch (dtype) {
-    case SPAR_HIP_FLOAT32: {
-      float* out = static_cast<float*>(output);
-      launch_map1(out, static_cast<const float*>(out), count,
-                  ConstantOp<float>{static_cast<float>(value)}, guard);
+    case SPAR_HIP_FLOAT32:
+      launch_fill_values<float>(static_cast<float*>(output), count, nullptr,
+                                static_cast<float>(value), 1.0F, false, guard);
       break;
-    }
-    case SPAR_HIP_FLOAT64: {
-      double* out = static_cast<double*>(output);
-      launch_map1(out, static_cast<const double*>(out), count, ConstantOp<double>{value}, guard);
+    case SPAR_HIP_FLOAT64:
+      launch_fill_values<double>(static_cast<double*>(output), count, nullptr, value, 1.0, false,
+                                 guard);
       break;
-    }
-    case SPAR_HIP_INT32: {
-      int32_t* out = static_cast<int32_t*>(output);
-      map1_scalar_kernel<int32_t, ConstantOp<int32_t>>
-          <<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
-              out, out, count, ConstantOp<int32_t>{static_cast<int32_t>(value)});
+    case SPAR_HIP_INT32:
+      launch_fill_values<int32_t>(static_cast<int32_t*>(output), count, nullptr,
+                                  static_cast<int32_t>(value), 1, false, guard);
       break;
-    }
-    default: {
-      int64_t* out = static_cast<int64_t*>(output);
-      map1_scalar_kernel<int64_t, ConstantOp<int64_t>>
-          <<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
-              out, out, count, ConstantOp<int64_t>{static_cast<int64_t>(value)});
+    default:
+      launch_fill_values<int64_t>(static_cast<int64_t*>(output), count, nullptr,
+                                  static_cast<int64_t>(value), 1, false, guard);
       break;
-    }
   }
   return finish(guard);
 }

@@ -137,6 +137,22 @@ __global__ void __launch_bounds__(256) zero_kernel(uint4* body, uint64_t vector_
   if (blockIdx.x == 0 && threadIdx.x < tail_bytes) tail[threadIdx.x] = 0;
 }
 
+// Reads every 16-byte word of a buffer with ordinary (cached) loads.  Any
+// dirty lines the reads evict are written back during this kernel, so a
+// timed kernel launched afterwards starts from a cold, clean cache.
+__global__ void __launch_bounds__(256) touch_kernel(const uint4* words, uint64_t count,
+                                                    unsigned* sink) {
+  unsigned acc = 0;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+       i += stride) {
+    const uint4 w = words[i];
+    acc ^= w.x ^ w.y ^ w.z ^ w.w;
+  }
+  // Written only for an impossible pattern so the loads cannot be elided.
+  if (acc == 0x9E3779B9u && sink != nullptr) *sink = acc;
+}
+
 __global__ void __launch_bounds__(256) zero_bytes_kernel(unsigned char* bytes, uint64_t count) {
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
@@ -268,6 +284,18 @@ extern "C" SparHipStatus spar_hip_zero(void* destination, uint64_t bytes, int de
     zero_bytes_kernel<<<static_cast<uint32_t>(blocks), 256, 0, guard.stream>>>(
         static_cast<unsigned char*>(destination), bytes);
   }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_touch(const void* buffer, uint64_t bytes, void* sink,
+                                        int device) {
+  if (bytes != 0 && (buffer == nullptr || !aligned16(buffer) || bytes % 16 != 0)) return invalid();
+  if (bytes == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const uint32_t blocks = static_cast<uint32_t>(guard.multiprocessors) * 8U;
+  touch_kernel<<<blocks, 256, 0, guard.stream>>>(static_cast<const uint4*>(buffer), bytes / 16,
+                                                 static_cast<unsigned*>(sink));
   return finish(guard);
 }
 

@@ -89,6 +89,7 @@ struct RowGeometry {
   FastDiv groups_per_row;  // inner / W
   int inner_unit[2];       // 1 if the operand is contiguous along the inner axis
   int reused[2];           // 1 if the operand is broadcast (read many times: keep it cached)
+  int stream_out;          // 1 to write the output with non-temporal stores
 };
 
 template <typename T, int NOPS, typename F>
@@ -155,7 +156,74 @@ __global__ void __launch_bounds__(kThreads)
             vec_set<T>(o, k, f(vec_get<T>(ra[u], k), vec_get<T>(rb[u], k)));
           }
         }
-        out_v[group] = o;
+        if (rg.stream_out) {
+          stream_store(out_v + group, o);
+        } else {
+          out_v[group] = o;
+        }
+      }
+    }
+  }
+}
+
+// Row-segment variant for long rows: workgroup t owns 256 groups of row
+// t / column_tiles, so the row decode is uniform (scalar registers, once per
+// workgroup) and each lane only adds its column before the load.
+template <typename T, int NOPS, typename F>
+__global__ void __launch_bounds__(kThreads)
+    row_tile_kernel(T* out, const T* a, const T* b, uint64_t tiles, uint64_t column_tiles,
+                    RowGeometry rg, F f) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  const KernelGeometry& g = rg.g;
+  const uint64_t inner = g.extents[0];
+  for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const uint64_t row = tile / column_tiles;
+    const uint64_t column = ((tile - row * column_tiles) * kThreads + threadIdx.x) * W;
+    uint64_t off0 = g.offsets[0];
+    uint64_t off1 = g.offsets[1];
+    uint64_t rem = row;
+    for (int k = 1; k < g.rank; ++k) {
+      const uint64_t q = rem / g.extents[k];
+      const uint64_t c = rem - q * g.extents[k];
+      rem = q;
+      off0 += c * g.strides[0][k];
+      if constexpr (NOPS == 2) off1 += c * g.strides[1][k];
+    }
+    if (column < inner) {
+      V ra, rb;
+      if (rg.inner_unit[0]) {
+        const V* p = reinterpret_cast<const V*>(a + off0 + column);
+        ra = rg.reused[0] ? *p : stream_load(p);
+      } else {
+        const T s = a[off0];
+#pragma unroll
+        for (int k = 0; k < W; ++k) vec_set<T>(ra, k, s);
+      }
+      if constexpr (NOPS == 2) {
+        if (rg.inner_unit[1]) {
+          const V* p = reinterpret_cast<const V*>(b + off1 + column);
+          rb = rg.reused[1] ? *p : stream_load(p);
+        } else {
+          const T s = b[off1];
+#pragma unroll
+          for (int k = 0; k < W; ++k) vec_set<T>(rb, k, s);
+        }
+      }
+      V o;
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        if constexpr (NOPS == 1) {
+          vec_set<T>(o, k, f(vec_get<T>(ra, k)));
+        } else {
+          vec_set<T>(o, k, f(vec_get<T>(ra, k), vec_get<T>(rb, k)));
+        }
+      }
+      V* target = reinterpret_cast<V*>(out + row * inner + column);
+      if (rg.stream_out) {
+        stream_store(target, o);
+      } else {
+        *target = o;
       }
     }
   }
@@ -288,6 +356,7 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
     rg.groups_per_row.init(static_cast<uint32_t>(inner / W));
     rg.inner_unit[0] = inner_unit[0];
     rg.inner_unit[1] = inner_unit[1];
+    rg.stream_out = stream_output(count * sizeof(T)) ? 1 : 0;
     for (int op = 0; op < NOPS; ++op) {
       rg.reused[op] = 0;
       for (int axis = 0; axis < view.rank; ++axis) {
@@ -295,6 +364,15 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
       }
     }
     const uint64_t groups = count / W;
+    const uint64_t groups_per_row = inner / W;
+    if (groups_per_row >= kThreads / 2) {
+      // Long rows: one workgroup per 256-group row segment.
+      const uint64_t column_tiles = (groups_per_row + kThreads - 1) / kThreads;
+      const uint64_t tiles = column_tiles * (count / inner);
+      row_tile_kernel<T, NOPS, F><<<capped_grid(tiles, 1), kThreads, 0, guard.stream>>>(
+          out, a, b, tiles, column_tiles, rg, f);
+      return;
+    }
     row_vector_kernel<T, NOPS, F>
         <<<capped_grid(groups, static_cast<uint64_t>(kThreads) * kUnroll), kThreads, 0,
            guard.stream>>>(out, a, b, groups, rg, f);

@@ -65,6 +65,7 @@ SIGNATURES = {
     "spar_hip_empty_cache": [_I],
     "spar_hip_memory_stats": [ctypes.POINTER(MemoryStats), _I],
     "spar_hip_zero": [_P, _U64, _I],
+    "spar_hip_touch": [_P, _U64, _P, _I],
     "spar_hip_copy_host_to_device": [_P, _P, _U64, _I],
     "spar_hip_copy_device_to_host": [_P, _P, _U64, _I],
     "spar_hip_copy_device_to_device": [_P, _I, _P, _I, _U64],
