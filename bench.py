@@ -243,10 +243,11 @@ def main():
     dominant = max(kernel_time, key=kernel_time.get)
     launches = sum(1 for _, k, _ in ops if k == dominant)
     achieved = kernel_bytes[dominant] / (kernel_time[dominant] * 1e-3) / 1e9
-    traffic_file = ROOT / "profiles" / "traffic.json"
-    traffic = None
-    if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get(dominant)
+    # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # (python3 -m spar_amd.rocprof_summary run ...), null until profiled.
+    from spar_amd.rocprof_summary import TRAFFIC_FILE, read_traffic
+
+    traffic = read_traffic(ROOT / "profiles" / TRAFFIC_FILE).get(dominant)
     roofline = {
         "bound": "hbm",
         "kernel": dominant,

@@ -1,0 +1,267 @@
+"""Profiles bench.py's default workload with rocprofv3 and writes two
+markdown summaries: per-kernel durations, and HBM bytes per dispatch from the
+FETCH_SIZE / WRITE_SIZE counters.
+
+    python3 -m spar_amd.rocprof_summary run --raw DIR --out DIR
+
+runs, as child processes (this process never touches the GPU):
+
+1. ``rocprofv3 --kernel-trace --stats`` over ``bench.py --no-cpu-baseline``;
+2. ``rocprofv3 --pmc FETCH_SIZE`` over ``bench.py --profile-loop 2``;
+3. ``rocprofv3 --pmc WRITE_SIZE`` over the same command.
+
+``bench.py --profile-loop`` runs the workload steps and then one plain
+contiguous copy of a 512 MiB tensor.  That copy's counter values calibrate
+the counters: it must move exactly 512 MiB each way, so each counter is
+scaled by 512 MiB / (its value on the copy).  A kernel's HBM traffic per
+launch is then scaled FETCH + scaled WRITE.
+
+``bench.py`` reads the ``hbm_bytes_per_launch`` lines of the traffic summary
+for its roofline ``traffic`` field.
+
+``summarize`` regenerates the markdown from an existing raw directory.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import json
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+
+# bench.py's kernel classes: a regex over the demangled kernel name, and
+# whether dispatches of that kernel count as launches of the class (helper
+# kernels such as the partial-sum combine add traffic but no launch).
+CLASSES = {
+    "broadcast_binary": [(r"::row_tile_kernel<|::row_vector_kernel<", True)],
+    "column_reduction": [(r"::column_kernel<", True), (r"::combine_columns_kernel<", False)],
+}
+COPY_PATTERN = r"CopyOp"
+CALIBRATION_BYTES = 512 << 20
+
+TRACE_ARGS = ["--no-cpu-baseline", "--steps", "20"]
+LOOP_ARGS = ["--profile-loop", "2"]
+STATS_FILE = "kernel_stats_x32x1024x4096.md"
+TRAFFIC_FILE = "hbm_traffic_x32x1024x4096.md"
+
+
+def short(name: str) -> str:
+    """Kernel name without namespaces, return type and argument list."""
+    name = re.sub(r"spar_hip::\(anonymous namespace\)::", "", name)
+    name = name.replace("spar_hip::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def commands(raw: Path):
+    bench = [sys.executable, str(ROOT / "bench.py")]
+    return {
+        "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d",
+                  str(raw / "trace"), "-o", "trace", "--"] + bench + TRACE_ARGS,
+        "fetch": ["rocprofv3", "--pmc", "FETCH_SIZE", "--output-format", "csv", "-d",
+                  str(raw / "fetch"), "-o", "fetch", "--"] + bench + LOOP_ARGS,
+        "write": ["rocprofv3", "--pmc", "WRITE_SIZE", "--output-format", "csv", "-d",
+                  str(raw / "write"), "-o", "write", "--"] + bench + LOOP_ARGS,
+        # The same benchmark without a profiler: the tracer slows launches
+        # bracketed by events, so bench.py's own timing is compared unprofiled.
+        "plain": bench + TRACE_ARGS,
+    }
+
+
+def shell(argv) -> str:
+    """The command as typed from the repository root."""
+    text = " ".join(argv)
+    text = text.replace(sys.executable, "python3").replace(str(ROOT) + "/", "")
+    return text
+
+
+def run(raw: Path, out: Path, limit: int) -> None:
+    raw.mkdir(parents=True, exist_ok=True)
+    for name, argv in commands(raw).items():
+        print(f"pass {name}: {shell(argv)}", flush=True)
+        log = raw / f"{name}.log"
+        with open(log, "w") as handle:
+            # rocprofv3 writes temporary files under TMPDIR; run it from /tmp.
+            proc = subprocess.run(["timeout", "-s", "KILL", str(limit)] + argv, cwd="/tmp",
+                                  env=dict(os.environ, TMPDIR="/tmp"), stdout=handle,
+                                  stderr=subprocess.STDOUT)
+        print(f"pass {name}: exit {proc.returncode}", flush=True)
+        if proc.returncode != 0:
+            sys.stdout.write(log.read_text()[-4000:])
+            raise SystemExit(proc.returncode)
+    summarize(raw, out)
+
+
+def bench_line(log: Path):
+    if not log.exists():
+        return None
+    for line in reversed(log.read_text().splitlines()):
+        line = line.strip()
+        if line.startswith("{") and '"roofline"' in line:
+            return json.loads(line)
+    return None
+
+
+def kernel_class(full_name: str):
+    if re.search(COPY_PATTERN, full_name):
+        return None, False
+    for cls, patterns in CLASSES.items():
+        for pattern, counts in patterns:
+            if re.search(pattern, full_name):
+                return cls, counts
+    return None, False
+
+
+def counters(path: Path):
+    rows = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        rows[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return rows
+
+
+def summarize(raw: Path, out: Path) -> None:
+    out.mkdir(parents=True, exist_ok=True)
+    cmds = commands(raw)
+    bench = bench_line(raw / "plain.log")
+    traced = bench_line(raw / "trace.log")
+
+    # --- kernel durations
+    stats = list(csv.DictReader(open(raw / "trace" / "trace_kernel_stats.csv")))
+    lines = [
+        "# Kernel durations: bench.py default workload, x[32,1024,4096] fp32",
+        "",
+        "Command (from the repository root):",
+        "",
+        "    " + shell(cmds["trace"]),
+        "",
+        "Every launch of the run: data generation, warm-up, the timed steps and the",
+        "per-op event timing.  Durations from the kernel trace.",
+        "",
+        "| kernel | class | calls | avg us | min us | max us | % time |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    class_ns = collections.defaultdict(float)
+    class_calls = collections.defaultdict(int)
+    for r in stats:
+        cls, counts = kernel_class(r["Name"])
+        lines.append(
+            f"| `{short(r['Name'])}` | {cls or ''} | {r['Calls']} | "
+            f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
+            f"{float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
+        if cls is not None:
+            class_ns[cls] += float(r["TotalDurationNs"])
+            if counts:
+                class_calls[cls] += int(r["Calls"])
+    lines += ["", "Average duration per launch of each bench.py kernel class (rocprofv3):", ""]
+    for cls in CLASSES:
+        if class_calls[cls]:
+            lines.append(f"- {cls}: {class_ns[cls] / class_calls[cls] / 1e3:.1f} us "
+                         f"over {class_calls[cls]} launches")
+    for label, line in (("without a profiler (`" + shell(cmds["plain"]) + "`)", bench),
+                        ("under the kernel trace above", traced)):
+        if line is None:
+            continue
+        roof = line["roofline"]
+        lines += ["", f"bench.py's own line {label}, timed with HIP events on the backend stream:",
+                  "",
+                  f"- value {line['value']} GB/s, {line['ms_per_step']} ms per step",
+                  f"- roofline kernel {roof['kernel']}: avg launch "
+                  f"{roof['avg_launch_ms'] * 1e3:.1f} us, achieved {roof['achieved']} GB/s "
+                  f"({roof['frac'] * 100:.1f}% of {roof['peak']:.0f} GB/s)"]
+    (out / STATS_FILE).write_text("\n".join(lines) + "\n")
+
+    # --- HBM traffic
+    fetch = counters(raw / "fetch" / "fetch_counter_collection.csv")
+    write = counters(raw / "write" / "write_counter_collection.csv")
+    copy = [k for k in fetch if re.search(COPY_PATTERN, k)]
+    if len(copy) != 1:
+        raise SystemExit(f"expected one calibration copy kernel, found {copy}")
+    copy = copy[0]
+    cal_kib = CALIBRATION_BYTES / 1024
+    fetch_copy = sum(fetch[copy]) / len(fetch[copy])
+    write_copy = sum(write[copy]) / len(write[copy])
+    f_scale = cal_kib / fetch_copy
+    w_scale = cal_kib / write_copy
+    lines = [
+        "# HBM traffic per dispatch: bench.py --profile-loop 2, x[32,1024,4096] fp32",
+        "",
+        "Commands (from the repository root), one counter per run:",
+        "",
+        "    " + shell(cmds["fetch"]),
+        "    " + shell(cmds["write"]),
+        "",
+        "Calibration: the run ends with a plain contiguous copy of 512 MiB "
+        f"(`{short(copy)}`), which reads FETCH_SIZE {fetch_copy:.0f} KiB and WRITE_SIZE "
+        f"{write_copy:.0f} KiB per dispatch; every counter value below is scaled by "
+        f"{f_scale:.4f} (fetch) and {w_scale:.4f} (write) to bytes.",
+        "",
+        "| kernel | class | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB per dispatch |",
+        "|---|---|---|---|---|---|",
+    ]
+    class_bytes = collections.defaultdict(float)
+    class_launches = collections.defaultdict(int)
+    for name, values in fetch.items():
+        fv = sum(values) / len(values)
+        wv = sum(write.get(name, [0.0])) / max(len(write.get(name, [])), 1)
+        per = (fv * f_scale + wv * w_scale) * 1024
+        cls, counts = kernel_class(name)
+        lines.append(f"| `{short(name)}` | {cls or ''} | {len(values)} | {fv:.0f} | {wv:.0f} | "
+                     f"{per / 1e6:.1f} |")
+        if cls is not None:
+            class_bytes[cls] += per * len(values)
+            if counts:
+                class_launches[cls] += len(values)
+    lines += ["", "HBM bytes per launch of each bench.py kernel class (all dispatches of the",
+              "class over its launches):", ""]
+    for cls in CLASSES:
+        if class_launches[cls]:
+            lines.append(f"- hbm_bytes_per_launch[{cls}] = "
+                         f"{round(class_bytes[cls] / class_launches[cls])}")
+    (out / TRAFFIC_FILE).write_text("\n".join(lines) + "\n")
+    print(f"wrote {out / STATS_FILE} and {out / TRAFFIC_FILE}", flush=True)
+
+
+def read_traffic(path: Path):
+    """{class: bytes per launch} from a traffic summary, or {} if absent."""
+    if not path.exists():
+        return {}
+    found = {}
+    for m in re.finditer(r"^- hbm_bytes_per_launch\[(\w+)\] = (\d+)$", path.read_text(), re.M):
+        found[m.group(1)] = int(m.group(2))
+    return found
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    sub = p.add_subparsers(dest="mode", required=True)
+    r = sub.add_parser("run")
+    r.add_argument("--raw", type=Path, required=True, help="directory for raw rocprofv3 output")
+    r.add_argument("--out", type=Path, required=True, help="directory for the markdown")
+    r.add_argument("--limit", type=int, default=240, help="seconds per rocprofv3 pass")
+    s = sub.add_parser("summarize")
+    s.add_argument("--raw", type=Path, required=True)
+    s.add_argument("--out", type=Path, required=True)
+    args = p.parse_args()
+    if args.mode == "run":
+        run(args.raw.resolve(), args.out.resolve(), args.limit)
+    else:
+        summarize(args.raw.resolve(), args.out.resolve())
+
+
+if __name__ == "__main__":
+    main()
