@@ -168,27 +168,32 @@ __global__ void __launch_bounds__(kThreads)
 
 // Row-segment variant for long rows: workgroup t owns 256 groups of row
 // t / column_tiles, so the row decode is uniform (scalar registers, once per
-// workgroup) and each lane only adds its column before the load.
+// workgroup, by multiply-shift division) and each lane only adds its column
+// before the load.  Requires tiles and rows below 2^31.
 template <typename T, int NOPS, typename F>
 __global__ void __launch_bounds__(kThreads)
-    row_tile_kernel(T* out, const T* a, const T* b, uint64_t tiles, uint64_t column_tiles,
+    row_tile_kernel(T* out, const T* a, const T* b, uint32_t tiles, FastDiv column_tiles,
                     RowGeometry rg, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const KernelGeometry& g = rg.g;
   const uint64_t inner = g.extents[0];
-  for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const uint64_t row = tile / column_tiles;
-    const uint64_t column = ((tile - row * column_tiles) * kThreads + threadIdx.x) * W;
+  for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const uint32_t row = column_tiles.div(tile);
+    const uint64_t column =
+        (static_cast<uint64_t>(tile - row * column_tiles.divisor) * kThreads + threadIdx.x) * W;
     uint64_t off0 = g.offsets[0];
     uint64_t off1 = g.offsets[1];
-    uint64_t rem = row;
-    for (int k = 1; k < g.rank; ++k) {
-      const uint64_t q = rem / g.extents[k];
-      const uint64_t c = rem - q * g.extents[k];
-      rem = q;
-      off0 += c * g.strides[0][k];
-      if constexpr (NOPS == 2) off1 += c * g.strides[1][k];
+    uint32_t rem = row;
+#pragma unroll
+    for (int k = 1; k < kMaxRank; ++k) {
+      if (k < g.rank) {
+        const uint32_t q = g.divisors[k].div(rem);
+        const uint64_t c = rem - q * g.divisors[k].divisor;
+        rem = q;
+        off0 += c * g.strides[0][k];
+        if constexpr (NOPS == 2) off1 += c * g.strides[1][k];
+      }
     }
     if (column < inner) {
       V ra, rb;
@@ -368,9 +373,11 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
     if (groups_per_row >= kThreads / 2) {
       // Long rows: one workgroup per 256-group row segment.
       const uint64_t column_tiles = (groups_per_row + kThreads - 1) / kThreads;
-      const uint64_t tiles = column_tiles * (count / inner);
+      const uint64_t tiles = column_tiles * (count / inner);  // < count / 128
+      FastDiv tiles_per_row;
+      tiles_per_row.init(static_cast<uint32_t>(column_tiles));
       row_tile_kernel<T, NOPS, F><<<capped_grid(tiles, 1), kThreads, 0, guard.stream>>>(
-          out, a, b, tiles, column_tiles, rg, f);
+          out, a, b, static_cast<uint32_t>(tiles), tiles_per_row, rg, f);
       return;
     }
     row_vector_kernel<T, NOPS, F>

@@ -303,6 +303,50 @@ def test_axis_reductions_3d(hip, dtype):
         check_axis(hip, base, perm, axes, dtype, f"3d perm {axes}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape,axes", [((300, 2048), [0]), ((3, 200, 1100), [1]),
+                                        ((2, 70, 4096), [0, 1]), ((5000, 1024), [0])])
+def test_column_reductions_wide_rows(hip, dtype, shape, axes):
+    """Rows of >= 256 vectors take the wave-per-column-range kernel; values
+    are quantised so that maxima tie, and NaNs sit in some columns."""
+    size = int(np.prod(shape))
+    base = np.round(inputs(28, size, dtype, with_specials=False) * 8) / 8
+    base = base.astype(dtype).reshape(shape)
+    check_axis(hip, base, base, axes, dtype, f"wide {shape} {axes}")
+    spiked = base.copy()
+    flat = spiked.reshape(-1, shape[-1])
+    flat[flat.shape[0] // 3, 5] = np.nan
+    flat[flat.shape[0] // 2, 5] = np.nan
+    flat[7, shape[-1] - 1] = np.inf
+    spiked[..., 9] = -np.inf  # a column of -inf: argmax is its first row
+    mx, am = ref.axis_max(spiked, axes)
+    assert_bitexact(axis_reduce(hip, spiked, spiked, axes, "max", dtype), mx, "wide max nan")
+    assert_bitexact(axis_reduce(hip, spiked, spiked, axes, "argmax", dtype), am, "wide argmax nan")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_max_argmax_negative_infinity_runs(hip, dtype):
+    """Rows long enough to be split over blocks, made of -inf runs: the answer
+    is the first -inf unless a NaN or a finite value appears later."""
+    cols = 200000
+    x = inputs(29, 4 * cols, dtype, with_specials=False).reshape(4, cols)
+    x[1:] = -np.inf
+    x[2, 150000] = np.nan
+    x[3, cols - 1] = 1.0
+    mx, am = ref.axis_max(x, [1])
+    assert list(am) == [int(np.argmax(x[0])), 0, 150000, cols - 1]
+    assert_bitexact(axis_reduce(hip, x, x, [1], "max", dtype), mx, "-inf rows max")
+    assert_bitexact(axis_reduce(hip, x, x, [1], "argmax", dtype), am, "-inf rows argmax")
+    flat = np.full(1 << 20, -np.inf, dtype=dtype)
+    out = out_buf(hip, (1,), np.int64)
+    hip.call("spar_hip_launch_reduction", out.ptr, dev(hip, flat).ptr, flat.size, tag(dtype),
+             hip.ARGMAX, 0)
+    assert out.to_numpy(np.int64, (1,))[0] == 0
+    hip.call("spar_hip_launch_reduction", out.ptr, dev(hip, flat).ptr, flat.size, tag(dtype),
+             hip.MAX, 0)
+    assert out.to_numpy(dtype, (1,))[0] == -np.inf
+
+
 def test_max_argmax_ties_nan_signed_zero(hip):
     rows = np.array([
         [1.0, 3.0, 3.0, 2.0],
