@@ -34,6 +34,19 @@ struct SliceStats {
   unsigned positive_infinities;
 };
 
+// Barrier for the reductions' LDS exchanges: waits for this wave's LDS
+// accesses (lgkmcnt(0)) and meets the other waves at s_barrier.  Unlike
+// __syncthreads() it is not a release fence, so global loads in flight, such
+// as the next row's direct-to-LDS prefetch into a separate stage buffer, keep
+// flying across it.  The signal fences stop the compiler from moving memory
+// accesses across the barrier; they emit no instructions.
+__device__ __forceinline__ void exchange_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt and expcnt unchanged, lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 template <typename T>
 __device__ __forceinline__ void stats_init(SliceStats<T>& s) {
   s.value = -static_cast<T>(__builtin_huge_val());
@@ -85,9 +98,9 @@ __device__ __forceinline__ SliceStats<T> block_stats(SliceStats<T> s) {
   constexpr int kWavesPerBlock = THREADS / kWave;
   __shared__ SliceStats<T> lds[kWavesPerBlock];
   s = wave_stats(s);
-  __syncthreads();
+  exchange_barrier();
   if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = s;
-  __syncthreads();
+  exchange_barrier();
   SliceStats<T> total = lds[0];
 #pragma unroll
   for (int w = 1; w < kWavesPerBlock; ++w) stats_merge(total, lds[w]);
@@ -99,9 +112,9 @@ __device__ __forceinline__ T block_sum(T value) {
   constexpr int kWavesPerBlock = THREADS / kWave;
   __shared__ T lds[kWavesPerBlock];
   value = wave_sum(value);
-  __syncthreads();
+  exchange_barrier();
   if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = value;
-  __syncthreads();
+  exchange_barrier();
   T total = lds[0];
 #pragma unroll
   for (int w = 1; w < kWavesPerBlock; ++w) total += lds[w];
@@ -127,6 +140,30 @@ __device__ __forceinline__ T undefined_value(const SliceStats<T>& s, T x) {
     const T probability = T(1) / static_cast<T>(s.positive_infinities);
     return x == positive_infinity<T>() ? probability : T(0);
   }
+}
+
+// e / total for many e and one total: q0 = e * (1 / total) corrected by one
+// residual step, q = q0 + (e - q0 * total) / total, with the residual exact
+// through a fused multiply-add (Markstein's correction).  The result is
+// within one ulp of the correctly rounded quotient (equal to it in almost
+// all cases) at three instructions instead of a full IEEE division.
+template <typename T>
+struct RowDivisor {
+  T total;
+  T reciprocal;
+  __device__ __forceinline__ explicit RowDivisor(T t) : total(t), reciprocal(T(1) / t) {}
+  __device__ __forceinline__ T operator()(T e) const {
+    const T q0 = e * reciprocal;
+    const T residual = __builtin_fma(-q0, total, e);
+    return __builtin_fma(residual, reciprocal, q0);
+  }
+};
+
+template <>
+__device__ __forceinline__ float RowDivisor<float>::operator()(float e) const {
+  const float q0 = e * reciprocal;
+  const float residual = __builtin_fmaf(-q0, total, e);
+  return __builtin_fmaf(residual, reciprocal, q0);
 }
 
 template <typename T>
@@ -170,7 +207,7 @@ __device__ __forceinline__ void load_row(T (&x)[E], const T* row, uint64_t n) {
 }
 
 template <typename T, int THREADS, int E, bool VEC, bool FULL>
-__device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n) {
+__device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n, bool stream_out) {
   if constexpr (VEC) {
     using V = typename Vec16<T>::type;
     constexpr int W = Vec16<T>::width;
@@ -181,7 +218,11 @@ __device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n) {
         V value;
 #pragma unroll
         for (int k = 0; k < W; ++k) vec_set<T>(value, k, y[v * W + k]);
-        *reinterpret_cast<V*>(row + col) = value;
+        if (stream_out) {
+          stream_store(reinterpret_cast<V*>(row + col), value);
+        } else {
+          *reinterpret_cast<V*>(row + col) = value;
+        }
       }
     }
   } else {
@@ -195,66 +236,290 @@ __device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n) {
 
 // ----------------------------------------------------- register-row kernels
 
-template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL>
+// Block-wide first-occurrence maximum of (value, column) pairs: the larger
+// value wins, equal values (including -0 and +0) keep the smaller column.
+// NaN never enters (a lane only takes an element that compares larger).
+template <typename T, int THREADS>
+__device__ __forceinline__ T block_max_first(T value, int32_t index) {
+  constexpr int kWavesPerBlock = THREADS / kWave;
+  __shared__ T lds_value[kWavesPerBlock];
+  __shared__ int32_t lds_index[kWavesPerBlock];
+#pragma unroll
+  for (int mask = kWave / 2; mask > 0; mask >>= 1) {
+    const T other = __shfl_xor(value, mask, kWave);
+    const int32_t other_index = __shfl_xor(index, mask, kWave);
+    const bool take = other > value || (other == value && other_index < index);
+    value = take ? other : value;
+    index = take ? other_index : index;
+  }
+  exchange_barrier();
+  if (threadIdx.x % kWave == 0) {
+    lds_value[threadIdx.x / kWave] = value;
+    lds_index[threadIdx.x / kWave] = index;
+  }
+  exchange_barrier();
+  T best = lds_value[0];
+  int32_t best_index = lds_index[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) {
+    const T other = lds_value[w];
+    const int32_t other_index = lds_index[w];
+    const bool take = other > best || (other == best && other_index < best_index);
+    best = take ? other : best;
+    best_index = take ? other_index : best_index;
+  }
+  return best;
+}
+
+// Forward over rows held in registers.  Each block walks rows blockIdx.x,
+// blockIdx.x + gridDim.x, ... (the grid is sized to the resident blocks) and,
+// when PREFETCH, issues the loads of its next row before computing the
+// current one, so a CU's HBM reads overlap its arithmetic.
+//
+// The fast path keeps no NaN or infinity bookkeeping: with m the
+// first-occurrence maximum over the non-NaN elements, S = sum exp(x - m) is
+// NaN exactly when the slice is undefined (a NaN element gives NaN - m; a +inf
+// maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
+// otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
+// row and apply the reference's special cases from full slice statistics.
+template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool PREFETCH>
 __global__ void __launch_bounds__(THREADS)
-    forward_row_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n) {
-  for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const T* row = in + r * n;
-    T x[E];
-    load_row<T, THREADS, E, VEC, FULL>(x, row, n);
-    SliceStats<T> s;
-    stats_init(s);
+    forward_row_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
+                       bool stream_out) {
+  T x[E];
+  T next[PREFETCH ? E : 1];
+  uint64_t r = blockIdx.x;
+  if constexpr (PREFETCH) {
+    if (r < rows) load_row<T, THREADS, E, VEC, FULL>(next, in + r * n, n);
+  }
+  for (; r < rows; r += gridDim.x) {
+    if constexpr (PREFETCH) {
+#pragma unroll
+      for (int j = 0; j < E; ++j) x[j] = next[j];
+      if (r + gridDim.x < rows) load_row<T, THREADS, E, VEC, FULL>(next, in + (r + gridDim.x) * n, n);
+    } else {
+      load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
+    }
+    // Lane maximum: columns reach a lane in increasing order, so a later
+    // element wins only if it is strictly larger.
+    T lane_max = -positive_infinity<T>();
+    int32_t lane_index = INT32_MAX;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       const uint64_t col = column_of<T, THREADS, VEC>(j);
-      if (FULL || col < n) stats_add(s, x[j], static_cast<int64_t>(col));
-    }
-    s = block_stats<T, THREADS>(s);
-    const bool bad = slice_undefined(s);
-    if (threadIdx.x == 0) undefined[r] = bad ? 1 : 0;
-    // The results overwrite x in place so one row costs E registers per lane.
-    if (bad) {
-#pragma unroll
-      for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
-    } else {
-      const T maximum = s.value;
-      T local = T(0);
-#pragma unroll
-      for (int j = 0; j < E; ++j) {
-        const uint64_t col = column_of<T, THREADS, VEC>(j);
-        if constexpr (LOG) {
-          x[j] = x[j] - maximum;
-          if (FULL || col < n) local += math_exp(x[j]);
-        } else {
-          x[j] = math_exp(x[j] - maximum);
-          if (FULL || col < n) local += x[j];
-        }
+      if (FULL || col < n) {
+        const bool take = x[j] > lane_max;
+        lane_max = take ? x[j] : lane_max;
+        lane_index = take ? static_cast<int32_t>(col) : lane_index;
       }
-      const T total = block_sum<T, THREADS>(local);
+    }
+    const T maximum = block_max_first<T, THREADS>(lane_max, lane_index);
+    // The results overwrite x in place so one row costs E registers per lane.
+    T local = T(0);
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint64_t col = column_of<T, THREADS, VEC>(j);
+      if constexpr (LOG) {
+        x[j] = x[j] - maximum;
+        if (FULL || col < n) local += math_exp(x[j]);
+      } else {
+        x[j] = math_exp(x[j] - maximum);
+        if (FULL || col < n) local += x[j];
+      }
+    }
+    const T total = block_sum<T, THREADS>(local);
+    const bool bad = total != total;
+    if (threadIdx.x == 0) undefined[r] = bad ? 1 : 0;
+    if (!bad) {
       if constexpr (LOG) {
         const T log_sum = math_log(total);
 #pragma unroll
         for (int j = 0; j < E; ++j) x[j] = x[j] - log_sum;
       } else {
+        const RowDivisor<T> divide(total);
 #pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = x[j] / total;
+        for (int j = 0; j < E; ++j) x[j] = divide(x[j]);
       }
+    } else {
+      load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
+      SliceStats<T> s;
+      stats_init(s);
+#pragma unroll
+      for (int j = 0; j < E; ++j) {
+        const uint64_t col = column_of<T, THREADS, VEC>(j);
+        if (FULL || col < n) stats_add(s, x[j], static_cast<int64_t>(col));
+      }
+      s = block_stats<T, THREADS>(s);
+#pragma unroll
+      for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
     }
-    store_row<T, THREADS, E, VEC, FULL>(out + r * n, x, n);
+    store_row<T, THREADS, E, VEC, FULL>(out + r * n, x, n, stream_out);
+  }
+}
+
+// ------------------------------------------- LDS-staged rows (prefetch)
+
+// s_waitcnt immediate that waits until at most `count` vector memory
+// operations are outstanding (vmcnt in bits 3:0 and 15:14) and leaves expcnt
+// (bits 6:4) and lgkmcnt (bits 11:8) at their maxima, i.e. unconstrained.
+constexpr int vmcnt_wait(int count) {
+  return (count & 0xF) | ((count >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+// Issues direct global-to-LDS loads (global_load_lds_dwordx4) of one row
+// into `stage`, laid out in column order.  Lane i of a wave writes the 16
+// bytes at the wave's LDS base + 16 i, so the base of vector group v for
+// wave w is (v * THREADS + 64 w) * W elements.
+template <typename T, int THREADS, int E, bool FULL>
+__device__ __forceinline__ void stage_row(T* stage, const T* row, uint64_t n) {
+  constexpr int W = Vec16<T>::width;
+  const int wave_base = (threadIdx.x / kWave) * kWave;
+#pragma unroll
+  for (int v = 0; v < E / W; ++v) {
+    const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
+    if (FULL || col < n) {
+      __builtin_amdgcn_global_load_lds(
+          (__attribute__((address_space(1))) void*)(row + col),
+          (__attribute__((address_space(3))) void*)(stage + (v * THREADS + wave_base) * W), 16,
+          0, 0);
+    }
+  }
+}
+
+template <typename T, int THREADS, int E, bool FULL>
+__device__ __forceinline__ void unstage_row(T (&x)[E], const T* stage, uint64_t n) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+#pragma unroll
+  for (int v = 0; v < E / W; ++v) {
+    const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
+    if (FULL || col < n) {
+      const V value = *reinterpret_cast<const V*>(stage + (v * THREADS + threadIdx.x) * W);
+#pragma unroll
+      for (int k = 0; k < W; ++k) x[v * W + k] = vec_get<T>(value, k);
+    }
+  }
+}
+
+// One row of the staged forward: copies the stage (row r, already landed)
+// into registers, starts staging row r + stride, computes, stores.
+//
+// The fast path keeps no NaN or infinity bookkeeping: with m the
+// first-occurrence maximum over the non-NaN elements, S = sum exp(x - m) is
+// NaN exactly when the slice is undefined (a NaN element gives NaN - m; a +inf
+// maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
+// otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
+// row and apply the reference's special cases from full slice statistics.
+template <typename T, int THREADS, int E, bool LOG, bool FULL>
+__device__ __forceinline__ void staged_forward_row(T* out, int32_t* undefined, const T* in,
+                                                   uint64_t rows, uint64_t n, uint64_t r,
+                                                   uint64_t stride, T* stage, bool stream_out) {
+  T x[E];
+  unstage_row<T, THREADS, E, FULL>(x, stage, n);
+  exchange_barrier();  // the stage is free for the next row
+  if (r + stride < rows) stage_row<T, THREADS, E, FULL>(stage, in + (r + stride) * n, n);
+  // Lane maximum: columns reach a lane in increasing order, so a later
+  // element wins only if it is strictly larger.
+  T lane_max = -positive_infinity<T>();
+  int32_t lane_index = INT32_MAX;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const uint64_t col = column_of<T, THREADS, true>(j);
+    if (FULL || col < n) {
+      const bool take = x[j] > lane_max;
+      lane_max = take ? x[j] : lane_max;
+      lane_index = take ? static_cast<int32_t>(col) : lane_index;
+    }
+  }
+  const T maximum = block_max_first<T, THREADS>(lane_max, lane_index);
+  T local = T(0);
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const uint64_t col = column_of<T, THREADS, true>(j);
+    if constexpr (LOG) {
+      x[j] = x[j] - maximum;
+      if (FULL || col < n) local += math_exp(x[j]);
+    } else {
+      x[j] = math_exp(x[j] - maximum);
+      if (FULL || col < n) local += x[j];
+    }
+  }
+  const T total = block_sum<T, THREADS>(local);
+  const bool bad = total != total;
+  if (threadIdx.x == 0) undefined[r] = bad ? 1 : 0;
+  if (!bad) {
+    if constexpr (LOG) {
+      const T log_sum = math_log(total);
+#pragma unroll
+      for (int j = 0; j < E; ++j) x[j] = x[j] - log_sum;
+    } else {
+      const RowDivisor<T> divide(total);
+#pragma unroll
+      for (int j = 0; j < E; ++j) x[j] = divide(x[j]);
+    }
+  } else {
+    load_row<T, THREADS, E, true, FULL>(x, in + r * n, n);
+    SliceStats<T> s;
+    stats_init(s);
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint64_t col = column_of<T, THREADS, true>(j);
+      if (FULL || col < n) stats_add(s, x[j], static_cast<int64_t>(col));
+    }
+    s = block_stats<T, THREADS>(s);
+#pragma unroll
+    for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
+  }
+  store_row<T, THREADS, E, true, FULL>(out + r * n, x, n, stream_out);
+}
+
+// Forward over rows (16-byte aligned, n a multiple of the vector width) in
+// which each block walks rows blockIdx.x, blockIdx.x + gridDim.x, ... (the
+// grid is sized to the resident blocks).  The next row streams from HBM into
+// an LDS stage while the current row is computed in registers, so a CU's
+// reads overlap its arithmetic without spending VGPRs on a second row, and
+// its stores drain while the following row is computed.
+template <typename T, int THREADS, int E, bool LOG, bool FULL>
+__global__ void __launch_bounds__(THREADS)
+    forward_row_staged_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
+                              bool stream_out) {
+  __shared__ __attribute__((aligned(16))) T stage[THREADS * E];
+  uint64_t r = blockIdx.x;
+  if (r >= rows) return;
+  stage_row<T, THREADS, E, FULL>(stage, in + r * n, n);
+  __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // nothing was issued after the staging loads
+  exchange_barrier();                          // every wave's staged loads have landed
+  staged_forward_row<T, THREADS, E, LOG, FULL>(out, undefined, in, rows, n, r, gridDim.x, stage,
+                                               stream_out);
+  for (r += gridDim.x; r < rows; r += gridDim.x) {
+    // Vector memory operations retire in issue order on this architecture.
+    // After the staging loads of row r, a wave of a full row issued at least
+    // E / W further operations (its row stores; wave 0 also its flag store),
+    // so waiting until at most E / W remain lands the staged row while the
+    // previous row's stores keep draining.  Partial rows skip stores per
+    // wave and wait for everything.
+    if constexpr (FULL) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(E / Vec16<T>::width));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
+    }
+    exchange_barrier();  // every wave's staged loads have landed
+    staged_forward_row<T, THREADS, E, LOG, FULL>(out, undefined, in, rows, n, r, gridDim.x, stage,
+                                                 stream_out);
   }
 }
 
 template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL>
 __global__ void __launch_bounds__(THREADS)
     backward_row_kernel(T* out, const T* gradient, const T* saved, const int32_t* undefined,
-                        uint64_t rows, uint64_t n) {
+                        uint64_t rows, uint64_t n, bool stream_out) {
   for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     T* out_row = out + r * n;
     T g[E];
     if (undefined[r] != 0) {
 #pragma unroll
       for (int j = 0; j < E; ++j) g[j] = quiet_nan<T>();
-      store_row<T, THREADS, E, VEC, FULL>(out_row, g, n);
+      store_row<T, THREADS, E, VEC, FULL>(out_row, g, n, stream_out);
       continue;
     }
     T y[E];
@@ -281,7 +546,7 @@ __global__ void __launch_bounds__(THREADS)
         g[j] = y[j] * (g[j] - reduced);
       }
     }
-    store_row<T, THREADS, E, VEC, FULL>(out_row, g, n);
+    store_row<T, THREADS, E, VEC, FULL>(out_row, g, n, stream_out);
   }
 }
 
@@ -312,11 +577,12 @@ __global__ void __launch_bounds__(kLoopThreads)
     for (uint64_t c = threadIdx.x; c < n; c += kLoopThreads) local += math_exp(row[c] - maximum);
     const T total = block_sum<T, kLoopThreads>(local);
     const T log_sum = LOG ? math_log(total) : T(0);
+    const RowDivisor<T> divide(total);
     for (uint64_t c = threadIdx.x; c < n; c += kLoopThreads) {
       if constexpr (LOG) {
         out_row[c] = (row[c] - maximum) - log_sum;
       } else {
-        out_row[c] = math_exp(row[c] - maximum) / total;
+        out_row[c] = divide(math_exp(row[c] - maximum));
       }
     }
   }
@@ -384,11 +650,12 @@ __global__ void __launch_bounds__(kSliceThreads)
     T total = T(0);
     for (uint64_t a = 0; a < axis_extent; ++a) total += math_exp(base[a * inner] - maximum);
     const T log_sum = LOG ? math_log(total) : T(0);
+    const RowDivisor<T> divide(total);
     for (uint64_t a = 0; a < axis_extent; ++a) {
       if constexpr (LOG) {
         out_base[a * inner] = (base[a * inner] - maximum) - log_sum;
       } else {
-        out_base[a * inner] = math_exp(base[a * inner] - maximum) / total;
+        out_base[a * inner] = divide(math_exp(base[a * inner] - maximum));
       }
     }
   }
@@ -434,45 +701,75 @@ uint32_t grid_for(uint64_t blocks) {
   return static_cast<uint32_t>(blocks > kMaxGrid ? kMaxGrid : blocks);
 }
 
+// Blocks of `kernel` resident on the device at once (at least one per CU).
+template <typename K>
+uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      per_cu < 1) {
+    per_cu = 1;
+  }
+  return static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(guard.multiprocessors);
+}
+
 // Register-row configurations (threads, elements per lane), smallest first;
 // FULL drops the bounds checks when the row exactly fills the registers.
+// The forward prefetches the next row when a second row array fits in 32
+// VGPRs per lane, with one block per resident slot walking many rows.
+template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL>
+void forward_rows_as(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
+                     const DeviceGuard& guard) {
+  // The LDS stage holds one row of THREADS * E elements (at most 128 KiB of
+  // the CU's 160 KiB).
+  constexpr bool kStaged = VEC && THREADS * E * sizeof(T) <= (128U << 10);
+  const bool stream_out = stream_output(rows * n * sizeof(T));
+  if constexpr (kStaged) {
+    auto kernel = forward_row_staged_kernel<T, THREADS, E, LOG, FULL>;
+    const uint64_t resident = resident_blocks(kernel, THREADS, guard);
+    kernel<<<grid_for(rows < resident ? rows : resident), THREADS, 0, guard.stream>>>(
+        out, undefined, in, rows, n, stream_out);
+  } else {
+    forward_row_kernel<T, THREADS, E, LOG, VEC, FULL, false>
+        <<<grid_for(rows), THREADS, 0, guard.stream>>>(out, undefined, in, rows, n, stream_out);
+  }
+}
+
 template <typename T, int THREADS, int E, bool LOG, bool VEC>
 void forward_rows(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
-                  hipStream_t stream) {
+                  const DeviceGuard& guard) {
   if (n == static_cast<uint64_t>(THREADS) * E) {
-    forward_row_kernel<T, THREADS, E, LOG, VEC, true>
-        <<<grid_for(rows), THREADS, 0, stream>>>(out, undefined, in, rows, n);
+    forward_rows_as<T, THREADS, E, LOG, VEC, true>(out, undefined, in, rows, n, guard);
   } else {
-    forward_row_kernel<T, THREADS, E, LOG, VEC, false>
-        <<<grid_for(rows), THREADS, 0, stream>>>(out, undefined, in, rows, n);
+    forward_rows_as<T, THREADS, E, LOG, VEC, false>(out, undefined, in, rows, n, guard);
   }
 }
 
 template <typename T, int THREADS, int E, bool LOG, bool VEC>
 void backward_rows(T* out, const T* gradient, const T* saved, const int32_t* undefined,
-                   uint64_t rows, uint64_t n, hipStream_t stream) {
+                   uint64_t rows, uint64_t n, const DeviceGuard& guard) {
+  const bool stream_out = stream_output(rows * n * sizeof(T));
   if (n == static_cast<uint64_t>(THREADS) * E) {
-    backward_row_kernel<T, THREADS, E, LOG, VEC, true>
-        <<<grid_for(rows), THREADS, 0, stream>>>(out, gradient, saved, undefined, rows, n);
+    backward_row_kernel<T, THREADS, E, LOG, VEC, true><<<grid_for(rows), THREADS, 0, guard.stream>>>(
+        out, gradient, saved, undefined, rows, n, stream_out);
   } else {
-    backward_row_kernel<T, THREADS, E, LOG, VEC, false>
-        <<<grid_for(rows), THREADS, 0, stream>>>(out, gradient, saved, undefined, rows, n);
+    backward_row_kernel<T, THREADS, E, LOG, VEC, false><<<grid_for(rows), THREADS, 0, guard.stream>>>(
+        out, gradient, saved, undefined, rows, n, stream_out);
   }
 }
 
 template <typename T, bool LOG, bool VEC>
 bool launch_forward_rows(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
-                         hipStream_t stream) {
+                         const DeviceGuard& guard) {
   if (n <= 256 * 4) {
-    forward_rows<T, 256, 4, LOG, VEC>(out, undefined, in, rows, n, stream);
+    forward_rows<T, 256, 4, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 256 * 16) {
-    forward_rows<T, 256, 16, LOG, VEC>(out, undefined, in, rows, n, stream);
+    forward_rows<T, 256, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 512 * 16) {
-    forward_rows<T, 512, 16, LOG, VEC>(out, undefined, in, rows, n, stream);
+    forward_rows<T, 512, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 1024 * 16) {
-    forward_rows<T, 1024, 16, LOG, VEC>(out, undefined, in, rows, n, stream);
+    forward_rows<T, 1024, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 1024 * 32) {
-    forward_rows<T, 1024, 32, LOG, VEC>(out, undefined, in, rows, n, stream);
+    forward_rows<T, 1024, 32, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else {
     return false;
   }
@@ -481,17 +778,17 @@ bool launch_forward_rows(T* out, int32_t* undefined, const T* in, uint64_t rows,
 
 template <typename T, bool LOG, bool VEC>
 bool launch_backward_rows(T* out, const T* gradient, const T* saved, const int32_t* undefined,
-                          uint64_t rows, uint64_t n, hipStream_t stream) {
+                          uint64_t rows, uint64_t n, const DeviceGuard& guard) {
   if (n <= 256 * 4) {
-    backward_rows<T, 256, 4, LOG, VEC>(out, gradient, saved, undefined, rows, n, stream);
+    backward_rows<T, 256, 4, LOG, VEC>(out, gradient, saved, undefined, rows, n, guard);
   } else if (n <= 256 * 16) {
-    backward_rows<T, 256, 16, LOG, VEC>(out, gradient, saved, undefined, rows, n, stream);
+    backward_rows<T, 256, 16, LOG, VEC>(out, gradient, saved, undefined, rows, n, guard);
   } else if (n <= 512 * 16) {
-    backward_rows<T, 512, 16, LOG, VEC>(out, gradient, saved, undefined, rows, n, stream);
+    backward_rows<T, 512, 16, LOG, VEC>(out, gradient, saved, undefined, rows, n, guard);
   } else if (n <= 1024 * 16) {
-    backward_rows<T, 1024, 16, LOG, VEC>(out, gradient, saved, undefined, rows, n, stream);
+    backward_rows<T, 1024, 16, LOG, VEC>(out, gradient, saved, undefined, rows, n, guard);
   } else if (n <= 1024 * 32) {
-    backward_rows<T, 1024, 32, LOG, VEC>(out, gradient, saved, undefined, rows, n, stream);
+    backward_rows<T, 1024, 32, LOG, VEC>(out, gradient, saved, undefined, rows, n, guard);
   } else {
     return false;
   }
@@ -505,8 +802,8 @@ void forward(void* output, int32_t* undefined, const void* input, uint64_t outer
   const T* in = static_cast<const T*>(input);
   if (inner == 1) {
     const bool vec = axis % Vec16<T>::width == 0 && aligned16(out) && aligned16(in);
-    const bool done = vec ? launch_forward_rows<T, LOG, true>(out, undefined, in, outer, axis, guard.stream)
-                          : launch_forward_rows<T, LOG, false>(out, undefined, in, outer, axis, guard.stream);
+    const bool done = vec ? launch_forward_rows<T, LOG, true>(out, undefined, in, outer, axis, guard)
+                          : launch_forward_rows<T, LOG, false>(out, undefined, in, outer, axis, guard);
     if (!done) {
       forward_loop_kernel<T, LOG><<<grid_for(outer), kLoopThreads, 0, guard.stream>>>(
           out, undefined, in, outer, axis);
@@ -527,8 +824,8 @@ void backward(void* output, const void* gradient, const void* saved, const int32
   if (inner == 1) {
     const bool vec = axis % Vec16<T>::width == 0 && aligned16(out) && aligned16(g) && aligned16(y);
     const bool done =
-        vec ? launch_backward_rows<T, LOG, true>(out, g, y, undefined, outer, axis, guard.stream)
-            : launch_backward_rows<T, LOG, false>(out, g, y, undefined, outer, axis, guard.stream);
+        vec ? launch_backward_rows<T, LOG, true>(out, g, y, undefined, outer, axis, guard)
+            : launch_backward_rows<T, LOG, false>(out, g, y, undefined, outer, axis, guard);
     if (!done) {
       backward_loop_kernel<T, LOG><<<grid_for(outer), kLoopThreads, 0, guard.stream>>>(
           out, g, y, undefined, outer, axis);
