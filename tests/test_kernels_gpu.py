@@ -157,11 +157,20 @@ def test_fill_from_scalar_divides_like_cpu(hip, dtype, divisor):
 
 # --------------------------------------------------------------- layouts
 
+def check_span(base, shape, strides, offset):
+    """Host-side guard: every element of the view lies inside `base`."""
+    assert offset >= 0, f"view starts before its base (offset {offset})"
+    last = offset + sum((d - 1) * s for d, s in zip(shape, strides) if d > 0)
+    assert all(s >= 0 for s in strides) and last < base.size, \
+        f"view reaches element {last} of a {base.size}-element base"
+
+
 def strided_copy(hip, base, view, dtype):
     """Runs spar_hip_launch_strided_copy on `view`, a numpy view of `base`."""
     item = base.itemsize
     offset = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // item
     strides = [s // item for s in view.strides]
+    check_span(base, view.shape, strides, offset)
     db = dev(hip, base)
     out = out_buf(hip, view.shape, dtype)
     hip.call("spar_hip_launch_strided_copy", out.ptr, db.ptr, view.ndim, hip.u64_array(view.shape),
@@ -203,6 +212,8 @@ def strided_binary(hip, left_base, left_view, right_base, right_view, op, dtype)
 
     ls, lo = geometry(left_base, lv)
     rs, ro = geometry(right_base, rv)
+    check_span(left_base, shape, ls, lo)
+    check_span(right_base, shape, rs, ro)
     dl, dr = dev(hip, left_base), dev(hip, right_base)
     out = out_buf(hip, shape, dtype)
     hip.call("spar_hip_launch_strided_binary", out.ptr, dl.ptr, hip.u64_array(ls), lo, dr.ptr,
@@ -243,6 +254,42 @@ def test_strided_binary_views(hip, dtype):
         assert_bitexact(got, want, name)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_transposed_views_vector_tiles(hip, dtype):
+    """Extents that are multiples of the vector width take the 16-byte tiled
+    transpose: partial tiles, batch axes, offsets, two transposed operands,
+    and a second operand read along q, broadcast along q, or gathered."""
+    base = inputs(40, 200 * 132, dtype).reshape(200, 132)
+    other = inputs(41, 132 * 200, dtype).reshape(132, 200)
+    twin = inputs(42, 200 * 132, dtype).reshape(200, 132)
+    mu = inputs(43, 132, dtype).reshape(132, 1)
+    wide = inputs(44, 132 * 600, dtype).reshape(132, 600)
+    cube = inputs(45, 5 * 64 * 36, dtype).reshape(5, 64, 36)
+    cube2 = inputs(46, 5 * 36 * 64, dtype).reshape(5, 36, 64)
+    binary_cases = [
+        ("T - contiguous", base, base.T, other, other),
+        ("T - T", base, base.T, twin, twin.T),
+        ("T - column", base, base.T, mu, mu),
+        ("T - gathered", base, base.T, wide, wide[:, ::3]),
+        ("contiguous - T", other, other, base, base.T),
+        ("offset T", base, base[4:196, 8:132].T, other, other[8:132, 4:196]),
+        ("unaligned offset T", base, base[1:197, 3:131].T, other, other[3:131, 1:197]),
+        ("batched T", cube, cube.transpose(0, 2, 1), cube2, cube2),
+        ("batch-outer T", cube, cube.transpose(2, 0, 1), cube, cube.transpose(2, 0, 1)),
+    ]
+    for name, lb, lv, rb, rv in binary_cases:
+        got, want = strided_binary(hip, lb, lv, rb, rv, "subtract", dtype)
+        assert_bitexact(got, want, name)
+    # Each view is passed with the array it was taken from (offsets are
+    # measured from that array's first element).
+    for name, owner, view in [("T", base, base.T), ("offset T", base, base[4:196, 8:132].T),
+                              ("batched T", cube, cube.transpose(0, 2, 1)),
+                              ("perm", cube, cube.transpose(2, 0, 1)),
+                              ("perm2", cube, cube.transpose(1, 2, 0))]:
+        assert_bitexact(strided_copy(hip, owner, view, dtype), ref.strided_copy(view),
+                        f"copy {name}")
+
+
 def test_strided_binary_odd_inner_extent(hip):
     # inner extent not a multiple of 4: row-vector path must not be taken
     x = inputs(20, 33 * 37, F32).reshape(33, 37)
@@ -257,6 +304,7 @@ def axis_reduce(hip, base, view, axes, op, dtype):
     item = np.dtype(dtype).itemsize
     offset = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // item
     strides = [s // item for s in view.strides]
+    check_span(base, view.shape, strides, offset)
     mask = 0
     for a in axes:
         mask |= 1 << a
