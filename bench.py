@@ -296,7 +296,7 @@ def main():
 
 # ----------------------------------------------------------------- suite
 
-def run_suite(hip, reps=10):
+def run_suite(hip, reps=20, warmup=3):
     """Times every op of the five benchmark configurations (one JSON line per
     op).  Before each timed launch, outside the timed region, a 512 MiB
     scratch buffer is read with ordinary cached loads (spar_hip_touch): that
@@ -310,11 +310,16 @@ def run_suite(hip, reps=10):
     flush_sink = hip.DeviceBuffer(8)
     start, stop = hip.Event(), hip.Event()
 
-    def measure(config, name, nbytes, launch, elements):
-        launch()
+    def measure(config, name, nbytes, launch, elements, prepare=None):
+        for _ in range(warmup):
+            if prepare is not None:
+                prepare()
+            launch()
         hip.synchronize()
         samples = []
         for _ in range(reps):
+            if prepare is not None:
+                prepare()
             hip.call("spar_hip_touch", flush.ptr, flush.nbytes, flush_sink.ptr, 0)
             start.record()
             launch()
@@ -339,16 +344,20 @@ def run_suite(hip, reps=10):
     # C1: contiguous elementwise on [4096, 4096]
     n = 4096 * 4096
     a, b, out = normal(n, 1), normal(n, 2), hip.DeviceBuffer(n * 4)
-    clipped = hip.DeviceBuffer(n * 4)
-    hip.call("spar_hip_launch_scalar", clipped.ptr, a.ptr, n, F, hip.ADD, 0.0, 0)
     for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
         measure("C1", name, 12 * n, lambda op=op: hip.call(
             "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0), n)
     measure("C1", "gelu(a)", 8 * n, lambda: hip.call(
         "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0), n)
+    # exp(clip(a, -10, 10)): the clip is the identity on this draw (checked here)
+    peak = hip.DeviceBuffer(8)
+    hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
+    for source in (a, out):  # max(a) and max(-a)
+        hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
+        assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
     measure("C1", "exp(a)", 8 * n, lambda: hip.call(
         "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0), n)
-    del a, b, out, clipped
+    del a, b, out
 
     # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
     R = 8192
@@ -388,26 +397,74 @@ def run_suite(hip, reps=10):
             rows, V, 1, F, log, 0), n)
     del logits, grad, probs, dx, undefined
 
-    # C5: LayerNorm-chain ops on a transposed view ([8192,4096] base viewed as
-    # [4096,8192]) and on a sliced [4096,8192] block of a [4608,9216] base.
+    # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
+    # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a
+    # [4608,9216] base, through the Tensor API: each op's events bracket its
+    # host-side dispatch and allocation as well as its kernels.  Then
+    # loss = sum(y * G) and loss.backward() into base, gamma and beta.
+    from spar_amd import spar
+
+    device = spar.Device.hip(0)
+    f32 = spar.DType.float32
     rows, cols = 4096, 8192
     n = rows * cols
-    base_t = normal(8192 * 4096, 7)
-    base_s = normal(4608 * 9216, 8)
-    mu = hip.DeviceBuffer(rows * 4)
-    out = hip.DeviceBuffer(n * 4)
-    offset = 256 * 9216 + 512
-    views = {"transposed": (base_t, [1, 4096], 0), "sliced": (base_s, [9216, 1], offset)}
-    for label, (base, strides, off) in views.items():
-        measure("C5", f"mean(x,1) {label}", 4 * n + 4 * rows, lambda base=base, strides=strides, off=off: hip.call(
-            "spar_hip_launch_axis_reduction", mu.ptr, base.ptr, 2, u([rows, cols]), u(strides), off,
-            2, F, hip.MEAN, 0), n)
-        measure("C5", f"x-mu {label}", 8 * n + 4 * rows, lambda base=base, strides=strides, off=off: hip.call(
-            "spar_hip_launch_strided_binary", out.ptr, base.ptr, u(strides), off, mu.ptr, u([1, 0]), 0,
-            2, u([rows, cols]), F, hip.SUBTRACT, 0), n)
-        measure("C5", f"contiguous() {label}", 8 * n, lambda base=base, strides=strides, off=off: hip.call(
-            "spar_hip_launch_strided_copy", out.ptr, base.ptr, 2, u([rows, cols]), u(strides), off, n, 4,
-            0), n)
+    T = 4 * n  # bytes of one full-tensor read or write
+    rng = spar.Random(7)
+    gamma = spar.random_uniform([cols], f32, rng, 0.5, 1.5, device)
+    beta = spar.random_uniform([cols], f32, rng, -0.1, 0.1, device)
+    G = spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device)
+    bases = {"transposed": spar.random_normal([8192, 4096], f32, rng, 0.0, 1.0, device),
+             "sliced": spar.random_normal([4608, 9216], f32, rng, 0.0, 1.0, device)}
+    for leaf in (gamma, beta, *bases.values()):
+        leaf.set_requires_grad(True)
+
+    def view_of(label):
+        base = bases[label]
+        return base.transpose(0, 1) if label == "transposed" else base.narrow(0, 256, rows).narrow(1, 512, cols)
+
+    def forward(x):
+        mu = spar.mean(x, [1], True)
+        xc = spar.subtract(x, mu)
+        var = spar.mean(spar.square(xc), [1], True)
+        xhat = spar.divide(xc, spar.sqrt(spar.add_scalar(var, 1e-5)))
+        y = spar.add(spar.multiply(xhat, gamma), beta)
+        return spar.sum(spar.multiply(y, G), None, False)
+
+    for label in bases:
+        x = view_of(label)
+        mu = spar.mean(x, [1], True)
+        measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows, lambda: spar.mean(x, [1], True), n)
+        measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows, lambda: spar.subtract(x, mu), n)
+        xc = spar.subtract(x, mu)
+        measure("C5", f"square(xc) {label}", 2 * T, lambda: spar.square(xc), n)
+        sq = spar.square(xc)
+        measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows, lambda: spar.mean(sq, [1], True), n)
+        var = spar.mean(sq, [1], True)
+        sd = spar.sqrt(spar.add_scalar(var, 1e-5))
+        measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows, lambda: spar.divide(xc, sd), n)
+        xhat = spar.divide(xc, sd)
+        measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols, lambda: spar.multiply(xhat, gamma), n)
+        yg = spar.multiply(xhat, gamma)
+        measure("C5", f"+beta {label}", 2 * T + 4 * cols, lambda: spar.add(yg, beta), n)
+        y = spar.add(yg, beta)
+        measure("C5", f"y*G {label}", 3 * T, lambda: spar.multiply(y, G), n)
+        yG = spar.multiply(y, G)
+        measure("C5", f"sum(y*G) {label}", T + 4, lambda: spar.sum(yG, None, False), n)
+        del mu, xc, sq, var, sd, xhat, yg, y, yG
+        # Whole forward, then backward.  Both are reported against the fused
+        # minimum: forward reads x and G once (the loss is a scalar);
+        # backward reads x and G and writes dx (gamma, beta grads are small).
+        measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T, lambda: forward(x), n)
+        losses = []
+
+        def prepare():
+            for leaf in (gamma, beta, bases[label]):
+                leaf.zero_grad()
+            losses[:] = [forward(view_of(label))]
+
+        measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
+                lambda: losses[0].backward(), n, prepare=prepare)
+        del losses
 
 
 if __name__ == "__main__":
