@@ -1,0 +1,272 @@
+"""Parity at the benchmark configurations' full sizes (C1-C5).
+
+Inputs come from the device generators with the benchmark's seeds and are
+copied back for the oracle, so both sides see the same bytes.  Where the
+oracle finishes in seconds at full size it checks every element; otherwise it
+checks sampled rows, and size-independent properties cover the whole output:
+probability rows sum to one, log-sum-exp of log-probabilities is zero,
+checksums of checksums agree, argmax points at the maximum, and gradients
+with a closed form (d beta = column sums of G) match it.
+"""
+import numpy as np
+import pytest
+
+from oracle import ops as ref
+from tests.helpers import assert_bitexact, assert_red, assert_ulp
+from tests.test_kernels_gpu import (log_softmax_tolerance_check, softmax_backward_bound,
+                                    softmax_tolerance_check)
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+def normal(hip, n, seed, std=1.0):
+    buffer = hip.DeviceBuffer(n * 4)
+    hip.call("spar_hip_random_normal", buffer.ptr, n, hip.FLOAT32, seed, 0.0, std, 0)
+    return buffer
+
+
+def uniform(hip, n, seed, low, high):
+    buffer = hip.DeviceBuffer(n * 4)
+    hip.call("spar_hip_random_uniform", buffer.ptr, n, hip.FLOAT32, seed, low, high, 0)
+    return buffer
+
+
+def host(buffer, shape, dtype=F32):
+    return buffer.to_numpy(dtype, shape)
+
+
+def norm2(a, axis=None, keepdims=False):
+    return np.sqrt(np.sum(np.square(a, dtype=np.float64), axis=axis, keepdims=keepdims))
+
+
+def sample_rows(count, total, seed):
+    rows = np.random.default_rng(seed).choice(total, size=count, replace=False)
+    return np.sort(np.concatenate([[0, total - 1], rows]))
+
+
+# ------------------------------------------------------------------ C1
+
+def test_c1_contiguous_elementwise(hip):
+    shape = (4096, 4096)
+    n = shape[0] * shape[1]
+    a, b, out = normal(hip, n, 1), normal(hip, n, 2), hip.DeviceBuffer(n * 4)
+    ha, hb = host(a, shape), host(b, shape)
+    for name, op in (("add", hip.ADD), ("multiply", hip.MULTIPLY)):
+        hip.call("spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, hip.FLOAT32, op, 0)
+        assert_bitexact(host(out, shape), ref.binary(ha, hb, name), f"C1 {name}")
+    assert np.abs(ha).max() <= 10.0  # exp(clip(a, -10, 10)) is exp(a) on this draw
+    for name, op in (("exp", hip.EXP), ("gelu", hip.GELU)):
+        hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, hip.FLOAT32, op, 0)
+        assert_ulp(host(out, shape), ref.unary(ha, name), 2, f"C1 {name}")
+
+
+# ------------------------------------------------------------------ C2
+
+def test_c2_broadcast_forward_and_backward(hip):
+    B, T, C = 32, 1024, 4096
+    n = B * T * C
+    u = hip.u64_array
+    x, G = normal(hip, n, 11), normal(hip, n, 14)
+    bias, scale = uniform(hip, C, 12, -0.1, 0.1), uniform(hip, B * C, 13, 0.5, 1.5)
+    hx, hG = host(x, (B, T, C)), host(G, (B, T, C))
+    hbias, hscale = host(bias, (C,)), host(scale, (B, 1, C))
+    y = hip.DeviceBuffer(n * 4)
+    shape, dense = u([B, T, C]), u([T * C, C, 1])
+
+    hip.call("spar_hip_launch_strided_binary", y.ptr, x.ptr, dense, 0, bias.ptr, u([0, 0, 1]), 0,
+             3, shape, hip.FLOAT32, hip.ADD, 0)
+    assert_bitexact(host(y, (B, T, C)), ref.binary(hx, hbias, "add"), "x + bias")
+    hip.call("spar_hip_launch_strided_binary", y.ptr, x.ptr, dense, 0, scale.ptr, u([C, 0, 1]), 0,
+             3, shape, hip.FLOAT32, hip.MULTIPLY, 0)
+    assert_bitexact(host(y, (B, T, C)), ref.binary(hx, hscale, "multiply"), "x * scale")
+    hip.call("spar_hip_launch_strided_binary", y.ptr, G.ptr, dense, 0, scale.ptr, u([C, 0, 1]), 0,
+             3, shape, hip.FLOAT32, hip.MULTIPLY, 0)
+    assert_bitexact(host(y, (B, T, C)), ref.binary(hG, hscale, "multiply"), "dx = G * scale")
+
+    # d bias = sum over (B, T) of G: every column against the oracle, and the
+    # checksum of checksums against the full sum of G
+    dbias = hip.DeviceBuffer(C * 4)
+    hip.call("spar_hip_launch_broadcast_reduce", dbias.ptr, G.ptr, 3, shape, 1, u([C]),
+             u([0] * 8), n, hip.FLOAT32, 0)
+    got = host(dbias, (C,))
+    assert_red(got, ref.reduce_gradient(hG, (C,)), B * T, norm2(hG, axis=(0, 1)), "d bias")
+    assert_red(np.sum(got, dtype=np.float64), ref.full_reduce(hG, "sum"), n, norm2(hG),
+               "sum of d bias vs sum of G")
+
+    # d scale = sum over T of G * x (fused), against multiply-then-reduce
+    dscale = hip.DeviceBuffer(B * C * 4)
+    hip.call("spar_hip_launch_multiply_reduce", dscale.ptr, G.ptr, x.ptr, 3, shape, 3,
+             u([B, 1, C]), n, hip.FLOAT32, 0)
+    product = ref.binary(hG, hx, "multiply")
+    assert_red(host(dscale, (B, 1, C)), ref.reduce_gradient(product, (B, 1, C)), T,
+               norm2(product, axis=1, keepdims=True), "d scale")
+
+
+# ------------------------------------------------------------------ C3
+
+def test_c3_axis_and_full_reductions(hip):
+    R = 8192
+    n = R * R
+    x = normal(hip, n, 3)
+    hx = host(x, (R, R))
+    u = hip.u64_array
+    out = hip.DeviceBuffer(R * 8)
+    sums = {}
+    for axis in (1, 0):
+        kept = 1 - axis
+
+        def run(code, dtype=F32):
+            hip.call("spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
+                     1 << axis, hip.FLOAT32, code, 0)
+            return host(out, (R,), dtype)
+
+        norm = norm2(hx, axis=axis)
+        want_sum = ref.axis_sum(hx, [axis])
+        sums[axis] = run(hip.SUM)
+        assert_red(sums[axis], want_sum, R, norm, f"sum axis {axis}")
+        assert_red(run(hip.MEAN), ref.scalar(want_sum, "divide", float(R)), R, norm / R,
+                   f"mean axis {axis}")
+        want_max, want_arg = ref.axis_max(hx, [axis])
+        got_max, got_arg = run(hip.MAX), run(hip.ARGMAX, np.int64)
+        assert_bitexact(got_max, want_max, f"max axis {axis}")
+        assert_bitexact(got_arg, want_arg, f"argmax axis {axis}")
+        picked = hx[got_arg, np.arange(R)] if axis == 0 else hx[np.arange(R), got_arg]
+        assert np.array_equal(picked, got_max), f"x[argmax] == max, axis {axis} (kept {kept})"
+    total = ref.full_reduce(hx, "sum")
+    for axis in (0, 1):
+        assert_red(np.sum(sums[axis], dtype=np.float64), total, n, norm2(hx),
+                   f"checksum of axis-{axis} sums")
+
+    n = 1 << 28
+    v = uniform(hip, n, 4, -1.0, 1.0)
+    hv = host(v, (n,))
+    scalar_out = hip.DeviceBuffer(8)
+    norm = norm2(hv)
+    for kind, code in (("sum", hip.SUM), ("mean", hip.MEAN)):
+        hip.call("spar_hip_launch_reduction", scalar_out.ptr, v.ptr, n, hip.FLOAT32, code, 0)
+        assert_red(host(scalar_out, (1,))[0], ref.full_reduce(hv, kind), n,
+                   norm / (n if kind == "mean" else 1), f"full {kind} 2^28")
+    hip.call("spar_hip_launch_reduction", scalar_out.ptr, v.ptr, n, hip.FLOAT32, hip.MAX, 0)
+    assert host(scalar_out, (1,))[0] == ref.full_reduce(hv, "max"), "full max 2^28"
+
+
+# ------------------------------------------------------------------ C4
+
+@pytest.mark.parametrize("log", [False, True])
+def test_c4_softmax_rows(hip, log):
+    rows, V = 8192, 32768
+    n = rows * V
+    logits, G = normal(hip, n, 5, np.sqrt(2.0)), normal(hip, n, 6)
+    out, dx = hip.DeviceBuffer(n * 4), hip.DeviceBuffer(n * 4)
+    undefined = hip.DeviceBuffer(rows * 4)
+    hip.call("spar_hip_launch_probability_forward", out.ptr, undefined.ptr, logits.ptr, rows, V, 1,
+             hip.FLOAT32, int(log), 0)
+    hip.call("spar_hip_launch_probability_backward", dx.ptr, G.ptr, out.ptr, undefined.ptr, rows,
+             V, 1, hip.FLOAT32, int(log), 0)
+    hl, hG = host(logits, (rows, V)), host(G, (rows, V))
+    hy, hdx = host(out, (rows, V)), host(dx, (rows, V))
+    assert not host(undefined, (rows,), np.int32).any(), "no C4 row is undefined"
+
+    # every row: probabilities sum to one / log-sum-exp is zero
+    eps = np.finfo(F32).eps
+    if log:
+        lse = np.log(np.sum(np.exp(hy.astype(np.float64)), axis=1))
+        assert np.all(np.abs(lse) <= 1e-6 * np.sqrt(V) + 8 * eps), "log-sum-exp of rows"
+    else:
+        assert np.all(hy >= 0)
+        row_sums = np.sum(hy, axis=1, dtype=np.float64)
+        assert np.all(np.abs(row_sums - 1.0) <= 1e-6 * np.sqrt(V) + 8 * eps), "rows sum to one"
+
+    # sampled rows against the oracle, forward and backward
+    picked = sample_rows(62, rows, 50 + int(log))
+    sub, gsub = np.ascontiguousarray(hl[picked]), np.ascontiguousarray(hG[picked])
+    if log:
+        want, flags = ref.log_softmax(sub, 1)
+        log_softmax_tolerance_check(hy[picked], want, V, F32, "C4 log_softmax rows")
+        want_dx = ref.log_softmax_backward(gsub, hy[picked], flags, 1)
+    else:
+        want, flags = ref.softmax_axis(sub, 1)
+        softmax_tolerance_check(hy[picked], want, V, F32, "C4 softmax rows")
+        want_dx = ref.softmax_axis_backward(gsub, hy[picked], flags, 1)
+    bound = softmax_backward_bound(gsub, hy[picked], V, F32, log)
+    err = np.abs(hdx[picked].astype(np.float64) - want_dx)
+    assert np.all(err <= bound), f"C4 backward rows: max excess {np.max(err - bound)}"
+
+
+# ------------------------------------------------------------------ C5
+
+@pytest.mark.parametrize("view", ["transposed", "sliced"])
+def test_c5_layernorm_chain(hip, view):
+    """The LayerNorm chain of the benchmark through the Tensor API, forward
+    and backward, on a [4096, 8192] view.  Rows are independent in the
+    forward and in d x, so sampled rows are checked against the oracle run on
+    those rows; d beta has the closed form sum over rows of G; d gamma is the
+    sum over rows of G * xhat (checked against float64)."""
+    from spar_amd import spar
+
+    import oracle.reference as R
+
+    rows, cols = 4096, 8192
+    device = spar.Device.hip(0)
+    rng = np.random.default_rng(60 if view == "transposed" else 61)
+    if view == "transposed":
+        base = rng.standard_normal((cols, rows)).astype(F32)
+    else:
+        base = rng.standard_normal((4608, 9216)).astype(F32)
+    gamma = rng.uniform(0.5, 1.5, cols).astype(F32)
+    beta = rng.uniform(-0.1, 0.1, cols).astype(F32)
+    G = rng.standard_normal((rows, cols)).astype(F32)
+
+    def view_of(lib_tensor, is_ref):
+        if view == "transposed":
+            return lib_tensor.transpose(0, 1)
+        return lib_tensor.narrow(0, 256, rows).narrow(1, 512, cols)
+
+    def chain(lib, x, g, b, w):
+        mu = lib.mean(x, [1], True)
+        xc = lib.subtract(x, mu)
+        var = lib.mean(lib.square(xc), [1], True)
+        xhat = lib.divide(xc, lib.sqrt(lib.add_scalar(var, 1e-5)))
+        y = lib.add(lib.multiply(xhat, g), b)
+        return xhat, y, lib.sum(lib.multiply(y, w), None, False)
+
+    tensors = []
+    for array in (base, gamma, beta, G):
+        t = spar.Tensor.from_numpy(array).to(device)
+        t.set_requires_grad(True)
+        tensors.append(t)
+    xhat, y, loss = chain(spar, view_of(tensors[0], False), tensors[1], tensors[2], tensors[3])
+    loss.backward()
+    cpu = spar.Device.cpu()
+    got_xhat, got_y = xhat.to(cpu).numpy(), y.to(cpu).numpy()
+    got_dbase = tensors[0].grad().to(cpu).numpy()
+    got_dgamma, got_dbeta = tensors[1].grad().to(cpu).numpy(), tensors[2].grad().to(cpu).numpy()
+    got_dx = got_dbase.T if view == "transposed" else got_dbase[256:256 + rows, 512:512 + cols]
+    if view == "sliced":
+        outside = got_dbase.copy()
+        outside[256:256 + rows, 512:512 + cols] = 0
+        assert not outside.any(), "gradient outside the slice is zero"
+
+    # sampled rows through the oracle's restatement of the same chain
+    picked = sample_rows(30, rows, 62)
+    x_host = base.T if view == "transposed" else base[256:256 + rows, 512:512 + cols]
+    sub = [R.RTensor.of(np.ascontiguousarray(x_host[picked]), requires_grad=True),
+           R.RTensor.of(gamma, requires_grad=True), R.RTensor.of(beta, requires_grad=True),
+           R.RTensor.of(np.ascontiguousarray(G[picked]))]
+    want_xhat, want_y, want_loss = chain(R, sub[0], sub[1], sub[2], sub[3])
+    want_loss.backward()
+    tol = 1e-6 * np.sqrt(cols) * 8
+    for name, got, want in (("xhat", got_xhat[picked], want_xhat.numpy()),
+                            ("y", got_y[picked], want_y.numpy()),
+                            ("dx", got_dx[picked], sub[0].grad().numpy())):
+        scale = np.max(np.abs(want), axis=1, keepdims=True) + 1e-30
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= tol * scale), f"C5 {view} {name}: max rel {np.max(err / scale)}"
+
+    # d beta = sum over rows of G (closed form); d gamma = sum over rows of G * xhat
+    assert_red(got_dbeta, ref.axis_sum(G, [0]), rows, norm2(G, axis=0), "d beta")
+    want_dgamma = np.sum(G.astype(np.float64) * got_xhat.astype(np.float64), axis=0)
+    norm = norm2(G.astype(np.float64) * got_xhat, axis=0)
+    assert_red(got_dgamma, want_dgamma, rows, norm * 4, "d gamma")
