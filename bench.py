@@ -464,6 +464,20 @@ def run_suite(hip, reps=20, warmup=3):
 
         measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
                 lambda: losses[0].backward(), n, prepare=prepare)
+
+        # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
+        # first made contiguous, inside the timed op.
+        measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
+                lambda: spar.layer_norm(x, gamma, beta, 1e-5), n)
+
+        def prepare_fused():
+            for leaf in (gamma, beta, bases[label]):
+                leaf.zero_grad()
+            y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
+            losses[:] = [spar.sum(spar.multiply(y, G), None, False)]
+
+        measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
+                lambda: losses[0].backward(), n, prepare=prepare_fused)
         del losses
 
 

@@ -307,6 +307,37 @@ struct SparHipStatus spar_hip_launch_probability_backward(
     void* output, const void* gradient, const void* saved_output, const int32_t* undefined_slices,
     uint64_t outer, uint64_t axis_extent, uint64_t inner, int dtype, int logarithmic, int device);
 
+/* ------------------------------------------------ fused row normalisation */
+
+/* Largest row length the fused normalisation kernels accept for `dtype`
+ * (16384 float32, 8192 float64; 0 for other dtypes).  Longer rows take the
+ * composed ops.  No reference counterpart. */
+uint64_t spar_hip_norm_max_extent(int dtype);
+
+/* LayerNorm (center = 1) or RMSNorm (center = 0) over the last axis of a
+ * contiguous [rows, extent] input, fused:
+ *   LayerNorm: mu = sum(x)/n, xc = x - mu, d = sqrt(sum(xc*xc)/n + eps),
+ *              y = (xc / d) * weight + bias
+ *   RMSNorm:   d = sqrt(sum(x*x)/n + eps), y = (x / d) * weight
+ * Writes y [rows, extent], d [rows] and, for LayerNorm, mu [rows] (`mean`
+ * and `bias` are ignored and may be NULL for RMSNorm).  Replaces the composed
+ * forward of RMSNorm, multiply(divide(x, sqrt(add_scalar(mean(square(x), -1,
+ * true), eps))), weight) (src/nn/rmsnorm.cpp:50-52), and the same chain with
+ * centring and a bias; the reference has no fused kernel for it. */
+struct SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void* denominator,
+                                                  const void* input, const void* weight,
+                                                  const void* bias, uint64_t rows, uint64_t extent,
+                                                  double epsilon, int center, int dtype,
+                                                  int device);
+
+/* Backward of the above from the saved mu and d: writes dx [rows, extent],
+ * d weight [extent] and, for LayerNorm, d bias [extent] (sums over rows in a
+ * fixed order).  Replaces the autograd backward of the composed chain. */
+struct SparHipStatus spar_hip_launch_norm_backward(
+    void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
+    const void* input, const void* weight, const void* mean, const void* denominator,
+    uint64_t rows, uint64_t extent, int center, int dtype, int device);
+
 /* ------------------------------------------------------ random generation */
 
 /* Fills `count` contiguous elements with Spar's SplitMix64 stream for `seed`

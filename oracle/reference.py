@@ -586,3 +586,23 @@ def log_softmax(x: RTensor, axis=None) -> RTensor:
         _record(out, [x], lambda g: [RTensor.of(
             C.log_softmax_backward(g.numpy(), saved.numpy(), undefined, axis))])
     return out
+
+
+# ------------------------------------------------------- normalisation
+
+def rms_norm(x: RTensor, weight: RTensor, epsilon: float = 1.0e-5) -> RTensor:
+    """RMSNorm::forward (nn/rmsnorm.cpp:41-53): the reference composes it from
+    ops, so autograd runs through each of them."""
+    axis = len(x.shape) - 1
+    mean_square = mean(square(x), [axis], True)
+    denominator = sqrt(add_scalar(mean_square, epsilon))
+    return multiply(divide(x, denominator), weight)
+
+
+def layer_norm(x: RTensor, weight: RTensor, bias: RTensor, epsilon: float = 1.0e-5) -> RTensor:
+    """Build-defined LayerNorm as the same composition with centring and a
+    bias: (x - mean) / sqrt(mean((x - mean)^2) + eps) * weight + bias."""
+    axis = len(x.shape) - 1
+    centred = subtract(x, mean(x, [axis], True))
+    denominator = sqrt(add_scalar(mean(square(centred), [axis], True), epsilon))
+    return add(multiply(divide(centred, denominator), weight), bias)

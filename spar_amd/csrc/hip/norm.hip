@@ -1,0 +1,575 @@
+// Fused row normalisation over the last axis: LayerNorm
+//   mu = sum(x) / n, xc = x - mu, var = sum(xc * xc) / n, d = sqrt(var + eps),
+//   y = (xc / d) * weight + bias
+// and RMSNorm (the same without centring or bias)
+//   d = sqrt(sum(x * x) / n + eps), y = (x / d) * weight.
+//
+// Spar composes these from separate ops: RMSNorm::forward is
+// multiply(divide(x, sqrt(add_scalar(mean(square(x), -1, true), eps))), w)
+// (src/nn/rmsnorm.cpp:50-52), about six tensor passes forward and a dozen
+// backward through autograd.  Here the forward reads x once and writes y once;
+// the backward reads x and dy once and writes dx once, and the weight / bias
+// gradients come from per-workgroup column partials combined in a fixed order.
+//
+// Each element is computed with the composed path's float operations (mean as
+// a sum divided by (T)n, eps rounded to T before the add, IEEE sqrt); only the
+// order of the row sums differs (a tree instead of a sequential scan).
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace spar_hip {
+namespace {
+
+constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
+
+template <typename T, int THREADS>
+__device__ __forceinline__ T norm_block_sum(T value) {
+  constexpr int kWavesPerBlock = THREADS / kWave;
+  __shared__ T lds[kWavesPerBlock];
+  value = wave_sum(value);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = value;
+  __syncthreads();
+  T total = lds[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) total += lds[w];
+  return total;
+}
+
+// Two sums at once (one exchange instead of two).
+template <typename T, int THREADS>
+__device__ __forceinline__ void norm_block_sum2(T& a, T& b) {
+  constexpr int kWavesPerBlock = THREADS / kWave;
+  __shared__ T lds[2][kWavesPerBlock];
+  a = wave_sum(a);
+  b = wave_sum(b);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) {
+    lds[0][threadIdx.x / kWave] = a;
+    lds[1][threadIdx.x / kWave] = b;
+  }
+  __syncthreads();
+  a = lds[0][0];
+  b = lds[1][0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) {
+    a += lds[0][w];
+    b += lds[1][w];
+  }
+}
+
+// Element j of a lane's register array sits at column col(j): 16-byte groups
+// interleaved across lanes (VEC) or single elements interleaved (scalar).
+template <typename T, int THREADS, bool VEC>
+__device__ __forceinline__ uint64_t norm_column(int j) {
+  if constexpr (VEC) {
+    constexpr int W = Vec16<T>::width;
+    return (static_cast<uint64_t>(j / W) * THREADS + threadIdx.x) * W + (j % W);
+  } else {
+    return static_cast<uint64_t>(j) * THREADS + threadIdx.x;
+  }
+}
+
+template <typename T, int THREADS, int E, bool VEC, bool FULL>
+__device__ __forceinline__ void norm_load(T (&x)[E], const T* row, uint64_t n) {
+  if constexpr (VEC) {
+    using V = typename Vec16<T>::type;
+    constexpr int W = Vec16<T>::width;
+#pragma unroll
+    for (int v = 0; v < E / W; ++v) {
+      const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
+      if (FULL || col < n) {
+        const V value = stream_load(reinterpret_cast<const V*>(row + col));
+#pragma unroll
+        for (int k = 0; k < W; ++k) x[v * W + k] = vec_get<T>(value, k);
+      } else {
+#pragma unroll
+        for (int k = 0; k < W; ++k) x[v * W + k] = T(0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint64_t col = norm_column<T, THREADS, false>(j);
+      x[j] = (FULL || col < n) ? row[col] : T(0);
+    }
+  }
+}
+
+// Cached loads of a per-column parameter (weight or bias), re-read per row.
+template <typename T, int THREADS, int E, bool VEC, bool FULL>
+__device__ __forceinline__ void norm_load_parameter(T (&p)[E], const T* parameter, uint64_t n) {
+  if constexpr (VEC) {
+    using V = typename Vec16<T>::type;
+    constexpr int W = Vec16<T>::width;
+#pragma unroll
+    for (int v = 0; v < E / W; ++v) {
+      const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
+      if (FULL || col < n) {
+        const V value = *reinterpret_cast<const V*>(parameter + col);
+#pragma unroll
+        for (int k = 0; k < W; ++k) p[v * W + k] = vec_get<T>(value, k);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint64_t col = norm_column<T, THREADS, false>(j);
+      if (FULL || col < n) p[j] = parameter[col];
+    }
+  }
+}
+
+template <typename T, int THREADS, int E, bool VEC, bool FULL>
+__device__ __forceinline__ void norm_store(T* row, const T (&y)[E], uint64_t n, bool stream_out) {
+  if constexpr (VEC) {
+    using V = typename Vec16<T>::type;
+    constexpr int W = Vec16<T>::width;
+#pragma unroll
+    for (int v = 0; v < E / W; ++v) {
+      const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
+      if (FULL || col < n) {
+        V value;
+#pragma unroll
+        for (int k = 0; k < W; ++k) vec_set<T>(value, k, y[v * W + k]);
+        if (stream_out) {
+          stream_store(reinterpret_cast<V*>(row + col), value);
+        } else {
+          *reinterpret_cast<V*>(row + col) = value;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint64_t col = norm_column<T, THREADS, false>(j);
+      if (FULL || col < n) row[col] = y[j];
+    }
+  }
+}
+
+// q / d for many q and one d: q0 = q * (1 / d) corrected by one residual
+// step through a fused multiply-add (Markstein), within one ulp of the IEEE
+// quotient and equal to it in almost all cases.
+template <typename T>
+struct Divisor {
+  T d;
+  T r;
+  __device__ __forceinline__ explicit Divisor(T value) : d(value), r(T(1) / value) {}
+  __device__ __forceinline__ T operator()(T q) const {
+    const T q0 = q * r;
+    return __builtin_fma(__builtin_fma(-q0, d, q), r, q0);
+  }
+};
+
+template <>
+__device__ __forceinline__ float Divisor<float>::operator()(float q) const {
+  const float q0 = q * r;
+  return __builtin_fmaf(__builtin_fmaf(-q0, d, q), r, q0);
+}
+
+template <typename T> __device__ __forceinline__ T norm_sqrt(T x);
+template <> __device__ __forceinline__ float norm_sqrt<float>(float x) { return sqrtf(x); }
+template <> __device__ __forceinline__ double norm_sqrt<double>(double x) { return sqrt(x); }
+
+// Forward: one row per workgroup iteration, the row held in registers.
+template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL>
+__global__ void __launch_bounds__(THREADS)
+    norm_forward_kernel(T* out, T* mean_out, T* denominator_out, const T* in, const T* weight,
+                        const T* bias, uint64_t rows, uint64_t n, T eps, bool stream_out) {
+  const T count = static_cast<T>(n);
+  for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    T x[E];
+    norm_load<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
+    T mu = T(0);
+    if constexpr (CENTER) {
+      T local = T(0);
+#pragma unroll
+      for (int j = 0; j < E; ++j) local += x[j];  // out-of-range entries are zero
+      mu = norm_block_sum<T, THREADS>(local) / count;
+#pragma unroll
+      for (int j = 0; j < E; ++j) {
+        const uint64_t col = norm_column<T, THREADS, VEC>(j);
+        x[j] = (FULL || col < n) ? x[j] - mu : T(0);
+      }
+    }
+    T local = T(0);
+#pragma unroll
+    for (int j = 0; j < E; ++j) local += x[j] * x[j];
+    const T variance = norm_block_sum<T, THREADS>(local) / count;
+    const T d = norm_sqrt<T>(variance + eps);
+    if (threadIdx.x == 0) {
+      if constexpr (CENTER) mean_out[r] = mu;
+      denominator_out[r] = d;
+    }
+    const Divisor<T> divide(d);
+    T w[E];
+    norm_load_parameter<T, THREADS, E, VEC, FULL>(w, weight, n);
+#pragma unroll
+    for (int j = 0; j < E; ++j) x[j] = divide(x[j]) * w[j];
+    if constexpr (CENTER) {
+      norm_load_parameter<T, THREADS, E, VEC, FULL>(w, bias, n);
+#pragma unroll
+      for (int j = 0; j < E; ++j) x[j] = x[j] + w[j];
+    }
+    norm_store<T, THREADS, E, VEC, FULL>(out + r * n, x, n, stream_out);
+  }
+}
+
+// Backward: with xhat = (x - mu) / d (x / d for RMSNorm) and g = dy * w,
+//   dx = (g - mean(g) - xhat * mean(g * xhat)) / d     (LayerNorm)
+//   dx = (g - xhat * mean(g * xhat)) / d               (RMSNorm)
+//   dw = sum over rows of dy * xhat, db = sum over rows of dy.
+// Each workgroup walks rows blockIdx.x, + gridDim.x, ... and keeps its dw and
+// db partials for its columns in registers; they are written once, as row
+// blockIdx.x of the [gridDim.x, n] partial arrays.
+template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL>
+__global__ void __launch_bounds__(THREADS)
+    norm_backward_kernel(T* dx, T* partial_weight, T* partial_bias, const T* dy, const T* in,
+                         const T* weight, const T* mean, const T* denominator, uint64_t rows,
+                         uint64_t n, bool stream_out) {
+  const T count = static_cast<T>(n);
+  T acc_w[E];
+  T acc_b[CENTER ? E : 1];
+#pragma unroll
+  for (int j = 0; j < E; ++j) acc_w[j] = T(0);
+  if constexpr (CENTER) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) acc_b[j] = T(0);
+  }
+  for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    T x[E];
+    T g[E];
+    norm_load<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
+    norm_load<T, THREADS, E, VEC, FULL>(g, dy + r * n, n);
+    const T mu = CENTER ? mean[r] : T(0);
+    const Divisor<T> divide(denominator[r]);
+    T sum_g = T(0);
+    T sum_gx = T(0);
+    // The weight is streamed one 16-byte group at a time (cached loads) so
+    // that a whole row of it never occupies registers.
+    constexpr int G = VEC ? Vec16<T>::width : 1;
+#pragma unroll
+    for (int v = 0; v < E / G; ++v) {
+      T w[G];
+      const uint64_t col0 = norm_column<T, THREADS, VEC>(v * G);
+      const bool in_row = FULL || col0 < n;
+      if constexpr (VEC) {
+        using V = typename Vec16<T>::type;
+        const V wv = in_row ? *reinterpret_cast<const V*>(weight + col0) : V{};
+#pragma unroll
+        for (int k = 0; k < G; ++k) w[k] = vec_get<T>(wv, k);
+      } else {
+        w[0] = in_row ? weight[col0] : T(0);
+      }
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const int j = v * G + k;
+        x[j] = in_row ? divide(x[j] - mu) : T(0);  // xhat
+        acc_w[j] += g[j] * x[j];
+        if constexpr (CENTER) acc_b[j] += g[j];
+        g[j] = g[j] * w[k];                         // dxhat (zero outside the row)
+        sum_g += g[j];
+        sum_gx += g[j] * x[j];
+      }
+    }
+    if constexpr (CENTER) {
+      norm_block_sum2<T, THREADS>(sum_g, sum_gx);
+    } else {
+      sum_gx = norm_block_sum<T, THREADS>(sum_gx);
+    }
+    const T mean_g = CENTER ? sum_g / count : T(0);
+    const T mean_gx = sum_gx / count;
+#pragma unroll
+    for (int j = 0; j < E; ++j) g[j] = divide(g[j] - mean_g - x[j] * mean_gx);
+    norm_store<T, THREADS, E, VEC, FULL>(dx + r * n, g, n, stream_out);
+  }
+  norm_store<T, THREADS, E, VEC, FULL>(partial_weight + blockIdx.x * n, acc_w, n, false);
+  if constexpr (CENTER) {
+    norm_store<T, THREADS, E, VEC, FULL>(partial_bias + blockIdx.x * n, acc_b, n, false);
+  }
+}
+
+// Column sums of [parts, n] partials in a fixed order: a 1024-lane block owns
+// 64 columns; wave w sums parts w, w + 16, ... in order and the 16 wave sums
+// are added in wave order, so the result does not depend on scheduling.
+constexpr int kCombineThreads = 1024;
+constexpr int kCombineWaves = kCombineThreads / kWave;
+
+template <typename T>
+__global__ void __launch_bounds__(kCombineThreads)
+    norm_combine_kernel(T* out, const T* partial, uint64_t parts, uint64_t n) {
+  __shared__ T lds[kCombineWaves][kWave];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const uint64_t groups = (n + kWave - 1) / kWave;
+  for (uint64_t group = blockIdx.x; group < groups; group += gridDim.x) {
+    const uint64_t col = group * kWave + lane;
+    T total = T(0);
+    if (col < n) {
+      for (uint64_t p = wave; p < parts; p += kCombineWaves) total += partial[p * n + col];
+    }
+    __syncthreads();
+    lds[wave][lane] = total;
+    __syncthreads();
+    if (wave == 0 && col < n) {
+      T sum = lds[0][lane];
+#pragma unroll
+      for (int w = 1; w < kCombineWaves; ++w) sum += lds[w][lane];
+      out[col] = sum;
+    }
+  }
+}
+
+uint32_t grid_for(uint64_t blocks) {
+  if (blocks == 0) blocks = 1;
+  return static_cast<uint32_t>(blocks > kMaxGrid ? kMaxGrid : blocks);
+}
+
+template <typename K>
+uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      per_cu < 1) {
+    per_cu = 1;
+  }
+  return static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(guard.multiprocessors);
+}
+
+struct NormArgs {
+  void* out;
+  void* mean;
+  void* denominator;
+  const void* input;
+  const void* weight;
+  const void* bias;
+  uint64_t rows;
+  uint64_t n;
+  double eps;
+  bool center;
+};
+
+template <typename T, int THREADS, int E, bool CENTER, bool VEC>
+void forward_as(const NormArgs& a, const DeviceGuard& guard) {
+  const bool full = a.n == static_cast<uint64_t>(THREADS) * E;
+  const bool stream_out = stream_output(a.rows * a.n * sizeof(T));
+  const T eps = static_cast<T>(a.eps);
+  auto launch = [&](auto kernel) {
+    kernel<<<grid_for(a.rows), THREADS, 0, guard.stream>>>(
+        static_cast<T*>(a.out), static_cast<T*>(a.mean), static_cast<T*>(a.denominator),
+        static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
+        static_cast<const T*>(a.bias), a.rows, a.n, eps, stream_out);
+  };
+  if (full) {
+    launch(norm_forward_kernel<T, THREADS, E, CENTER, VEC, true>);
+  } else {
+    launch(norm_forward_kernel<T, THREADS, E, CENTER, VEC, false>);
+  }
+}
+
+struct NormBackwardArgs {
+  void* dx;
+  void* dweight;
+  void* dbias;
+  const void* dy;
+  const void* input;
+  const void* weight;
+  const void* mean;
+  const void* denominator;
+  uint64_t rows;
+  uint64_t n;
+  bool center;
+};
+
+template <typename T, int THREADS, int E, bool CENTER, bool VEC>
+hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard& guard) {
+  const bool full = a.n == static_cast<uint64_t>(THREADS) * E;
+  const bool stream_out = stream_output(a.rows * a.n * sizeof(T));
+  auto kernel = full ? norm_backward_kernel<T, THREADS, E, CENTER, VEC, true>
+                     : norm_backward_kernel<T, THREADS, E, CENTER, VEC, false>;
+  // Two workgroups per CU (bounded by occupancy): enough rows in flight per
+  // CU while keeping the [grid, n] partials small.
+  uint64_t grid = resident_blocks(kernel, THREADS, guard);
+  const uint64_t wanted = static_cast<uint64_t>(guard.multiprocessors) * 2;
+  if (grid > wanted) grid = wanted;
+  if (grid > a.rows) grid = a.rows;
+  const uint64_t parts = (CENTER ? 2 : 1) * grid * a.n;
+  void* scratch = nullptr;
+  hipError_t error = scratch_allocate(&scratch, parts * sizeof(T), device);
+  if (error != hipSuccess) return error;
+  T* partial_weight = static_cast<T*>(scratch);
+  T* partial_bias = CENTER ? partial_weight + grid * a.n : nullptr;
+  kernel<<<static_cast<uint32_t>(grid), THREADS, 0, guard.stream>>>(
+      static_cast<T*>(a.dx), partial_weight, partial_bias, static_cast<const T*>(a.dy),
+      static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
+      static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n,
+      stream_out);
+  const uint32_t combine_grid = grid_for((a.n + kWave - 1) / kWave);
+  norm_combine_kernel<T><<<combine_grid, kCombineThreads, 0, guard.stream>>>(
+      static_cast<T*>(a.dweight), partial_weight, grid, a.n);
+  if constexpr (CENTER) {
+    norm_combine_kernel<T><<<combine_grid, kCombineThreads, 0, guard.stream>>>(
+        static_cast<T*>(a.dbias), partial_bias, grid, a.n);
+  }
+  error = hipGetLastError();
+  scratch_release(scratch, device);  // stream-ordered reuse
+  return error;
+}
+
+// Register-row configurations (threads, elements per lane) by row length,
+// chosen so that the forward (x and one parameter row) and the backward (x,
+// g, a parameter row and two accumulators) stay within the VGPR budget of
+// their workgroup size.  Rows up to kMaxExtent (float32) / kMaxExtent / 2
+// (float64) elements.
+constexpr uint64_t kMaxExtent = 16384;
+
+template <typename T, bool CENTER, bool VEC>
+bool dispatch_forward(const NormArgs& a, const DeviceGuard& guard) {
+  const uint64_t n = a.n;
+  if (n <= 256 * 4) {
+    forward_as<T, 256, 4, CENTER, VEC>(a, guard);
+    return true;
+  }
+  if (n <= 256 * 16) {
+    forward_as<T, 256, 16, CENTER, VEC>(a, guard);
+    return true;
+  }
+  if constexpr (sizeof(T) == 4) {
+    if (n <= 256 * 32) {
+      forward_as<T, 256, 32, CENTER, VEC>(a, guard);
+      return true;
+    }
+    if (n <= 1024 * 16) {
+      forward_as<T, 1024, 16, CENTER, VEC>(a, guard);
+      return true;
+    }
+  } else {
+    if (n <= 512 * 16) {
+      forward_as<T, 512, 16, CENTER, VEC>(a, guard);
+      return true;
+    }
+  }
+  return false;
+}
+
+template <typename T, bool CENTER, bool VEC>
+hipError_t dispatch_backward(const NormBackwardArgs& a, int device, const DeviceGuard& guard,
+                             bool& handled) {
+  const uint64_t n = a.n;
+  handled = true;
+  if (n <= 256 * 4) return backward_as<T, 256, 4, CENTER, VEC>(a, device, guard);
+  if (n <= 256 * 16) return backward_as<T, 256, 16, CENTER, VEC>(a, device, guard);
+  if (n <= 512 * 16) return backward_as<T, 512, 16, CENTER, VEC>(a, device, guard);
+  if constexpr (sizeof(T) == 4) {
+    // 512 lanes (two waves per SIMD, 256 VGPRs each) rather than 1024 (128)
+    if (n <= 512 * 32) return backward_as<T, 512, 32, CENTER, VEC>(a, device, guard);
+  }
+  handled = false;
+  return hipSuccess;
+}
+
+bool aligned_rows(const void* p, uint64_t n, int width) {
+  return p == nullptr || (aligned16(p) && n % static_cast<uint64_t>(width) == 0);
+}
+
+}  // namespace
+}  // namespace spar_hip
+
+using namespace spar_hip;
+
+extern "C" uint64_t spar_hip_norm_max_extent(int dtype) {
+  return dtype == SPAR_HIP_FLOAT32 ? kMaxExtent : dtype == SPAR_HIP_FLOAT64 ? kMaxExtent / 2 : 0;
+}
+
+extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void* denominator,
+                                                      const void* input, const void* weight,
+                                                      const void* bias, uint64_t rows,
+                                                      uint64_t extent, double epsilon, int center,
+                                                      int dtype, int device) {
+  if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
+      extent > spar_hip_norm_max_extent(dtype) || !(epsilon >= 0.0) ||
+      (rows != 0 && (output == nullptr || denominator == nullptr || input == nullptr ||
+                     weight == nullptr || (center && (mean == nullptr || bias == nullptr))))) {
+    return invalid();
+  }
+  if (rows == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const NormArgs a{output, mean, denominator, input, weight, bias, rows, extent, epsilon,
+                   center != 0};
+  const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
+  const bool vec = aligned_rows(output, extent, width) && aligned_rows(input, extent, width) &&
+                   aligned_rows(weight, extent, width) && aligned_rows(bias, extent, width);
+  bool done = false;
+  if (dtype == SPAR_HIP_FLOAT32) {
+    if (center) {
+      done = vec ? dispatch_forward<float, true, true>(a, guard)
+                 : dispatch_forward<float, true, false>(a, guard);
+    } else {
+      done = vec ? dispatch_forward<float, false, true>(a, guard)
+                 : dispatch_forward<float, false, false>(a, guard);
+    }
+  } else {
+    if (center) {
+      done = vec ? dispatch_forward<double, true, true>(a, guard)
+                 : dispatch_forward<double, true, false>(a, guard);
+    } else {
+      done = vec ? dispatch_forward<double, false, true>(a, guard)
+                 : dispatch_forward<double, false, false>(a, guard);
+    }
+  }
+  if (!done) return invalid();
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_norm_backward(
+    void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
+    const void* input, const void* weight, const void* mean, const void* denominator,
+    uint64_t rows, uint64_t extent, int center, int dtype, int device) {
+  if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
+      extent > spar_hip_norm_max_extent(dtype) ||
+      (rows != 0 &&
+       (input_gradient == nullptr || weight_gradient == nullptr || output_gradient == nullptr ||
+        input == nullptr || weight == nullptr || denominator == nullptr ||
+        (center && (mean == nullptr || bias_gradient == nullptr))))) {
+    return invalid();
+  }
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (rows == 0) {
+    // no rows: the parameter gradients are zero (fill kernels, no memset)
+    const uint64_t bytes = extent * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8);
+    SparHipStatus status = spar_hip_zero(weight_gradient, bytes, device);
+    if (status.code == 0 && center) status = spar_hip_zero(bias_gradient, bytes, device);
+    return status;
+  }
+  const NormBackwardArgs a{input_gradient, weight_gradient, bias_gradient, output_gradient,
+                           input, weight, mean, denominator, rows, extent, center != 0};
+  const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
+  const bool vec = aligned_rows(input_gradient, extent, width) &&
+                   aligned_rows(output_gradient, extent, width) &&
+                   aligned_rows(input, extent, width) && aligned_rows(weight, extent, width);
+  bool handled = false;
+  hipError_t error = hipSuccess;
+  if (dtype == SPAR_HIP_FLOAT32) {
+    if (center) {
+      error = vec ? dispatch_backward<float, true, true>(a, device, guard, handled)
+                  : dispatch_backward<float, true, false>(a, device, guard, handled);
+    } else {
+      error = vec ? dispatch_backward<float, false, true>(a, device, guard, handled)
+                  : dispatch_backward<float, false, false>(a, device, guard, handled);
+    }
+  } else {
+    if (center) {
+      error = vec ? dispatch_backward<double, true, true>(a, device, guard, handled)
+                  : dispatch_backward<double, true, false>(a, device, guard, handled);
+    } else {
+      error = vec ? dispatch_backward<double, false, true>(a, device, guard, handled)
+                  : dispatch_backward<double, false, false>(a, device, guard, handled);
+    }
+  }
+  if (!handled) return invalid();
+  if (error != hipSuccess) return runtime(error);
+  return finish(guard);
+}

@@ -77,4 +77,14 @@ namespace spar {
 [[nodiscard]] Tensor log_softmax(const Tensor& input);
 [[nodiscard]] Tensor log_softmax(const Tensor& input, std::size_t axis);
 
+// ------------------------------------------------------- normalisation
+/// addition: fused RMSNorm over the last axis, the computation of
+/// nn::RMSNorm::forward (src/nn/rmsnorm.cpp:41-53):
+/// (x / sqrt(mean(x*x, -1) + eps)) * weight, weight of the last extent.
+[[nodiscard]] Tensor rms_norm(const Tensor& input, const Tensor& weight, double epsilon = 1.0e-5);
+/// addition: fused LayerNorm over the last axis:
+/// ((x - mean(x)) / sqrt(mean((x - mean(x))^2) + eps)) * weight + bias.
+[[nodiscard]] Tensor layer_norm(const Tensor& input, const Tensor& weight, const Tensor& bias,
+                                double epsilon = 1.0e-5);
+
 }  // namespace spar

@@ -1,0 +1,144 @@
+// Fused LayerNorm and RMSNorm over the last axis (additions; the reference
+// composes RMSNorm from ops in RMSNorm::forward, src/nn/rmsnorm.cpp:41-53, and
+// has no LayerNorm).  The forward and backward each run one fused kernel pair
+// (spar_hip_launch_norm_forward / _backward); rows longer than the fused
+// kernels accept take the composed ops, which compute the same function.
+#include <cmath>
+#include <optional>
+#include <stdexcept>
+#include <string>
+
+#include "autograd_internal.hpp"
+#include "bridge.hpp"
+#include "spar/ops.hpp"
+
+namespace spar {
+namespace {
+
+using detail::HipTensorAccess;
+namespace hip = detail::hip;
+
+// Mirrors the argument checks of RMSNorm (rmsnorm.cpp:18-32, :41-49).
+void validate(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
+              const char* name) {
+  if (input.rank() == 0) throw std::invalid_argument{std::string{name} + " input must have rank at least 1"};
+  if (!is_floating(input.dtype())) {
+    throw std::invalid_argument{std::string{name} + " requires a floating-point dtype"};
+  }
+  detail::require_hip(input, name);
+  if (!std::isfinite(epsilon) || epsilon <= 0.0) {
+    throw std::invalid_argument{std::string{name} + " epsilon must be finite and positive"};
+  }
+  const auto extent{input.shape()[input.rank() - 1]};
+  for (const Tensor* parameter : {&weight, bias}) {
+    if (parameter == nullptr) continue;
+    if (parameter->rank() != 1 || parameter->shape()[0] != extent) {
+      throw std::invalid_argument{std::string{name} +
+                                  " input final dimension does not match its parameters"};
+    }
+    if (parameter->dtype() != input.dtype()) {
+      throw std::invalid_argument{std::string{name} + " input dtype does not match its parameters"};
+    }
+    if (parameter->device() != input.device()) {
+      throw std::invalid_argument{std::string{name} + " input and parameters are on different devices"};
+    }
+  }
+}
+
+// The composed computation (rmsnorm.cpp:50-52 for RMSNorm; the same chain
+// with centring and a bias for LayerNorm), for rows the fused kernels do not
+// take.
+Tensor composed(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon) {
+  const std::size_t axis{input.rank() - 1};
+  if (bias == nullptr) {
+    const Tensor mean_square{mean(square(input), axis, true)};
+    const Tensor denominator{sqrt(add_scalar(mean_square, epsilon))};
+    return multiply(divide(input, denominator), weight);
+  }
+  const Tensor centred{subtract(input, mean(input, axis, true))};
+  const Tensor denominator{sqrt(add_scalar(mean(square(centred), axis, true), epsilon))};
+  return add(multiply(divide(centred, denominator), weight), *bias);
+}
+
+Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
+             const char* name) {
+  const bool center{bias != nullptr};
+  const std::size_t extent{static_cast<std::size_t>(input.shape()[input.rank() - 1])};
+  if (extent > spar_hip_norm_max_extent(hip::dtype_tag(input.dtype())) || input.numel() == 0) {
+    return composed(input, weight, bias, epsilon);
+  }
+  const std::size_t rows{input.numel() / extent};
+  const Tensor x{input.is_contiguous() ? input : input.contiguous()};
+  const Tensor w{weight.is_contiguous() ? weight : weight.contiguous()};
+  std::optional<Tensor> b;
+  if (center) b = bias->is_contiguous() ? *bias : bias->contiguous();
+  const Shape row_shape{static_cast<Shape::dimension_type>(rows)};
+  Tensor output{input.shape(), input.dtype(), input.device()};
+  std::optional<Tensor> mean_rows;
+  if (center) mean_rows.emplace(row_shape, input.dtype(), input.device());
+  Tensor denominator{row_shape, input.dtype(), input.device()};
+  const int device{input.device().index()};
+  hip::check(spar_hip_launch_norm_forward(
+                 HipTensorAccess::mutable_data(output),
+                 center ? HipTensorAccess::mutable_data(*mean_rows) : nullptr,
+                 HipTensorAccess::mutable_data(denominator), HipTensorAccess::data(x),
+                 HipTensorAccess::data(w), center ? HipTensorAccess::data(*b) : nullptr, rows,
+                 extent, epsilon, center ? 1 : 0, hip::dtype_tag(input.dtype()), device),
+             name, input.device());
+
+  const bool grad_x{x.requires_grad()}, grad_w{weight.requires_grad()};
+  const bool grad_b{center && bias->requires_grad()};
+  if (grad_x || grad_w || grad_b) {
+    std::vector<Tensor> parents;
+    if (grad_x) parents.push_back(x);
+    if (grad_w) parents.push_back(weight);
+    if (grad_b) parents.push_back(*bias);
+    const Tensor saved_x{x.detach()}, saved_w{w.detach()};
+    const Shape weight_shape{weight.shape()};
+    detail::record_operation(
+        output, std::move(parents),
+        [saved_x, saved_w, mean_rows, denominator, rows, extent, center, grad_x, grad_w, grad_b,
+         weight_shape, name](const Tensor& gradient) {
+          const Tensor dy{gradient.is_contiguous() ? gradient.detach()
+                                                   : gradient.detach().contiguous()};
+          Tensor dx{saved_x.shape(), saved_x.dtype(), saved_x.device()};
+          Tensor dw{weight_shape, saved_x.dtype(), saved_x.device()};
+          std::optional<Tensor> db;
+          if (center) db.emplace(weight_shape, saved_x.dtype(), saved_x.device());
+          hip::check(spar_hip_launch_norm_backward(
+                         HipTensorAccess::mutable_data(dx), HipTensorAccess::mutable_data(dw),
+                         center ? HipTensorAccess::mutable_data(*db) : nullptr,
+                         HipTensorAccess::data(dy), HipTensorAccess::data(saved_x),
+                         HipTensorAccess::data(saved_w),
+                         center ? HipTensorAccess::data(*mean_rows) : nullptr,
+                         HipTensorAccess::data(denominator), rows, extent, center ? 1 : 0,
+                         hip::dtype_tag(saved_x.dtype()), saved_x.device().index()),
+                     std::string{name} + " backward", saved_x.device());
+          std::vector<Tensor> contributions;
+          if (grad_x) contributions.push_back(dx);
+          if (grad_w) contributions.push_back(dw);
+          if (grad_b) contributions.push_back(*db);
+          return contributions;
+        });
+  }
+  return output;
+}
+
+}  // namespace
+
+Tensor layer_norm(const Tensor& input, const Tensor& weight, const Tensor& bias, double epsilon) {
+  validate(input, weight, &bias, epsilon, "layer_norm");
+  return fused(input, weight, &bias, epsilon, "layer_norm");
+}
+
+Tensor rms_norm(const Tensor& input, const Tensor& weight, double epsilon) {
+  validate(input, weight, nullptr, epsilon, "rms_norm");
+  // The composed forward starts with square(input), and unary ops reject
+  // non-contiguous inputs (unary.cpp:19-21); the fused op keeps that error.
+  if (!input.is_contiguous()) {
+    throw std::invalid_argument{"Unary operations currently require contiguous tensors"};
+  }
+  return fused(input, weight, nullptr, epsilon, "rms_norm");
+}
+
+}  // namespace spar

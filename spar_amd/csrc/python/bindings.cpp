@@ -239,6 +239,10 @@ PYBIND11_MODULE(_spar, m) {
           return axis.is_none() ? spar::log_softmax(x) : spar::log_softmax(x, axis.cast<std::size_t>());
         },
         py::arg("input"), py::arg("axis") = py::none());
+  m.def("rms_norm", &spar::rms_norm, py::arg("input"), py::arg("weight"),
+        py::arg("epsilon") = 1.0e-5, py::call_guard<py::gil_scoped_release>());
+  m.def("layer_norm", &spar::layer_norm, py::arg("input"), py::arg("weight"), py::arg("bias"),
+        py::arg("epsilon") = 1.0e-5, py::call_guard<py::gil_scoped_release>());
   m.def("reduce_gradient_to_shape", [](const Tensor& g, const std::vector<std::int64_t>& s) {
     return spar::detail::reduce_gradient_to_shape(g, to_shape(s));
   });

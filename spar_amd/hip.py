@@ -57,7 +57,8 @@ _I = ctypes.c_int
 _D = ctypes.c_double
 _U64P = ctypes.POINTER(ctypes.c_uint64)
 
-# name -> argument types (every entry point returns Status except error_string)
+# name -> argument types (every entry point returns Status except error_string and
+# norm_max_extent)
 SIGNATURES = {
     "spar_hip_device_count": [ctypes.POINTER(ctypes.c_int)],
     "spar_hip_allocate": [ctypes.POINTER(ctypes.c_void_p), _U64, _I],
@@ -92,6 +93,8 @@ SIGNATURES = {
     "spar_hip_launch_multiply_reduce": [_P, _P, _P, _U64, _U64P, _U64, _U64P, _U64, _I, _I],
     "spar_hip_launch_probability_forward": [_P, _P, _P, _U64, _U64, _U64, _I, _I, _I],
     "spar_hip_launch_probability_backward": [_P, _P, _P, _P, _U64, _U64, _U64, _I, _I, _I],
+    "spar_hip_launch_norm_forward": [_P, _P, _P, _P, _P, _P, _U64, _U64, _D, _I, _I, _I],
+    "spar_hip_launch_norm_backward": [_P, _P, _P, _P, _P, _P, _P, _P, _U64, _U64, _I, _I, _I],
     "spar_hip_random_uniform": [_P, _U64, _I, _U64, _D, _D, _I],
     "spar_hip_random_normal": [_P, _U64, _I, _U64, _D, _D, _I],
 }
@@ -117,6 +120,8 @@ def load() -> ctypes.CDLL:
         fn.restype = Status
     lib.spar_hip_error_string.argtypes = [ctypes.c_int]
     lib.spar_hip_error_string.restype = ctypes.c_char_p
+    lib.spar_hip_norm_max_extent.argtypes = [ctypes.c_int]
+    lib.spar_hip_norm_max_extent.restype = ctypes.c_uint64
     _lib = lib
     return lib
 

@@ -270,3 +270,46 @@ def test_c5_layernorm_chain(hip, view):
     want_dgamma = np.sum(G.astype(np.float64) * got_xhat.astype(np.float64), axis=0)
     norm = norm2(G.astype(np.float64) * got_xhat, axis=0)
     assert_red(got_dgamma, want_dgamma, rows, norm * 4, "d gamma")
+
+
+def test_c5_fused_layernorm_matches_chain(hip):
+    """The fused LayerNorm on the C5 transposed view against the composed
+    chain (validated against the oracle above), forward and backward, at
+    full size."""
+    from spar_amd import spar
+
+    from tests.test_norm_gpu import assert_rows, dx_terms
+
+    rows, cols = 4096, 8192
+    device, cpu = spar.Device.hip(0), spar.Device.cpu()
+    rng = np.random.default_rng(63)
+    base = rng.standard_normal((cols, rows)).astype(F32)
+    gamma = rng.uniform(0.5, 1.5, cols).astype(F32)
+    beta = rng.uniform(-0.1, 0.1, cols).astype(F32)
+    G = rng.standard_normal((rows, cols)).astype(F32)
+
+    def run(fused):
+        ts = []
+        for array in (base, gamma, beta, G):
+            t = spar.Tensor.from_numpy(array).to(device)
+            t.set_requires_grad(True)
+            ts.append(t)
+        x = ts[0].transpose(0, 1)
+        if fused:
+            y = spar.layer_norm(x, ts[1], ts[2], 1e-5)
+        else:
+            mu = spar.mean(x, [1], True)
+            xc = spar.subtract(x, mu)
+            sd = spar.sqrt(spar.add_scalar(spar.mean(spar.square(xc), [1], True), 1e-5))
+            y = spar.add(spar.multiply(spar.divide(xc, sd), ts[1]), ts[2])
+        spar.sum(spar.multiply(y, ts[3]), None, False).backward()
+        return [y.to(cpu).numpy()] + [t.grad().to(cpu).numpy() for t in ts[:3]]
+
+    fused, chain = run(True), run(False)
+    assert_rows(fused[0], chain[0], cols, F32, "C5 fused y", 16.0)
+    assert_rows(fused[1].T, chain[1].T, cols, F32, "C5 fused dx", 32.0,
+                dx_terms(G, gamma, base.T, True))
+    for i, name in ((2, "d gamma"), (3, "d beta")):
+        scale = np.max(np.abs(chain[i]))
+        err = np.max(np.abs(fused[i].astype(np.float64) - chain[i]))
+        assert err <= 1e-6 * np.sqrt(rows) * 16 * scale, f"C5 fused {name}: {err} vs {scale}"

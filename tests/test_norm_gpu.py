@@ -1,0 +1,301 @@
+"""Fused LayerNorm / RMSNorm against the oracle's composition of the
+reference's ops (RMSNorm::forward, nn/rmsnorm.cpp:50-52; LayerNorm is the
+same chain with centring and a bias).
+
+The fused kernels compute every element with the composed path's float
+operations; only the order of the two row sums differs (a tree instead of a
+sequential scan).  Each row statistic therefore differs by at most red(n)
+(relative 1e-6 sqrt(n) at the row's natural scale), and every output element
+of the row moves by that relative amount of the row's magnitude, plus a few
+roundings.  The bounds below are those, with the row's largest output as the
+scale -- for dx, the largest term of the difference it is, since
+dx = (g w - mean(g w) - xhat mean(g w xhat)) / d cancels (entirely so for a
+one-element RMSNorm row, where xhat^2 is nearly 1).
+"""
+import numpy as np
+import pytest
+
+import oracle.reference as R
+from oracle import ops as ref
+from tests.helpers import assert_red
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = np.float32, np.float64
+EPSILON = 1.0e-5
+
+
+def tag(dtype):
+    return 0 if np.dtype(dtype) == F32 else 1
+
+
+_alive = []
+
+
+@pytest.fixture(autouse=True)
+def _release_buffers():
+    yield
+    _alive.clear()
+
+
+def dev(hip, array):
+    buffer = hip.DeviceBuffer.from_numpy(np.ascontiguousarray(array))
+    _alive.append(buffer)
+    return buffer
+
+
+def out_buf(hip, count, dtype):
+    buffer = hip.DeviceBuffer(max(count, 1) * np.dtype(dtype).itemsize)
+    _alive.append(buffer)
+    return buffer
+
+
+def data(rows, n, dtype, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, n)) * 2 + 0.5).astype(dtype)
+    w = rng.uniform(0.5, 1.5, n).astype(dtype)
+    b = rng.uniform(-0.1, 0.1, n).astype(dtype)
+    g = rng.standard_normal((rows, n)).astype(dtype)
+    return x, w, b, g
+
+
+def composed_forward(x, w, b, center):
+    """The composed chain through the oracle's op loops: (y, mu, d)."""
+    n = x.shape[1]
+    mu = None
+    xc = x
+    if center:
+        mu = ref.scalar(ref.axis_sum(x, [1]), "divide", float(n))
+        xc = ref.binary(x, mu[:, None], "subtract")
+    var = ref.scalar(ref.axis_sum(ref.unary(xc, "square"), [1]), "divide", float(n))
+    d = ref.unary(ref.scalar(var, "add", EPSILON), "sqrt")
+    y = ref.binary(ref.binary(xc, d[:, None], "divide"), w, "multiply")
+    if center:
+        y = ref.binary(y, b, "add")
+    return y, mu, d
+
+
+def row_bound(want, n, dtype, factor=8.0, terms=None):
+    """factor * 1e-6 sqrt(n) + 8 eps of the row's scale: its largest |value|,
+    or, where the value is a difference of larger terms (dx), the largest
+    term of that difference."""
+    scale = np.max(np.abs(want.astype(np.float64)), axis=-1, keepdims=True)
+    if terms is not None:
+        scale = np.maximum(scale, np.max(terms, axis=-1, keepdims=True))
+    return (factor * 1e-6 * np.sqrt(n) + 8 * np.finfo(dtype).eps) * scale + np.finfo(dtype).tiny
+
+
+def assert_rows(got, want, n, dtype, what, factor=8.0, terms=None):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bound = row_bound(want, n, dtype, factor, terms)
+    assert np.all(err <= bound), f"{what}: worst excess {np.max(err - bound)}"
+
+
+def dx_terms(g, w, x, center):
+    """|g w| / d per element: the size of the terms dx = (g w - ...) / d
+    subtracts (float64 statistics)."""
+    x64 = x.astype(np.float64)
+    xc = x64 - x64.mean(axis=-1, keepdims=True) if center else x64
+    d = np.sqrt(np.mean(xc * xc, axis=-1, keepdims=True) + EPSILON)
+    return np.abs(g.astype(np.float64) * w.astype(np.float64)) / d
+
+
+def shapes(dtype):
+    limit = 16384 if dtype == F32 else 8192
+    return [(5, 1), (3, 3), (7, 8), (64, 100), (9, 1000), (4, 1030), (33, 4096), (6, 8192),
+            (3, limit), (2, limit - 4), (3, limit - 1)]
+
+
+def forward_device(hip, x, w, b, center, dtype):
+    rows, n = x.shape
+    y, mu, d = out_buf(hip, rows * n, dtype), out_buf(hip, rows, dtype), out_buf(hip, rows, dtype)
+    dx = dev(hip, x)
+    hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr, dx.ptr,
+             dev(hip, w).ptr, dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center),
+             tag(dtype), 0)
+    return (y.to_numpy(dtype, (rows, n)), mu.to_numpy(dtype, (rows,)) if center else None,
+            d.to_numpy(dtype, (rows,)), (dx, mu, d))
+
+
+def test_max_extent(hip):
+    lib = hip.load()
+    assert lib.spar_hip_norm_max_extent(0) == 16384
+    assert lib.spar_hip_norm_max_extent(1) == 8192
+    assert lib.spar_hip_norm_max_extent(2) == 0
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
+def test_norm_forward_kernel(hip, dtype, center):
+    for index, (rows, n) in enumerate(shapes(dtype)):
+        x, w, b, _ = data(rows, n, dtype, 100 + index)
+        got_y, got_mu, got_d, _ = forward_device(hip, x, w, b, center, dtype)
+        want_y, want_mu, want_d = composed_forward(x, w, b, center)
+        what = f"{'layer' if center else 'rms'} norm {rows}x{n} {np.dtype(dtype).name}"
+        if center:
+            assert_red(got_mu, want_mu, n, np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=1)) / n,
+                       what + " mean")
+        assert np.all(np.abs(got_d.astype(np.float64) - want_d) <=
+                      (4e-6 * np.sqrt(n) + 4 * np.finfo(dtype).eps) * want_d), what + " d"
+        assert_rows(got_y, want_y, n, dtype, what + " y")
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
+def test_norm_backward_kernel(hip, dtype, center):
+    for index, (rows, n) in enumerate(shapes(dtype)[:-2] + [(300, 64), (1000, 12)]):
+        x, w, b, g = data(rows, n, dtype, 200 + index)
+        _, _, _, (dx_in, mu, d) = forward_device(hip, x, w, b, center, dtype)
+        dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
+        hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
+                 dev(hip, g).ptr, dx_in.ptr, dev(hip, w).ptr, mu.ptr if center else None, d.ptr,
+                 rows, n, int(center), tag(dtype), 0)
+        tx = R.RTensor.of(x, requires_grad=True)
+        tw = R.RTensor.of(w, requires_grad=True)
+        tb = R.RTensor.of(b, requires_grad=True)
+        y = R.layer_norm(tx, tw, tb, EPSILON) if center else R.rms_norm(tx, tw, EPSILON)
+        R.sum(R.multiply(y, R.RTensor.of(g))).backward()
+        what = f"{'layer' if center else 'rms'} norm backward {rows}x{n} {np.dtype(dtype).name}"
+        assert_rows(dx.to_numpy(dtype, (rows, n)), tx.grad().numpy(), n, dtype, what + " dx", 16.0,
+                    dx_terms(g, w, x, center))
+        # d weight = sum over rows of g * xhat: red(rows) plus each term's
+        # relative perturbation through xhat
+        _, _, want_d = composed_forward(x, w, b, center)
+        xc = x.astype(np.float64) - (x.astype(np.float64).mean(axis=1, keepdims=True) if center else 0)
+        terms = np.abs(g.astype(np.float64) * xc / want_d[:, None])
+        norm = np.sqrt(np.sum(terms ** 2, axis=0))
+        slack = 8e-6 * np.sqrt(n) * np.sum(terms, axis=0)
+        err = np.abs(dw.to_numpy(dtype, (n,)).astype(np.float64) - tw.grad().numpy())
+        bound = 1e-6 * np.sqrt(rows) * np.maximum(np.abs(tw.grad().numpy()), norm) + slack + 1e-30
+        assert np.all(err <= bound), f"{what} d weight: worst excess {np.max(err - bound)}"
+        if center:
+            assert_red(db.to_numpy(dtype, (n,)), tb.grad().numpy(), rows,
+                       np.sqrt(np.sum(g.astype(np.float64) ** 2, axis=0)), what + " d bias")
+
+
+def test_norm_entry_points_reject_bad_arguments(hip):
+    lib = hip.load()
+    p = out_buf(hip, 64, F32).ptr
+    bad = [
+        (p, p, p, p, p, p, 4, 0, EPSILON, 1, 0, 0),           # extent 0
+        (p, p, p, p, p, p, 4, 16385, EPSILON, 1, 0, 0),       # beyond the float32 limit
+        (p, p, p, p, p, p, 4, 8193, EPSILON, 1, 1, 0),        # beyond the float64 limit
+        (p, None, p, p, p, p, 4, 8, EPSILON, 1, 0, 0),        # LayerNorm without mean
+        (p, p, p, p, p, None, 4, 8, EPSILON, 1, 0, 0),        # LayerNorm without bias
+        (p, p, p, p, p, p, 4, 8, EPSILON, 2, 0, 0),           # center flag
+        (p, p, p, p, p, p, 4, 8, EPSILON, 1, 2, 0),           # integer dtype
+        (p, p, p, p, p, p, 4, 8, -1.0, 1, 0, 0),              # negative epsilon
+    ]
+    for args in bad:
+        assert lib.spar_hip_launch_norm_forward(*args).code == 1, args
+    assert lib.spar_hip_launch_norm_backward(p, p, None, p, p, p, p, p, 4, 8, 1, 0, 0).code == 1
+    # zero rows: parameter gradients are zero, nothing else is touched
+    dw, db = out_buf(hip, 8, F32), out_buf(hip, 8, F32)
+    hip.call("spar_hip_launch_norm_backward", None, dw.ptr, db.ptr, None, None, p, None, None, 0,
+             8, 1, 0, 0)
+    assert not dw.to_numpy(F32, (8,)).any() and not db.to_numpy(F32, (8,)).any()
+
+
+# ------------------------------------------------------------------ API
+
+@pytest.fixture(scope="module")
+def sp():
+    from spar_amd import spar
+
+    if spar.hip_device_count() < 1:
+        pytest.fail("no HIP device visible to a gpu-marked test")
+    return spar
+
+
+def api_both(sp, arrays, build):
+    device = sp.Device.hip(0)
+    on_device = []
+    for a in arrays:
+        t = sp.Tensor.from_numpy(np.ascontiguousarray(a)).to(device)
+        t.set_requires_grad(True)
+        on_device.append(t)
+    on_oracle = [R.RTensor.of(a, requires_grad=True) for a in arrays]
+    yd, yr = build(sp, on_device), build(R, on_oracle)
+    cpu = sp.Device.cpu()
+    got_y = yd.to(cpu).numpy()
+    want_y = yr.numpy()
+    return got_y, want_y, on_device, on_oracle
+
+
+def test_rms_norm_rejects_views_like_the_composition(sp):
+    # RMSNorm::forward starts with square(x), which throws on a
+    # non-contiguous input (unary.cpp:19-21); the fused op keeps that error.
+    x, w, _, _ = data(8, 12, F32, 302)
+    base = np.ascontiguousarray(x.T)
+    device = sp.Device.hip(0)
+    view = sp.Tensor.from_numpy(base).to(device).transpose(0, 1)
+    weight = sp.Tensor.from_numpy(w).to(device)
+    with pytest.raises(ValueError, match="contiguous"):
+        sp.rms_norm(view, weight)
+    with pytest.raises(ValueError, match="contiguous"):
+        R.rms_norm(R.RTensor.of(base).transpose(0, 1), R.RTensor.of(w))
+
+
+# (RMSNorm on a transposed view is an error, tested above.)
+@pytest.mark.parametrize("center,layout", [(True, "contiguous"), (True, "transposed"),
+                                           (False, "contiguous")])
+def test_norm_api_forward_backward(sp, center, layout):
+    rows, n = 96, 520
+    x, w, b, g = data(rows, n, F32, 300)
+    base = np.ascontiguousarray(x.T) if layout == "transposed" else x
+
+    def build(lib, t):
+        xv = t[0].transpose(0, 1) if layout == "transposed" else t[0]
+        y = lib.layer_norm(xv, t[1], t[2], EPSILON) if center else lib.rms_norm(xv, t[1], EPSILON)
+        loss = lib.sum(lib.multiply(y, t[3]))
+        loss.backward()
+        return y
+
+    got_y, want_y, td, tr = api_both(sp, [base, w, b, g], build)
+    assert_rows(got_y, want_y, n, F32, f"api y {layout}")
+    cpu = sp.Device.cpu()
+    dx_got, dx_want = td[0].grad().to(cpu).numpy(), tr[0].grad().numpy()
+    if layout == "transposed":
+        dx_got, dx_want = dx_got.T, dx_want.T
+    # both gradients are back in [rows, n] orientation here
+    assert_rows(dx_got, dx_want, n, F32, f"api dx {layout}", 16.0, dx_terms(g, w, x, center))
+    for i in (1, 2) if center else (1,):
+        got, want = td[i].grad().to(cpu).numpy(), tr[i].grad().numpy()
+        scale = np.max(np.abs(want))
+        assert np.max(np.abs(got - want)) <= 1e-6 * np.sqrt(rows * n) * 8 * scale, f"api grad {i}"
+    if not center:  # the unused bias never received a gradient
+        with pytest.raises(sp.LogicError):
+            td[2].grad()
+
+
+def test_norm_api_long_rows_use_composed_ops(sp):
+    # rows longer than the fused kernels accept take the composed ops
+    rows, n = 3, 20000
+    x, w, b, g = data(rows, n, F32, 301)
+
+    def build(lib, t):
+        y = lib.rms_norm(t[0], t[1], EPSILON)
+        lib.sum(lib.multiply(y, t[2])).backward()
+        return y
+
+    got_y, want_y, td, tr = api_both(sp, [x, w, g], build)
+    assert_rows(got_y, want_y, n, F32, "composed y")
+    assert_rows(td[0].grad().to(sp.Device.cpu()).numpy(), tr[0].grad().numpy(), n, F32,
+                "composed dx", 16.0, dx_terms(g, w, x, False))
+
+
+def test_norm_api_errors(sp):
+    device = sp.Device.hip(0)
+    x = sp.Tensor.from_numpy(np.ones((4, 8), F32)).to(device)
+    w = sp.Tensor.from_numpy(np.ones(8, F32)).to(device)
+    w_bad = sp.Tensor.from_numpy(np.ones(7, F32)).to(device)
+    with pytest.raises(ValueError):
+        sp.rms_norm(x, w_bad)
+    with pytest.raises(ValueError):
+        sp.layer_norm(x, w, w_bad)
+    with pytest.raises(ValueError):
+        sp.rms_norm(x, w, 0.0)
+    with pytest.raises(ValueError):
+        sp.rms_norm(x, sp.Tensor.from_numpy(np.ones(8, F64)).to(device))
+    with pytest.raises(RuntimeError):
+        sp.rms_norm(sp.Tensor.from_numpy(np.ones((4, 8), F32)), w)
