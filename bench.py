@@ -395,7 +395,44 @@ def run_suite(hip, reps=20, warmup=3):
         measure("C4", f"{label} backward", 12 * n + 4 * rows, lambda log=log: hip.call(
             "spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
             rows, V, 1, F, log, 0), n)
-    del logits, grad, probs, dx, undefined
+    # C4 as a loss: cross entropy over the same logits, fused (one read of the
+    # logits forward; one read and one write backward) and composed as the
+    # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
+    # log_softmax backward), with the same targets.
+    targets = hip.DeviceBuffer(rows * 8)
+    hip.call("spar_hip_copy_host_to_device", targets.ptr,
+             np.random.default_rng(9).integers(0, V, rows).astype(np.int64).ctypes.data,
+             rows * 8, 0)
+    losses, row_max, row_log_sum = (hip.DeviceBuffer(rows * 4) for _ in range(3))
+    invalid = hip.DeviceBuffer(4)
+    loss_grad = uniform(rows, 10, 0.5, 1.5)
+    small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
+    measure("C4", "cross_entropy forward (fused)", 4 * n + small, lambda: hip.call(
+        "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
+        undefined.ptr, invalid.ptr, logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
+    measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, lambda: hip.call(
+        "spar_hip_launch_cross_entropy_backward", dx.ptr, loss_grad.ptr, logits.ptr, row_max.ptr,
+        row_log_sum.ptr, undefined.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
+
+    def composed_forward():
+        hip.call("spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows,
+                 V, 1, F, 1, 0)
+        hip.call("spar_hip_launch_nll_forward", losses.ptr, probs.ptr, targets.ptr, rows, V, 0, F,
+                 hip.INT64, 0, 0)
+
+    def composed_backward():
+        hip.call("spar_hip_zero", grad.ptr, n * 4, 0)
+        hip.call("spar_hip_launch_nll_backward", grad.ptr, loss_grad.ptr, targets.ptr, rows, V, 0,
+                 F, hip.INT64, 0, 0)
+        hip.call("spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
+                 rows, V, 1, F, 1, 0)
+
+    # reported against the fused kernels' bytes, so the ratio is the speed-up
+    measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
+            composed_forward, n)
+    measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
+            composed_backward, n)
+    del logits, grad, probs, dx, undefined, targets, losses, row_max, row_log_sum, invalid, loss_grad
 
     # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
     # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a

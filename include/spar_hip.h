@@ -338,6 +338,61 @@ struct SparHipStatus spar_hip_launch_norm_backward(
     const void* input, const void* weight, const void* mean, const void* denominator,
     uint64_t rows, uint64_t extent, int center, int dtype, int device);
 
+/* --------------------------------------------- cross entropy (log-softmax + NLL) */
+
+/* Sets *invalid_target (host memory) to 1 if any of `count` class indices
+ * (target_dtype SPAR_HIP_INT32 or SPAR_HIP_INT64) is negative or >= classes,
+ * else 0.  Synchronises.  Replaces spar_cuda_validate_targets
+ * (cuda_kernels.hpp:105-107). */
+struct SparHipStatus spar_hip_validate_targets(int32_t* invalid_target, const void* targets,
+                                               uint64_t count, uint64_t classes,
+                                               int target_dtype, int device);
+
+/* output[i] = -log_probabilities[row(i) * classes + target(i)]: row(i) = i and
+ * target(i) = targets[i], or for the language-model form (language_model = 1)
+ * with sequences of sequence_length, i = b * (T-1) + t reads row b*T + t and
+ * target targets[b*T + t + 1].  Replaces spar_cuda_launch_nll_forward
+ * (cuda_kernels.hpp:108-112). */
+struct SparHipStatus spar_hip_launch_nll_forward(void* output, const void* log_probabilities,
+                                                 const void* targets, uint64_t output_count,
+                                                 uint64_t classes, uint64_t sequence_length,
+                                                 int dtype, int target_dtype, int language_model,
+                                                 int device);
+
+/* Scatter of the above's gradient into a zeroed [rows, classes] output:
+ * output[row(i) * classes + target(i)] = 0 - gradient[i].  Replaces
+ * spar_cuda_launch_nll_backward (cuda_kernels.hpp:113-117). */
+struct SparHipStatus spar_hip_launch_nll_backward(void* output, const void* gradient,
+                                                  const void* targets, uint64_t output_count,
+                                                  uint64_t classes, uint64_t sequence_length,
+                                                  int dtype, int target_dtype, int language_model,
+                                                  int device);
+
+/* Fused log_softmax -> NLL forward over logits [logits_rows, classes]:
+ * losses (one per target, indexed as above) = -log_softmax(row)[target],
+ * computed with log-softmax's operations; saves each row's maximum and
+ * log of its exp-sum, and its undefined flag (log-softmax's special cases).
+ * *invalid_target (device memory) is set to 1 if a target is out of range;
+ * that target's loss is NaN and its logit is not read.  Replaces
+ * log_softmax + select_nll_cuda in cross_entropy / language_model_cross_entropy
+ * (cross_entropy.cpp:146-214) without materialising the log-probabilities;
+ * the reference has no fused kernel. */
+struct SparHipStatus spar_hip_launch_cross_entropy_forward(
+    void* losses, void* row_max, void* row_log_sum, int32_t* undefined_rows,
+    int32_t* invalid_target, const void* logits, const void* targets, uint64_t logits_rows,
+    uint64_t classes, uint64_t sequence_length, int dtype, int target_dtype, int language_model,
+    int device);
+
+/* Its backward: logits_gradient = g - exp(lp) * g_t with g the NLL gradient
+ * (g_t = 0 - loss_gradient at the target, zero elsewhere) and lp recomputed
+ * from the saved row statistics -- the reference's nll_gradient followed by
+ * log_softmax's backward (softmax.cpp:406-444), in one pass. */
+struct SparHipStatus spar_hip_launch_cross_entropy_backward(
+    void* logits_gradient, const void* loss_gradient, const void* logits, const void* row_max,
+    const void* row_log_sum, const int32_t* undefined_rows, const void* targets,
+    uint64_t logits_rows, uint64_t classes, uint64_t sequence_length, int dtype,
+    int target_dtype, int language_model, int device);
+
 /* ------------------------------------------------------ random generation */
 
 /* Fills `count` contiguous elements with Spar's SplitMix64 stream for `seed`

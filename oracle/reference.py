@@ -606,3 +606,73 @@ def layer_norm(x: RTensor, weight: RTensor, bias: RTensor, epsilon: float = 1.0e
     centred = subtract(x, mean(x, [axis], True))
     denominator = sqrt(add_scalar(mean(square(centred), [axis], True), epsilon))
     return add(multiply(divide(centred, denominator), weight), bias)
+
+
+# ------------------------------------------------------------ cross entropy
+
+def _validated_targets(targets: np.ndarray, classes: int) -> np.ndarray:
+    """validated_targets (loss/cross_entropy.cpp:17-46): Int32/Int64 class
+    indices in [0, classes), flattened in logical order."""
+    if targets.dtype not in (np.int32, np.int64):
+        raise ValueError("cross_entropy targets must have Int32 or Int64 dtype")
+    flat = np.ascontiguousarray(targets).reshape(-1).astype(np.int64)
+    if np.any(flat < 0) or np.any(flat >= classes):
+        raise IndexError("cross_entropy target is outside the class range")
+    return flat
+
+
+def _select_nll(lp: RTensor, targets: np.ndarray, rows: np.ndarray, output_shape) -> RTensor:
+    """select_nll / nll_values / nll_gradient (loss/cross_entropy.cpp:56-105):
+    losses = -lp[row, target]; the gradient is a zero tensor with
+    0 - upstream at each (row, target)."""
+    classes = lp.shape[-1]
+    index = rows * classes + targets
+    values = -np.ascontiguousarray(lp.numpy()).reshape(-1)[index]
+    out = RTensor.of(values.reshape(tuple(output_shape)))
+    if lp.requires_grad:
+        shape, dtype = tuple(lp.shape), lp.numpy().dtype
+
+        def backward(g):
+            contribution = np.zeros(int(np.prod(shape)), dtype=dtype)
+            contribution[index] = contribution[index] - np.ascontiguousarray(g.numpy()).reshape(-1)
+            return [RTensor.of(contribution.reshape(shape))]
+
+        _record(out, [lp], backward)
+    return out
+
+
+def _reduce_loss(losses: RTensor, reduction: str) -> RTensor:
+    """reduce_loss (loss/cross_entropy.cpp:107-117)."""
+    if reduction == "none":
+        return losses
+    if reduction == "sum":
+        return sum(losses)
+    if reduction == "mean":
+        return mean(losses)
+    raise ValueError("cross_entropy received an unknown Reduction")
+
+
+def cross_entropy(logits: RTensor, targets: np.ndarray, reduction: str = "mean") -> RTensor:
+    """cross_entropy, CPU path (loss/cross_entropy.cpp:131-160)."""
+    if targets.size == 0:
+        raise ValueError("cross_entropy requires at least one target")
+    if tuple(targets.shape) != tuple(logits.shape[:-1]):
+        raise ValueError("cross_entropy target shape does not match logits")
+    classes = logits.shape[-1]
+    flat = _validated_targets(targets, classes)
+    lp = log_softmax(logits, len(logits.shape) - 1)
+    return _reduce_loss(_select_nll(lp, flat, np.arange(flat.size, dtype=np.int64),
+                                    targets.shape), reduction)
+
+
+def language_model_cross_entropy(logits: RTensor, token_ids: np.ndarray,
+                                 reduction: str = "mean") -> RTensor:
+    """language_model_cross_entropy, CPU path (loss/cross_entropy.cpp:162-212):
+    position t of each sequence predicts token t + 1."""
+    batch, sequence, classes = logits.shape
+    tokens = _validated_targets(token_ids, classes).reshape(batch, sequence)
+    targets = tokens[:, 1:].reshape(-1)
+    rows = (np.arange(batch, dtype=np.int64)[:, None] * sequence +
+            np.arange(sequence - 1, dtype=np.int64)[None, :]).reshape(-1)
+    lp = log_softmax(logits, 2)
+    return _reduce_loss(_select_nll(lp, targets, rows, (batch, sequence - 1)), reduction)

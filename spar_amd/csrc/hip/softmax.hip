@@ -837,6 +837,307 @@ void backward(void* output, const void* gradient, const void* saved, const int32
          guard.stream>>>(out, g, y, undefined, outer, axis, inner);
 }
 
+// ------------------------------------------- cross entropy (log-softmax + NLL)
+
+// Target of logits row `row` and the index of its loss, for plain
+// cross entropy (one target per row) or the language-model form, where
+// position t of a length-T sequence predicts token t + 1 and the last
+// position has no target (cross_entropy.cpp:146-214).
+struct TargetMap {
+  uint64_t sequence_length;  // 0: plain cross entropy
+  __device__ __forceinline__ bool lookup(uint64_t row, uint64_t& target_index,
+                                         uint64_t& output_index) const {
+    if (sequence_length == 0) {
+      target_index = row;
+      output_index = row;
+      return true;
+    }
+    const uint64_t batch = row / sequence_length;
+    const uint64_t time = row - batch * sequence_length;
+    if (time + 1 == sequence_length) return false;
+    target_index = row + 1;
+    output_index = batch * (sequence_length - 1) + time;
+    return true;
+  }
+};
+
+constexpr int kEntropyThreads = 256;
+
+// Row statistics in one streaming pass, branch-free: each lane keeps a
+// running maximum m and s = sum exp(x - m); per batch of 8 vectors it takes
+// the batch maximum (v_max, which passes over NaN), rescales s once by
+// exp(m - m_new) and adds exp(x - m_new) per element, where a -inf element
+// adds exactly 0 (as it does to a row with a finite maximum).  A NaN element
+// makes s NaN (NaN - m) and a +inf maximum does too (inf - inf); a row of
+// nothing above -inf keeps m = -inf.  Only the sign of a zero maximum can
+// differ from the first-occurrence rule, which changes no loss or gradient.
+template <typename T>
+__device__ __forceinline__ T rescaled(T s, T m, T top) {
+  return s == T(0) ? T(0) : s * math_exp(m - top);
+}
+
+template <typename T>
+__device__ __forceinline__ T exp_term(T x, T top) {
+  return x == -positive_infinity<T>() ? T(0) : math_exp(x - top);
+}
+
+template <typename T> __device__ __forceinline__ T fmax_of(T a, T b);
+template <> __device__ __forceinline__ float fmax_of<float>(float a, float b) { return fmaxf(a, b); }
+template <> __device__ __forceinline__ double fmax_of<double>(double a, double b) { return fmax(a, b); }
+
+// Block-wide merge of the lanes' (m, s): the maximum M of the lane maxima
+// (wave shuffles, then the waves through LDS), then each lane's sum rescaled
+// once by exp(m - M) and the rescaled sums added (wave sums, then in wave
+// order).
+template <typename T, int THREADS>
+__device__ __forceinline__ void block_online(T& m, T& s) {
+  constexpr int kWavesPerBlock = THREADS / kWave;
+  __shared__ T lds_m[kWavesPerBlock];
+  __shared__ T lds_s[kWavesPerBlock];
+  T wave_m = m;
+#pragma unroll
+  for (int mask = kWave / 2; mask > 0; mask >>= 1) {
+    wave_m = fmax_of(wave_m, __shfl_xor(wave_m, mask, kWave));
+  }
+  const T wave_s = wave_sum(rescaled(s, m, wave_m));
+  exchange_barrier();
+  if (threadIdx.x % kWave == 0) {
+    lds_m[threadIdx.x / kWave] = wave_m;
+    lds_s[threadIdx.x / kWave] = wave_s;
+  }
+  exchange_barrier();
+  T top = lds_m[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) top = fmax_of(top, lds_m[w]);
+  T total = T(0);
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) total += rescaled(lds_s[w], lds_m[w], top);
+  m = top;
+  s = total;
+}
+
+// Forward: one streaming pass per logits row (non-temporal 16-byte loads,
+// batches of eight per lane) gives the row maximum m and S = sum exp(x - m);
+// then loss = -((x_t - m) - log S), the log-softmax value at the target
+// negated, with log-softmax's operations.  S carries the rescaling roundings
+// of the online sum (a few ulp; log-softmax's tolerance covers it).  The
+// target and its logit are fetched at the start of the row.  Saves m and
+// log S per row for the backward.  A row is undefined when S is NaN or the
+// row has no element above -inf (log-softmax's special cases then apply,
+// from a second read of that row).  An out-of-range target is never read: it
+// sets *invalid.
+template <typename T, typename I, bool VEC>
+__global__ void __launch_bounds__(kEntropyThreads)
+    entropy_forward_kernel(T* losses, T* row_max, T* row_log_sum, int32_t* undefined,
+                           int32_t* invalid, const T* logits, const I* targets, uint64_t rows,
+                           uint64_t classes, TargetMap map) {
+  constexpr int W = VEC ? Vec16<T>::width : 1;
+  constexpr int U = 8;
+  using V = typename Vec16<T>::type;
+  constexpr uint64_t kStep = static_cast<uint64_t>(kEntropyThreads) * W;
+  for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const T* row = logits + r * classes;
+    // lane 0 looks up the target and its logit while the row streams in
+    bool has_target = false;
+    bool target_ok = false;
+    uint64_t output_index = 0;
+    T target_logit = T(0);
+    if (threadIdx.x == 0) {
+      uint64_t target_index;
+      has_target = map.lookup(r, target_index, output_index);
+      if (has_target) {
+        const I target = targets[target_index];
+        target_ok = target >= 0 && static_cast<uint64_t>(target) < classes;
+        if (target_ok) target_logit = row[static_cast<uint64_t>(target)];
+      }
+    }
+    T m = -positive_infinity<T>();
+    T s = T(0);
+    for (uint64_t base = static_cast<uint64_t>(threadIdx.x) * W; base < classes;
+         base += kStep * U) {
+      T x[U * W];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint64_t c = base + u * kStep;
+        if (c < classes) {
+          if constexpr (VEC) {
+            const V v = stream_load(reinterpret_cast<const V*>(row + c));
+#pragma unroll
+            for (int k = 0; k < W; ++k) x[u * W + k] = vec_get<T>(v, k);
+          } else {
+            x[u] = row[c];
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < W; ++k) x[u * W + k] = -positive_infinity<T>();
+        }
+      }
+      T top = m;
+#pragma unroll
+      for (int j = 0; j < U * W; ++j) top = fmax_of(top, x[j]);
+      T batch = T(0);
+#pragma unroll
+      for (int j = 0; j < U * W; ++j) batch += exp_term(x[j], top);
+      s = rescaled(s, m, top) + batch;
+      m = top;
+    }
+    block_online<T, kEntropyThreads>(m, s);
+    const T maximum = m;
+    const bool bad = s != s || maximum == -positive_infinity<T>();
+    SliceStats<T> stats;
+    if (bad) {
+      stats_init(stats);
+      for (uint64_t c = threadIdx.x; c < classes; c += kEntropyThreads) {
+        stats_add(stats, row[c], static_cast<int64_t>(c));
+      }
+      stats = block_stats<T, kEntropyThreads>(stats);
+    }
+    if (threadIdx.x == 0) {
+      const T log_sum = math_log(s);
+      undefined[r] = bad ? 1 : 0;
+      row_max[r] = maximum;
+      row_log_sum[r] = log_sum;
+      if (has_target) {
+        if (!target_ok) {
+          *invalid = 1;
+          losses[output_index] = quiet_nan<T>();
+        } else {
+          const T lp = bad ? undefined_value<T, true>(stats, target_logit)
+                           : (target_logit - maximum) - log_sum;
+          losses[output_index] = -lp;
+        }
+      }
+    }
+  }
+}
+
+// Backward through NLL and log-softmax at once.  The reference's gradient of
+// the selected losses is a zero tensor with g_t = 0 - u at each row's target
+// (u the upstream loss gradient; cross_entropy.cpp:69-81), and log-softmax's
+// backward turns it into dx = g - exp(lp) * s with s = sum of g = g_t
+// (softmax.cpp:406-444).  Here lp = (x - m) - log S is recomputed with the
+// forward's operations, so dx is that expression without either tensor
+// materialised; undefined rows are NaN.  Tiles of 256 x W columns of one row.
+template <typename T, typename I, bool VEC>
+__global__ void __launch_bounds__(kEntropyThreads)
+    entropy_backward_kernel(T* dx, const T* loss_gradient, const T* logits, const T* row_max,
+                            const T* row_log_sum, const int32_t* undefined, const I* targets,
+                            uint64_t rows, uint64_t classes, uint64_t column_tiles,
+                            TargetMap map, bool stream_out) {
+  constexpr int W = VEC ? Vec16<T>::width : 1;
+  using V = typename Vec16<T>::type;
+  const uint64_t tiles = rows * column_tiles;
+  for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const uint64_t r = tile / column_tiles;
+    const uint64_t c = ((tile - r * column_tiles) * kEntropyThreads + threadIdx.x) * W;
+    if (c >= classes) continue;
+    uint64_t target_index, output_index;
+    T g_t = T(0);
+    uint64_t t = classes;  // no target column
+    if (map.lookup(r, target_index, output_index)) {
+      g_t = T(0) - loss_gradient[output_index];
+      t = static_cast<uint64_t>(targets[target_index]);
+    }
+    const bool bad = undefined[r] != 0;
+    const T m = row_max[r];
+    const T log_sum = row_log_sum[r];
+    T values[W];
+    if constexpr (VEC) {
+      const V v = stream_load(reinterpret_cast<const V*>(logits + r * classes + c));
+#pragma unroll
+      for (int k = 0; k < W; ++k) values[k] = vec_get<T>(v, k);
+    } else {
+      values[0] = logits[r * classes + c];
+    }
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const T lp = (values[k] - m) - log_sum;
+      const T g = (c + k == t) ? g_t : T(0);
+      values[k] = bad ? quiet_nan<T>() : g - math_exp(lp) * g_t;
+    }
+    if constexpr (VEC) {
+      V o;
+#pragma unroll
+      for (int k = 0; k < W; ++k) vec_set<T>(o, k, values[k]);
+      V* target = reinterpret_cast<V*>(dx + r * classes + c);
+      if (stream_out) {
+        stream_store(target, o);
+      } else {
+        *target = o;
+      }
+    } else {
+      dx[r * classes + c] = values[0];
+    }
+  }
+}
+
+// The reference's separate NLL kernels (cuda_kernels.cu:313-365), for callers
+// that keep the composed log_softmax -> NLL path.
+template <typename I>
+__global__ void __launch_bounds__(256)
+    validate_targets_kernel(int32_t* invalid, const I* targets, uint64_t count, uint64_t classes) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+       i += stride) {
+    const I target = targets[i];
+    if (target < 0 || static_cast<uint64_t>(target) >= classes) *invalid = 1;
+  }
+}
+
+struct OutputMap {
+  uint64_t sequence_length;  // 0: plain
+  __device__ __forceinline__ void lookup(uint64_t index, uint64_t& target_index,
+                                         uint64_t& source_row) const {
+    if (sequence_length == 0) {
+      target_index = index;
+      source_row = index;
+      return;
+    }
+    const uint64_t prediction = sequence_length - 1;
+    const uint64_t batch = index / prediction;
+    const uint64_t time = index - batch * prediction;
+    target_index = batch * sequence_length + time + 1;
+    source_row = batch * sequence_length + time;
+  }
+};
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256)
+    nll_forward_kernel(T* output, const T* log_probabilities, const I* targets, uint64_t count,
+                       uint64_t classes, OutputMap map) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+       i += stride) {
+    uint64_t target_index, source_row;
+    map.lookup(i, target_index, source_row);
+    output[i] = -log_probabilities[source_row * classes + static_cast<uint64_t>(targets[target_index])];
+  }
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256)
+    nll_backward_kernel(T* output, const T* gradient, const I* targets, uint64_t count,
+                        uint64_t classes, OutputMap map) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+       i += stride) {
+    uint64_t target_index, source_row;
+    map.lookup(i, target_index, source_row);
+    // the CPU path's values[...] -= upstream over a zero tensor (cross_entropy.cpp:78-80)
+    output[source_row * classes + static_cast<uint64_t>(targets[target_index])] = T(0) - gradient[i];
+  }
+}
+
+uint32_t stride_grid(uint64_t count, const DeviceGuard& guard) {
+  uint64_t blocks = (count + 255) / 256;
+  const uint64_t cap = static_cast<uint64_t>(guard.multiprocessors) * 16;
+  if (blocks > cap) blocks = cap;
+  if (blocks == 0) blocks = 1;
+  return static_cast<uint32_t>(blocks);
+}
+
+bool valid_target_dtype(int dtype) { return dtype == SPAR_HIP_INT32 || dtype == SPAR_HIP_INT64; }
+
 bool geometry_ok(uint64_t outer, uint64_t axis_extent, uint64_t inner) {
   if (inner == 0 || outer == 0 || axis_extent == 0) return false;
   if (outer > UINT64_MAX / inner) return false;
@@ -903,6 +1204,251 @@ extern "C" SparHipStatus spar_hip_launch_probability_backward(
     } else {
       backward<double, false>(output, gradient, saved_output, undefined_slices, outer,
                               axis_extent, inner, guard);
+    }
+  }
+  return finish(guard);
+}
+
+namespace {
+
+template <typename T, typename I>
+void launch_entropy_forward(void* losses, void* row_max, void* row_log_sum,
+                            int32_t* undefined_rows, int32_t* invalid, const void* logits,
+                            const void* targets, uint64_t rows, uint64_t classes,
+                            TargetMap map, const DeviceGuard& guard) {
+  const bool vec = classes % Vec16<T>::width == 0 && aligned16(logits);
+  auto launch = [&](auto kernel) {
+    kernel<<<grid_for(rows), kEntropyThreads, 0, guard.stream>>>(
+        static_cast<T*>(losses), static_cast<T*>(row_max), static_cast<T*>(row_log_sum),
+        undefined_rows, invalid, static_cast<const T*>(logits), static_cast<const I*>(targets),
+        rows, classes, map);
+  };
+  if (vec) {
+    launch(entropy_forward_kernel<T, I, true>);
+  } else {
+    launch(entropy_forward_kernel<T, I, false>);
+  }
+}
+
+template <typename T, typename I>
+void launch_entropy_backward(void* logits_gradient, const void* loss_gradient,
+                             const void* logits, const void* row_max, const void* row_log_sum,
+                             const int32_t* undefined_rows, const void* targets, uint64_t rows,
+                             uint64_t classes, TargetMap map, const DeviceGuard& guard) {
+  const bool vec = classes % Vec16<T>::width == 0 && aligned16(logits) &&
+                   aligned16(logits_gradient);
+  const uint64_t width = vec ? Vec16<T>::width : 1;
+  const uint64_t column_tiles = (classes + kEntropyThreads * width - 1) / (kEntropyThreads * width);
+  const bool stream_out = stream_output(rows * classes * sizeof(T));
+  auto launch = [&](auto kernel) {
+    kernel<<<grid_for(rows * column_tiles), kEntropyThreads, 0, guard.stream>>>(
+        static_cast<T*>(logits_gradient), static_cast<const T*>(loss_gradient),
+        static_cast<const T*>(logits), static_cast<const T*>(row_max),
+        static_cast<const T*>(row_log_sum), undefined_rows, static_cast<const I*>(targets), rows,
+        classes, column_tiles, map, stream_out);
+  };
+  if (vec) {
+    launch(entropy_backward_kernel<T, I, true>);
+  } else {
+    launch(entropy_backward_kernel<T, I, false>);
+  }
+}
+
+bool entropy_geometry_ok(uint64_t rows, uint64_t classes, uint64_t sequence_length,
+                         int language_model) {
+  if (rows == 0 || classes == 0 || classes > kIndex32Limit) return false;
+  if (language_model != 0 && language_model != 1) return false;
+  if (language_model) return sequence_length >= 2 && rows % sequence_length == 0;
+  return rows <= UINT64_MAX / classes;
+}
+
+}  // namespace
+
+// Validates class indices: *invalid_target (host memory) becomes 1 if any
+// target is negative or >= classes.  Synchronises.
+extern "C" SparHipStatus spar_hip_validate_targets(int32_t* invalid_target, const void* targets,
+                                                   uint64_t count, uint64_t classes,
+                                                   int target_dtype, int device) {
+  if (invalid_target == nullptr || !valid_target_dtype(target_dtype) || classes == 0 ||
+      (count != 0 && targets == nullptr)) {
+    return invalid();
+  }
+  *invalid_target = 0;
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  void* flag = nullptr;
+  hipError_t error = scratch_allocate(&flag, sizeof(int32_t), device);
+  if (error != hipSuccess) return runtime(error);
+  SparHipStatus status = spar_hip_zero(flag, sizeof(int32_t), device);
+  if (status.code == 0) {
+    if (target_dtype == SPAR_HIP_INT32) {
+      validate_targets_kernel<int32_t><<<stride_grid(count, guard), 256, 0, guard.stream>>>(
+          static_cast<int32_t*>(flag), static_cast<const int32_t*>(targets), count, classes);
+    } else {
+      validate_targets_kernel<int64_t><<<stride_grid(count, guard), 256, 0, guard.stream>>>(
+          static_cast<int32_t*>(flag), static_cast<const int64_t*>(targets), count, classes);
+    }
+    status = finish(guard);
+  }
+  if (status.code == 0) status = spar_hip_copy_device_to_host(invalid_target, flag, sizeof(int32_t), device);
+  scratch_release(flag, device);
+  return status;
+}
+
+extern "C" SparHipStatus spar_hip_launch_nll_forward(void* output, const void* log_probabilities,
+                                                     const void* targets, uint64_t output_count,
+                                                     uint64_t classes, uint64_t sequence_length,
+                                                     int dtype, int target_dtype,
+                                                     int language_model, int device) {
+  if (!valid_float_dtype(dtype) || !valid_target_dtype(target_dtype) || classes == 0 ||
+      (language_model != 0 && language_model != 1) || (language_model && sequence_length < 2) ||
+      (output_count != 0 && (output == nullptr || log_probabilities == nullptr || targets == nullptr))) {
+    return invalid();
+  }
+  if (output_count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const OutputMap map{language_model ? sequence_length : 0};
+  const uint32_t grid = stride_grid(output_count, guard);
+  if (dtype == SPAR_HIP_FLOAT32) {
+    if (target_dtype == SPAR_HIP_INT32) {
+      nll_forward_kernel<float, int32_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<float*>(output), static_cast<const float*>(log_probabilities),
+          static_cast<const int32_t*>(targets), output_count, classes, map);
+    } else {
+      nll_forward_kernel<float, int64_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<float*>(output), static_cast<const float*>(log_probabilities),
+          static_cast<const int64_t*>(targets), output_count, classes, map);
+    }
+  } else {
+    if (target_dtype == SPAR_HIP_INT32) {
+      nll_forward_kernel<double, int32_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<double*>(output), static_cast<const double*>(log_probabilities),
+          static_cast<const int32_t*>(targets), output_count, classes, map);
+    } else {
+      nll_forward_kernel<double, int64_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<double*>(output), static_cast<const double*>(log_probabilities),
+          static_cast<const int64_t*>(targets), output_count, classes, map);
+    }
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_nll_backward(void* output, const void* gradient,
+                                                      const void* targets, uint64_t output_count,
+                                                      uint64_t classes, uint64_t sequence_length,
+                                                      int dtype, int target_dtype,
+                                                      int language_model, int device) {
+  if (!valid_float_dtype(dtype) || !valid_target_dtype(target_dtype) || classes == 0 ||
+      (language_model != 0 && language_model != 1) || (language_model && sequence_length < 2) ||
+      (output_count != 0 && (output == nullptr || gradient == nullptr || targets == nullptr))) {
+    return invalid();
+  }
+  if (output_count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const OutputMap map{language_model ? sequence_length : 0};
+  const uint32_t grid = stride_grid(output_count, guard);
+  if (dtype == SPAR_HIP_FLOAT32) {
+    if (target_dtype == SPAR_HIP_INT32) {
+      nll_backward_kernel<float, int32_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<float*>(output), static_cast<const float*>(gradient),
+          static_cast<const int32_t*>(targets), output_count, classes, map);
+    } else {
+      nll_backward_kernel<float, int64_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<float*>(output), static_cast<const float*>(gradient),
+          static_cast<const int64_t*>(targets), output_count, classes, map);
+    }
+  } else {
+    if (target_dtype == SPAR_HIP_INT32) {
+      nll_backward_kernel<double, int32_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<double*>(output), static_cast<const double*>(gradient),
+          static_cast<const int32_t*>(targets), output_count, classes, map);
+    } else {
+      nll_backward_kernel<double, int64_t><<<grid, 256, 0, guard.stream>>>(
+          static_cast<double*>(output), static_cast<const double*>(gradient),
+          static_cast<const int64_t*>(targets), output_count, classes, map);
+    }
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_cross_entropy_forward(
+    void* losses, void* row_max, void* row_log_sum, int32_t* undefined_rows,
+    int32_t* invalid_target, const void* logits, const void* targets, uint64_t logits_rows,
+    uint64_t classes, uint64_t sequence_length, int dtype, int target_dtype, int language_model,
+    int device) {
+  if (!valid_float_dtype(dtype) || !valid_target_dtype(target_dtype) ||
+      !entropy_geometry_ok(logits_rows, classes, sequence_length, language_model) ||
+      losses == nullptr || row_max == nullptr || row_log_sum == nullptr ||
+      undefined_rows == nullptr || invalid_target == nullptr || logits == nullptr ||
+      targets == nullptr) {
+    return invalid();
+  }
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  SparHipStatus status = spar_hip_zero(invalid_target, sizeof(int32_t), device);
+  if (status.code != 0) return status;
+  const TargetMap map{language_model ? sequence_length : 0};
+  if (dtype == SPAR_HIP_FLOAT32) {
+    if (target_dtype == SPAR_HIP_INT32) {
+      launch_entropy_forward<float, int32_t>(losses, row_max, row_log_sum, undefined_rows,
+                                             invalid_target, logits, targets, logits_rows,
+                                             classes, map, guard);
+    } else {
+      launch_entropy_forward<float, int64_t>(losses, row_max, row_log_sum, undefined_rows,
+                                             invalid_target, logits, targets, logits_rows,
+                                             classes, map, guard);
+    }
+  } else {
+    if (target_dtype == SPAR_HIP_INT32) {
+      launch_entropy_forward<double, int32_t>(losses, row_max, row_log_sum, undefined_rows,
+                                              invalid_target, logits, targets, logits_rows,
+                                              classes, map, guard);
+    } else {
+      launch_entropy_forward<double, int64_t>(losses, row_max, row_log_sum, undefined_rows,
+                                              invalid_target, logits, targets, logits_rows,
+                                              classes, map, guard);
+    }
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_cross_entropy_backward(
+    void* logits_gradient, const void* loss_gradient, const void* logits, const void* row_max,
+    const void* row_log_sum, const int32_t* undefined_rows, const void* targets,
+    uint64_t logits_rows, uint64_t classes, uint64_t sequence_length, int dtype,
+    int target_dtype, int language_model, int device) {
+  if (!valid_float_dtype(dtype) || !valid_target_dtype(target_dtype) ||
+      !entropy_geometry_ok(logits_rows, classes, sequence_length, language_model) ||
+      logits_gradient == nullptr || loss_gradient == nullptr || logits == nullptr ||
+      row_max == nullptr || row_log_sum == nullptr || undefined_rows == nullptr ||
+      targets == nullptr) {
+    return invalid();
+  }
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  const TargetMap map{language_model ? sequence_length : 0};
+  if (dtype == SPAR_HIP_FLOAT32) {
+    if (target_dtype == SPAR_HIP_INT32) {
+      launch_entropy_backward<float, int32_t>(logits_gradient, loss_gradient, logits, row_max,
+                                              row_log_sum, undefined_rows, targets, logits_rows,
+                                              classes, map, guard);
+    } else {
+      launch_entropy_backward<float, int64_t>(logits_gradient, loss_gradient, logits, row_max,
+                                              row_log_sum, undefined_rows, targets, logits_rows,
+                                              classes, map, guard);
+    }
+  } else {
+    if (target_dtype == SPAR_HIP_INT32) {
+      launch_entropy_backward<double, int32_t>(logits_gradient, loss_gradient, logits, row_max,
+                                               row_log_sum, undefined_rows, targets, logits_rows,
+                                               classes, map, guard);
+    } else {
+      launch_entropy_backward<double, int64_t>(logits_gradient, loss_gradient, logits, row_max,
+                                               row_log_sum, undefined_rows, targets, logits_rows,
+                                               classes, map, guard);
     }
   }
   return finish(guard);

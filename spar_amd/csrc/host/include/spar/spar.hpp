@@ -3,6 +3,7 @@
 #pragma once
 
 #include "spar/core.hpp"
+#include "spar/loss.hpp"
 #include "spar/ops.hpp"
 #include "spar/random.hpp"
 #include "spar/tensor.hpp"

@@ -239,6 +239,18 @@ PYBIND11_MODULE(_spar, m) {
           return axis.is_none() ? spar::log_softmax(x) : spar::log_softmax(x, axis.cast<std::size_t>());
         },
         py::arg("input"), py::arg("axis") = py::none());
+  auto loss = m.def_submodule("loss", "spar::loss (src/loss/cross_entropy.cppm)");
+  py::enum_<spar::loss::Reduction>(loss, "Reduction")
+      .value("None_", spar::loss::Reduction::None)
+      .value("Sum", spar::loss::Reduction::Sum)
+      .value("Mean", spar::loss::Reduction::Mean);
+  loss.def("cross_entropy", &spar::loss::cross_entropy, py::arg("logits"), py::arg("targets"),
+           py::arg("reduction") = spar::loss::Reduction::Mean,
+           py::call_guard<py::gil_scoped_release>());
+  loss.def("language_model_cross_entropy", &spar::loss::language_model_cross_entropy,
+           py::arg("logits"), py::arg("token_ids"),
+           py::arg("reduction") = spar::loss::Reduction::Mean,
+           py::call_guard<py::gil_scoped_release>());
   m.def("rms_norm", &spar::rms_norm, py::arg("input"), py::arg("weight"),
         py::arg("epsilon") = 1.0e-5, py::call_guard<py::gil_scoped_release>());
   m.def("layer_norm", &spar::layer_norm, py::arg("input"), py::arg("weight"), py::arg("bias"),

@@ -288,3 +288,64 @@ def test_golden_fixtures():
             assert_bitexact(got, want, case["name"])
         else:
             assert_ulp(got, want, case["tolerance_ulp"], case["name"])
+
+
+def _closed_form_lp(x):
+    x = x.astype(np.float64)
+    z = x - x.max(axis=-1, keepdims=True)
+    return z - np.log(np.exp(z).sum(axis=-1, keepdims=True))
+
+
+@pytest.mark.parametrize("reduction", ["none", "sum", "mean"])
+def test_cross_entropy_restatement_closed_form(reduction):
+    """loss_i = -lp[i, t_i] and dlogits = (softmax - onehot) * dreduce, from
+    float64 closed forms; a dropped sign or a wrong target index fails."""
+    import oracle.reference as R
+
+    rng = np.random.default_rng(70)
+    x = (rng.standard_normal((6, 7, 11)) * 2).astype(np.float32)
+    t = rng.integers(0, 11, (6, 7)).astype(np.int32)
+    logits = R.RTensor.of(x, requires_grad=True)
+    loss = R.cross_entropy(logits, t, reduction)
+    lp = _closed_form_lp(x)
+    per = -np.take_along_axis(lp, t[..., None].astype(np.int64), -1)[..., 0]
+    want = {"none": per, "sum": per.sum(), "mean": per.mean()}[reduction]
+    assert np.allclose(loss.numpy(), want, rtol=2e-6, atol=2e-6)
+    R.sum(loss).backward() if reduction == "none" else loss.backward()
+    onehot = np.zeros_like(lp)
+    np.put_along_axis(onehot, t[..., None].astype(np.int64), 1.0, -1)
+    scale = 1.0 / t.size if reduction == "mean" else 1.0
+    assert np.allclose(logits.grad().numpy(), (np.exp(lp) - onehot) * scale, rtol=2e-5, atol=1e-7)
+
+
+def test_language_model_cross_entropy_restatement_shifts_targets():
+    import oracle.reference as R
+
+    rng = np.random.default_rng(71)
+    x = rng.standard_normal((3, 5, 9)).astype(np.float32)
+    ids = rng.integers(0, 9, (3, 5)).astype(np.int64)
+    logits = R.RTensor.of(x, requires_grad=True)
+    loss = R.language_model_cross_entropy(logits, ids, "none")
+    lp = _closed_form_lp(x)
+    want = -np.take_along_axis(lp[:, :-1], ids[:, 1:, None], -1)[..., 0]
+    assert loss.shape == (3, 4) and np.allclose(loss.numpy(), want, rtol=2e-6, atol=2e-6)
+    R.sum(loss).backward()
+    grad = logits.grad().numpy()
+    assert not grad[:, -1].any(), "the last position has no target"
+    onehot = np.zeros_like(lp[:, :-1])
+    np.put_along_axis(onehot, ids[:, 1:, None], 1.0, -1)
+    assert np.allclose(grad[:, :-1], np.exp(lp[:, :-1]) - onehot, rtol=2e-5, atol=1e-7)
+
+
+def test_cross_entropy_restatement_errors():
+    import oracle.reference as R
+
+    logits = R.RTensor.of(np.zeros((2, 3), np.float32))
+    with pytest.raises(IndexError):
+        R.cross_entropy(logits, np.array([0, 3], np.int64))
+    with pytest.raises(IndexError):
+        R.cross_entropy(logits, np.array([-1, 0], np.int32))
+    with pytest.raises(ValueError):
+        R.cross_entropy(logits, np.array([0.0, 1.0], np.float32))
+    with pytest.raises(ValueError):
+        R.cross_entropy(logits, np.array([0, 1, 2], np.int64))
