@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--suite", action="store_true", help="also measure every config op")
+    p.add_argument("--suite-only", default=None,
+                   help="comma-separated suite sections to run (C1,C3,C4,C5,optim)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-loop", type=int, default=0,
                    help="run only N steps of the workload (for rocprofv3) and exit")
@@ -289,14 +291,14 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(hip, work)
     print(json.dumps(result), flush=True)
-    if args.suite:
+    if args.suite or args.suite_only:
         del work
-        run_suite(hip)
+        run_suite(hip, only=None if args.suite_only is None else args.suite_only.split(","))
 
 
 # ----------------------------------------------------------------- suite
 
-def run_suite(hip, reps=20, warmup=3):
+def run_suite(hip, reps=20, warmup=3, only=None):
     """Times every op of the five benchmark configurations (one JSON line per
     op).  Before each timed launch, outside the timed region, a 512 MiB
     scratch buffer is read with ordinary cached loads (spar_hip_touch): that
@@ -341,181 +343,206 @@ def run_suite(hip, reps=20, warmup=3):
         hip.call("spar_hip_random_uniform", buf.ptr, n, F, seed, low, high, 0)
         return buf
 
-    # C1: contiguous elementwise on [4096, 4096]
-    n = 4096 * 4096
-    a, b, out = normal(n, 1), normal(n, 2), hip.DeviceBuffer(n * 4)
-    for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
-        measure("C1", name, 12 * n, lambda op=op: hip.call(
-            "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0), n)
-    measure("C1", "gelu(a)", 8 * n, lambda: hip.call(
-        "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0), n)
-    # exp(clip(a, -10, 10)): the clip is the identity on this draw (checked here)
-    peak = hip.DeviceBuffer(8)
-    hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
-    for source in (a, out):  # max(a) and max(-a)
-        hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
-        assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
-    measure("C1", "exp(a)", 8 * n, lambda: hip.call(
-        "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0), n)
-    del a, b, out
+    def c1():
+        # C1: contiguous elementwise on [4096, 4096]
+        n = 4096 * 4096
+        a, b, out = normal(n, 1), normal(n, 2), hip.DeviceBuffer(n * 4)
+        for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
+            measure("C1", name, 12 * n, lambda op=op: hip.call(
+                "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0), n)
+        measure("C1", "gelu(a)", 8 * n, lambda: hip.call(
+            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0), n)
+        # exp(clip(a, -10, 10)): the clip is the identity on this draw (checked here)
+        peak = hip.DeviceBuffer(8)
+        hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
+        for source in (a, out):  # max(a) and max(-a)
+            hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
+            assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
+        measure("C1", "exp(a)", 8 * n, lambda: hip.call(
+            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0), n)
+        del a, b, out
 
-    # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
-    R = 8192
-    n = R * R
-    x = normal(n, 3)
-    out = hip.DeviceBuffer(R * 8)
-    codes = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}
-    for axis in (1, 0):
-        for name, code in codes.items():
-            out_bytes = R * (8 if name == "argmax" else 4)
-            measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, lambda code=code, axis=axis: hip.call(
-                "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
-                1 << axis, F, code, 0), n)
-    del x
-    n = 1 << 28
-    v = uniform(n, 4, -1.0, 1.0)
-    for name in ("sum", "mean", "max"):
-        measure("C3", f"full {name} 2^28", 4 * n + 4, lambda name=name: hip.call(
-            "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0), n)
-    del v, out
+    def c3():
+        # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
+        R = 8192
+        n = R * R
+        x = normal(n, 3)
+        out = hip.DeviceBuffer(R * 8)
+        codes = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}
+        for axis in (1, 0):
+            for name, code in codes.items():
+                out_bytes = R * (8 if name == "argmax" else 4)
+                measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, lambda code=code, axis=axis: hip.call(
+                    "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
+                    1 << axis, F, code, 0), n)
+        del x
+        n = 1 << 28
+        v = uniform(n, 4, -1.0, 1.0)
+        for name in ("sum", "mean", "max"):
+            measure("C3", f"full {name} 2^28", 4 * n + 4, lambda name=name: hip.call(
+                "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0), n)
+        del v, out
 
-    # C4: row softmax / log-softmax on [8192, 32768]
-    rows, V = 8192, 32768
-    n = rows * V
-    logits = normal(n, 5, np.sqrt(2.0))
-    grad = normal(n, 6)
-    probs = hip.DeviceBuffer(n * 4)
-    dx = hip.DeviceBuffer(n * 4)
-    undefined = hip.DeviceBuffer(rows * 4)
-    for log in (0, 1):
-        label = "log_softmax" if log else "softmax"
-        measure("C4", f"{label} forward", 8 * n + 4 * rows, lambda log=log: hip.call(
-            "spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows, V, 1,
-            F, log, 0), n)
-        measure("C4", f"{label} backward", 12 * n + 4 * rows, lambda log=log: hip.call(
-            "spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
-            rows, V, 1, F, log, 0), n)
-    # C4 as a loss: cross entropy over the same logits, fused (one read of the
-    # logits forward; one read and one write backward) and composed as the
-    # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
-    # log_softmax backward), with the same targets.
-    targets = hip.DeviceBuffer(rows * 8)
-    hip.call("spar_hip_copy_host_to_device", targets.ptr,
-             np.random.default_rng(9).integers(0, V, rows).astype(np.int64).ctypes.data,
-             rows * 8, 0)
-    losses, row_max, row_log_sum = (hip.DeviceBuffer(rows * 4) for _ in range(3))
-    invalid = hip.DeviceBuffer(4)
-    loss_grad = uniform(rows, 10, 0.5, 1.5)
-    small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
-    measure("C4", "cross_entropy forward (fused)", 4 * n + small, lambda: hip.call(
-        "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
-        undefined.ptr, invalid.ptr, logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
-    measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, lambda: hip.call(
-        "spar_hip_launch_cross_entropy_backward", dx.ptr, loss_grad.ptr, logits.ptr, row_max.ptr,
-        row_log_sum.ptr, undefined.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
+    def c4():
+        # C4: row softmax / log-softmax on [8192, 32768]
+        rows, V = 8192, 32768
+        n = rows * V
+        logits = normal(n, 5, np.sqrt(2.0))
+        grad = normal(n, 6)
+        probs = hip.DeviceBuffer(n * 4)
+        dx = hip.DeviceBuffer(n * 4)
+        undefined = hip.DeviceBuffer(rows * 4)
+        for log in (0, 1):
+            label = "log_softmax" if log else "softmax"
+            measure("C4", f"{label} forward", 8 * n + 4 * rows, lambda log=log: hip.call(
+                "spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows, V, 1,
+                F, log, 0), n)
+            measure("C4", f"{label} backward", 12 * n + 4 * rows, lambda log=log: hip.call(
+                "spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
+                rows, V, 1, F, log, 0), n)
+        # C4 as a loss: cross entropy over the same logits, fused (one read of the
+        # logits forward; one read and one write backward) and composed as the
+        # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
+        # log_softmax backward), with the same targets.
+        targets = hip.DeviceBuffer(rows * 8)
+        hip.call("spar_hip_copy_host_to_device", targets.ptr,
+                 np.random.default_rng(9).integers(0, V, rows).astype(np.int64).ctypes.data,
+                 rows * 8, 0)
+        losses, row_max, row_log_sum = (hip.DeviceBuffer(rows * 4) for _ in range(3))
+        invalid = hip.DeviceBuffer(4)
+        loss_grad = uniform(rows, 10, 0.5, 1.5)
+        small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
+        measure("C4", "cross_entropy forward (fused)", 4 * n + small, lambda: hip.call(
+            "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
+            undefined.ptr, invalid.ptr, logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
+        measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, lambda: hip.call(
+            "spar_hip_launch_cross_entropy_backward", dx.ptr, loss_grad.ptr, logits.ptr, row_max.ptr,
+            row_log_sum.ptr, undefined.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
 
-    def composed_forward():
-        hip.call("spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows,
-                 V, 1, F, 1, 0)
-        hip.call("spar_hip_launch_nll_forward", losses.ptr, probs.ptr, targets.ptr, rows, V, 0, F,
-                 hip.INT64, 0, 0)
+        def composed_forward():
+            hip.call("spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows,
+                     V, 1, F, 1, 0)
+            hip.call("spar_hip_launch_nll_forward", losses.ptr, probs.ptr, targets.ptr, rows, V, 0, F,
+                     hip.INT64, 0, 0)
 
-    def composed_backward():
-        hip.call("spar_hip_zero", grad.ptr, n * 4, 0)
-        hip.call("spar_hip_launch_nll_backward", grad.ptr, loss_grad.ptr, targets.ptr, rows, V, 0,
-                 F, hip.INT64, 0, 0)
-        hip.call("spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
-                 rows, V, 1, F, 1, 0)
+        def composed_backward():
+            hip.call("spar_hip_zero", grad.ptr, n * 4, 0)
+            hip.call("spar_hip_launch_nll_backward", grad.ptr, loss_grad.ptr, targets.ptr, rows, V, 0,
+                     F, hip.INT64, 0, 0)
+            hip.call("spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
+                     rows, V, 1, F, 1, 0)
 
-    # reported against the fused kernels' bytes, so the ratio is the speed-up
-    measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
-            composed_forward, n)
-    measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
-            composed_backward, n)
-    del logits, grad, probs, dx, undefined, targets, losses, row_max, row_log_sum, invalid, loss_grad
+        # reported against the fused kernels' bytes, so the ratio is the speed-up
+        measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
+                composed_forward, n)
+        measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
+                composed_backward, n)
+        del logits, grad, probs, dx, undefined, targets, losses, row_max, row_log_sum, invalid, loss_grad
 
-    # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
-    # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a
-    # [4608,9216] base, through the Tensor API: each op's events bracket its
-    # host-side dispatch and allocation as well as its kernels.  Then
-    # loss = sum(y * G) and loss.backward() into base, gamma and beta.
-    from spar_amd import spar
+    def c5():
+        # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
+        # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a
+        # [4608,9216] base, through the Tensor API: each op's events bracket its
+        # host-side dispatch and allocation as well as its kernels.  Then
+        # loss = sum(y * G) and loss.backward() into base, gamma and beta.
+        from spar_amd import spar
 
-    device = spar.Device.hip(0)
-    f32 = spar.DType.float32
-    rows, cols = 4096, 8192
-    n = rows * cols
-    T = 4 * n  # bytes of one full-tensor read or write
-    rng = spar.Random(7)
-    gamma = spar.random_uniform([cols], f32, rng, 0.5, 1.5, device)
-    beta = spar.random_uniform([cols], f32, rng, -0.1, 0.1, device)
-    G = spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device)
-    bases = {"transposed": spar.random_normal([8192, 4096], f32, rng, 0.0, 1.0, device),
-             "sliced": spar.random_normal([4608, 9216], f32, rng, 0.0, 1.0, device)}
-    for leaf in (gamma, beta, *bases.values()):
-        leaf.set_requires_grad(True)
+        device = spar.Device.hip(0)
+        f32 = spar.DType.float32
+        rows, cols = 4096, 8192
+        n = rows * cols
+        T = 4 * n  # bytes of one full-tensor read or write
+        rng = spar.Random(7)
+        gamma = spar.random_uniform([cols], f32, rng, 0.5, 1.5, device)
+        beta = spar.random_uniform([cols], f32, rng, -0.1, 0.1, device)
+        G = spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device)
+        bases = {"transposed": spar.random_normal([8192, 4096], f32, rng, 0.0, 1.0, device),
+                 "sliced": spar.random_normal([4608, 9216], f32, rng, 0.0, 1.0, device)}
+        for leaf in (gamma, beta, *bases.values()):
+            leaf.set_requires_grad(True)
 
-    def view_of(label):
-        base = bases[label]
-        return base.transpose(0, 1) if label == "transposed" else base.narrow(0, 256, rows).narrow(1, 512, cols)
+        def view_of(label):
+            base = bases[label]
+            return base.transpose(0, 1) if label == "transposed" else base.narrow(0, 256, rows).narrow(1, 512, cols)
 
-    def forward(x):
-        mu = spar.mean(x, [1], True)
-        xc = spar.subtract(x, mu)
-        var = spar.mean(spar.square(xc), [1], True)
-        xhat = spar.divide(xc, spar.sqrt(spar.add_scalar(var, 1e-5)))
-        y = spar.add(spar.multiply(xhat, gamma), beta)
-        return spar.sum(spar.multiply(y, G), None, False)
+        def forward(x):
+            mu = spar.mean(x, [1], True)
+            xc = spar.subtract(x, mu)
+            var = spar.mean(spar.square(xc), [1], True)
+            xhat = spar.divide(xc, spar.sqrt(spar.add_scalar(var, 1e-5)))
+            y = spar.add(spar.multiply(xhat, gamma), beta)
+            return spar.sum(spar.multiply(y, G), None, False)
 
-    for label in bases:
-        x = view_of(label)
-        mu = spar.mean(x, [1], True)
-        measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows, lambda: spar.mean(x, [1], True), n)
-        measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows, lambda: spar.subtract(x, mu), n)
-        xc = spar.subtract(x, mu)
-        measure("C5", f"square(xc) {label}", 2 * T, lambda: spar.square(xc), n)
-        sq = spar.square(xc)
-        measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows, lambda: spar.mean(sq, [1], True), n)
-        var = spar.mean(sq, [1], True)
-        sd = spar.sqrt(spar.add_scalar(var, 1e-5))
-        measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows, lambda: spar.divide(xc, sd), n)
-        xhat = spar.divide(xc, sd)
-        measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols, lambda: spar.multiply(xhat, gamma), n)
-        yg = spar.multiply(xhat, gamma)
-        measure("C5", f"+beta {label}", 2 * T + 4 * cols, lambda: spar.add(yg, beta), n)
-        y = spar.add(yg, beta)
-        measure("C5", f"y*G {label}", 3 * T, lambda: spar.multiply(y, G), n)
-        yG = spar.multiply(y, G)
-        measure("C5", f"sum(y*G) {label}", T + 4, lambda: spar.sum(yG, None, False), n)
-        del mu, xc, sq, var, sd, xhat, yg, y, yG
-        # Whole forward, then backward.  Both are reported against the fused
-        # minimum: forward reads x and G once (the loss is a scalar);
-        # backward reads x and G and writes dx (gamma, beta grads are small).
-        measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T, lambda: forward(x), n)
-        losses = []
+        for label in bases:
+            x = view_of(label)
+            mu = spar.mean(x, [1], True)
+            measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows, lambda: spar.mean(x, [1], True), n)
+            measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows, lambda: spar.subtract(x, mu), n)
+            xc = spar.subtract(x, mu)
+            measure("C5", f"square(xc) {label}", 2 * T, lambda: spar.square(xc), n)
+            sq = spar.square(xc)
+            measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows, lambda: spar.mean(sq, [1], True), n)
+            var = spar.mean(sq, [1], True)
+            sd = spar.sqrt(spar.add_scalar(var, 1e-5))
+            measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows, lambda: spar.divide(xc, sd), n)
+            xhat = spar.divide(xc, sd)
+            measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols, lambda: spar.multiply(xhat, gamma), n)
+            yg = spar.multiply(xhat, gamma)
+            measure("C5", f"+beta {label}", 2 * T + 4 * cols, lambda: spar.add(yg, beta), n)
+            y = spar.add(yg, beta)
+            measure("C5", f"y*G {label}", 3 * T, lambda: spar.multiply(y, G), n)
+            yG = spar.multiply(y, G)
+            measure("C5", f"sum(y*G) {label}", T + 4, lambda: spar.sum(yG, None, False), n)
+            del mu, xc, sq, var, sd, xhat, yg, y, yG
+            # Whole forward, then backward.  Both are reported against the fused
+            # minimum: forward reads x and G once (the loss is a scalar);
+            # backward reads x and G and writes dx (gamma, beta grads are small).
+            measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T, lambda: forward(x), n)
+            losses = []
 
-        def prepare():
-            for leaf in (gamma, beta, bases[label]):
-                leaf.zero_grad()
-            losses[:] = [forward(view_of(label))]
+            def prepare():
+                for leaf in (gamma, beta, bases[label]):
+                    leaf.zero_grad()
+                losses[:] = [forward(view_of(label))]
 
-        measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
-                lambda: losses[0].backward(), n, prepare=prepare)
+            measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
+                    lambda: losses[0].backward(), n, prepare=prepare)
 
-        # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
-        # first made contiguous, inside the timed op.
-        measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
-                lambda: spar.layer_norm(x, gamma, beta, 1e-5), n)
+            # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
+            # first made contiguous, inside the timed op.
+            measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
+                    lambda: spar.layer_norm(x, gamma, beta, 1e-5), n)
 
-        def prepare_fused():
-            for leaf in (gamma, beta, bases[label]):
-                leaf.zero_grad()
-            y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
-            losses[:] = [spar.sum(spar.multiply(y, G), None, False)]
+            def prepare_fused():
+                for leaf in (gamma, beta, bases[label]):
+                    leaf.zero_grad()
+                y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
+                losses[:] = [spar.sum(spar.multiply(y, G), None, False)]
 
-        measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
-                lambda: losses[0].backward(), n, prepare=prepare_fused)
-        del losses
+            measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
+                    lambda: losses[0].backward(), n, prepare=prepare_fused)
+            del losses
+
+    def optim():
+        # Optimizer: one AdamW step, the gradient-norm summary and the clip scaling
+        # over GPT-2 small's 124,439,808 fp32 parameters held as one flat buffer.
+        n = 124_439_808
+        p, g = normal(n, 81), normal(n, 82, 1e-2)
+        m, v = normal(n, 83, 1e-3), uniform(n, 84, 0.0, 1e-5)
+        summary = hip.DeviceBuffer(64)
+        c1, c2 = 1.0 - 0.9 ** 1000, 1.0 - 0.95 ** 1000
+        measure("optim", "adamw step (fp32, double math)", 28 * n, lambda: hip.call(
+            "spar_hip_launch_adamw", p.ptr, g.ptr, m.ptr, v.ptr, n, F, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+            c1, c2, 0), n)
+        measure("optim", "gradient norm summary", 4 * n, lambda: hip.call(
+            "spar_hip_launch_gradient_norm_summary", summary.ptr, g.ptr, n, F, 0), n)
+        measure("optim", "scale gradients in place", 8 * n, lambda: hip.call(
+            "spar_hip_launch_scale_in_place", g.ptr, n, F, 1.0, 0), n)
+
+    sections = {"C1": c1, "C3": c3, "C4": c4, "C5": c5, "optim": optim}
+    for name, section in sections.items():
+        if only is None or name in only:
+            section()
 
 
 if __name__ == "__main__":

@@ -109,6 +109,18 @@ struct SparHipMemoryStats {
   uint64_t cache_hits;        /* allocations served from a free list         */
 };
 
+/* Summary of a gradient's sum of squares; replaces struct SparCudaNormSummary
+ * (cuda_kernels.hpp:99-104), same fields and layout: the norm is
+ * scale * sqrt(scaled_sum_squares) over the finite elements, with scale the
+ * largest finite magnitude ({0, 1} when there is none), and the flags record
+ * infinities and NaNs (training/gradients.cpp:27-97). */
+struct SparHipNormSummary {
+  double scale;
+  double scaled_sum_squares;
+  int has_infinity;
+  int has_nan;
+};
+
 /* ---------------------------------------------------------------- runtime */
 
 /* Number of visible HIP devices (replaces the cudaGetDeviceCount check in
@@ -392,6 +404,44 @@ struct SparHipStatus spar_hip_launch_cross_entropy_backward(
     const void* row_log_sum, const int32_t* undefined_rows, const void* targets,
     uint64_t logits_rows, uint64_t classes, uint64_t sequence_length, int dtype,
     int target_dtype, int language_model, int device);
+
+/* ---------------------------------------------- optimizer and gradient norm */
+
+/* Summary of `count` contiguous gradient elements (Float32 or Float64) into
+ * *host_summary.  Synchronises.  The same function as the reference's
+ * StableSumSquares over the elements up to rounding (the reference's own
+ * CUDA kernel combines in another order than its CPU loop too).  Replaces
+ * spar_cuda_gradient_norm_summary (cuda_kernels.hpp:118-120). */
+struct SparHipStatus spar_hip_gradient_norm_summary(struct SparHipNormSummary* host_summary,
+                                                    const void* gradient, uint64_t count,
+                                                    int dtype, int device);
+
+/* The same summary written to *summary in device memory on the device's
+ * stream, without synchronising, so a caller can summarise many gradients and
+ * read them back with one copy (no reference counterpart; the reference
+ * synchronises per gradient, training/gradients.cpp:119). */
+struct SparHipStatus spar_hip_launch_gradient_norm_summary(struct SparHipNormSummary* summary,
+                                                           const void* gradient, uint64_t count,
+                                                           int dtype, int device);
+
+/* values[i] = (T)((double)values[i] * factor) in place; factor must be
+ * finite.  Replaces spar_cuda_launch_scale_in_place (cuda_kernels.hpp:121-122). */
+struct SparHipStatus spar_hip_launch_scale_in_place(void* values, uint64_t count, int dtype,
+                                                    double factor, int device);
+
+/* One AdamW step over `count` contiguous elements, in place on the parameter
+ * and both moments, with the bias corrections 1 - beta^step supplied by the
+ * caller: per element, in double, m = (T)(beta1 m + (1 - beta1) g),
+ * v = (T)(beta2 v + (1 - beta2) g g), p = (T)(p (1 - lr wd) -
+ * lr (m / c1) / (sqrt(v / c2) + eps)), each operation rounded as written
+ * (optim/adamw.cpp:37-61), so results are the CPU path's bits.  Replaces
+ * spar_cuda_launch_adamw (cuda_kernels.hpp:123-128). */
+struct SparHipStatus spar_hip_launch_adamw(void* parameter, const void* gradient,
+                                           void* first_moment, void* second_moment,
+                                           uint64_t count, int dtype, double learning_rate,
+                                           double beta1, double beta2, double epsilon,
+                                           double weight_decay, double first_correction,
+                                           double second_correction, int device);
 
 /* ------------------------------------------------------ random generation */
 

@@ -45,6 +45,7 @@ def _signatures():
         ("spar_oracle_uniform_float", ctypes.c_float, [_U64P]),
         ("spar_oracle_uniform_double", _D, [_U64P]),
         ("spar_oracle_strided_copy", None, [_P, _P, _U64, _U64, _U64P, _U64P, _U64]),
+        ("spar_oracle_adamw_correction", _D, [_D, _U64]),
     ]
     for suffix, scalar in (("f32", ctypes.c_float), ("f64", ctypes.c_double)):
         sigs += [
@@ -68,6 +69,9 @@ def _signatures():
             (f"spar_oracle_softmax_full_backward_{suffix}", None, [_P, _P, _P, _U64, _I]),
             (f"spar_oracle_log_softmax_{suffix}", None, [_P, _P, _P, _U64, _U64P, _U64P, _U64, _I64]),
             (f"spar_oracle_log_softmax_backward_{suffix}", None, [_P, _P, _P, _P, _U64, _U64, _U64]),
+            (f"spar_oracle_adamw_{suffix}", None, [_P, _P, _P, _P, _U64, _D, _D, _D, _D, _D, _D, _D]),
+            (f"spar_oracle_sum_squares_add_{suffix}", None, [_P, _P, _P, _U64]),
+            (f"spar_oracle_scale_{suffix}", None, [_P, _U64, _D]),
         ]
     return sigs
 

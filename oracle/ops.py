@@ -8,6 +8,7 @@ and returns a new contiguous array.
 from __future__ import annotations
 
 import ctypes
+import math
 
 import numpy as np
 
@@ -229,3 +230,89 @@ class Random:
         fn("spar_oracle_random_normal", dtype)(ptr(out), out.size, ctypes.byref(self.state),
                                                float(mean), float(stddev))
         return out
+
+
+# ------------------------------------------------ optimizer and gradient norm
+
+def adamw_correction(beta: float, step: int) -> float:
+    """1 - beta^step (optim/adamw.cpp:48-49), with the C library's pow."""
+    return float(lib().spar_oracle_adamw_correction(float(beta), int(step)))
+
+
+def adamw(parameter: np.ndarray, gradient: np.ndarray, first: np.ndarray, second: np.ndarray,
+          learning_rate: float, beta1: float, beta2: float, epsilon: float, weight_decay: float,
+          first_correction: float, second_correction: float) -> None:
+    """update_values (optim/adamw.cpp:37-61) in place on contiguous arrays."""
+    for a in (parameter, gradient, first, second):
+        if not a.flags.c_contiguous or a.dtype != parameter.dtype or a.size != parameter.size:
+            raise ValueError("adamw takes contiguous arrays of one dtype and size")
+    fn("spar_oracle_adamw", parameter.dtype)(
+        ptr(parameter), ptr(gradient), ptr(first), ptr(second), parameter.size,
+        float(learning_rate), float(beta1), float(beta2), float(epsilon), float(weight_decay),
+        float(first_correction), float(second_correction))
+
+
+class SumSquares:
+    """StableSumSquares (training/gradients.cpp:28-88): `add` feeds elements in
+    order through the C loop; `combine` and `norm` are the host-side rules."""
+
+    def __init__(self):
+        self.state = np.array([0.0, 1.0], np.float64)
+        self.flags = np.zeros(2, np.int32)
+
+    @property
+    def scale(self) -> float:
+        return float(self.state[0])
+
+    @property
+    def scaled_sum_squares(self) -> float:
+        return float(self.state[1])
+
+    @property
+    def has_infinity(self) -> bool:
+        return bool(self.flags[0])
+
+    @property
+    def has_nan(self) -> bool:
+        return bool(self.flags[1])
+
+    def add(self, values: np.ndarray) -> "SumSquares":
+        values = np.ascontiguousarray(values)
+        fn("spar_oracle_sum_squares_add", values.dtype)(ptr(self.state), ptr(self.flags),
+                                                        ptr(values), values.size)
+        return self
+
+    def combine(self, scale: float, scaled_sum_squares: float, has_infinity: bool,
+                has_nan: bool) -> "SumSquares":
+        """gradients.cpp:57-77."""
+        self.flags[1] |= int(bool(has_nan))
+        self.flags[0] |= int(bool(has_infinity))
+        if scale == 0.0:
+            return self
+        if self.state[0] == 0.0:
+            self.state[:] = (scale, scaled_sum_squares)
+            return self
+        mine, total = self.state[0], self.state[1]
+        if mine < scale:
+            ratio = mine / scale
+            self.state[:] = (scale, scaled_sum_squares + total * ratio * ratio)
+        else:
+            ratio = scale / mine
+            self.state[1] = total + scaled_sum_squares * ratio * ratio
+        return self
+
+    def norm(self) -> float:
+        """gradients.cpp:79-87."""
+        if self.has_nan:
+            return math.nan
+        if self.has_infinity:
+            return math.inf
+        scale = float(self.state[0])
+        return 0.0 if scale == 0.0 else scale * math.sqrt(float(self.state[1]))
+
+
+def scale(values: np.ndarray, factor: float) -> None:
+    """scale_gradient (training/gradients.cpp:97-101) in place."""
+    if not values.flags.c_contiguous:
+        raise ValueError("scale takes a contiguous array")
+    fn("spar_oracle_scale", values.dtype)(ptr(values), values.size, float(factor))

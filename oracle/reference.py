@@ -676,3 +676,70 @@ def language_model_cross_entropy(logits: RTensor, token_ids: np.ndarray,
             np.arange(sequence - 1, dtype=np.int64)[None, :]).reshape(-1)
     lp = log_softmax(logits, 2)
     return _reduce_loss(_select_nll(lp, targets, rows, (batch, sequence - 1)), reduction)
+
+
+# ------------------------------------------------ optimizer and gradient norm
+#
+# Parameters are given by their gradient arrays (None for a Parameter without
+# a gradient) and value arrays; the logic below is the CPU path of
+# training/gradients.cpp and optim/adamw.cpp on them.
+
+def global_grad_norm(gradients) -> float:
+    """global_grad_norm, CPU path (training/gradients.cpp:105-137): one
+    StableSumSquares fed every element of every active gradient in order."""
+    accumulator = C.SumSquares()
+    for gradient in gradients:
+        if gradient is not None:
+            accumulator.add(gradient)
+    return accumulator.norm()
+
+
+def scale_gradients(gradients, factor: float) -> None:
+    """scale_gradients, CPU path (training/gradients.cpp:139-174), in place."""
+    if not math.isfinite(factor):
+        raise ValueError("Gradient scale factor must be finite")
+    for gradient in gradients:
+        if gradient is not None:
+            C.scale(gradient, factor)
+
+
+def clip_grad_norm(gradients, max_norm: float):
+    """clip_grad_norm (training/gradients.cpp:176-190): (total_norm, scale,
+    clipped), scaling the gradients in place when clipped."""
+    if not math.isfinite(max_norm) or max_norm < 0.0:
+        raise ValueError("Maximum gradient norm must be finite and nonnegative")
+    total = global_grad_norm(gradients)
+    if not math.isfinite(total):
+        raise RuntimeError("Cannot clip nonfinite gradients")
+    if total == 0.0 or total <= max_norm:
+        return total, 1.0, False
+    factor = max_norm / total
+    scale_gradients(gradients, factor)
+    return total, factor, True
+
+
+class AdamW:
+    """AdamW, CPU path (optim/adamw.cpp:67-170): per-parameter moments (zeros
+    of the parameter's dtype on first use) and step counters; `step` updates
+    each parameter array with a gradient in place."""
+
+    def __init__(self, parameters, learning_rate=1.0e-3, beta1=0.9, beta2=0.999,
+                 epsilon=1.0e-8, weight_decay=0.01):
+        self.parameters = list(parameters)
+        self.learning_rate = learning_rate
+        self.beta1, self.beta2 = beta1, beta2
+        self.epsilon, self.weight_decay = epsilon, weight_decay
+        self.states = [None] * len(self.parameters)
+
+    def step(self, gradients) -> None:
+        for index, (value, gradient) in enumerate(zip(self.parameters, gradients)):
+            if gradient is None:
+                continue
+            if self.states[index] is None:
+                self.states[index] = [np.zeros_like(value), np.zeros_like(value), 0]
+            state = self.states[index]
+            state[2] += 1
+            C.adamw(value, np.ascontiguousarray(gradient, value.dtype), state[0], state[1],
+                    self.learning_rate, self.beta1, self.beta2, self.epsilon, self.weight_decay,
+                    C.adamw_correction(self.beta1, state[2]),
+                    C.adamw_correction(self.beta2, state[2]))

@@ -110,6 +110,11 @@ void spar_oracle_random_normal_f64(double* out, uint64_t count, uint64_t* state,
 
 /* ------------------------------------------------------------ layouts */
 
+/* optim/adamw.cpp:48-49 */
+double spar_oracle_adamw_correction(double beta, uint64_t step) {
+  return 1.0 - pow(beta, (double)step);
+}
+
 /* Tensor::materialize_cpu_logical (core/tensor.cpp:142-167), by payload size. */
 void spar_oracle_strided_copy(void* out, const void* base, uint64_t element_size, uint64_t rank,
                               const uint64_t* extents, const uint64_t* strides, uint64_t offset) {

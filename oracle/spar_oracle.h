@@ -19,6 +19,8 @@ void spar_oracle_random_uniform_f32(float* out, uint64_t count, uint64_t* state,
 void spar_oracle_random_uniform_f64(double* out, uint64_t count, uint64_t* state, double low, double high);
 void spar_oracle_random_normal_f32(float* out, uint64_t count, uint64_t* state, double mean, double stddev);
 void spar_oracle_random_normal_f64(double* out, uint64_t count, uint64_t* state, double mean, double stddev);
+/* 1 - beta^step, the AdamW bias correction (optim/adamw.cpp:48-49). */
+double spar_oracle_adamw_correction(double beta, uint64_t step);
 void spar_oracle_strided_copy(void* out, const void* base, uint64_t element_size, uint64_t rank,
                               const uint64_t* extents, const uint64_t* strides, uint64_t offset);
 

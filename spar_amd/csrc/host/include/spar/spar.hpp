@@ -5,5 +5,6 @@
 #include "spar/core.hpp"
 #include "spar/loss.hpp"
 #include "spar/ops.hpp"
+#include "spar/optim.hpp"
 #include "spar/random.hpp"
 #include "spar/tensor.hpp"

@@ -251,6 +251,61 @@ PYBIND11_MODULE(_spar, m) {
            py::arg("logits"), py::arg("token_ids"),
            py::arg("reduction") = spar::loss::Reduction::Mean,
            py::call_guard<py::gil_scoped_release>());
+  auto nn = m.def_submodule("nn", "spar::nn::Parameter (src/nn/parameter.cppm)");
+  py::class_<spar::nn::Parameter>(nn, "Parameter")
+      .def(py::init<Tensor>(), py::arg("initial_value"))
+      .def("tensor", &spar::nn::Parameter::tensor)
+      .def("requires_grad", &spar::nn::Parameter::requires_grad)
+      .def("shares_identity_with", &spar::nn::Parameter::shares_identity_with)
+      .def("set_requires_grad", &spar::nn::Parameter::set_requires_grad, py::arg("enabled"))
+      .def("has_grad", &spar::nn::Parameter::has_grad)
+      .def("grad", &spar::nn::Parameter::grad)
+      .def("zero_grad", &spar::nn::Parameter::zero_grad)
+      .def("clone", &spar::nn::Parameter::clone);
+  auto training = m.def_submodule("training", "spar::training (src/training/gradients.cppm)");
+  py::class_<spar::training::ClipGradNormResult>(training, "ClipGradNormResult")
+      .def_readonly("total_norm", &spar::training::ClipGradNormResult::total_norm)
+      .def_readonly("scale", &spar::training::ClipGradNormResult::scale)
+      .def_readonly("clipped", &spar::training::ClipGradNormResult::clipped);
+  training.def("global_grad_norm", [](std::vector<spar::nn::Parameter> parameters) {
+    py::gil_scoped_release release;
+    return spar::training::global_grad_norm(parameters);
+  }, py::arg("parameters"));
+  training.def("scale_gradients", [](std::vector<spar::nn::Parameter> parameters, double factor) {
+    py::gil_scoped_release release;
+    spar::training::scale_gradients(parameters, factor);
+  }, py::arg("parameters"), py::arg("factor"));
+  training.def("clip_grad_norm", [](std::vector<spar::nn::Parameter> parameters, double max_norm) {
+    py::gil_scoped_release release;
+    return spar::training::clip_grad_norm(parameters, max_norm);
+  }, py::arg("parameters"), py::arg("max_norm"));
+  auto optim = m.def_submodule("optim", "spar::optim::AdamW (src/optim/adamw.cppm)");
+  py::class_<spar::optim::AdamWParameterState>(optim, "AdamWParameterState")
+      .def(py::init([](Tensor first, Tensor second, std::uint64_t step) {
+             return spar::optim::AdamWParameterState{std::move(first), std::move(second), step};
+           }),
+           py::arg("first_moment"), py::arg("second_moment"), py::arg("step"))
+      .def_readwrite("first_moment", &spar::optim::AdamWParameterState::first_moment)
+      .def_readwrite("second_moment", &spar::optim::AdamWParameterState::second_moment)
+      .def_readwrite("step", &spar::optim::AdamWParameterState::step);
+  py::class_<spar::optim::AdamW>(optim, "AdamW")
+      .def(py::init<std::vector<spar::nn::Parameter>, double, double, double, double, double>(),
+           py::arg("parameters") = std::vector<spar::nn::Parameter>{},
+           py::arg("learning_rate") = 1.0e-3, py::arg("beta1") = 0.9, py::arg("beta2") = 0.999,
+           py::arg("epsilon") = 1.0e-8, py::arg("weight_decay") = 0.01)
+      .def("step", &spar::optim::AdamW::step, py::call_guard<py::gil_scoped_release>())
+      .def("zero_grad", &spar::optim::AdamW::zero_grad)
+      .def("parameter_count", &spar::optim::AdamW::parameter_count)
+      .def("learning_rate", &spar::optim::AdamW::learning_rate)
+      .def("set_learning_rate", &spar::optim::AdamW::set_learning_rate, py::arg("learning_rate"))
+      .def("beta1", &spar::optim::AdamW::beta1)
+      .def("beta2", &spar::optim::AdamW::beta2)
+      .def("epsilon", &spar::optim::AdamW::epsilon)
+      .def("weight_decay", &spar::optim::AdamW::weight_decay)
+      .def("tracks", &spar::optim::AdamW::tracks, py::arg("parameter"))
+      .def("parameter_state", &spar::optim::AdamW::parameter_state, py::arg("parameter"))
+      .def("set_parameter_state", &spar::optim::AdamW::set_parameter_state, py::arg("parameter"),
+           py::arg("state"));
   m.def("rms_norm", &spar::rms_norm, py::arg("input"), py::arg("weight"),
         py::arg("epsilon") = 1.0e-5, py::call_guard<py::gil_scoped_release>());
   m.def("layer_norm", &spar::layer_norm, py::arg("input"), py::arg("weight"), py::arg("bias"),

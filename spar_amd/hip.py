@@ -43,6 +43,11 @@ class MemoryStats(ctypes.Structure):
                 ("cache_hits", ctypes.c_uint64)]
 
 
+class NormSummary(ctypes.Structure):
+    _fields_ = [("scale", ctypes.c_double), ("scaled_sum_squares", ctypes.c_double),
+                ("has_infinity", ctypes.c_int), ("has_nan", ctypes.c_int)]
+
+
 class HipError(RuntimeError):
     def __init__(self, name: str, status: Status, message: str):
         super().__init__(f"{name} failed: {message} (code {status.code}, hip error {status.hip_error})")
@@ -102,6 +107,10 @@ SIGNATURES = {
                                               _I, _I],
     "spar_hip_launch_cross_entropy_backward": [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _U64, _I,
                                                _I, _I, _I],
+    "spar_hip_gradient_norm_summary": [ctypes.POINTER(NormSummary), _P, _U64, _I, _I],
+    "spar_hip_launch_gradient_norm_summary": [_P, _P, _U64, _I, _I],
+    "spar_hip_launch_scale_in_place": [_P, _U64, _I, _D, _I],
+    "spar_hip_launch_adamw": [_P, _P, _P, _P, _U64, _I, _D, _D, _D, _D, _D, _D, _D, _I],
     "spar_hip_random_uniform": [_P, _U64, _I, _U64, _D, _D, _I],
     "spar_hip_random_normal": [_P, _U64, _I, _U64, _D, _D, _I],
 }

@@ -349,3 +349,155 @@ def test_cross_entropy_restatement_errors():
         R.cross_entropy(logits, np.array([0.0, 1.0], np.float32))
     with pytest.raises(ValueError):
         R.cross_entropy(logits, np.array([0, 1, 2], np.int64))
+
+
+# ------------------------------------------------ optimizer and gradient norm
+#
+# The reference has no fixtures for these either.  AdamW is pinned against
+# torch.optim.AdamW in float64 (the same decoupled-decay algorithm written
+# with different but mathematically equal operations) and closed forms; the
+# norm accumulator against numpy's L2 norm, exact maxima and the documented
+# special cases; scaling against exact rational arithmetic.
+
+def _torch_adamw(p, grads, lr, b1, b2, eps, wd):
+    import torch
+
+    t = torch.tensor(p, dtype=torch.float64, requires_grad=True)
+    opt = torch.optim.AdamW([t], lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd,
+                            foreach=False)
+    for g in grads:
+        t.grad = torch.tensor(g, dtype=torch.float64)
+        opt.step()
+    return t.detach().numpy()
+
+
+@pytest.mark.parametrize("lr,b1,b2,eps,wd", [(1e-3, 0.9, 0.999, 1e-8, 0.01),
+                                             (0.05, 0.5, 0.9, 1e-6, 0.1),
+                                             (0.01, 0.0, 0.0, 1e-3, 0.0)])
+def test_adamw_restatement_matches_torch_float64(lr, b1, b2, eps, wd):
+    rng = np.random.default_rng(90)
+    p0 = rng.standard_normal(257)
+    grads = [rng.standard_normal(257) * 10.0 ** rng.integers(-3, 3) for _ in range(7)]
+    p = p0.copy()
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    for step, g in enumerate(grads, start=1):
+        O.adamw(p, g, m, v, lr, b1, b2, eps, wd, O.adamw_correction(b1, step),
+                O.adamw_correction(b2, step))
+    want = _torch_adamw(p0, grads, lr, b1, b2, eps, wd)
+    scale = np.abs(p0) + lr * len(grads)
+    assert np.all(np.abs(p - want) <= 1e-13 * scale), np.max(np.abs(p - want) / scale)
+
+
+def test_adamw_restatement_closed_forms():
+    rng = np.random.default_rng(91)
+    lr, b1, b2, eps, wd = 0.01, 0.9, 0.999, 1e-8, 0.1
+    # step 1 from zero moments: m_hat = g, v_hat = g^2, so p -= lr g / (|g| + eps)
+    p0 = rng.standard_normal(64)
+    g = rng.standard_normal(64)
+    p, m, v = p0.copy(), np.zeros(64), np.zeros(64)
+    O.adamw(p, g, m, v, lr, b1, b2, eps, wd, O.adamw_correction(b1, 1), O.adamw_correction(b2, 1))
+    want = p0 * (1 - lr * wd) - lr * g / (np.abs(g) + eps)
+    assert np.allclose(p, want, rtol=0, atol=1e-15)
+    assert np.allclose(m, (1 - b1) * g, rtol=1e-15, atol=0)
+    assert np.allclose(v, (1 - b2) * g * g, rtol=1e-15, atol=0)
+    # a constant gradient keeps m_hat = g and v_hat = g^2 at every step, so
+    # each step moves by lr sign(g) (bias correction exact in the limit)
+    p, m, v = p0.copy(), np.zeros(64), np.zeros(64)
+    for step in range(1, 21):
+        O.adamw(p, g, m, v, lr, b1, b2, eps, 0.0, O.adamw_correction(b1, step),
+                O.adamw_correction(b2, step))
+    assert np.allclose(p, p0 - 20 * lr * g / (np.abs(g) + eps), rtol=0, atol=1e-12)
+    # zero gradients: only the decoupled decay acts, p_t = p (1 - lr wd)^t
+    p, m, v = p0.copy(), np.zeros(64), np.zeros(64)
+    for step in range(1, 6):
+        O.adamw(p, np.zeros(64), m, v, lr, b1, b2, eps, wd, O.adamw_correction(b1, step),
+                O.adamw_correction(b2, step))
+    assert np.allclose(p, p0 * (1 - lr * wd) ** 5, rtol=1e-15, atol=0)
+    assert not m.any() and not v.any()
+    assert O.adamw_correction(0.9, 3) == 1 - 0.9 ** 3
+
+
+def test_adamw_restatement_rounds_moments_to_float32():
+    """For float32 parameters the moments are stored as float32 and the step
+    reads them back: the result equals the float64 step computed from the
+    float32-rounded moments, and differs from an unrounded float64 update."""
+    rng = np.random.default_rng(92)
+    p = rng.standard_normal(512).astype(F32)
+    g = rng.standard_normal(512).astype(F32)
+    m = rng.standard_normal(512).astype(F32) * F32(0.1)
+    v = np.abs(rng.standard_normal(512)).astype(F32) * F32(0.01)
+    lr, b1, b2, eps, wd, c1, c2 = 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.5, 0.25
+    p32, m32, v32 = p.copy(), m.copy(), v.copy()
+    O.adamw(p32, g, m32, v32, lr, b1, b2, eps, wd, c1, c2)
+    g64 = g.astype(F64)
+    m_want = (b1 * m.astype(F64) + (1 - b1) * g64).astype(F32)
+    v_want = (b2 * v.astype(F64) + (1 - b2) * g64 * g64).astype(F32)
+    assert_bitexact(m32, m_want, "float32 first moment")
+    assert_bitexact(v32, v_want, "float32 second moment")
+    step = lr * (m_want.astype(F64) / c1) / (np.sqrt(v_want.astype(F64) / c2) + eps)
+    assert_bitexact(p32, (p.astype(F64) * (1 - lr * wd) - step).astype(F32), "float32 parameter")
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+def test_sum_squares_restatement(dtype):
+    rng = np.random.default_rng(93)
+    for n in (1, 2, 17, 10000):
+        x = (rng.standard_normal(n) * 10.0 ** rng.integers(-5, 5, n)).astype(dtype)
+        acc = O.SumSquares().add(x)
+        assert acc.scale == float(np.max(np.abs(x)))
+        assert acc.scaled_sum_squares >= 1.0
+        want = float(np.linalg.norm(x.astype(F64)))
+        assert abs(acc.norm() - want) <= 1e-13 * want
+    # squares that overflow or underflow double: the scaled form stays exact
+    for magnitude in (1e300, 1e-300):
+        x = rng.standard_normal(1000) * magnitude
+        want = float(np.linalg.norm(x / magnitude)) * magnitude
+        assert abs(O.SumSquares().add(x).norm() - want) <= 1e-13 * want
+    # special cases (gradients.cpp:79-87): NaN beats infinity, zeros and empty give 0
+    assert math.isnan(O.SumSquares().add(np.array([1.0, np.inf, np.nan], dtype)).norm())
+    inf = O.SumSquares().add(np.array([1.0, -np.inf, 2.0], dtype))
+    assert inf.norm() == math.inf and inf.has_infinity and not inf.has_nan
+    assert inf.scale == 2.0 and inf.scaled_sum_squares == 1.25
+    assert O.SumSquares().add(np.zeros(5, dtype)).norm() == 0.0
+    empty = O.SumSquares().add(np.zeros(0, dtype))
+    assert (empty.scale, empty.scaled_sum_squares, empty.norm()) == (0.0, 1.0, 0.0)
+    # combining two halves' accumulators matches feeding all elements
+    x = rng.standard_normal(999).astype(dtype)
+    a, b = O.SumSquares().add(x[:400]), O.SumSquares().add(x[400:])
+    a.combine(b.scale, b.scaled_sum_squares, b.has_infinity, b.has_nan)
+    whole = O.SumSquares().add(x)
+    assert a.scale == whole.scale
+    assert abs(a.norm() - whole.norm()) <= 1e-14 * whole.norm()
+
+
+def test_scale_restatement_rounds_through_double():
+    from fractions import Fraction
+
+    rng = np.random.default_rng(94)
+    x = rng.standard_normal(300).astype(F32)
+    for factor in (0.1, 1.0 / 3.0, 2.0 ** -7, 12345.678):
+        got = x.copy()
+        O.scale(got, factor)
+        want = np.array([np.float32(float(Fraction(float(v)) * Fraction(factor))) for v in x], F32)
+        assert_bitexact(got, want, f"scale by {factor}")
+    got = x.astype(F64)
+    O.scale(got, 2.0 ** 10)
+    assert_bitexact(got, x.astype(F64) * 1024.0, "power-of-two scale is exact")
+
+
+def test_clip_grad_norm_restatement():
+    import oracle.reference as R
+
+    rng = np.random.default_rng(95)
+    grads = [rng.standard_normal(100).astype(F32), None, rng.standard_normal((3, 7)).astype(F32)]
+    total = float(np.sqrt(sum(np.sum(g.astype(F64) ** 2) for g in grads if g is not None)))
+    assert abs(R.global_grad_norm(grads) - total) <= 1e-13 * total
+    kept = [None if g is None else g.copy() for g in grads]
+    assert R.clip_grad_norm(kept, 2 * total) == (R.global_grad_norm(grads), 1.0, False)
+    norm, factor, clipped = R.clip_grad_norm(kept, 1.0)
+    assert clipped and factor == 1.0 / norm
+    assert abs(R.global_grad_norm(kept) - 1.0) <= 1e-6
+    with pytest.raises(ValueError):
+        R.clip_grad_norm(kept, -1.0)
+    with pytest.raises(RuntimeError):
+        R.clip_grad_norm([np.array([np.nan], F32)], 1.0)
