@@ -149,7 +149,10 @@ struct SparHipStatus spar_hip_touch(const void* buffer, uint64_t bytes, void* si
 
 /* Copies (cuda_runtime.cppm:176-237).  Host<->device copies return after the
  * copy has completed (the host buffer may be reused at once); device-to-device
- * copies are stream-ordered.  Cross-device copies use hipMemcpyPeerAsync. */
+ * copies are stream-ordered.  Cross-device copies use hipMemcpyPeerAsync on the
+ * destination's stream, ordered after the source stream's pending work, and
+ * the source stream waits for the copy; the host does not wait (the reference
+ * stages them through host memory, cuda_runtime.cppm:226-228). */
 struct SparHipStatus spar_hip_copy_host_to_device(void* destination, const void* source,
                                                   uint64_t bytes, int device);
 struct SparHipStatus spar_hip_copy_device_to_host(void* destination, const void* source,

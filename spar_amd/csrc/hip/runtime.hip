@@ -335,18 +335,39 @@ extern "C" SparHipStatus spar_hip_copy_device_to_device(void* destination, int d
         hipMemcpyAsync(destination, source, bytes, hipMemcpyDeviceToDevice, guard.stream);
     return error == hipSuccess ? ok() : runtime(error);
   }
-  // Cross-device: order after the source's pending work, then copy on the
-  // destination's stream.
-  {
-    DeviceGuard source_guard;
-    if (enter(source_device, source_guard) != hipSuccess) return runtime(source_guard.error);
-    const hipError_t error = hipStreamSynchronize(source_guard.stream);
-    if (error != hipSuccess) return runtime(error);
+  // Cross-device, without a host wait: the peer copy runs on the
+  // destination's stream after the source stream's pending work (event
+  // `ready`), and the source stream waits for the copy (event `copied`) before
+  // anything later on it, such as a kernel that reuses the source block after
+  // the caller frees it, can touch the source.
+  DeviceGuard source_guard;
+  if (enter(source_device, source_guard) != hipSuccess) return runtime(source_guard.error);
+  const hipStream_t source_stream = source_guard.stream;
+  hipEvent_t ready = nullptr;
+  hipError_t error = hipEventCreateWithFlags(&ready, hipEventDisableTiming);
+  if (error == hipSuccess) error = hipEventRecord(ready, source_stream);
+  if (error != hipSuccess) {
+    if (ready != nullptr) static_cast<void>(hipEventDestroy(ready));
+    return runtime(error);
   }
-  DeviceGuard guard;
-  if (enter(destination_device, guard) != hipSuccess) return runtime(guard.error);
-  const hipError_t error = hipMemcpyPeerAsync(destination, destination_device, source,
-                                              source_device, bytes, guard.stream);
+  hipEvent_t copied = nullptr;
+  {
+    DeviceGuard guard;
+    if (enter(destination_device, guard) != hipSuccess) {
+      static_cast<void>(hipEventDestroy(ready));
+      return runtime(guard.error);
+    }
+    error = hipStreamWaitEvent(guard.stream, ready, 0);
+    if (error == hipSuccess) {
+      error = hipMemcpyPeerAsync(destination, destination_device, source, source_device, bytes,
+                                 guard.stream);
+    }
+    if (error == hipSuccess) error = hipEventCreateWithFlags(&copied, hipEventDisableTiming);
+    if (error == hipSuccess) error = hipEventRecord(copied, guard.stream);
+  }
+  static_cast<void>(hipEventDestroy(ready));
+  if (error == hipSuccess) error = hipStreamWaitEvent(source_stream, copied, 0);
+  if (copied != nullptr) static_cast<void>(hipEventDestroy(copied));
   return error == hipSuccess ? ok() : runtime(error);
 }
 
