@@ -32,19 +32,20 @@ __global__ void __launch_bounds__(kThreads)
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
-  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  constexpr int U = VectorsPerLane<F>::value;
+  const uint64_t tile = static_cast<uint64_t>(kThreads) * U;
   const V* in_v = reinterpret_cast<const V*>(in);
   V* out_v = reinterpret_cast<V*>(out);
   for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < vectors;
        base += static_cast<uint64_t>(gridDim.x) * tile) {
-    V r[kUnroll];
+    V r[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
       if (i < vectors) r[u] = stream_load(in_v + i);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
       if (i < vectors) {
         V o;
@@ -129,9 +130,9 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-uint32_t vector_grid(uint64_t count, int width) {
+uint32_t vector_grid(uint64_t count, int width, int vectors_per_lane = kUnroll) {
   const uint64_t vectors = count / static_cast<uint64_t>(width);
-  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  const uint64_t tile = static_cast<uint64_t>(kThreads) * vectors_per_lane;
   uint64_t blocks = (vectors + tile - 1) / tile;
   if (blocks == 0) blocks = 1;
   if (blocks > kMaxGrid) blocks = kMaxGrid;
@@ -149,8 +150,9 @@ uint32_t scalar_grid(uint64_t count, const DeviceGuard& guard) {
 template <typename T, typename F>
 void launch_map1(T* out, const T* in, uint64_t count, F f, const DeviceGuard& guard) {
   if (aligned16(out) && aligned16(in)) {
-    map1_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
-        out, in, count, f, stream_output(count * sizeof(T)));
+    map1_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width, VectorsPerLane<F>::value),
+                            kThreads, 0, guard.stream>>>(out, in, count, f,
+                                                         stream_output(count * sizeof(T)));
   } else {
     map1_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         out, in, count, f);

@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "common.hpp"
 #include "spar_hip.h"
 
 namespace spar_hip {
@@ -134,21 +135,14 @@ struct SiluOp {
 struct TanhOp {
   template <typename T> __device__ __forceinline__ T operator()(T x) const { return math_tanh(x); }
 };
-// gelu(x) = (0.5 * x) * erfc(-x / sqrt(2)), evaluated in double precision
-// and rounded once to T.  The erfc form avoids the cancellation of
-// 0.5 * x * (1 + erf(x / sqrt(2))) for x << 0; double evaluation makes the
-// float32 result the correctly rounded value in all but near-halfway cases
-// (float32 erfcf implementations differ by several ulp in the tail).
+// gelu(x) = (0.5 * x) * erfc(-x / sqrt(2)), defined as its double-precision
+// value rounded once to T.  The erfc form avoids the cancellation of
+// 0.5 * x * (1 + erf(x / sqrt(2))) for x << 0.  fp64 inputs use the device
+// library's erfc.
 __device__ __forceinline__ double gelu_double(double x) {
   const double t = -x * 0.70710678118654752440;
   return (0.5 * x) * erfc(t);
 }
-struct GeluOp {
-  __device__ __forceinline__ float operator()(float x) const {
-    return static_cast<float>(gelu_double(static_cast<double>(x)));
-  }
-  __device__ __forceinline__ double operator()(double x) const { return gelu_double(x); }
-};
 
 // gelu'(x) = Phi(x) + x phi(x) = 0.5 erfc(-x/sqrt 2) + x exp(-x^2/2)/sqrt(2 pi),
 // in double precision, rounded once.
@@ -157,14 +151,123 @@ __device__ __forceinline__ double gelu_derivative_double(double x) {
   const double pdf = exp(-0.5 * (x * x)) * 0.39894228040143267794;
   return cdf + x * pdf;
 }
+
+// fp32 inputs need the double value only to within 2^-24 relative for the
+// rounded float32 result to stay within 1 ulp of the definition's, which a
+// short dedicated evaluation gives at a fraction of a full double erfc's
+// cost (the library erfc made GELU compute-bound at 29% of HBM bandwidth).
+// The normal upper tail Q(a) = 0.5 erfc(a / sqrt 2), 0 <= a <= 15, is
+// exp(-a^2/2) * M(a) with M(a) = 0.5 erfcx(a / sqrt 2) a degree-10
+// polynomial in t = s - mid, s = 1 / (1 + a / 3.5), relative error 2.0e-9
+// (coefficients from fit_normal_tail.py).  a^2 / 2 is exact in double for a
+// float a; its exp uses a Cody-Waite reduction by ln 2 and a degree-8 Taylor
+// polynomial on |r| <= ln(2)/2 (error 2.0e-10).  The reciprocal is
+// v_rcp_f64 (measured 2^-24.4) with one Newton step.  Checked on every
+// float32 input against the double definition: GELU within 1 ulp (0.23% of
+// inputs differ by 1 ulp, mostly ties of subnormal results); the derivative
+// within 1 ulp except for x in [-0.7576, -0.7473], where Phi(x) + x phi(x)
+// cancels near its root and the error stays below 2.4e-10 absolute.
+constexpr double kTailInvKappa = 0x1.2492492492492p-2;
+constexpr double kTailMid = 0x1.306eb3e45306fp-1;
+constexpr double kTailCoefficient[11] = {
+    0x1.2c6f5bb4f12e0p-3,  0x1.ef6b2713cfd1fp-2,  0x1.51f19eed9c16dp-1,
+    0x1.3908154c15e3dp-1,  0x1.431e8a1b994a1p-2,  -0x1.fbad36cff239fp-8,
+    -0x1.c7e02fce56efcp-4, -0x1.202d9626843f4p-6, 0x1.8884025989592p-5,
+    0x1.a5cb80b2edea0p-8,  -0x1.4bebcb7e53f99p-6,
+};
+
+// A wave-uniform constant placed in a scalar register at its use, so that
+// the fma reads it from there instead of from a vector register copied for
+// each step (what the compiler otherwise does when the constants are hoisted
+// out of a kernel's loop).
+__device__ __forceinline__ double scalar_constant(double c) {
+  asm volatile("" : "+s"(c));
+  return c;
+}
+
+// exp(y) for -113 <= y <= 0.
+__device__ __forceinline__ double exp_nonpositive(double y) {
+  constexpr double kLog2e = 0x1.71547652b82fep0;
+  constexpr double kLn2High = 0x1.62e42fefa39efp-1;
+  constexpr double kLn2Low = 0x1.abc9e3b39803fp-56;
+  const double k = __builtin_rint(y * kLog2e);
+  double r = __builtin_fma(-k, kLn2High, y);
+  r = __builtin_fma(-k, kLn2Low, r);
+  double p = 1.0 / 40320.0;
+  p = __builtin_fma(p, r, scalar_constant(1.0 / 5040.0));
+  p = __builtin_fma(p, r, scalar_constant(1.0 / 720.0));
+  p = __builtin_fma(p, r, scalar_constant(1.0 / 120.0));
+  p = __builtin_fma(p, r, scalar_constant(1.0 / 24.0));
+  p = __builtin_fma(p, r, scalar_constant(1.0 / 6.0));
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  return __builtin_ldexp(p, static_cast<int>(k));
+}
+
+struct NormalTail {
+  double density;  // exp(-a^2 / 2)
+  double upper;    // Q(a) = 0.5 erfc(a / sqrt 2)
+};
+
+// 0 <= a <= 15.
+__device__ __forceinline__ NormalTail normal_tail(double a) {
+  const double d = __builtin_fma(a, kTailInvKappa, 1.0);
+  double s = __builtin_amdgcn_rcp(d);
+  s = __builtin_fma(s, __builtin_fma(-d, s, 1.0), s);
+  const double t = s - kTailMid;
+  double m = kTailCoefficient[10];
+#pragma unroll
+  for (int i = 9; i >= 0; --i) m = __builtin_fma(m, t, scalar_constant(kTailCoefficient[i]));
+  const double density = exp_nonpositive((a * a) * -0.5);
+  return NormalTail{density, density * m};
+}
+
+// Any input, without branches: |x| is clamped to 15, and the results
+// outside [-15, 15] are patched.  There the exact GELU and derivative round
+// to -0 in float32 below -15; above 15, GELU rounds to x and the derivative
+// to 1, which the clamped evaluation already gives for finite x.  +inf maps
+// to +inf (GELU) and -inf to NaN, as (0.5 x) erfc(-x / sqrt 2) does, and both
+// infinities give a NaN derivative (x exp(-x^2/2) = inf * 0).  NaN inputs
+// propagate through the arithmetic.
+__device__ __forceinline__ float gelu_float(float value) {
+  const double x = value;
+  const NormalTail tail = normal_tail(fmin(__builtin_fabs(x), 15.0));
+  const double xq = x * tail.upper;
+  float out = static_cast<float>(x < 0.0 ? xq : x - xq);
+  out = value < -15.0f ? -0.0f : out;
+  out = __builtin_isinf(value) ? (value > 0.0f ? value : __builtin_nanf("")) : out;
+  return out;
+}
+
+__device__ __forceinline__ float gelu_derivative_float(float value) {
+  const double x = value;
+  const NormalTail tail = normal_tail(fmin(__builtin_fabs(x), 15.0));
+  const double cdf = x < 0.0 ? tail.upper : 1.0 - tail.upper;
+  float out = static_cast<float>(cdf + x * (tail.density * 0.39894228040143267794));
+  out = value < -15.0f ? -0.0f : out;
+  out = __builtin_isinf(value) ? __builtin_nanf("") : out;
+  return out;
+}
+
+// Ops with tens of fp64 operations per element take two vectors per lane
+// in the contiguous kernels, for more independent work per wave.
+template <typename F> struct VectorsPerLane { static constexpr int value = 1; };
+
+struct GeluOp {
+  __device__ __forceinline__ float operator()(float x) const { return gelu_float(x); }
+  __device__ __forceinline__ double operator()(double x) const { return gelu_double(x); }
+};
+
 struct GeluDerivativeOp {
-  __device__ __forceinline__ float operator()(float x) const {
-    return static_cast<float>(gelu_derivative_double(static_cast<double>(x)));
-  }
+  __device__ __forceinline__ float operator()(float x) const { return gelu_derivative_float(x); }
   __device__ __forceinline__ double operator()(double x) const {
     return gelu_derivative_double(x);
   }
 };
+
+template <> struct VectorsPerLane<GeluOp> { static constexpr int value = 2; };
+template <> struct VectorsPerLane<GeluDerivativeOp> { static constexpr int value = 2; };
 
 template <typename Body>
 inline bool dispatch_unary(int operation, Body&& body) {

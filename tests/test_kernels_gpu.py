@@ -107,6 +107,35 @@ def test_unary(hip, dtype, op):
         assert_ulp(got, want, 4 if (dtype == F64 and composite) else 2, op)
 
 
+def test_gelu_float32_sweep(hip):
+    """Every 256th float32 bit pattern (2^24 inputs spanning every exponent
+    and both signs, with the infinities and NaNs) through GELU and its
+    derivative against the oracle's double-precision definition.  GELU is
+    within 1 ulp everywhere; the derivative is within 1 ulp except for x in
+    [-0.7576, -0.7473], where Phi(x) + x phi(x) cancels near its root and the
+    bound is 2.4e-10 absolute (both measured on all 2^32 inputs on the CPU)."""
+    bits = (np.arange(1 << 24, dtype=np.uint64) * 256 + 77).astype(np.uint32)
+    x = bits.view(F32)
+    x = np.concatenate([x, np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -15.0, 15.0,
+                                     -0.7518, np.finfo(F32).tiny, -np.finfo(F32).max], F32)])
+    n = x.size
+    out = out_buf(hip, (n,), F32)
+    d = dev(hip, x)
+    hip.call("spar_hip_launch_unary", out.ptr, d.ptr, n, 0, hip.GELU, 0)
+    assert_ulp(out.to_numpy(F32, (n,)), ref.unary(x, "gelu"), 1, "gelu sweep")
+    hip.call("spar_hip_launch_unary", out.ptr, d.ptr, n, 0, hip.GELU_DERIVATIVE, 0)
+    got = out.to_numpy(F32, (n,))
+    want = ref.unary(x, "gelu_derivative")
+    assert np.array_equal(np.isnan(got), np.isnan(want)), "gelu' NaN positions"
+    finite = np.isfinite(want)
+    assert np.array_equal(got[~finite & ~np.isnan(want)], want[~finite & ~np.isnan(want)])
+    err = np.abs(got[finite].astype(np.float64) - want[finite].astype(np.float64))
+    ulp = np.spacing(np.abs(want[finite])).astype(np.float64)
+    near_root = (x[finite] >= -0.7576) & (x[finite] <= -0.7473)
+    bad = (err > ulp) & ~(near_root & (err <= 2.4e-10))
+    assert not bad.any(), f"gelu' sweep: {int(bad.sum())} outside the bound, e.g. x={x[finite][bad][:3]}"
+
+
 def test_exp_clipped_config_range(hip):
     # exp over N(0,1) clipped to [-10, 10], the elementwise benchmark input
     x = np.clip(np.random.default_rng(5).standard_normal(1 << 20), -10, 10).astype(F32)
