@@ -337,6 +337,8 @@ __global__ void __launch_bounds__(kThreads)
 // [32768, 4096] fp32 column sum: ~6.95 TB/s with 512 blocks of 256-row
 // segments, the rate of a plain contiguous read of the same bytes, against
 // ~6.0 TB/s for the interleaved-wave layout above.
+constexpr int kColumnRowsInFlight = 4;
+
 template <typename T, Kind K, int NIN>
 __global__ void __launch_bounds__(kThreads)
     column_wide_kernel(const T* a, const T* b, uint64_t outer, uint64_t n,
@@ -360,12 +362,13 @@ __global__ void __launch_bounds__(kThreads)
     for (int k = 0; k < W; ++k) acc[k].init();
     const uint64_t base = row_offset(map, o) + column;
     uint64_t r = begin;
-    for (; r + 3 < end; r += 4) {
-      typename Vec16<T>::type v[4];
+    constexpr int R = kColumnRowsInFlight;
+    for (; r + (R - 1) < end; r += R) {
+      typename Vec16<T>::type v[R];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride);
+      for (int u = 0; u < R; ++u) v[u] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < R; ++u) {
 #pragma unroll
         for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v[u], k), static_cast<int64_t>(r + u));
       }
