@@ -20,6 +20,12 @@ launch is then scaled FETCH + scaled WRITE.
 for its roofline ``traffic`` field.
 
 ``summarize`` regenerates the markdown from an existing raw directory.
+
+    python3 -m spar_amd.rocprof_summary suite --section optim --raw DIR --out DIR
+
+profiles one ``bench.py --suite-only SECTION`` run with ``--kernel-trace
+--stats`` and runs the same command without a profiler, then writes a
+per-kernel duration table next to the suite's own event-timed lines.
 """
 from __future__ import annotations
 
@@ -236,6 +242,85 @@ def summarize(raw: Path, out: Path) -> None:
     print(f"wrote {out / STATS_FILE} and {out / TRAFFIC_FILE}", flush=True)
 
 
+# Suite sections: the workload each one times, for the summary's name and title.
+SUITE_WORKLOADS = {
+    "C1": ("c1_4096x4096", "C1 contiguous elementwise on [4096, 4096] fp32"),
+    "C3": ("c3_8192x8192", "C3 axis reductions on [8192, 8192] and full reductions of 2^28 fp32"),
+    "C4": ("c4_8192x32768", "C4 softmax, log-softmax and cross entropy on [8192, 32768] fp32"),
+    "C5": ("c5_4096x8192", "C5 LayerNorm chain and fused layer_norm on [4096, 8192] fp32 views"),
+    "optim": ("optim_124439808", "AdamW, gradient-norm summary and scaling over 124,439,808 fp32"),
+}
+SUITE_ARGS = ["--no-cpu-baseline", "--steps", "2", "--warmup", "1", "--suite-only"]
+
+
+def suite_file(section: str) -> str:
+    return f"kernel_stats_suite_{SUITE_WORKLOADS[section][0]}.md"
+
+
+def suite_commands(raw: Path, section: str):
+    bench = [sys.executable, str(ROOT / "bench.py")] + SUITE_ARGS + [section]
+    return {
+        "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d",
+                  str(raw / "trace"), "-o", "trace", "--"] + bench,
+        "plain": bench,
+    }
+
+
+def run_suite(raw: Path, out: Path, section: str, limit: int) -> None:
+    raw.mkdir(parents=True, exist_ok=True)
+    for name, argv in suite_commands(raw, section).items():
+        print(f"pass {name}: {shell(argv)}", flush=True)
+        log = raw / f"{name}.log"
+        with open(log, "w") as handle:
+            proc = subprocess.run(["timeout", "-s", "KILL", str(limit)] + argv, cwd="/tmp",
+                                  env=dict(os.environ, TMPDIR="/tmp"), stdout=handle,
+                                  stderr=subprocess.STDOUT)
+        print(f"pass {name}: exit {proc.returncode}", flush=True)
+        if proc.returncode != 0:
+            sys.stdout.write(log.read_text()[-4000:])
+            raise SystemExit(proc.returncode)
+    summarize_suite(raw, out, section)
+
+
+def summarize_suite(raw: Path, out: Path, section: str) -> None:
+    out.mkdir(parents=True, exist_ok=True)
+    cmds = suite_commands(raw, section)
+    stats = list(csv.DictReader(open(raw / "trace" / "trace_kernel_stats.csv")))
+    title = SUITE_WORKLOADS[section][1]
+    lines = [
+        f"# Kernel durations: bench.py suite section {section}, {title}",
+        "",
+        "Generated (from the repository root) by",
+        "",
+        f"    python3 -m spar_amd.rocprof_summary suite --section {section} "
+        f"--raw gpurun_out/suite_prof_{section} --out profiles",
+        "",
+        "which runs",
+        "",
+        "    " + shell(cmds["trace"]),
+        "",
+        "Every launch of the run, including bench.py's default workload (two steps)",
+        "and the cache-evicting reads (`touch_kernel`) before each timed launch.",
+        "Durations from the kernel trace.",
+        "",
+        "| kernel | calls | avg us | min us | max us | % time |",
+        "|---|---|---|---|---|---|",
+    ]
+    for r in stats:
+        lines.append(
+            f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+            f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+            f"{float(r['Percentage']):.2f} |")
+    suite_lines = [line for line in (raw / "plain.log").read_text().splitlines()
+                   if line.startswith('{"suite"')]
+    lines += ["", "The suite's own lines without a profiler (`" + shell(cmds["plain"]) + "`),",
+              "each op timed cold with HIP events (median of 20):", "", "```"]
+    lines += suite_lines
+    lines += ["```"]
+    (out / suite_file(section)).write_text("\n".join(lines) + "\n")
+    print(f"wrote {out / suite_file(section)}", flush=True)
+
+
 def read_traffic(path: Path):
     """{class: bytes per launch} from a traffic summary, or {} if absent."""
     if not path.exists():
@@ -256,9 +341,16 @@ def main():
     s = sub.add_parser("summarize")
     s.add_argument("--raw", type=Path, required=True)
     s.add_argument("--out", type=Path, required=True)
+    q = sub.add_parser("suite")
+    q.add_argument("--section", required=True, choices=sorted(SUITE_WORKLOADS))
+    q.add_argument("--raw", type=Path, required=True)
+    q.add_argument("--out", type=Path, required=True)
+    q.add_argument("--limit", type=int, default=240, help="seconds per pass")
     args = p.parse_args()
     if args.mode == "run":
         run(args.raw.resolve(), args.out.resolve(), args.limit)
+    elif args.mode == "suite":
+        run_suite(args.raw.resolve(), args.out.resolve(), args.section, args.limit)
     else:
         summarize(args.raw.resolve(), args.out.resolve())
 
