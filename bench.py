@@ -298,13 +298,33 @@ def main():
 
 # ----------------------------------------------------------------- suite
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def rotation(set_bytes):
+    """Buffer sets to rotate so that the other sets touched between two uses
+    of one set total at least three times the Infinity Cache."""
+    return max(3, -(-3 * MALL_BYTES // max(set_bytes, 1)) + 1)
+
+
 def run_suite(hip, reps=20, warmup=3, only=None):
     """Times every op of the five benchmark configurations (one JSON line per
-    op).  Before each timed launch, outside the timed region, a 512 MiB
-    scratch buffer is read with ordinary cached loads (spar_hip_touch): that
-    evicts the 256 MB Infinity Cache and writes back the previous launch's
-    dirty lines, whose write-back would otherwise land inside the timed
-    kernel."""
+    op), two ways:
+
+    * steady state ("ms", "GB/s", "frac"): back-to-back launches rotating over
+      input/output sets that together exceed the Infinity Cache several times,
+      so every launch reads from HBM and pays for the write-back of the dirty
+      lines its predecessors left; HIP events bracket the whole run, which is
+      divided by the number of launches;
+    * cold ("cold_ms", "cold_GB/s"): one launch after a 512 MiB cached read
+      (spar_hip_touch) that evicts the Infinity Cache and writes back its dirty
+      lines, bracketed by its own events (median of `reps`).  It includes the
+      launch's dispatch latency, and it excludes the write-back of what the
+      launch itself leaves dirty in the cache, which flatters ordinary stores
+      against non-temporal ones.
+
+    Ops that need a fresh graph per launch (the backward chains) are timed cold
+    only."""
     F = hip.FLOAT32
     u = hip.u64_array
     flush = hip.DeviceBuffer(512 << 20)
@@ -312,11 +332,14 @@ def run_suite(hip, reps=20, warmup=3, only=None):
     flush_sink = hip.DeviceBuffer(8)
     start, stop = hip.Event(), hip.Event()
 
-    def measure(config, name, nbytes, launch, elements, prepare=None):
+    def measure(config, name, nbytes, launches, elements, prepare=None):
+        if callable(launches):
+            launches = [launches]
         for _ in range(warmup):
-            if prepare is not None:
-                prepare()
-            launch()
+            for launch in launches:
+                if prepare is not None:
+                    prepare()
+                launch()
         hip.synchronize()
         samples = []
         for _ in range(reps):
@@ -324,14 +347,30 @@ def run_suite(hip, reps=20, warmup=3, only=None):
                 prepare()
             hip.call("spar_hip_touch", flush.ptr, flush.nbytes, flush_sink.ptr, 0)
             start.record()
-            launch()
+            launches[0]()
             stop.record()
             samples.append(start.elapsed_ms(stop))
-        ms = statistics.median(samples)
+        cold = statistics.median(samples)
+        line = {"suite": config, "op": name}
+        if prepare is None and len(launches) > 1:
+            count = max(reps, 2 * len(launches))
+            hip.synchronize()
+            start.record()
+            for k in range(count):
+                launches[k % len(launches)]()
+            stop.record()
+            ms = start.elapsed_ms(stop) / count
+            line["timing"] = f"steady, {len(launches)} rotated sets"
+        else:
+            ms = cold
+            line["timing"] = "cold"
         gbps = nbytes / (ms * 1e-3) / 1e9
-        print(json.dumps({"suite": config, "op": name, "ms": round(ms, 5), "GB/s": round(gbps, 1),
-                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": nbytes,
-                          "elements_per_s": round(elements / (ms * 1e-3), 1)}), flush=True)
+        line.update({"ms": round(ms, 5), "GB/s": round(gbps, 1),
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": nbytes,
+                     "elements_per_s": round(elements / (ms * 1e-3), 1),
+                     "cold_ms": round(cold, 5),
+                     "cold_GB/s": round(nbytes / (cold * 1e-3) / 1e9, 1)})
+        print(json.dumps(line), flush=True)
 
     def normal(n, seed, std=1.0):
         buf = hip.DeviceBuffer(n * 4)
@@ -344,62 +383,73 @@ def run_suite(hip, reps=20, warmup=3, only=None):
         return buf
 
     def c1():
-        # C1: contiguous elementwise on [4096, 4096]
+        # C1: contiguous elementwise on [4096, 4096]; set 0 carries the
+        # benchmark seeds, the other sets only rotate the cache.
         n = 4096 * 4096
-        a, b, out = normal(n, 1), normal(n, 2), hip.DeviceBuffer(n * 4)
+        sets = [(normal(n, 1 + 100 * k), normal(n, 2 + 100 * k), hip.DeviceBuffer(n * 4))
+                for k in range(rotation(12 * n))]
         for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
-            measure("C1", name, 12 * n, lambda op=op: hip.call(
-                "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0), n)
-        measure("C1", "gelu(a)", 8 * n, lambda: hip.call(
-            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0), n)
-        # exp(clip(a, -10, 10)): the clip is the identity on this draw (checked here)
+            measure("C1", name, 12 * n, [lambda a=a, b=b, out=out, op=op: hip.call(
+                "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0) for a, b, out in sets], n)
+        measure("C1", "gelu(a)", 8 * n, [lambda a=a, out=out: hip.call(
+            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0) for a, _, out in sets], n)
+        # exp(clip(a, -10, 10)): the clip is the identity on these draws (checked here)
         peak = hip.DeviceBuffer(8)
-        hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
-        for source in (a, out):  # max(a) and max(-a)
-            hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
-            assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
-        measure("C1", "exp(a)", 8 * n, lambda: hip.call(
-            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0), n)
-        del a, b, out
+        for a, _, out in sets:
+            hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
+            for source in (a, out):  # max(a) and max(-a)
+                hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
+                assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
+        measure("C1", "exp(a)", 8 * n, [lambda a=a, out=out: hip.call(
+            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0) for a, _, out in sets], n)
+        del sets
 
     def c3():
         # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
         R = 8192
         n = R * R
-        x = normal(n, 3)
-        out = hip.DeviceBuffer(R * 8)
+        sets = [(normal(n, 3 + 100 * k), hip.DeviceBuffer(R * 8)) for k in range(rotation(4 * n))]
         codes = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}
         for axis in (1, 0):
             for name, code in codes.items():
                 out_bytes = R * (8 if name == "argmax" else 4)
-                measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, lambda code=code, axis=axis: hip.call(
-                    "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
-                    1 << axis, F, code, 0), n)
-        del x
+                measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, [
+                    lambda x=x, out=out, code=code, axis=axis: hip.call(
+                        "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
+                        1 << axis, F, code, 0) for x, out in sets], n)
+        del sets
         n = 1 << 28
-        v = uniform(n, 4, -1.0, 1.0)
+        sets = [(uniform(n, 4 + 100 * k, -1.0, 1.0), hip.DeviceBuffer(8))
+                for k in range(rotation(4 * n))]
         for name in ("sum", "mean", "max"):
-            measure("C3", f"full {name} 2^28", 4 * n + 4, lambda name=name: hip.call(
-                "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0), n)
-        del v, out
+            measure("C3", f"full {name} 2^28", 4 * n + 4, [lambda v=v, out=out, name=name: hip.call(
+                "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0)
+                for v, out in sets], n)
+        del sets
 
     def c4():
         # C4: row softmax / log-softmax on [8192, 32768]
         rows, V = 8192, 32768
         n = rows * V
-        logits = normal(n, 5, np.sqrt(2.0))
-        grad = normal(n, 6)
-        probs = hip.DeviceBuffer(n * 4)
-        dx = hip.DeviceBuffer(n * 4)
-        undefined = hip.DeviceBuffer(rows * 4)
+        count = rotation(16 * n)
+
+        class Set:
+            def __init__(self, k):
+                self.logits = normal(n, 5 + 100 * k, np.sqrt(2.0))
+                self.grad = normal(n, 6 + 100 * k)
+                self.probs = hip.DeviceBuffer(n * 4)
+                self.dx = hip.DeviceBuffer(n * 4)
+                self.undefined = hip.DeviceBuffer(rows * 4)
+
+        sets = [Set(k) for k in range(count)]
         for log in (0, 1):
             label = "log_softmax" if log else "softmax"
-            measure("C4", f"{label} forward", 8 * n + 4 * rows, lambda log=log: hip.call(
-                "spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows, V, 1,
-                F, log, 0), n)
-            measure("C4", f"{label} backward", 12 * n + 4 * rows, lambda log=log: hip.call(
-                "spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
-                rows, V, 1, F, log, 0), n)
+            measure("C4", f"{label} forward", 8 * n + 4 * rows, [lambda s=s, log=log: hip.call(
+                "spar_hip_launch_probability_forward", s.probs.ptr, s.undefined.ptr, s.logits.ptr,
+                rows, V, 1, F, log, 0) for s in sets], n)
+            measure("C4", f"{label} backward", 12 * n + 4 * rows, [lambda s=s, log=log: hip.call(
+                "spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
+                s.undefined.ptr, rows, V, 1, F, log, 0) for s in sets], n)
         # C4 as a loss: cross entropy over the same logits, fused (one read of the
         # logits forward; one read and one write backward) and composed as the
         # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
@@ -412,39 +462,48 @@ def run_suite(hip, reps=20, warmup=3, only=None):
         invalid = hip.DeviceBuffer(4)
         loss_grad = uniform(rows, 10, 0.5, 1.5)
         small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
-        measure("C4", "cross_entropy forward (fused)", 4 * n + small, lambda: hip.call(
+        measure("C4", "cross_entropy forward (fused)", 4 * n + small, [lambda s=s: hip.call(
             "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
-            undefined.ptr, invalid.ptr, logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
-        measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, lambda: hip.call(
-            "spar_hip_launch_cross_entropy_backward", dx.ptr, loss_grad.ptr, logits.ptr, row_max.ptr,
-            row_log_sum.ptr, undefined.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0), n)
+            s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0)
+            for s in sets], n)
+        # the backward of each set uses that set's forward statistics
+        for s in sets:
+            s.row_max, s.row_log_sum = hip.DeviceBuffer(rows * 4), hip.DeviceBuffer(rows * 4)
+            hip.call("spar_hip_launch_cross_entropy_forward", losses.ptr, s.row_max.ptr,
+                     s.row_log_sum.ptr, s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows,
+                     V, 0, F, hip.INT64, 0, 0)
+        measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, [lambda s=s: hip.call(
+            "spar_hip_launch_cross_entropy_backward", s.dx.ptr, loss_grad.ptr, s.logits.ptr,
+            s.row_max.ptr, s.row_log_sum.ptr, s.undefined.ptr, targets.ptr, rows, V, 0, F,
+            hip.INT64, 0, 0) for s in sets], n)
 
-        def composed_forward():
-            hip.call("spar_hip_launch_probability_forward", probs.ptr, undefined.ptr, logits.ptr, rows,
-                     V, 1, F, 1, 0)
-            hip.call("spar_hip_launch_nll_forward", losses.ptr, probs.ptr, targets.ptr, rows, V, 0, F,
-                     hip.INT64, 0, 0)
-
-        def composed_backward():
-            hip.call("spar_hip_zero", grad.ptr, n * 4, 0)
-            hip.call("spar_hip_launch_nll_backward", grad.ptr, loss_grad.ptr, targets.ptr, rows, V, 0,
+        def composed_forward(s):
+            hip.call("spar_hip_launch_probability_forward", s.probs.ptr, s.undefined.ptr,
+                     s.logits.ptr, rows, V, 1, F, 1, 0)
+            hip.call("spar_hip_launch_nll_forward", losses.ptr, s.probs.ptr, targets.ptr, rows, V, 0,
                      F, hip.INT64, 0, 0)
-            hip.call("spar_hip_launch_probability_backward", dx.ptr, grad.ptr, probs.ptr, undefined.ptr,
-                     rows, V, 1, F, 1, 0)
+
+        def composed_backward(s):
+            hip.call("spar_hip_zero", s.grad.ptr, n * 4, 0)
+            hip.call("spar_hip_launch_nll_backward", s.grad.ptr, loss_grad.ptr, targets.ptr, rows, V,
+                     0, F, hip.INT64, 0, 0)
+            hip.call("spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
+                     s.undefined.ptr, rows, V, 1, F, 1, 0)
 
         # reported against the fused kernels' bytes, so the ratio is the speed-up
         measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
-                composed_forward, n)
+                [lambda s=s: composed_forward(s) for s in sets], n)
         measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
-                composed_backward, n)
-        del logits, grad, probs, dx, undefined, targets, losses, row_max, row_log_sum, invalid, loss_grad
+                [lambda s=s: composed_backward(s) for s in sets], n)
+        del sets, targets, losses, row_max, row_log_sum, invalid, loss_grad
 
     def c5():
         # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
         # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a
-        # [4608,9216] base, through the Tensor API: each op's events bracket its
+        # [4608,9216] base, through the Tensor API: each op's time includes its
         # host-side dispatch and allocation as well as its kernels.  Then
-        # loss = sum(y * G) and loss.backward() into base, gamma and beta.
+        # loss = sum(y * G) and loss.backward() into base, gamma and beta.  Each
+        # rotated set has its own base, G and chain intermediates.
         from spar_amd import spar
 
         device = spar.Device.hip(0)
@@ -455,17 +514,19 @@ def run_suite(hip, reps=20, warmup=3, only=None):
         rng = spar.Random(7)
         gamma = spar.random_uniform([cols], f32, rng, 0.5, 1.5, device)
         beta = spar.random_uniform([cols], f32, rng, -0.1, 0.1, device)
-        G = spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device)
-        bases = {"transposed": spar.random_normal([8192, 4096], f32, rng, 0.0, 1.0, device),
-                 "sliced": spar.random_normal([4608, 9216], f32, rng, 0.0, 1.0, device)}
-        for leaf in (gamma, beta, *bases.values()):
+        count = rotation(3 * T)
+        Gs = [spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device) for _ in range(count)]
+        shapes = {"transposed": [8192, 4096], "sliced": [4608, 9216]}
+        bases = {label: [spar.random_normal(shape, f32, rng, 0.0, 1.0, device) for _ in range(count)]
+                 for label, shape in shapes.items()}
+        for leaf in (gamma, beta, *bases["transposed"], *bases["sliced"]):
             leaf.set_requires_grad(True)
 
-        def view_of(label):
-            base = bases[label]
+        def view_of(label, k=0):
+            base = bases[label][k]
             return base.transpose(0, 1) if label == "transposed" else base.narrow(0, 256, rows).narrow(1, 512, cols)
 
-        def forward(x):
+        def forward(x, G):
             mu = spar.mean(x, [1], True)
             xc = spar.subtract(x, mu)
             var = spar.mean(spar.square(xc), [1], True)
@@ -474,36 +535,49 @@ def run_suite(hip, reps=20, warmup=3, only=None):
             return spar.sum(spar.multiply(y, G), None, False)
 
         for label in bases:
-            x = view_of(label)
-            mu = spar.mean(x, [1], True)
-            measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows, lambda: spar.mean(x, [1], True), n)
-            measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows, lambda: spar.subtract(x, mu), n)
-            xc = spar.subtract(x, mu)
-            measure("C5", f"square(xc) {label}", 2 * T, lambda: spar.square(xc), n)
-            sq = spar.square(xc)
-            measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows, lambda: spar.mean(sq, [1], True), n)
-            var = spar.mean(sq, [1], True)
-            sd = spar.sqrt(spar.add_scalar(var, 1e-5))
-            measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows, lambda: spar.divide(xc, sd), n)
-            xhat = spar.divide(xc, sd)
-            measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols, lambda: spar.multiply(xhat, gamma), n)
-            yg = spar.multiply(xhat, gamma)
-            measure("C5", f"+beta {label}", 2 * T + 4 * cols, lambda: spar.add(yg, beta), n)
-            y = spar.add(yg, beta)
-            measure("C5", f"y*G {label}", 3 * T, lambda: spar.multiply(y, G), n)
-            yG = spar.multiply(y, G)
-            measure("C5", f"sum(y*G) {label}", T + 4, lambda: spar.sum(yG, None, False), n)
-            del mu, xc, sq, var, sd, xhat, yg, y, yG
+            chains = []
+            for k in range(count):
+                c = {"x": view_of(label, k), "G": Gs[k]}
+                c["mu"] = spar.mean(c["x"], [1], True)
+                c["xc"] = spar.subtract(c["x"], c["mu"])
+                c["sq"] = spar.square(c["xc"])
+                c["var"] = spar.mean(c["sq"], [1], True)
+                c["sd"] = spar.sqrt(spar.add_scalar(c["var"], 1e-5))
+                c["xhat"] = spar.divide(c["xc"], c["sd"])
+                c["yg"] = spar.multiply(c["xhat"], gamma)
+                c["y"] = spar.add(c["yg"], beta)
+                c["yG"] = spar.multiply(c["y"], c["G"])
+                chains.append(c)
+
+            def each(fn):
+                return [lambda c=c: fn(c) for c in chains]
+
+            measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows,
+                    each(lambda c: spar.mean(c["x"], [1], True)), n)
+            measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows,
+                    each(lambda c: spar.subtract(c["x"], c["mu"])), n)
+            measure("C5", f"square(xc) {label}", 2 * T, each(lambda c: spar.square(c["xc"])), n)
+            measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows,
+                    each(lambda c: spar.mean(c["sq"], [1], True)), n)
+            measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows,
+                    each(lambda c: spar.divide(c["xc"], c["sd"])), n)
+            measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols,
+                    each(lambda c: spar.multiply(c["xhat"], gamma)), n)
+            measure("C5", f"+beta {label}", 2 * T + 4 * cols, each(lambda c: spar.add(c["yg"], beta)), n)
+            measure("C5", f"y*G {label}", 3 * T, each(lambda c: spar.multiply(c["y"], c["G"])), n)
+            measure("C5", f"sum(y*G) {label}", T + 4, each(lambda c: spar.sum(c["yG"], None, False)), n)
+            del chains
             # Whole forward, then backward.  Both are reported against the fused
             # minimum: forward reads x and G once (the loss is a scalar);
             # backward reads x and G and writes dx (gamma, beta grads are small).
-            measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T, lambda: forward(x), n)
+            measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T,
+                    [lambda k=k: forward(view_of(label, k), Gs[k]) for k in range(count)], n)
             losses = []
 
             def prepare():
-                for leaf in (gamma, beta, bases[label]):
+                for leaf in (gamma, beta, bases[label][0]):
                     leaf.zero_grad()
-                losses[:] = [forward(view_of(label))]
+                losses[:] = [forward(view_of(label), Gs[0])]
 
             measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
                     lambda: losses[0].backward(), n, prepare=prepare)
@@ -511,13 +585,14 @@ def run_suite(hip, reps=20, warmup=3, only=None):
             # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
             # first made contiguous, inside the timed op.
             measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
-                    lambda: spar.layer_norm(x, gamma, beta, 1e-5), n)
+                    [lambda k=k: spar.layer_norm(view_of(label, k), gamma, beta, 1e-5)
+                     for k in range(count)], n)
 
             def prepare_fused():
-                for leaf in (gamma, beta, bases[label]):
+                for leaf in (gamma, beta, bases[label][0]):
                     leaf.zero_grad()
                 y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
-                losses[:] = [spar.sum(spar.multiply(y, G), None, False)]
+                losses[:] = [spar.sum(spar.multiply(y, Gs[0]), None, False)]
 
             measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
                     lambda: losses[0].backward(), n, prepare=prepare_fused)
@@ -527,17 +602,21 @@ def run_suite(hip, reps=20, warmup=3, only=None):
         # Optimizer: one AdamW step, the gradient-norm summary and the clip scaling
         # over GPT-2 small's 124,439,808 fp32 parameters held as one flat buffer.
         n = 124_439_808
-        p, g = normal(n, 81), normal(n, 82, 1e-2)
-        m, v = normal(n, 83, 1e-3), uniform(n, 84, 0.0, 1e-5)
-        summary = hip.DeviceBuffer(64)
+        count = rotation(16 * n)
+        sets = [(normal(n, 81 + 100 * k), normal(n, 82 + 100 * k, 1e-2),
+                 normal(n, 83 + 100 * k, 1e-3), uniform(n, 84 + 100 * k, 0.0, 1e-5),
+                 hip.DeviceBuffer(64)) for k in range(count)]
         c1, c2 = 1.0 - 0.9 ** 1000, 1.0 - 0.95 ** 1000
-        measure("optim", "adamw step (fp32, double math)", 28 * n, lambda: hip.call(
-            "spar_hip_launch_adamw", p.ptr, g.ptr, m.ptr, v.ptr, n, F, 3e-4, 0.9, 0.95, 1e-8, 0.1,
-            c1, c2, 0), n)
-        measure("optim", "gradient norm summary", 4 * n, lambda: hip.call(
-            "spar_hip_launch_gradient_norm_summary", summary.ptr, g.ptr, n, F, 0), n)
-        measure("optim", "scale gradients in place", 8 * n, lambda: hip.call(
-            "spar_hip_launch_scale_in_place", g.ptr, n, F, 1.0, 0), n)
+        measure("optim", "adamw step (fp32, double math)", 28 * n, [
+            lambda p=p, g=g, m=m, v=v: hip.call(
+                "spar_hip_launch_adamw", p.ptr, g.ptr, m.ptr, v.ptr, n, F, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+                c1, c2, 0) for p, g, m, v, _ in sets], n)
+        measure("optim", "gradient norm summary", 4 * n, [lambda g=g, summary=summary: hip.call(
+            "spar_hip_launch_gradient_norm_summary", summary.ptr, g.ptr, n, F, 0)
+            for _, g, _, _, summary in sets], n)
+        measure("optim", "scale gradients in place", 8 * n, [lambda g=g: hip.call(
+            "spar_hip_launch_scale_in_place", g.ptr, n, F, 1.0, 0) for _, g, _, _, _ in sets], n)
+        del sets
 
     sections = {"C1": c1, "C3": c3, "C4": c4, "C5": c5, "optim": optim}
     for name, section in sections.items():

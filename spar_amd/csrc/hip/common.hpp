@@ -187,21 +187,56 @@ __device__ __forceinline__ V stream_load(const V* pointer) {
   return __builtin_nontemporal_load(pointer);
 }
 
-// Streaming write: a non-temporal store.  Measured on MI355X over runs of
-// back-to-back launches (512 MiB operands, random data), a fp32 add reaches
-// ~6.45 TB/s with non-temporal stores and ~6.25 TB/s with ordinary ones: an
-// ordinary store leaves up to 256 MB of dirty lines in the Infinity Cache
-// whose write-back then competes with the next kernel's traffic.  Outputs
-// smaller than kStreamStoreBytes keep ordinary stores so that the consumer
-// of a small result can still find it in cache.
-template <typename V>
-__device__ __forceinline__ void stream_store(V* pointer, V value) {
-  __builtin_nontemporal_store(value, pointer);
-}
-
 constexpr uint64_t kStreamStoreBytes = uint64_t{64} << 20;
 
 inline bool stream_output(uint64_t bytes) { return bytes >= kStreamStoreBytes; }
+
+// Streaming write: NT selects a non-temporal store.  Measured on MI355X over
+// runs of back-to-back launches (512 MiB operands, random data), a fp32 add
+// reaches ~6.45 TB/s with non-temporal stores and ~6.25 TB/s with ordinary
+// ones: an ordinary store leaves up to 256 MB of dirty lines in the Infinity
+// Cache whose write-back then competes with the next kernel's traffic.
+// Outputs smaller than kStreamStoreBytes keep ordinary stores so that the
+// consumer of a small result can still find it in cache.
+//
+// The policy is fixed at compile time.  A run-time choice such as
+// `if (flag) nontemporal_store(p, v); else *p = v;` does not survive
+// optimisation: the compiler sinks both stores into one ordinary store and
+// drops the non-temporal hint (checked in the gfx950 assembly), so every
+// kernel takes the policy as a template parameter and launchers select the
+// instantiation with `with_policy`.
+template <bool NT, typename V>
+__device__ __forceinline__ void store_vector(V* pointer, V value) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(value, pointer);
+  } else {
+    *pointer = value;
+  }
+}
+
+template <bool NT, typename V>
+__device__ __forceinline__ V load_vector_policy(const V* pointer) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(pointer);
+  } else {
+    return *pointer;
+  }
+}
+
+template <bool B>
+struct Policy {
+  static constexpr bool value = B;
+};
+
+// Calls body(Policy<true>{}) or body(Policy<false>{}).
+template <typename Body>
+inline void with_policy(bool flag, Body&& body) {
+  if (flag) {
+    body(Policy<true>{});
+  } else {
+    body(Policy<false>{});
+  }
+}
 
 inline bool aligned16(const void* pointer) {
   return (reinterpret_cast<uintptr_t>(pointer) & 15U) == 0;

@@ -26,9 +26,9 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 1;
 constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
 
-template <typename T, typename F>
+template <typename T, typename F, bool NT>
 __global__ void __launch_bounds__(kThreads)
-    map1_vec_kernel(T* out, const T* in, uint64_t count, F f, bool stream_out) {
+    map1_vec_kernel(T* out, const T* in, uint64_t count, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
@@ -51,11 +51,7 @@ __global__ void __launch_bounds__(kThreads)
         V o;
 #pragma unroll
         for (int k = 0; k < W; ++k) vec_set<T>(o, k, f(vec_get<T>(r[u], k)));
-        if (stream_out) {
-          stream_store(out_v + i, o);
-        } else {
-          out_v[i] = o;
-        }
+        store_vector<NT>(out_v + i, o);
       }
     }
   }
@@ -65,9 +61,9 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-template <typename T, typename F>
+template <typename T, typename F, bool NT>
 __global__ void __launch_bounds__(kThreads)
-    map2_vec_kernel(T* out, const T* a, const T* b, uint64_t count, F f, bool stream_out) {
+    map2_vec_kernel(T* out, const T* a, const T* b, uint64_t count, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
@@ -96,11 +92,7 @@ __global__ void __launch_bounds__(kThreads)
         for (int k = 0; k < W; ++k) {
           vec_set<T>(o, k, f(vec_get<T>(ra[u], k), vec_get<T>(rb[u], k)));
         }
-        if (stream_out) {
-          stream_store(out_v + i, o);
-        } else {
-          out_v[i] = o;
-        }
+        store_vector<NT>(out_v + i, o);
       }
     }
   }
@@ -150,9 +142,11 @@ uint32_t scalar_grid(uint64_t count, const DeviceGuard& guard) {
 template <typename T, typename F>
 void launch_map1(T* out, const T* in, uint64_t count, F f, const DeviceGuard& guard) {
   if (aligned16(out) && aligned16(in)) {
-    map1_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width, VectorsPerLane<F>::value),
-                            kThreads, 0, guard.stream>>>(out, in, count, f,
-                                                         stream_output(count * sizeof(T)));
+    with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
+      map1_vec_kernel<T, F, decltype(nt)::value>
+          <<<vector_grid(count, Vec16<T>::width, VectorsPerLane<F>::value), kThreads, 0,
+             guard.stream>>>(out, in, count, f);
+    });
   } else {
     map1_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         out, in, count, f);
@@ -162,8 +156,10 @@ void launch_map1(T* out, const T* in, uint64_t count, F f, const DeviceGuard& gu
 template <typename T, typename F>
 void launch_map2(T* out, const T* a, const T* b, uint64_t count, F f, const DeviceGuard& guard) {
   if (aligned16(out) && aligned16(a) && aligned16(b)) {
-    map2_vec_kernel<T, F><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
-        out, a, b, count, f, stream_output(count * sizeof(T)));
+    with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
+      map2_vec_kernel<T, F, decltype(nt)::value>
+          <<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(out, a, b, count, f);
+    });
   } else {
     map2_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         out, a, b, count, f);
@@ -181,10 +177,9 @@ __device__ __forceinline__ T fill_value(const T* scalar, T value, T divisor, boo
   return divide ? v / divisor : v;
 }
 
-template <typename T>
+template <typename T, bool NT>
 __global__ void __launch_bounds__(kThreads)
-    fill_vec_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide,
-                    bool stream_out) {
+    fill_vec_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const T v = fill_value(scalar, value, divisor, divide);
@@ -196,11 +191,7 @@ __global__ void __launch_bounds__(kThreads)
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors;
        i += stride) {
-    if (stream_out) {
-      stream_store(out_v + i, o);
-    } else {
-      out_v[i] = o;
-    }
+    store_vector<NT>(out_v + i, o);
   }
   if (blockIdx.x == 0) {
     const uint64_t i = vectors * W + threadIdx.x;
@@ -223,8 +214,11 @@ template <typename T>
 void launch_fill_values(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide,
                         const DeviceGuard& guard) {
   if (aligned16(out)) {
-    fill_vec_kernel<T><<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
-        out, count, scalar, value, divisor, divide, stream_output(count * sizeof(T)));
+    with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
+      fill_vec_kernel<T, decltype(nt)::value>
+          <<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
+              out, count, scalar, value, divisor, divide);
+    });
   } else {
     fill_scalar_kernel<T><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         out, count, scalar, value, divisor, divide);

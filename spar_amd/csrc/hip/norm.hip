@@ -121,8 +121,9 @@ __device__ __forceinline__ void norm_load_parameter(T (&p)[E], const T* paramete
   }
 }
 
-template <typename T, int THREADS, int E, bool VEC, bool FULL>
-__device__ __forceinline__ void norm_store(T* row, const T (&y)[E], uint64_t n, bool stream_out) {
+// NT: non-temporal stores (outputs of 64 MiB or more).
+template <typename T, int THREADS, int E, bool VEC, bool FULL, bool NT>
+__device__ __forceinline__ void norm_store(T* row, const T (&y)[E], uint64_t n) {
   if constexpr (VEC) {
     using V = typename Vec16<T>::type;
     constexpr int W = Vec16<T>::width;
@@ -133,11 +134,7 @@ __device__ __forceinline__ void norm_store(T* row, const T (&y)[E], uint64_t n, 
         V value;
 #pragma unroll
         for (int k = 0; k < W; ++k) vec_set<T>(value, k, y[v * W + k]);
-        if (stream_out) {
-          stream_store(reinterpret_cast<V*>(row + col), value);
-        } else {
-          *reinterpret_cast<V*>(row + col) = value;
-        }
+        store_vector<NT>(reinterpret_cast<V*>(row + col), value);
       }
     }
   } else {
@@ -174,10 +171,10 @@ template <> __device__ __forceinline__ float norm_sqrt<float>(float x) { return 
 template <> __device__ __forceinline__ double norm_sqrt<double>(double x) { return sqrt(x); }
 
 // Forward: one row per workgroup iteration, the row held in registers.
-template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL>
+template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     norm_forward_kernel(T* out, T* mean_out, T* denominator_out, const T* in, const T* weight,
-                        const T* bias, uint64_t rows, uint64_t n, T eps, bool stream_out) {
+                        const T* bias, uint64_t rows, uint64_t n, T eps) {
   const T count = static_cast<T>(n);
   for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     T x[E];
@@ -213,7 +210,7 @@ __global__ void __launch_bounds__(THREADS)
 #pragma unroll
       for (int j = 0; j < E; ++j) x[j] = x[j] + w[j];
     }
-    norm_store<T, THREADS, E, VEC, FULL>(out + r * n, x, n, stream_out);
+    norm_store<T, THREADS, E, VEC, FULL, NT>(out + r * n, x, n);
   }
 }
 
@@ -224,11 +221,11 @@ __global__ void __launch_bounds__(THREADS)
 // Each workgroup walks rows blockIdx.x, + gridDim.x, ... and keeps its dw and
 // db partials for its columns in registers; they are written once, as row
 // blockIdx.x of the [gridDim.x, n] partial arrays.
-template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL>
+template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     norm_backward_kernel(T* dx, T* partial_weight, T* partial_bias, const T* dy, const T* in,
                          const T* weight, const T* mean, const T* denominator, uint64_t rows,
-                         uint64_t n, bool stream_out) {
+                         uint64_t n) {
   const T count = static_cast<T>(n);
   T acc_w[E];
   T acc_b[CENTER ? E : 1];
@@ -283,11 +280,11 @@ __global__ void __launch_bounds__(THREADS)
     const T mean_gx = sum_gx / count;
 #pragma unroll
     for (int j = 0; j < E; ++j) g[j] = divide(g[j] - mean_g - x[j] * mean_gx);
-    norm_store<T, THREADS, E, VEC, FULL>(dx + r * n, g, n, stream_out);
+    norm_store<T, THREADS, E, VEC, FULL, NT>(dx + r * n, g, n);
   }
-  norm_store<T, THREADS, E, VEC, FULL>(partial_weight + blockIdx.x * n, acc_w, n, false);
+  norm_store<T, THREADS, E, VEC, FULL, false>(partial_weight + blockIdx.x * n, acc_w, n);
   if constexpr (CENTER) {
-    norm_store<T, THREADS, E, VEC, FULL>(partial_bias + blockIdx.x * n, acc_b, n, false);
+    norm_store<T, THREADS, E, VEC, FULL, false>(partial_bias + blockIdx.x * n, acc_b, n);
   }
 }
 
@@ -353,19 +350,21 @@ struct NormArgs {
 template <typename T, int THREADS, int E, bool CENTER, bool VEC>
 void forward_as(const NormArgs& a, const DeviceGuard& guard) {
   const bool full = a.n == static_cast<uint64_t>(THREADS) * E;
-  const bool stream_out = stream_output(a.rows * a.n * sizeof(T));
   const T eps = static_cast<T>(a.eps);
   auto launch = [&](auto kernel) {
     kernel<<<grid_for(a.rows), THREADS, 0, guard.stream>>>(
         static_cast<T*>(a.out), static_cast<T*>(a.mean), static_cast<T*>(a.denominator),
         static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
-        static_cast<const T*>(a.bias), a.rows, a.n, eps, stream_out);
+        static_cast<const T*>(a.bias), a.rows, a.n, eps);
   };
-  if (full) {
-    launch(norm_forward_kernel<T, THREADS, E, CENTER, VEC, true>);
-  } else {
-    launch(norm_forward_kernel<T, THREADS, E, CENTER, VEC, false>);
-  }
+  with_policy(stream_output(a.rows * a.n * sizeof(T)), [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    if (full) {
+      launch(norm_forward_kernel<T, THREADS, E, CENTER, VEC, true, NT>);
+    } else {
+      launch(norm_forward_kernel<T, THREADS, E, CENTER, VEC, false, NT>);
+    }
+  });
 }
 
 struct NormBackwardArgs {
@@ -385,12 +384,18 @@ struct NormBackwardArgs {
 template <typename T, int THREADS, int E, bool CENTER, bool VEC>
 hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard& guard) {
   const bool full = a.n == static_cast<uint64_t>(THREADS) * E;
-  const bool stream_out = stream_output(a.rows * a.n * sizeof(T));
-  auto kernel = full ? norm_backward_kernel<T, THREADS, E, CENTER, VEC, true>
-                     : norm_backward_kernel<T, THREADS, E, CENTER, VEC, false>;
+  const bool stream = stream_output(a.rows * a.n * sizeof(T));
+  // The four instantiations share one register budget, so any of them gives
+  // the occupancy bound.
+  auto kernel_for = [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    return full ? norm_backward_kernel<T, THREADS, E, CENTER, VEC, true, NT>
+                : norm_backward_kernel<T, THREADS, E, CENTER, VEC, false, NT>;
+  };
   // Two workgroups per CU (bounded by occupancy): enough rows in flight per
   // CU while keeping the [grid, n] partials small.
-  uint64_t grid = resident_blocks(kernel, THREADS, guard);
+  uint64_t grid = stream ? resident_blocks(kernel_for(Policy<true>{}), THREADS, guard)
+                         : resident_blocks(kernel_for(Policy<false>{}), THREADS, guard);
   const uint64_t wanted = static_cast<uint64_t>(guard.multiprocessors) * 2;
   if (grid > wanted) grid = wanted;
   if (grid > a.rows) grid = a.rows;
@@ -400,11 +405,12 @@ hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard&
   if (error != hipSuccess) return error;
   T* partial_weight = static_cast<T*>(scratch);
   T* partial_bias = CENTER ? partial_weight + grid * a.n : nullptr;
-  kernel<<<static_cast<uint32_t>(grid), THREADS, 0, guard.stream>>>(
-      static_cast<T*>(a.dx), partial_weight, partial_bias, static_cast<const T*>(a.dy),
-      static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
-      static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n,
-      stream_out);
+  with_policy(stream, [&](auto nt) {
+    kernel_for(nt)<<<static_cast<uint32_t>(grid), THREADS, 0, guard.stream>>>(
+        static_cast<T*>(a.dx), partial_weight, partial_bias, static_cast<const T*>(a.dy),
+        static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
+        static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n);
+  });
   const uint32_t combine_grid = grid_for((a.n + kWave - 1) / kWave);
   norm_combine_kernel<T><<<combine_grid, kCombineThreads, 0, guard.stream>>>(
       static_cast<T*>(a.dweight), partial_weight, grid, a.n);

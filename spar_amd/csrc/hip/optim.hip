@@ -93,10 +93,10 @@ __device__ __forceinline__ void adamw_element(T& parameter, T gradient, T& first
 // traffic and no arithmetic runs no faster, so the double math is hidden.
 constexpr int kAdamwUnroll = 2;
 
-template <typename T>
+template <typename T, bool NT>
 __global__ void __launch_bounds__(kThreads)
     adamw_vec_kernel(T* parameter, const T* gradient, T* first, T* second, uint64_t count,
-                     AdamwStep step, bool stream_out) {
+                     AdamwStep step) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   constexpr int U = kAdamwUnroll;
@@ -141,15 +141,9 @@ __global__ void __launch_bounds__(kThreads)
         vec_set<T>(m[u], k, mk);
         vec_set<T>(s[u], k, sk);
       }
-      if (stream_out) {
-        stream_store(m_v + i, m[u]);
-        stream_store(s_v + i, s[u]);
-        stream_store(p_v + i, p[u]);
-      } else {
-        m_v[i] = m[u];
-        s_v[i] = s[u];
-        p_v[i] = p[u];
-      }
+      store_vector<NT>(m_v + i, m[u]);
+      store_vector<NT>(s_v + i, s[u]);
+      store_vector<NT>(p_v + i, p[u]);
     }
   }
   if (blockIdx.x == 0) {
@@ -174,9 +168,11 @@ void launch_adamw(T* parameter, const T* gradient, T* first, T* second, uint64_t
                   const AdamwStep& step, const DeviceGuard& guard) {
   if (aligned16(parameter) && aligned16(gradient) && aligned16(first) && aligned16(second)) {
     const uint64_t vectors = count / Vec16<T>::width;
-    adamw_vec_kernel<T><<<tile_grid((vectors + kAdamwUnroll - 1) / kAdamwUnroll), kThreads, 0,
-                          guard.stream>>>(
-        parameter, gradient, first, second, count, step, stream_output(3 * count * sizeof(T)));
+    with_policy(stream_output(3 * count * sizeof(T)), [&](auto nt) {
+      adamw_vec_kernel<T, decltype(nt)::value>
+          <<<tile_grid((vectors + kAdamwUnroll - 1) / kAdamwUnroll), kThreads, 0, guard.stream>>>(
+              parameter, gradient, first, second, count, step);
+    });
   } else {
     adamw_scalar_kernel<T><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         parameter, gradient, first, second, count, step);
@@ -191,9 +187,9 @@ __device__ __forceinline__ T scaled(T value, double factor) {
   return static_cast<T>(static_cast<double>(value) * factor);
 }
 
-template <typename T>
+template <typename T, bool NT>
 __global__ void __launch_bounds__(kThreads)
-    scale_vec_kernel(T* values, uint64_t count, double factor, bool stream_out) {
+    scale_vec_kernel(T* values, uint64_t count, double factor) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
@@ -203,11 +199,7 @@ __global__ void __launch_bounds__(kThreads)
     V v = stream_load(v_v + i);
 #pragma unroll
     for (int k = 0; k < W; ++k) vec_set<T>(v, k, scaled(vec_get<T>(v, k), factor));
-    if (stream_out) {
-      stream_store(v_v + i, v);
-    } else {
-      v_v[i] = v;
-    }
+    store_vector<NT>(v_v + i, v);
   }
   if (blockIdx.x == 0) {
     const uint64_t i = vectors * W + threadIdx.x;
@@ -228,8 +220,10 @@ __global__ void __launch_bounds__(kThreads)
 template <typename T>
 void launch_scale(T* values, uint64_t count, double factor, const DeviceGuard& guard) {
   if (aligned16(values)) {
-    scale_vec_kernel<T><<<tile_grid(count / Vec16<T>::width), kThreads, 0, guard.stream>>>(
-        values, count, factor, stream_output(count * sizeof(T)));
+    with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
+      scale_vec_kernel<T, decltype(nt)::value>
+          <<<tile_grid(count / Vec16<T>::width), kThreads, 0, guard.stream>>>(values, count, factor);
+    });
   } else {
     scale_scalar_kernel<T><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
         values, count, factor);

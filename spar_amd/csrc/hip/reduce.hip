@@ -70,6 +70,46 @@ template <typename T> struct Acc<T, Kind::Max> {
   }
 };
 
+// Accumulator of the streaming row and column scans: the same rules as Acc,
+// but max/argmax keep a 32-bit index relative to the start of the scanned
+// range, which saves 64-bit index arithmetic on every element (the planner
+// keeps every range below kMaxScanRange elements).  finish(base) rebases it
+// into an Acc.
+constexpr uint64_t kMaxScanRange = uint64_t{1} << 31;
+
+template <typename T, Kind K> struct ScanAcc;
+
+template <typename T> struct ScanAcc<T, Kind::Sum> {
+  T value;
+  __device__ __forceinline__ void init() { value = T(0); }
+  __device__ __forceinline__ void add(T x, uint32_t) { value += x; }
+  __device__ __forceinline__ Acc<T, Kind::Sum> finish(int64_t) const {
+    Acc<T, Kind::Sum> acc;
+    acc.value = value;
+    return acc;
+  }
+};
+
+template <typename T> struct ScanAcc<T, Kind::Max> {
+  T value;
+  uint32_t index;
+  __device__ __forceinline__ void init() {
+    value = argmax_identity<T>().value;
+    index = UINT32_MAX;
+  }
+  __device__ __forceinline__ void add(T x, uint32_t i) {
+    const bool take = !(x <= value) && value == value;
+    value = take ? x : value;
+    index = take ? i : index;
+  }
+  __device__ __forceinline__ Acc<T, Kind::Max> finish(int64_t base) const {
+    Acc<T, Kind::Max> acc;
+    acc.best.value = value;
+    acc.best.index = index == UINT32_MAX ? INT64_MAX : base + static_cast<int64_t>(index);
+    return acc;
+  }
+};
+
 // Reads one element: the input itself, or the product of two inputs that
 // share strides (each product rounded to T, as multiply() would store it).
 template <typename T, int NIN>
@@ -189,34 +229,38 @@ __global__ void __launch_bounds__(kThreads)
     const uint64_t begin = split * segment;
     const uint64_t end = begin + segment < n ? begin + segment : n;
     const uint64_t base = row_offset(map, row);
-    Acc<T, K> acc[4];
+    // Indices relative to `begin` (segments are below kMaxScanRange).
+    ScanAcc<T, K> scan[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u].init();
+    for (int u = 0; u < 4; ++u) scan[u].init();
     if constexpr (VEC) {
-      const uint64_t step = static_cast<uint64_t>(kThreads) * W;
+      constexpr uint32_t step = static_cast<uint32_t>(kThreads) * W;
       uint64_t i = begin + static_cast<uint64_t>(threadIdx.x) * W;
       for (; i + 3 * step < end; i += 4 * step) {
         typename Vec16<T>::type v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) v[u] = load_vector<T, NIN>(a, b, base + i + u * step);
+        const uint32_t relative = static_cast<uint32_t>(i - begin);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
 #pragma unroll
-          for (int k = 0; k < W; ++k) {
-            acc[u].add(vec_get<T>(v[u], k), static_cast<int64_t>(i + u * step + k));
-          }
+          for (int k = 0; k < W; ++k) scan[u].add(vec_get<T>(v[u], k), relative + u * step + k);
         }
       }
       for (; i < end; i += step) {
         const auto v = load_vector<T, NIN>(a, b, base + i);
+        const uint32_t relative = static_cast<uint32_t>(i - begin);
 #pragma unroll
-        for (int k = 0; k < W; ++k) acc[0].add(vec_get<T>(v, k), static_cast<int64_t>(i + k));
+        for (int k = 0; k < W; ++k) scan[0].add(vec_get<T>(v, k), relative + k);
       }
     } else {
       for (uint64_t i = begin + threadIdx.x; i < end; i += kThreads) {
-        acc[0].add(load_value<T, NIN>(a, b, base + i), static_cast<int64_t>(i));
+        scan[0].add(load_value<T, NIN>(a, b, base + i), static_cast<uint32_t>(i - begin));
       }
     }
+    Acc<T, K> acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = scan[u].finish(static_cast<int64_t>(begin));
     acc[0].merge(acc[1]);
     acc[2].merge(acc[3]);
     acc[0].merge(acc[2]);
@@ -330,21 +374,28 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// Wide rows (inner >= 256 vectors): each wave owns 64 x W columns of its own
-// and walks every row of the block's segment, four rows in flight, so no
-// cross-wave combine is needed; a block's four waves cover 256 x W adjacent
-// columns and read 4 KiB contiguous per row.  Measured on MI355X for a
-// [32768, 4096] fp32 column sum: ~6.95 TB/s with 512 blocks of 256-row
-// segments, the rate of a plain contiguous read of the same bytes, against
-// ~6.0 TB/s for the interleaved-wave layout above.
-constexpr int kColumnRowsInFlight = 4;
-
-template <typename T, Kind K, int NIN>
+// Wide rows (inner >= 256 vectors): each wave owns VPL x 64 x W adjacent
+// columns (lane l holds the 16-byte groups l, l + 64, ..., so one row of the
+// wave's columns is VPL x 1 KiB contiguous) and walks every row of the
+// block's segment, R rows in flight; no cross-wave combine is needed.  A
+// block's four waves cover 4 x VPL x 64 x W adjacent columns.  Measured on
+// MI355X (steady state, two kernels including the combine):
+//
+//   shape (reduced axis first)      VPL=1, R=4, 2 blocks/CU   VPL=4, R=2, 1 block/CU
+//   [8192, 8192]  axis 0            47.1 us                    42.4 us
+//   [32768, 4096] axis 0            81.3 us                    80.9 us
+//   [32, 1024, 4096] G*x, axis 1    162.8 us                   155.7 us
+//   [8192, 4096]  axis 0            26.5 us                    25.8 us
+//
+// VPL = 4 needs the row length to be a multiple of 4 x 256 groups; other
+// wide rows take VPL = 1.
+template <typename T, Kind K, int NIN, int VPL, int R>
 __global__ void __launch_bounds__(kThreads)
     column_wide_kernel(const T* a, const T* b, uint64_t outer, uint64_t n,
                        uint64_t reduced_stride, uint64_t inner, uint64_t column_blocks,
                        uint64_t splits, uint64_t segment, RowMap map, Sink<T> sink) {
   constexpr int W = Vec16<T>::width;
+  constexpr uint64_t kGroupStride = static_cast<uint64_t>(kWave) * W;  // columns between a lane's groups
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const uint64_t total_blocks = outer * splits * column_blocks;
@@ -353,38 +404,62 @@ __global__ void __launch_bounds__(kThreads)
     const uint64_t rest = block / column_blocks;
     const uint64_t split = rest % splits;
     const uint64_t o = rest / splits;
-    const uint64_t column = ((cb * kWaves + wave) * kWave + lane) * W;
-    if (column >= inner) continue;  // inner is a multiple of W: all W columns exist
+    const uint64_t column = ((cb * kWaves + wave) * VPL * kWave + lane) * W;
+    // inner is a multiple of W, and of 256 x VPL x W when VPL > 1: every group exists
+    if (column >= inner) continue;
     const uint64_t begin = split * segment;
     const uint64_t end = begin + segment < n ? begin + segment : n;
-    Acc<T, K> acc[W];
+    ScanAcc<T, K> scan[VPL][W];
 #pragma unroll
-    for (int k = 0; k < W; ++k) acc[k].init();
+    for (int g = 0; g < VPL; ++g) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) scan[g][k].init();
+    }
     const uint64_t base = row_offset(map, o) + column;
     uint64_t r = begin;
-    constexpr int R = kColumnRowsInFlight;
     for (; r + (R - 1) < end; r += R) {
-      typename Vec16<T>::type v[R];
-#pragma unroll
-      for (int u = 0; u < R; ++u) v[u] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride);
+      typename Vec16<T>::type v[R][VPL];
 #pragma unroll
       for (int u = 0; u < R; ++u) {
 #pragma unroll
-        for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v[u], k), static_cast<int64_t>(r + u));
+        for (int g = 0; g < VPL; ++g) {
+          v[u][g] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride + g * kGroupStride);
+        }
+      }
+      // Keep all R x VPL loads in flight: without this barrier the scheduler
+      // interleaves the max/argmax compare-and-selects with the loads to save
+      // registers and leaves about three loads outstanding.
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t relative = static_cast<uint32_t>(r - begin);
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+#pragma unroll
+        for (int g = 0; g < VPL; ++g) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) scan[g][k].add(vec_get<T>(v[u][g], k), relative + u);
+        }
       }
     }
     for (; r < end; ++r) {
-      const auto v = load_vector<T, NIN>(a, b, base + r * reduced_stride);
+      const uint32_t relative = static_cast<uint32_t>(r - begin);
 #pragma unroll
-      for (int k = 0; k < W; ++k) acc[k].add(vec_get<T>(v, k), static_cast<int64_t>(r));
+      for (int g = 0; g < VPL; ++g) {
+        const auto v = load_vector<T, NIN>(a, b, base + r * reduced_stride + g * kGroupStride);
+#pragma unroll
+        for (int k = 0; k < W; ++k) scan[g][k].add(vec_get<T>(v, k), relative);
+      }
     }
 #pragma unroll
-    for (int k = 0; k < W; ++k) {
-      if (begin < end) acc[k].seal(static_cast<int64_t>(begin));
-      // Output slot: final [outer, inner]; partial [outer, splits, inner].
-      const uint64_t slot = sink.partial ? (o * splits + split) * inner + column + k
-                                         : o * inner + column + k;
-      sink_write<T, K>(sink, slot, acc[k]);
+    for (int g = 0; g < VPL; ++g) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        Acc<T, K> total = scan[g][k].finish(static_cast<int64_t>(begin));
+        if (begin < end) total.seal(static_cast<int64_t>(begin));
+        // Output slot: final [outer, inner]; partial [outer, splits, inner].
+        const uint64_t c = column + g * kGroupStride + k;
+        const uint64_t slot = sink.partial ? (o * splits + split) * inner + c : o * inner + c;
+        sink_write<T, K>(sink, slot, total);
+      }
     }
   }
 }
@@ -593,7 +668,8 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     for (int k = 0; k < plan.kept_rank; ++k) {
       if (plan.kept_strides[k] % W != 0) vec = false;
     }
-    // Split long rows when there are too few rows to fill the device.
+    // Split long rows when there are too few rows to fill the device, and
+    // keep every segment below kMaxScanRange elements.
     uint64_t splits = 1;
     const uint64_t min_segment = static_cast<uint64_t>(kThreads) * W * 8;
     if (rows < target_blocks && n >= 2 * min_segment) {
@@ -602,6 +678,8 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
       if (splits > max_splits) splits = max_splits;
       if (splits < 1) splits = 1;
     }
+    const uint64_t range_splits = (n + kMaxScanRange / 2 - 1) / (kMaxScanRange / 2);
+    if (splits < range_splits) splits = range_splits;
     uint64_t segment = (n + splits - 1) / splits;
     if (vec) segment = (segment + W - 1) / W * W;
     splits = (n + segment - 1) / segment;
@@ -636,27 +714,36 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     for (int k = 0; k < plan.kept_rank - 1; ++k) {
       if (plan.kept_strides[k] % W != 0) vec = false;
     }
-    // Wide rows: waves own columns (2 blocks per CU, >= 64 rows per split);
-    // otherwise waves interleave rows (8 blocks per CU, >= 16 rows per wave).
+    // Wide rows: waves own columns.  Rows of whole 4-group blocks take 4
+    // groups per lane, 2 rows in flight, one block per CU and >= 16 rows per
+    // split; other wide rows 1 group per lane, 4 rows in flight, 2 blocks per
+    // CU and >= 64 rows per split.  Narrow rows: waves interleave rows (8
+    // blocks per CU, >= 16 rows per wave).
     const bool wide = vec && inner / W >= static_cast<uint64_t>(kWaves) * kWave;
-    const uint64_t columns_per_block =
-        static_cast<uint64_t>(kWave) * (vec ? W : 1) * (wide ? kWaves : 1);
+    const bool quad = wide && (inner / W) % (static_cast<uint64_t>(kThreads) * 4) == 0;
+    const uint64_t columns_per_block = static_cast<uint64_t>(kWave) * (vec ? W : 1) *
+                                       (wide ? kWaves : 1) * (quad ? 4 : 1);
     const uint64_t column_blocks = (inner + columns_per_block - 1) / columns_per_block;
     const uint64_t base_blocks = outer * column_blocks;
     uint64_t splits = 1;
-    const uint64_t min_rows = wide ? 64 : 16 * kWaves;
-    const uint64_t wanted_blocks = static_cast<uint64_t>(cus) * (wide ? 2 : 8);
+    const uint64_t min_rows = quad ? 16 : wide ? 64 : 16 * kWaves;
+    const uint64_t wanted_blocks = static_cast<uint64_t>(cus) * (quad ? 1 : wide ? 2 : 8);
     if (base_blocks < wanted_blocks && n >= 2 * min_rows) {
       splits = (wanted_blocks + base_blocks - 1) / base_blocks;
       if (splits > n / min_rows) splits = n / min_rows;
       if (splits < 1) splits = 1;
     }
+    const uint64_t range_splits = (n + kMaxScanRange / 2 - 1) / (kMaxScanRange / 2);
+    if (splits < range_splits) splits = range_splits;
     const uint64_t segment = (n + splits - 1) / splits;
     splits = (n + segment - 1) / segment;
     auto launch = [&](const Sink<T>& s) {
       const uint32_t grid = grid_for(outer * splits * column_blocks);
-      if (wide) {
-        column_wide_kernel<T, K, NIN><<<grid, kThreads, 0, guard.stream>>>(
+      if (quad) {
+        column_wide_kernel<T, K, NIN, 4, 2><<<grid, kThreads, 0, guard.stream>>>(
+            a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
+      } else if (wide) {
+        column_wide_kernel<T, K, NIN, 1, 4><<<grid, kThreads, 0, guard.stream>>>(
             a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
       } else if (vec) {
         column_kernel<T, K, NIN, true><<<grid, kThreads, 0, guard.stream>>>(

@@ -206,8 +206,9 @@ __device__ __forceinline__ void load_row(T (&x)[E], const T* row, uint64_t n) {
   }
 }
 
-template <typename T, int THREADS, int E, bool VEC, bool FULL>
-__device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n, bool stream_out) {
+// NT: non-temporal stores (outputs of 64 MiB or more).
+template <typename T, int THREADS, int E, bool VEC, bool FULL, bool NT>
+__device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n) {
   if constexpr (VEC) {
     using V = typename Vec16<T>::type;
     constexpr int W = Vec16<T>::width;
@@ -218,11 +219,7 @@ __device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n, b
         V value;
 #pragma unroll
         for (int k = 0; k < W; ++k) vec_set<T>(value, k, y[v * W + k]);
-        if (stream_out) {
-          stream_store(reinterpret_cast<V*>(row + col), value);
-        } else {
-          *reinterpret_cast<V*>(row + col) = value;
-        }
+        store_vector<NT>(reinterpret_cast<V*>(row + col), value);
       }
     }
   } else {
@@ -282,10 +279,9 @@ __device__ __forceinline__ T block_max_first(T value, int32_t index) {
 // maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
 // otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
 // row and apply the reference's special cases from full slice statistics.
-template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool PREFETCH>
+template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool PREFETCH, bool NT>
 __global__ void __launch_bounds__(THREADS)
-    forward_row_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
-                       bool stream_out) {
+    forward_row_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n) {
   T x[E];
   T next[PREFETCH ? E : 1];
   uint64_t r = blockIdx.x;
@@ -353,7 +349,7 @@ __global__ void __launch_bounds__(THREADS)
 #pragma unroll
       for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
     }
-    store_row<T, THREADS, E, VEC, FULL>(out + r * n, x, n, stream_out);
+    store_row<T, THREADS, E, VEC, FULL, NT>(out + r * n, x, n);
   }
 }
 
@@ -410,10 +406,10 @@ __device__ __forceinline__ void unstage_row(T (&x)[E], const T* stage, uint64_t 
 // maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
 // otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
 // row and apply the reference's special cases from full slice statistics.
-template <typename T, int THREADS, int E, bool LOG, bool FULL>
+template <typename T, int THREADS, int E, bool LOG, bool FULL, bool NT>
 __device__ __forceinline__ void staged_forward_row(T* out, int32_t* undefined, const T* in,
                                                    uint64_t rows, uint64_t n, uint64_t r,
-                                                   uint64_t stride, T* stage, bool stream_out) {
+                                                   uint64_t stride, T* stage) {
   T x[E];
   unstage_row<T, THREADS, E, FULL>(x, stage, n);
   exchange_barrier();  // the stage is free for the next row
@@ -470,7 +466,7 @@ __device__ __forceinline__ void staged_forward_row(T* out, int32_t* undefined, c
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
   }
-  store_row<T, THREADS, E, true, FULL>(out + r * n, x, n, stream_out);
+  store_row<T, THREADS, E, true, FULL, NT>(out + r * n, x, n);
 }
 
 // Forward over rows (16-byte aligned, n a multiple of the vector width) in
@@ -479,18 +475,18 @@ __device__ __forceinline__ void staged_forward_row(T* out, int32_t* undefined, c
 // an LDS stage while the current row is computed in registers, so a CU's
 // reads overlap its arithmetic without spending VGPRs on a second row, and
 // its stores drain while the following row is computed.
-template <typename T, int THREADS, int E, bool LOG, bool FULL>
+template <typename T, int THREADS, int E, bool LOG, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
-    forward_row_staged_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
-                              bool stream_out) {
+    forward_row_staged_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows,
+                              uint64_t n) {
   __shared__ __attribute__((aligned(16))) T stage[THREADS * E];
   uint64_t r = blockIdx.x;
   if (r >= rows) return;
   stage_row<T, THREADS, E, FULL>(stage, in + r * n, n);
   __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // nothing was issued after the staging loads
   exchange_barrier();                          // every wave's staged loads have landed
-  staged_forward_row<T, THREADS, E, LOG, FULL>(out, undefined, in, rows, n, r, gridDim.x, stage,
-                                               stream_out);
+  staged_forward_row<T, THREADS, E, LOG, FULL, NT>(out, undefined, in, rows, n, r, gridDim.x,
+                                                   stage);
   for (r += gridDim.x; r < rows; r += gridDim.x) {
     // Vector memory operations retire in issue order on this architecture.
     // After the staging loads of row r, a wave of a full row issued at least
@@ -504,22 +500,22 @@ __global__ void __launch_bounds__(THREADS)
       __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
     }
     exchange_barrier();  // every wave's staged loads have landed
-    staged_forward_row<T, THREADS, E, LOG, FULL>(out, undefined, in, rows, n, r, gridDim.x, stage,
-                                                 stream_out);
+    staged_forward_row<T, THREADS, E, LOG, FULL, NT>(out, undefined, in, rows, n, r, gridDim.x,
+                                                     stage);
   }
 }
 
-template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL>
+template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     backward_row_kernel(T* out, const T* gradient, const T* saved, const int32_t* undefined,
-                        uint64_t rows, uint64_t n, bool stream_out) {
+                        uint64_t rows, uint64_t n) {
   for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     T* out_row = out + r * n;
     T g[E];
     if (undefined[r] != 0) {
 #pragma unroll
       for (int j = 0; j < E; ++j) g[j] = quiet_nan<T>();
-      store_row<T, THREADS, E, VEC, FULL>(out_row, g, n, stream_out);
+      store_row<T, THREADS, E, VEC, FULL, NT>(out_row, g, n);
       continue;
     }
     T y[E];
@@ -546,7 +542,7 @@ __global__ void __launch_bounds__(THREADS)
         g[j] = y[j] * (g[j] - reduced);
       }
     }
-    store_row<T, THREADS, E, VEC, FULL>(out_row, g, n, stream_out);
+    store_row<T, THREADS, E, VEC, FULL, NT>(out_row, g, n);
   }
 }
 
@@ -722,16 +718,18 @@ void forward_rows_as(T* out, int32_t* undefined, const T* in, uint64_t rows, uin
   // The LDS stage holds one row of THREADS * E elements (at most 128 KiB of
   // the CU's 160 KiB).
   constexpr bool kStaged = VEC && THREADS * E * sizeof(T) <= (128U << 10);
-  const bool stream_out = stream_output(rows * n * sizeof(T));
-  if constexpr (kStaged) {
-    auto kernel = forward_row_staged_kernel<T, THREADS, E, LOG, FULL>;
-    const uint64_t resident = resident_blocks(kernel, THREADS, guard);
-    kernel<<<grid_for(rows < resident ? rows : resident), THREADS, 0, guard.stream>>>(
-        out, undefined, in, rows, n, stream_out);
-  } else {
-    forward_row_kernel<T, THREADS, E, LOG, VEC, FULL, false>
-        <<<grid_for(rows), THREADS, 0, guard.stream>>>(out, undefined, in, rows, n, stream_out);
-  }
+  with_policy(stream_output(rows * n * sizeof(T)), [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    if constexpr (kStaged) {
+      auto kernel = forward_row_staged_kernel<T, THREADS, E, LOG, FULL, NT>;
+      const uint64_t resident = resident_blocks(kernel, THREADS, guard);
+      kernel<<<grid_for(rows < resident ? rows : resident), THREADS, 0, guard.stream>>>(
+          out, undefined, in, rows, n);
+    } else {
+      forward_row_kernel<T, THREADS, E, LOG, VEC, FULL, false, NT>
+          <<<grid_for(rows), THREADS, 0, guard.stream>>>(out, undefined, in, rows, n);
+    }
+  });
 }
 
 template <typename T, int THREADS, int E, bool LOG, bool VEC>
@@ -747,14 +745,16 @@ void forward_rows(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64
 template <typename T, int THREADS, int E, bool LOG, bool VEC>
 void backward_rows(T* out, const T* gradient, const T* saved, const int32_t* undefined,
                    uint64_t rows, uint64_t n, const DeviceGuard& guard) {
-  const bool stream_out = stream_output(rows * n * sizeof(T));
-  if (n == static_cast<uint64_t>(THREADS) * E) {
-    backward_row_kernel<T, THREADS, E, LOG, VEC, true><<<grid_for(rows), THREADS, 0, guard.stream>>>(
-        out, gradient, saved, undefined, rows, n, stream_out);
-  } else {
-    backward_row_kernel<T, THREADS, E, LOG, VEC, false><<<grid_for(rows), THREADS, 0, guard.stream>>>(
-        out, gradient, saved, undefined, rows, n, stream_out);
-  }
+  with_policy(stream_output(rows * n * sizeof(T)), [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    if (n == static_cast<uint64_t>(THREADS) * E) {
+      backward_row_kernel<T, THREADS, E, LOG, VEC, true, NT>
+          <<<grid_for(rows), THREADS, 0, guard.stream>>>(out, gradient, saved, undefined, rows, n);
+    } else {
+      backward_row_kernel<T, THREADS, E, LOG, VEC, false, NT>
+          <<<grid_for(rows), THREADS, 0, guard.stream>>>(out, gradient, saved, undefined, rows, n);
+    }
+  });
 }
 
 template <typename T, bool LOG, bool VEC>
@@ -1018,12 +1018,12 @@ __global__ void __launch_bounds__(kEntropyThreads)
 // (softmax.cpp:406-444).  Here lp = (x - m) - log S is recomputed with the
 // forward's operations, so dx is that expression without either tensor
 // materialised; undefined rows are NaN.  Tiles of 256 x W columns of one row.
-template <typename T, typename I, bool VEC>
+template <typename T, typename I, bool VEC, bool NT>
 __global__ void __launch_bounds__(kEntropyThreads)
     entropy_backward_kernel(T* dx, const T* loss_gradient, const T* logits, const T* row_max,
                             const T* row_log_sum, const int32_t* undefined, const I* targets,
                             uint64_t rows, uint64_t classes, uint64_t column_tiles,
-                            TargetMap map, bool stream_out) {
+                            TargetMap map) {
   constexpr int W = VEC ? Vec16<T>::width : 1;
   using V = typename Vec16<T>::type;
   const uint64_t tiles = rows * column_tiles;
@@ -1059,12 +1059,7 @@ __global__ void __launch_bounds__(kEntropyThreads)
       V o;
 #pragma unroll
       for (int k = 0; k < W; ++k) vec_set<T>(o, k, values[k]);
-      V* target = reinterpret_cast<V*>(dx + r * classes + c);
-      if (stream_out) {
-        stream_store(target, o);
-      } else {
-        *target = o;
-      }
+      store_vector<NT>(reinterpret_cast<V*>(dx + r * classes + c), o);
     } else {
       dx[r * classes + c] = values[0];
     }
@@ -1239,18 +1234,19 @@ void launch_entropy_backward(void* logits_gradient, const void* loss_gradient,
                    aligned16(logits_gradient);
   const uint64_t width = vec ? Vec16<T>::width : 1;
   const uint64_t column_tiles = (classes + kEntropyThreads * width - 1) / (kEntropyThreads * width);
-  const bool stream_out = stream_output(rows * classes * sizeof(T));
   auto launch = [&](auto kernel) {
     kernel<<<grid_for(rows * column_tiles), kEntropyThreads, 0, guard.stream>>>(
         static_cast<T*>(logits_gradient), static_cast<const T*>(loss_gradient),
         static_cast<const T*>(logits), static_cast<const T*>(row_max),
         static_cast<const T*>(row_log_sum), undefined_rows, static_cast<const I*>(targets), rows,
-        classes, column_tiles, map, stream_out);
+        classes, column_tiles, map);
   };
   if (vec) {
-    launch(entropy_backward_kernel<T, I, true>);
+    with_policy(stream_output(rows * classes * sizeof(T)), [&](auto nt) {
+      launch(entropy_backward_kernel<T, I, true, decltype(nt)::value>);
+    });
   } else {
-    launch(entropy_backward_kernel<T, I, false>);
+    launch(entropy_backward_kernel<T, I, false, false>);
   }
 }
 

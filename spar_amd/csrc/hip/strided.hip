@@ -88,11 +88,91 @@ struct RowGeometry {
   KernelGeometry g;        // full coalesced geometry (axis 0 = innermost)
   FastDiv groups_per_row;  // inner / W
   int inner_unit[2];       // 1 if the operand is contiguous along the inner axis
-  int reused[2];           // 1 if the operand is broadcast (read many times: keep it cached)
-  int stream_out;          // 1 to write the output with non-temporal stores
 };
 
+// Offsets of row `row` (the outer axes of g, innermost first from index 1).
+template <int NOPS>
+__device__ __forceinline__ void row_offsets(const KernelGeometry& g, uint32_t row, uint64_t& off0,
+                                            uint64_t& off1) {
+  off0 = g.offsets[0];
+  off1 = g.offsets[1];
+  uint32_t rem = row;
+#pragma unroll
+  for (int k = 1; k < kMaxRank; ++k) {
+    if (k < g.rank) {
+      const uint32_t q = g.divisors[k].div(rem);
+      const uint64_t c = rem - q * g.divisors[k].divisor;
+      rem = q;
+      off0 += c * g.strides[0][k];
+      if constexpr (NOPS == 2) off1 += c * g.strides[1][k];
+    }
+  }
+}
+
+// How a row kernel reads one operand's 16-byte group at (row offset, column):
+//   kStreamGroup: contiguous along the row and read once (non-temporal load);
+//   kCachedGroup: contiguous along the row and broadcast across rows, so it is
+//                 re-read for every row (ordinary, cached load);
+//   kSplatGroup:  broadcast along the row (inner stride 0): one value splat.
+// The mode is a template parameter of the long-row kernel so that its loads
+// form straight-line code: with a run-time choice per operand the compiler
+// waits for every outstanding load before the next one is issued.
+constexpr int kStreamGroup = 0;
+constexpr int kCachedGroup = 1;
+constexpr int kSplatGroup = 2;
+
+template <typename T, int MODE>
+__device__ __forceinline__ typename Vec16<T>::type row_group(const T* base, uint64_t row_offset,
+                                                             uint64_t column) {
+  using V = typename Vec16<T>::type;
+  V v;
+  if constexpr (MODE == kSplatGroup) {
+    const T s = base[row_offset];
+#pragma unroll
+    for (int k = 0; k < Vec16<T>::width; ++k) vec_set<T>(v, k, s);
+  } else {
+    v = load_vector_policy<MODE == kStreamGroup>(
+        reinterpret_cast<const V*>(base + row_offset + column));
+  }
+  return v;
+}
+
+// Run-time form for the short-row kernel: contiguous operands stream
+// (non-temporal), operands broadcast along the row are splat.
+template <typename T>
+__device__ __forceinline__ typename Vec16<T>::type row_group_any(const T* base,
+                                                                 uint64_t row_offset,
+                                                                 uint64_t column, int inner_unit) {
+  using V = typename Vec16<T>::type;
+  V v;
+  if (inner_unit) {
+    v = stream_load(reinterpret_cast<const V*>(base + row_offset + column));
+  } else {
+    const T s = base[row_offset];
+#pragma unroll
+    for (int k = 0; k < Vec16<T>::width; ++k) vec_set<T>(v, k, s);
+  }
+  return v;
+}
+
 template <typename T, int NOPS, typename F>
+__device__ __forceinline__ typename Vec16<T>::type apply_group(F f, const typename Vec16<T>::type& ra,
+                                                               const typename Vec16<T>::type& rb) {
+  typename Vec16<T>::type o;
+#pragma unroll
+  for (int k = 0; k < Vec16<T>::width; ++k) {
+    if constexpr (NOPS == 1) {
+      vec_set<T>(o, k, f(vec_get<T>(ra, k)));
+    } else {
+      vec_set<T>(o, k, f(vec_get<T>(ra, k), vec_get<T>(rb, k)));
+    }
+  }
+  return o;
+}
+
+// Short rows: each lane decodes the row of its own group.  NT: non-temporal
+// output stores.
+template <typename T, int NOPS, typename F, bool NT>
 __global__ void __launch_bounds__(kThreads)
     row_vector_kernel(T* out, const T* a, const T* b, uint64_t groups, RowGeometry rg, F f) {
   using V = typename Vec16<T>::type;
@@ -110,126 +190,58 @@ __global__ void __launch_bounds__(kThreads)
       if (group < groups) {
         const uint32_t row = rg.groups_per_row.div(static_cast<uint32_t>(group));
         const uint32_t column = (static_cast<uint32_t>(group) - row * rg.groups_per_row.divisor) * W;
-        uint64_t off0 = g.offsets[0];
-        uint64_t off1 = g.offsets[1];
-        uint32_t rem = row;
-#pragma unroll
-        for (int k = 1; k < kMaxRank; ++k) {
-          if (k < g.rank) {
-            const uint32_t q = g.divisors[k].div(rem);
-            const uint32_t c = rem - q * g.divisors[k].divisor;
-            rem = q;
-            off0 += static_cast<uint64_t>(c) * g.strides[0][k];
-            if constexpr (NOPS == 2) off1 += static_cast<uint64_t>(c) * g.strides[1][k];
-          }
-        }
-        if (rg.inner_unit[0]) {
-          const V* p = reinterpret_cast<const V*>(a + off0 + column);
-          ra[u] = rg.reused[0] ? *p : stream_load(p);
-        } else {
-          const T s = a[off0];
-#pragma unroll
-          for (int k = 0; k < W; ++k) vec_set<T>(ra[u], k, s);
-        }
-        if constexpr (NOPS == 2) {
-          if (rg.inner_unit[1]) {
-            const V* p = reinterpret_cast<const V*>(b + off1 + column);
-            rb[u] = rg.reused[1] ? *p : stream_load(p);
-          } else {
-            const T s = b[off1];
-#pragma unroll
-            for (int k = 0; k < W; ++k) vec_set<T>(rb[u], k, s);
-          }
-        }
+        uint64_t off0, off1;
+        row_offsets<NOPS>(g, row, off0, off1);
+        ra[u] = row_group_any<T>(a, off0, column, rg.inner_unit[0]);
+        if constexpr (NOPS == 2) rb[u] = row_group_any<T>(b, off1, column, rg.inner_unit[1]);
       }
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t group = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
-      if (group < groups) {
-        V o;
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-          if constexpr (NOPS == 1) {
-            vec_set<T>(o, k, f(vec_get<T>(ra[u], k)));
-          } else {
-            vec_set<T>(o, k, f(vec_get<T>(ra[u], k), vec_get<T>(rb[u], k)));
-          }
-        }
-        if (rg.stream_out) {
-          stream_store(out_v + group, o);
-        } else {
-          out_v[group] = o;
-        }
-      }
+      if (group < groups) store_vector<NT>(out_v + group, apply_group<T, NOPS>(f, ra[u], rb[u]));
     }
   }
 }
 
-// Row-segment variant for long rows: workgroup t owns 256 groups of row
-// t / column_tiles, so the row decode is uniform (scalar registers, once per
-// workgroup, by multiply-shift division) and each lane only adds its column
-// before the load.  Requires tiles and rows below 2^31.
-template <typename T, int NOPS, typename F>
+// Row-segment variant for long rows of a view of rank <= 3: workgroup t owns
+// 256 groups (one per lane) of row t / column_tiles.  The row's operand
+// offsets come from its two outer coordinates, (row mod e1, row / e1), with
+// one multiply-shift division in scalar registers; each lane then only adds
+// its column.  One group per lane and many short workgroups measured fastest
+// on MI355X for x[32768, 4096] + bias[4096] (steady state, 1 GiB moved):
+// 168 us, against 174 us for two consecutive rows per workgroup, 178 us for
+// four, and 173 / 183 us for two / four column segments of one row.  Requires
+// tiles and rows below 2^31.
+struct RowTileGeometry {
+  uint64_t inner;        // row length (elements), a multiple of W
+  uint32_t tiles;        // column tiles x rows
+  FastDiv column_tiles;  // 256-group segments per row
+  FastDiv outer1;        // extent of the axis above the row (1 for a single row)
+  uint64_t offsets[2];
+  uint64_t stride1[2];   // operand strides of that axis
+  uint64_t stride2[2];   // operand strides of the axis above it (0 when absent)
+};
+
+template <typename T, int NOPS, typename F, bool NT, int MODE_A, int MODE_B>
 __global__ void __launch_bounds__(kThreads)
-    row_tile_kernel(T* out, const T* a, const T* b, uint32_t tiles, FastDiv column_tiles,
-                    RowGeometry rg, F f) {
+    row_tile_kernel(T* out, const T* a, const T* b, RowTileGeometry rg, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
-  const KernelGeometry& g = rg.g;
-  const uint64_t inner = g.extents[0];
-  for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const uint32_t row = column_tiles.div(tile);
+  for (uint32_t tile = blockIdx.x; tile < rg.tiles; tile += gridDim.x) {
+    const uint32_t row = rg.column_tiles.div(tile);
     const uint64_t column =
-        (static_cast<uint64_t>(tile - row * column_tiles.divisor) * kThreads + threadIdx.x) * W;
-    uint64_t off0 = g.offsets[0];
-    uint64_t off1 = g.offsets[1];
-    uint32_t rem = row;
-#pragma unroll
-    for (int k = 1; k < kMaxRank; ++k) {
-      if (k < g.rank) {
-        const uint32_t q = g.divisors[k].div(rem);
-        const uint64_t c = rem - q * g.divisors[k].divisor;
-        rem = q;
-        off0 += c * g.strides[0][k];
-        if constexpr (NOPS == 2) off1 += c * g.strides[1][k];
-      }
-    }
-    if (column < inner) {
+        (static_cast<uint64_t>(tile - row * rg.column_tiles.divisor) * kThreads + threadIdx.x) * W;
+    const uint32_t c2 = rg.outer1.div(row);
+    const uint32_t c1 = row - c2 * rg.outer1.divisor;
+    const uint64_t off0 = rg.offsets[0] + c1 * rg.stride1[0] + c2 * rg.stride2[0];
+    const uint64_t off1 = rg.offsets[1] + c1 * rg.stride1[1] + c2 * rg.stride2[1];
+    if (column < rg.inner) {
       V ra, rb;
-      if (rg.inner_unit[0]) {
-        const V* p = reinterpret_cast<const V*>(a + off0 + column);
-        ra = rg.reused[0] ? *p : stream_load(p);
-      } else {
-        const T s = a[off0];
-#pragma unroll
-        for (int k = 0; k < W; ++k) vec_set<T>(ra, k, s);
-      }
-      if constexpr (NOPS == 2) {
-        if (rg.inner_unit[1]) {
-          const V* p = reinterpret_cast<const V*>(b + off1 + column);
-          rb = rg.reused[1] ? *p : stream_load(p);
-        } else {
-          const T s = b[off1];
-#pragma unroll
-          for (int k = 0; k < W; ++k) vec_set<T>(rb, k, s);
-        }
-      }
-      V o;
-#pragma unroll
-      for (int k = 0; k < W; ++k) {
-        if constexpr (NOPS == 1) {
-          vec_set<T>(o, k, f(vec_get<T>(ra, k)));
-        } else {
-          vec_set<T>(o, k, f(vec_get<T>(ra, k), vec_get<T>(rb, k)));
-        }
-      }
-      V* target = reinterpret_cast<V*>(out + row * inner + column);
-      if (rg.stream_out) {
-        stream_store(target, o);
-      } else {
-        *target = o;
-      }
+      ra = row_group<T, MODE_A>(a, off0, column);
+      if constexpr (NOPS == 2) rb = row_group<T, MODE_B>(b, off1, column);
+      store_vector<NT>(reinterpret_cast<V*>(out + row * rg.inner + column),
+                       apply_group<T, NOPS>(f, ra, rb));
     }
   }
 }
@@ -470,6 +482,23 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+template <int M>
+struct GroupMode {
+  static constexpr int value = M;
+};
+
+// Calls body(GroupMode<mode>{}) for a run-time row-group mode.
+template <typename Body>
+void with_group_mode(int mode, Body&& body) {
+  if (mode == kSplatGroup) {
+    body(GroupMode<kSplatGroup>{});
+  } else if (mode == kCachedGroup) {
+    body(GroupMode<kCachedGroup>{});
+  } else {
+    body(GroupMode<kStreamGroup>{});
+  }
+}
+
 uint32_t capped_grid(uint64_t work, uint64_t per_block) {
   uint64_t blocks = (work + per_block - 1) / per_block;
   if (blocks == 0) blocks = 1;
@@ -584,28 +613,59 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
     rg.groups_per_row.init(static_cast<uint32_t>(inner / W));
     rg.inner_unit[0] = inner_unit[0];
     rg.inner_unit[1] = inner_unit[1];
-    rg.stream_out = stream_output(count * sizeof(T)) ? 1 : 0;
+    // An operand with a zero stride on some axis of extent > 1 is re-read:
+    // it takes cached loads; every other operand streams.
+    bool reused[2] = {false, false};
     for (int op = 0; op < NOPS; ++op) {
-      rg.reused[op] = 0;
       for (int axis = 0; axis < view.rank; ++axis) {
-        if (view.strides[op][axis] == 0 && view.extents[axis] > 1) rg.reused[op] = 1;
+        if (view.strides[op][axis] == 0 && view.extents[axis] > 1) reused[op] = true;
       }
+    }
+    int mode[2] = {kStreamGroup, kStreamGroup};
+    for (int op = 0; op < NOPS; ++op) {
+      mode[op] = !inner_unit[op] ? kSplatGroup : reused[op] ? kCachedGroup : kStreamGroup;
     }
     const uint64_t groups = count / W;
     const uint64_t groups_per_row = inner / W;
-    if (groups_per_row >= kThreads / 2) {
+    const uint64_t rows = count / inner;
+    const bool long_rows = groups_per_row >= kThreads / 2 && view.rank <= 3 &&
+                           !(NOPS == 2 && mode[0] == kSplatGroup && mode[1] == kSplatGroup);
+    with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
+      constexpr bool NT = decltype(nt)::value;
+      if (!long_rows) {
+        row_vector_kernel<T, NOPS, F, NT>
+            <<<capped_grid(groups, static_cast<uint64_t>(kThreads) * kUnroll), kThreads, 0,
+               guard.stream>>>(out, a, b, groups, rg, f);
+        return;
+      }
       // Long rows: one workgroup per 256-group row segment.
+      RowTileGeometry tg{};
+      tg.inner = inner;
       const uint64_t column_tiles = (groups_per_row + kThreads - 1) / kThreads;
-      const uint64_t tiles = column_tiles * (count / inner);  // < count / 128
-      FastDiv tiles_per_row;
-      tiles_per_row.init(static_cast<uint32_t>(column_tiles));
-      row_tile_kernel<T, NOPS, F><<<capped_grid(tiles, 1), kThreads, 0, guard.stream>>>(
-          out, a, b, static_cast<uint32_t>(tiles), tiles_per_row, rg, f);
-      return;
-    }
-    row_vector_kernel<T, NOPS, F>
-        <<<capped_grid(groups, static_cast<uint64_t>(kThreads) * kUnroll), kThreads, 0,
-           guard.stream>>>(out, a, b, groups, rg, f);
+      tg.tiles = static_cast<uint32_t>(column_tiles * rows);  // < count / 128
+      tg.column_tiles.init(static_cast<uint32_t>(column_tiles));
+      // Outer axes: axis1 directly above the row, axis2 above it (rank 3).
+      const int axis1 = view.rank - 2;
+      tg.outer1.init(axis1 >= 0 ? static_cast<uint32_t>(view.extents[axis1]) : 1U);
+      for (int op = 0; op < NOPS; ++op) {
+        tg.offsets[op] = view.offsets[op];
+        tg.stride1[op] = axis1 >= 0 ? view.strides[op][axis1] : 0;
+        tg.stride2[op] = view.rank == 3 ? view.strides[op][0] : 0;
+      }
+      with_group_mode(mode[0], [&](auto mode_a) {
+        with_group_mode(NOPS == 2 ? mode[1] : kStreamGroup, [&](auto mode_b) {
+          constexpr int MA = decltype(mode_a)::value;
+          constexpr int MB = decltype(mode_b)::value;
+          if constexpr ((NOPS == 1 && MB != kStreamGroup) ||
+                        (MA == kSplatGroup && MB == kSplatGroup)) {
+            return;  // never selected (see long_rows and the NOPS == 1 mode above)
+          } else {
+            row_tile_kernel<T, NOPS, F, NT, MA, MB>
+                <<<capped_grid(tg.tiles, 1), kThreads, 0, guard.stream>>>(out, a, b, tg, f);
+          }
+        });
+      });
+    });
     return;
   }
 
