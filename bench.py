@@ -127,20 +127,22 @@ class Workload:
 
 
 def time_ops(hip, ops, reps=20, warmup=3):
-    """Median and mean event time (ms) of each op, each launch bracketed by
-    HIP events recorded on the backend's stream."""
+    """Per-launch time (ms) of each op: `reps` back-to-back launches of the op
+    bracketed by one pair of HIP events on the backend's stream, divided by
+    `reps`, so no event sits between two launches.  Every op streams at least
+    512 MiB, twice the Infinity Cache, so repeated launches read from HBM."""
     for _ in range(warmup):
         for _, _, launch in ops:
             launch()
     hip.synchronize()
-    times = {name: [] for name, _, _ in ops}
+    times = {}
     start, stop = hip.Event(), hip.Event()
-    for _ in range(reps):
-        for name, _, launch in ops:
-            start.record()
+    for name, _, launch in ops:
+        start.record()
+        for _ in range(reps):
             launch()
-            stop.record()
-            times[name].append(start.elapsed_ms(stop))
+        stop.record()
+        times[name] = start.elapsed_ms(stop) / reps
     return times
 
 
@@ -236,7 +238,7 @@ def main():
     kernel_time = {}
     kernel_bytes = {}
     for name, kernel, _ in ops:
-        mean_ms = statistics.mean(times[name])
+        mean_ms = times[name]
         gbps = nbytes[name] / (mean_ms * 1e-3) / 1e9
         per_op[name] = {"kernel": kernel, "ms": round(mean_ms, 5), "GB/s": round(gbps, 1),
                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": nbytes[name]}

@@ -61,8 +61,15 @@ template <typename T> struct Acc<T, Kind::Max> {
     best.value = take ? x : best.value;
     best.index = take ? index : best.index;
   }
+  // The full rule, as selects: NaN first (the earlier of two NaNs), then
+  // the larger value, then the earlier index.
   __device__ __forceinline__ void merge(const Acc& other) {
-    argmax_update(best, other.best.value, other.best.index);
+    const T v = other.best.value;
+    const T b = best.value;
+    const bool earlier = other.best.index < best.index;
+    const bool better = v > b || (v == b && earlier) || (v != v && (b == b || earlier));
+    best.value = better ? v : b;
+    best.index = better ? other.best.index : best.index;
   }
   __device__ __forceinline__ void wave_reduce() { best = wave_argmax(best); }
   __device__ __forceinline__ void seal(int64_t first) {
@@ -79,10 +86,15 @@ constexpr uint64_t kMaxScanRange = uint64_t{1} << 31;
 
 template <typename T, Kind K> struct ScanAcc;
 
+// Each has two forms of add: `add`, the exact rule, and `add_ordered`, which
+// is exact when no element is NaN.  The streaming kernels scan with
+// add_ordered, note whether any element was NaN (one unordered compare per
+// pair of elements), and rescan with `add` only the lanes that saw one.
 template <typename T> struct ScanAcc<T, Kind::Sum> {
   T value;
   __device__ __forceinline__ void init() { value = T(0); }
   __device__ __forceinline__ void add(T x, uint32_t) { value += x; }
+  __device__ __forceinline__ void add_ordered(T x, uint32_t) { value += x; }
   __device__ __forceinline__ Acc<T, Kind::Sum> finish(int64_t) const {
     Acc<T, Kind::Sum> acc;
     acc.value = value;
@@ -99,6 +111,13 @@ template <typename T> struct ScanAcc<T, Kind::Max> {
   }
   __device__ __forceinline__ void add(T x, uint32_t i) {
     const bool take = !(x <= value) && value == value;
+    value = take ? x : value;
+    index = take ? i : index;
+  }
+  // Without NaNs the value never becomes NaN, and a later element wins only
+  // if it is strictly larger: one ordered compare and two selects.
+  __device__ __forceinline__ void add_ordered(T x, uint32_t i) {
+    const bool take = x > value;
     value = take ? x : value;
     index = take ? i : index;
   }
@@ -153,17 +172,23 @@ __device__ __forceinline__ Acc<T, K> block_reduce(Acc<T, K> acc) {
 }
 
 // Where a reduction writes: final outputs, or partials for a second pass.
+// A max/argmax partial keeps its index relative to the first index of its
+// split (every split is below kMaxScanRange elements), as 32 bits: the
+// combine adds split x segment back.  Sealed partials always hold an index.
 template <typename T>
 struct Sink {
-  T* values;            // final values (Sum/Mean/Max) or partial values
-  int64_t* indices;     // argmax output or partial indices (may be null)
-  int operation;        // SPAR_HIP_SUM / MEAN / MAX / ARGMAX
-  T mean_divisor;       // (T)count for MEAN
-  int partial;          // 1: write raw partials (values + indices)
+  T* values;                  // final values (Sum/Mean/Max) or partial values
+  int64_t* indices;           // argmax output (may be null)
+  uint32_t* partial_indices;  // max/argmax partial indices, relative to the split
+  int operation;              // SPAR_HIP_SUM / MEAN / MAX / ARGMAX
+  T mean_divisor;             // (T)count for MEAN
+  int partial;                // 1: write raw partials (values + relative indices)
 };
 
+// Writes one result; `first` is the first index of the accumulator's split.
 template <typename T, Kind K>
-__device__ __forceinline__ void sink_write(const Sink<T>& sink, uint64_t slot, const Acc<T, K>& acc) {
+__device__ __forceinline__ void sink_write(const Sink<T>& sink, uint64_t slot, const Acc<T, K>& acc,
+                                           int64_t first) {
   if constexpr (K == Kind::Sum) {
     T v = acc.value;
     if (!sink.partial && sink.operation == SPAR_HIP_MEAN) v = v / sink.mean_divisor;
@@ -171,13 +196,27 @@ __device__ __forceinline__ void sink_write(const Sink<T>& sink, uint64_t slot, c
   } else {
     if (sink.partial) {
       sink.values[slot] = acc.best.value;
-      sink.indices[slot] = acc.best.index;
+      sink.partial_indices[slot] = static_cast<uint32_t>(acc.best.index - first);
     } else if (sink.operation == SPAR_HIP_ARGMAX) {
       sink.indices[slot] = acc.best.index;
     } else {
       sink.values[slot] = acc.best.value;
     }
   }
+}
+
+// Reads partial `slot` of split `split` (splits of `segment` elements).
+template <typename T, Kind K>
+__device__ __forceinline__ Acc<T, K> partial_read(const T* values, const uint32_t* indices,
+                                                  uint64_t slot, uint64_t split, uint64_t segment) {
+  Acc<T, K> acc;
+  if constexpr (K == Kind::Sum) {
+    acc.value = values[slot];
+  } else {
+    acc.best.value = values[slot];
+    acc.best.index = static_cast<int64_t>(split * segment + indices[slot]);
+  }
+  return acc;
 }
 
 // Row offsets: the kept axes (innermost first) with their strides.
@@ -234,6 +273,9 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int u = 0; u < 4; ++u) scan[u].init();
     if constexpr (VEC) {
+      // Ordered scan; `unordered` records whether this lane saw a NaN (for
+      // max/argmax: one unordered compare per pair of elements).
+      bool unordered = false;
       constexpr uint32_t step = static_cast<uint32_t>(kThreads) * W;
       uint64_t i = begin + static_cast<uint64_t>(threadIdx.x) * W;
       for (; i + 3 * step < end; i += 4 * step) {
@@ -244,14 +286,39 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
 #pragma unroll
-          for (int k = 0; k < W; ++k) scan[u].add(vec_get<T>(v[u], k), relative + u * step + k);
+          for (int k = 0; k < W; ++k) {
+            scan[u].add_ordered(vec_get<T>(v[u], k), relative + u * step + k);
+            if constexpr (K == Kind::Max) {
+              if (u % 2 == 1) {
+                unordered |= __builtin_isunordered(vec_get<T>(v[u], k), vec_get<T>(v[u - 1], k));
+              }
+            }
+          }
         }
       }
       for (; i < end; i += step) {
         const auto v = load_vector<T, NIN>(a, b, base + i);
         const uint32_t relative = static_cast<uint32_t>(i - begin);
 #pragma unroll
-        for (int k = 0; k < W; ++k) scan[0].add(vec_get<T>(v, k), relative + k);
+        for (int k = 0; k < W; ++k) {
+          scan[0].add_ordered(vec_get<T>(v, k), relative + k);
+          if constexpr (K == Kind::Max) unordered |= __builtin_isunordered(vec_get<T>(v, k), T(0));
+        }
+      }
+      if constexpr (K == Kind::Max) {
+        // A lane that saw a NaN rescans its elements, in increasing index
+        // order, with the exact rule (the block merge does not depend on how
+        // elements are split among the lane's accumulators).
+        if (unordered) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) scan[u].init();
+          for (uint64_t j = begin + static_cast<uint64_t>(threadIdx.x) * W; j < end; j += step) {
+            const auto v = load_vector<T, NIN>(a, b, base + j);
+            const uint32_t relative = static_cast<uint32_t>(j - begin);
+#pragma unroll
+            for (int k = 0; k < W; ++k) scan[0].add(vec_get<T>(v, k), relative + k);
+          }
+        }
       }
     } else {
       for (uint64_t i = begin + threadIdx.x; i < end; i += kThreads) {
@@ -266,7 +333,7 @@ __global__ void __launch_bounds__(kThreads)
     acc[0].merge(acc[2]);
     Acc<T, K> total = block_reduce<T, K>(acc[0]);
     if (begin < end) total.seal(static_cast<int64_t>(begin));
-    if (threadIdx.x == 0) sink_write<T, K>(sink, block, total);
+    if (threadIdx.x == 0) sink_write<T, K>(sink, block, total, static_cast<int64_t>(begin));
   }
 }
 
@@ -274,23 +341,30 @@ __global__ void __launch_bounds__(kThreads)
 // consecutive partials with a fixed tree.
 template <typename T, Kind K>
 __global__ void __launch_bounds__(kThreads)
-    combine_rows_kernel(const T* part_values, const int64_t* part_indices, uint64_t outputs,
-                        uint64_t parts, Sink<T> sink) {
+    combine_rows_kernel(const T* part_values, const uint32_t* part_indices, uint64_t outputs,
+                        uint64_t parts, uint64_t segment, Sink<T> sink) {
   for (uint64_t o = blockIdx.x; o < outputs; o += gridDim.x) {
     Acc<T, K> acc;
     acc.init();
-    for (uint64_t s = threadIdx.x; s < parts; s += kThreads) {
-      Acc<T, K> other;
-      if constexpr (K == Kind::Sum) {
-        other.value = part_values[o * parts + s];
-      } else {
-        other.best.value = part_values[o * parts + s];
-        other.best.index = part_indices[o * parts + s];
+    // Batches of 8 partials: every load of a batch is issued before the first
+    // merge, as in combine_columns_kernel.
+    constexpr int kBatch = 8;
+    for (uint64_t s0 = threadIdx.x; s0 < parts; s0 += kThreads * kBatch) {
+      Acc<T, K> part[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const uint64_t s = s0 + static_cast<uint64_t>(j) * kThreads;
+        if (s < parts) {
+          part[j] = partial_read<T, K>(part_values, part_indices, o * parts + s, s, segment);
+        } else {
+          part[j].init();
+        }
       }
-      acc.merge(other);
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) acc.merge(part[j]);
     }
     const Acc<T, K> total = block_reduce<T, K>(acc);
-    if (threadIdx.x == 0) sink_write<T, K>(sink, o, total);
+    if (threadIdx.x == 0) sink_write<T, K>(sink, o, total, 0);
   }
 }
 
@@ -367,7 +441,7 @@ __global__ void __launch_bounds__(kThreads)
           // Output slot: final [outer, inner]; partial [outer, splits, inner].
           const uint64_t slot = sink.partial ? (o * splits + split) * inner + column + k
                                              : o * inner + column + k;
-          sink_write<T, K>(sink, slot, total);
+          sink_write<T, K>(sink, slot, total, static_cast<int64_t>(begin));
         }
       }
     }
@@ -416,29 +490,48 @@ __global__ void __launch_bounds__(kThreads)
       for (int k = 0; k < W; ++k) scan[g][k].init();
     }
     const uint64_t base = row_offset(map, o) + column;
-    uint64_t r = begin;
-    for (; r + (R - 1) < end; r += R) {
-      typename Vec16<T>::type v[R][VPL];
+    using V = typename Vec16<T>::type;
+    auto load_batch = [&](V (&v)[R][VPL], uint64_t first) {
 #pragma unroll
       for (int u = 0; u < R; ++u) {
 #pragma unroll
         for (int g = 0; g < VPL; ++g) {
-          v[u][g] = load_vector<T, NIN>(a, b, base + (r + u) * reduced_stride + g * kGroupStride);
+          v[u][g] = load_vector<T, NIN>(a, b, base + (first + u) * reduced_stride + g * kGroupStride);
         }
       }
+    };
+    // Ordered scan; `unordered` records whether this lane saw a NaN (for
+    // max/argmax: one unordered compare per pair of rows).
+    bool unordered = false;
+    auto scan_batch = [&](const V (&v)[R][VPL], uint64_t first) {
+      const uint32_t relative = static_cast<uint32_t>(first - begin);
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+#pragma unroll
+        for (int g = 0; g < VPL; ++g) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) {
+            scan[g][k].add_ordered(vec_get<T>(v[u][g], k), relative + u);
+            if constexpr (K == Kind::Max) {
+              if (u % 2 == 1 || u == R - 1) {
+                const T x = vec_get<T>(v[u][g], k);
+                const T y = vec_get<T>(v[u - (u % 2)][g], k);
+                unordered |= __builtin_isunordered(x, y);
+              }
+            }
+          }
+        }
+      }
+    };
+    uint64_t r = begin;
+    for (; r + (R - 1) < end; r += R) {
+      V v[R][VPL];
+      load_batch(v, r);
       // Keep all R x VPL loads in flight: without this barrier the scheduler
       // interleaves the max/argmax compare-and-selects with the loads to save
       // registers and leaves about three loads outstanding.
       __builtin_amdgcn_sched_barrier(0);
-      const uint32_t relative = static_cast<uint32_t>(r - begin);
-#pragma unroll
-      for (int u = 0; u < R; ++u) {
-#pragma unroll
-        for (int g = 0; g < VPL; ++g) {
-#pragma unroll
-          for (int k = 0; k < W; ++k) scan[g][k].add(vec_get<T>(v[u][g], k), relative + u);
-        }
-      }
+      scan_batch(v, r);
     }
     for (; r < end; ++r) {
       const uint32_t relative = static_cast<uint32_t>(r - begin);
@@ -446,34 +539,87 @@ __global__ void __launch_bounds__(kThreads)
       for (int g = 0; g < VPL; ++g) {
         const auto v = load_vector<T, NIN>(a, b, base + r * reduced_stride + g * kGroupStride);
 #pragma unroll
-        for (int k = 0; k < W; ++k) scan[g][k].add(vec_get<T>(v, k), relative);
+        for (int k = 0; k < W; ++k) {
+          scan[g][k].add_ordered(vec_get<T>(v, k), relative);
+          if constexpr (K == Kind::Max) unordered |= __builtin_isunordered(vec_get<T>(v, k), T(0));
+        }
+      }
+    }
+    if constexpr (K == Kind::Max) {
+      // A lane that saw a NaN rescans its columns with the exact rule.
+      if (unordered) {
+#pragma unroll
+        for (int g = 0; g < VPL; ++g) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) scan[g][k].init();
+        }
+        for (uint64_t row = begin; row < end; ++row) {
+          const uint32_t relative = static_cast<uint32_t>(row - begin);
+#pragma unroll
+          for (int g = 0; g < VPL; ++g) {
+            const auto v = load_vector<T, NIN>(a, b, base + row * reduced_stride + g * kGroupStride);
+#pragma unroll
+            for (int k = 0; k < W; ++k) scan[g][k].add(vec_get<T>(v, k), relative);
+          }
+        }
       }
     }
 #pragma unroll
     for (int g = 0; g < VPL; ++g) {
+      const uint64_t c = column + g * kGroupStride;
+      Acc<T, K> total[W];
 #pragma unroll
       for (int k = 0; k < W; ++k) {
-        Acc<T, K> total = scan[g][k].finish(static_cast<int64_t>(begin));
-        if (begin < end) total.seal(static_cast<int64_t>(begin));
-        // Output slot: final [outer, inner]; partial [outer, splits, inner].
-        const uint64_t c = column + g * kGroupStride + k;
-        const uint64_t slot = sink.partial ? (o * splits + split) * inner + c : o * inner + c;
-        sink_write<T, K>(sink, slot, total);
+        total[k] = scan[g][k].finish(static_cast<int64_t>(begin));
+        if (begin < end) total[k].seal(static_cast<int64_t>(begin));
+      }
+      if (sink.partial) {
+        // Partials [outer, splits, inner]: the group's W values (and W
+        // relative indices) go out as one vector store each.
+        const uint64_t slot = (o * splits + split) * inner + c;
+        V values;
+        uint32_t indices[W];
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          if constexpr (K == Kind::Sum) {
+            vec_set<T>(values, k, total[k].value);
+          } else {
+            vec_set<T>(values, k, total[k].best.value);
+            indices[k] = static_cast<uint32_t>(total[k].best.index - static_cast<int64_t>(begin));
+          }
+        }
+        *reinterpret_cast<V*>(sink.values + slot) = values;
+        if constexpr (K == Kind::Max) {
+          if constexpr (W == 4) {
+            *reinterpret_cast<i32x4*>(sink.partial_indices + slot) =
+                i32x4{static_cast<int32_t>(indices[0]), static_cast<int32_t>(indices[1]),
+                      static_cast<int32_t>(indices[2]), static_cast<int32_t>(indices[3])};
+          } else {
+#pragma unroll
+            for (int k = 0; k < W; ++k) sink.partial_indices[slot + k] = indices[k];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          sink_write<T, K>(sink, o * inner + c + k, total[k], static_cast<int64_t>(begin));
+        }
       }
     }
   }
 }
 
 // Second pass after column splits: a 1024-lane block owns 64 columns of one
-// outer index; wave w sums splits w, w+16, ... and the 16 wave partials are
-// combined in wave order, so the result is deterministic.
+// outer index; wave w combines splits w, w+16, ... in order and the 16 wave
+// results are combined by a fixed LDS tree, so the result is deterministic.
 constexpr int kCombineThreads = 1024;
 constexpr int kCombineWaves = kCombineThreads / kWave;
+constexpr int kCombineBatch = 8;
 
 template <typename T, Kind K>
 __global__ void __launch_bounds__(kCombineThreads)
-    combine_columns_kernel(const T* part_values, const int64_t* part_indices, uint64_t outer,
-                           uint64_t splits, uint64_t inner, Sink<T> sink) {
+    combine_columns_kernel(const T* part_values, const uint32_t* part_indices, uint64_t outer,
+                           uint64_t splits, uint64_t segment, uint64_t inner, Sink<T> sink) {
   __shared__ Acc<T, K> lds[kCombineWaves][kWave];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
@@ -484,27 +630,37 @@ __global__ void __launch_bounds__(kCombineThreads)
     Acc<T, K> acc;
     acc.init();
     if (i < inner) {
-      for (uint64_t s = wave; s < splits; s += kCombineWaves) {
-        const uint64_t slot = (o * splits + s) * inner + i;
-        Acc<T, K> other;
-        if constexpr (K == Kind::Sum) {
-          other.value = part_values[slot];
-        } else {
-          other.best.value = part_values[slot];
-          other.best.index = part_indices[slot];
+      // Batches of kCombineBatch partials: every load of a batch is issued
+      // before the first merge (a max/argmax merge branches, and merging
+      // after each load would wait for each load in turn).
+      for (uint64_t s0 = wave; s0 < splits; s0 += kCombineWaves * kCombineBatch) {
+        Acc<T, K> part[kCombineBatch];
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) {
+          const uint64_t s = s0 + static_cast<uint64_t>(j) * kCombineWaves;
+          if (s < splits) {
+            part[j] = partial_read<T, K>(part_values, part_indices, (o * splits + s) * inner + i, s,
+                                         segment);
+          } else {
+            part[j].init();
+          }
         }
-        acc.merge(other);
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) acc.merge(part[j]);
       }
     }
     __syncthreads();
     lds[wave][lane] = acc;
     __syncthreads();
-    if (wave == 0 && i < inner) {
-      Acc<T, K> total = lds[0][lane];
 #pragma unroll
-      for (int w = 1; w < kCombineWaves; ++w) total.merge(lds[w][lane]);
-      sink_write<T, K>(sink, o * inner + i, total);
+    for (int half = kCombineWaves / 2; half > 0; half /= 2) {
+      if (wave < half) {
+        acc.merge(lds[wave + half][lane]);
+        lds[wave][lane] = acc;
+      }
+      __syncthreads();
     }
+    if (wave == 0 && i < inner) sink_write<T, K>(sink, o * inner + i, acc, 0);
   }
 }
 
@@ -542,7 +698,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     acc.wave_reduce();
     if (red.count != 0) acc.seal(0);
-    if (lane == 0) sink_write<T, K>(sink, o, acc);
+    if (lane == 0) sink_write<T, K>(sink, o, acc, 0);
   }
 }
 
@@ -630,7 +786,7 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     hipError_t error = scratch_allocate(&values, slots * sizeof(T), device);
     if (error != hipSuccess) return error;
     if constexpr (K == Kind::Max) {
-      error = scratch_allocate(&indices, slots * sizeof(int64_t), device);
+      error = scratch_allocate(&indices, slots * sizeof(uint32_t), device);
       if (error != hipSuccess) {
         scratch_release(values, device);
         return error;
@@ -639,7 +795,8 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     Sink<T> partial = sink;
     partial.partial = 1;
     partial.values = static_cast<T*>(values);
-    partial.indices = static_cast<int64_t*>(indices);
+    partial.indices = nullptr;
+    partial.partial_indices = static_cast<uint32_t*>(indices);
     body(partial);
     scratch_release(values, device);
     scratch_release(indices, device);
@@ -699,7 +856,7 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     return with_partials(rows * splits, [&](const Sink<T>& partial) {
       launch(partial);
       combine_rows_kernel<T, K><<<grid_for(rows), kThreads, 0, guard.stream>>>(
-          partial.values, partial.indices, rows, splits, final_sink());
+          partial.values, partial.partial_indices, rows, splits, segment, final_sink());
     });
   }
 
@@ -761,7 +918,8 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
       launch(partial);
       combine_columns_kernel<T, K>
           <<<grid_for(outer * ((inner + kWave - 1) / kWave)), kCombineThreads, 0, guard.stream>>>(
-              partial.values, partial.indices, outer, splits, inner, final_sink());
+              partial.values, partial.partial_indices, outer, splits, segment, inner,
+              final_sink());
     });
   }
 

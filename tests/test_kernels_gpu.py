@@ -402,6 +402,31 @@ def test_column_reductions_wide_rows(hip, dtype, shape, axes):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape,axes", [((96, 8192), [0]), ((8, 8192), [1]), ((3, 40, 4096), [1])])
+def test_max_argmax_nan_rescan(hip, dtype, shape, axes):
+    """The scans compare NaN-free data with one ordered compare and rescan
+    exactly the lanes that saw a NaN: NaNs (the first one wins), ties, signed
+    zeros and -inf columns on the 4-group column path and the row path."""
+    size = int(np.prod(shape))
+    x = (np.round(inputs(31, size, dtype, with_specials=False) * 4) / 4).astype(dtype).reshape(shape)
+    flat = x.reshape(-1, shape[-1])
+    r = flat.shape[0]
+    flat[r // 5, 100] = np.nan
+    flat[r // 2, 100] = np.nan
+    flat[r - 1, 4097 % shape[-1]] = np.nan
+    flat[:, 7] = -0.0
+    flat[r // 3, 7] = 0.0
+    flat[:, 8] = -np.inf
+    flat[2, 9] = np.inf
+    flat[r - 1, 9] = np.inf
+    for v in range(8):  # one NaN per 4-element group of a lane, in different rows
+        flat[(v * 7) % r, 2048 + 64 * v] = np.nan
+    mx, am = ref.axis_max(x, axes)
+    assert_bitexact(axis_reduce(hip, x, x, axes, "max", dtype), mx, f"nan rescan max {shape}")
+    assert_bitexact(axis_reduce(hip, x, x, axes, "argmax", dtype), am, f"nan rescan argmax {shape}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_max_argmax_negative_infinity_runs(hip, dtype):
     """Rows long enough to be split over blocks, made of -inf runs: the answer
     is the first -inf unless a NaN or a finite value appears later."""
