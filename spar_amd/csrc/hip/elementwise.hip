@@ -19,21 +19,25 @@
 namespace spar_hip {
 namespace {
 
-// One 16-byte vector per lane per tile and one tile per workgroup: on MI355X
-// this beats deeper per-lane unrolling for streaming kernels (many short
-// workgroups keep every CU's memory pipeline full until the end of the grid).
-constexpr int kThreads = 256;
+// One 16-byte vector per lane per tile and one tile per single-wave
+// workgroup: on MI355X this beats deeper per-lane unrolling and larger
+// workgroups for streaming kernels (many short workgroups keep every CU's
+// memory pipeline full until the end of the grid).  A broadcast add over
+// x[32768, 4096] (1 GiB moved, steady state) took 161 / 162 / 165 / 169 us
+// with workgroups of 64 / 128 / 256 / 512 lanes.
+constexpr int kThreads = 256;        // grid-stride scalar kernels
+constexpr int kVectorThreads = 64;   // streaming vector kernels
 constexpr int kUnroll = 1;
 constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
 
 template <typename T, typename F, bool NT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kVectorThreads)
     map1_vec_kernel(T* out, const T* in, uint64_t count, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
   constexpr int U = VectorsPerLane<F>::value;
-  const uint64_t tile = static_cast<uint64_t>(kThreads) * U;
+  const uint64_t tile = static_cast<uint64_t>(kVectorThreads) * U;
   const V* in_v = reinterpret_cast<const V*>(in);
   V* out_v = reinterpret_cast<V*>(out);
   for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < vectors;
@@ -41,12 +45,12 @@ __global__ void __launch_bounds__(kThreads)
     V r[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads + threadIdx.x;
       if (i < vectors) r[u] = stream_load(in_v + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads + threadIdx.x;
       if (i < vectors) {
         V o;
 #pragma unroll
@@ -62,12 +66,12 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 template <typename T, typename F, bool NT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kVectorThreads)
     map2_vec_kernel(T* out, const T* a, const T* b, uint64_t count, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
-  const uint64_t tile = static_cast<uint64_t>(kThreads) * kUnroll;
+  const uint64_t tile = static_cast<uint64_t>(kVectorThreads) * kUnroll;
   const V* a_v = reinterpret_cast<const V*>(a);
   const V* b_v = reinterpret_cast<const V*>(b);
   V* out_v = reinterpret_cast<V*>(out);
@@ -77,7 +81,7 @@ __global__ void __launch_bounds__(kThreads)
     V rb[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads + threadIdx.x;
       if (i < vectors) {
         ra[u] = stream_load(a_v + i);
         rb[u] = stream_load(b_v + i);
@@ -85,7 +89,7 @@ __global__ void __launch_bounds__(kThreads)
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads + threadIdx.x;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads + threadIdx.x;
       if (i < vectors) {
         V o;
 #pragma unroll
@@ -124,7 +128,7 @@ __global__ void __launch_bounds__(kThreads)
 
 uint32_t vector_grid(uint64_t count, int width, int vectors_per_lane = kUnroll) {
   const uint64_t vectors = count / static_cast<uint64_t>(width);
-  const uint64_t tile = static_cast<uint64_t>(kThreads) * vectors_per_lane;
+  const uint64_t tile = static_cast<uint64_t>(kVectorThreads) * vectors_per_lane;
   uint64_t blocks = (vectors + tile - 1) / tile;
   if (blocks == 0) blocks = 1;
   if (blocks > kMaxGrid) blocks = kMaxGrid;
@@ -144,7 +148,7 @@ void launch_map1(T* out, const T* in, uint64_t count, F f, const DeviceGuard& gu
   if (aligned16(out) && aligned16(in)) {
     with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
       map1_vec_kernel<T, F, decltype(nt)::value>
-          <<<vector_grid(count, Vec16<T>::width, VectorsPerLane<F>::value), kThreads, 0,
+          <<<vector_grid(count, Vec16<T>::width, VectorsPerLane<F>::value), kVectorThreads, 0,
              guard.stream>>>(out, in, count, f);
     });
   } else {
@@ -158,7 +162,8 @@ void launch_map2(T* out, const T* a, const T* b, uint64_t count, F f, const Devi
   if (aligned16(out) && aligned16(a) && aligned16(b)) {
     with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
       map2_vec_kernel<T, F, decltype(nt)::value>
-          <<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(out, a, b, count, f);
+          <<<vector_grid(count, Vec16<T>::width), kVectorThreads, 0, guard.stream>>>(out, a, b,
+                                                                                    count, f);
     });
   } else {
     map2_scalar_kernel<T, F><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
@@ -178,7 +183,7 @@ __device__ __forceinline__ T fill_value(const T* scalar, T value, T divisor, boo
 }
 
 template <typename T, bool NT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kVectorThreads)
     fill_vec_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
@@ -188,8 +193,8 @@ __global__ void __launch_bounds__(kThreads)
   for (int k = 0; k < W; ++k) vec_set<T>(o, k, v);
   const uint64_t vectors = count / W;
   V* out_v = reinterpret_cast<V*>(out);
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
-  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kVectorThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kVectorThreads + threadIdx.x; i < vectors;
        i += stride) {
     store_vector<NT>(out_v + i, o);
   }
@@ -216,7 +221,7 @@ void launch_fill_values(T* out, uint64_t count, const T* scalar, T value, T divi
   if (aligned16(out)) {
     with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
       fill_vec_kernel<T, decltype(nt)::value>
-          <<<vector_grid(count, Vec16<T>::width), kThreads, 0, guard.stream>>>(
+          <<<vector_grid(count, Vec16<T>::width), kVectorThreads, 0, guard.stream>>>(
               out, count, scalar, value, divisor, divide);
     });
   } else {

@@ -609,35 +609,44 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// Second pass after column splits: a 1024-lane block owns 64 columns of one
-// outer index; wave w combines splits w, w+16, ... in order and the 16 wave
-// results are combined by a fixed LDS tree, so the result is deterministic.
+// Second pass after column splits.  A 1024-lane block holds 16 / P groups of
+// P waves; each group owns 64 columns of one outer index, its wave p combines
+// splits p, p + P, ... in order, and the group's P results are combined by a
+// fixed LDS tree, so the result is deterministic.  P grows with the number
+// of splits: few splits need no split parallelism, and a block of 16 waves
+// on one column range would then be mostly idle.
 constexpr int kCombineThreads = 1024;
 constexpr int kCombineWaves = kCombineThreads / kWave;
 constexpr int kCombineBatch = 8;
 
-template <typename T, Kind K>
+template <typename T, Kind K, int P>
 __global__ void __launch_bounds__(kCombineThreads)
     combine_columns_kernel(const T* part_values, const uint32_t* part_indices, uint64_t outer,
                            uint64_t splits, uint64_t segment, uint64_t inner, Sink<T> sink) {
+  constexpr int kGroups = kCombineWaves / P;
   __shared__ Acc<T, K> lds[kCombineWaves][kWave];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const uint64_t groups = (inner + kWave - 1) / kWave;
-  for (uint64_t block = blockIdx.x; block < outer * groups; block += gridDim.x) {
-    const uint64_t o = block / groups;
-    const uint64_t i = (block - o * groups) * kWave + lane;
+  const int group = wave / P;
+  const int p = wave % P;
+  const uint64_t ranges = (inner + kWave - 1) / kWave;  // 64-column ranges per outer index
+  const uint64_t blocks = outer * ((ranges + kGroups - 1) / kGroups);
+  for (uint64_t block = blockIdx.x; block < blocks; block += gridDim.x) {
+    const uint64_t range = block * kGroups + group;  // over outer x ranges, ranges padded
+    const uint64_t o = range / (((ranges + kGroups - 1) / kGroups) * kGroups);
+    const uint64_t r = range - o * (((ranges + kGroups - 1) / kGroups) * kGroups);
+    const uint64_t i = r * kWave + lane;
+    const bool valid = r < ranges && i < inner;
     Acc<T, K> acc;
     acc.init();
-    if (i < inner) {
+    if (valid) {
       // Batches of kCombineBatch partials: every load of a batch is issued
-      // before the first merge (a max/argmax merge branches, and merging
-      // after each load would wait for each load in turn).
-      for (uint64_t s0 = wave; s0 < splits; s0 += kCombineWaves * kCombineBatch) {
+      // before the first merge, so a lane waits for one batch at a time.
+      for (uint64_t s0 = p; s0 < splits; s0 += P * kCombineBatch) {
         Acc<T, K> part[kCombineBatch];
 #pragma unroll
         for (int j = 0; j < kCombineBatch; ++j) {
-          const uint64_t s = s0 + static_cast<uint64_t>(j) * kCombineWaves;
+          const uint64_t s = s0 + static_cast<uint64_t>(j) * P;
           if (s < splits) {
             part[j] = partial_read<T, K>(part_values, part_indices, (o * splits + s) * inner + i, s,
                                          segment);
@@ -649,18 +658,20 @@ __global__ void __launch_bounds__(kCombineThreads)
         for (int j = 0; j < kCombineBatch; ++j) acc.merge(part[j]);
       }
     }
-    __syncthreads();
-    lds[wave][lane] = acc;
-    __syncthreads();
-#pragma unroll
-    for (int half = kCombineWaves / 2; half > 0; half /= 2) {
-      if (wave < half) {
-        acc.merge(lds[wave + half][lane]);
-        lds[wave][lane] = acc;
-      }
+    if constexpr (P > 1) {
       __syncthreads();
+      lds[wave][lane] = acc;
+      __syncthreads();
+#pragma unroll
+      for (int half = P / 2; half > 0; half /= 2) {
+        if (p < half) {
+          acc.merge(lds[wave + half][lane]);
+          lds[wave][lane] = acc;
+        }
+        __syncthreads();
+      }
     }
-    if (wave == 0 && i < inner) sink_write<T, K>(sink, o * inner + i, acc, 0);
+    if (p == 0 && valid) sink_write<T, K>(sink, o * inner + i, acc, 0);
   }
 }
 
@@ -916,10 +927,19 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     }
     return with_partials(outer * splits * inner, [&](const Sink<T>& partial) {
       launch(partial);
-      combine_columns_kernel<T, K>
-          <<<grid_for(outer * ((inner + kWave - 1) / kWave)), kCombineThreads, 0, guard.stream>>>(
-              partial.values, partial.partial_indices, outer, splits, segment, inner,
-              final_sink());
+      const uint64_t ranges = (inner + kWave - 1) / kWave;
+      auto combine = [&](auto kernel, uint64_t groups) {
+        kernel<<<grid_for(outer * ((ranges + groups - 1) / groups)), kCombineThreads, 0,
+                 guard.stream>>>(partial.values, partial.partial_indices, outer, splits, segment,
+                                 inner, final_sink());
+      };
+      if (splits >= 128) {
+        combine(combine_columns_kernel<T, K, 16>, 1);
+      } else if (splits >= 16) {
+        combine(combine_columns_kernel<T, K, 4>, 4);
+      } else {
+        combine(combine_columns_kernel<T, K, 1>, 16);
+      }
     });
   }
 

@@ -204,19 +204,23 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// Row-segment variant for long rows of a view of rank <= 3: workgroup t owns
-// 256 groups (one per lane) of row t / column_tiles.  The row's operand
-// offsets come from its two outer coordinates, (row mod e1, row / e1), with
-// one multiply-shift division in scalar registers; each lane then only adds
-// its column.  One group per lane and many short workgroups measured fastest
-// on MI355X for x[32768, 4096] + bias[4096] (steady state, 1 GiB moved):
-// 168 us, against 174 us for two consecutive rows per workgroup, 178 us for
-// four, and 173 / 183 us for two / four column segments of one row.  Requires
-// tiles and rows below 2^31.
+// Row-segment variant for long rows of a view of rank <= 3: a single-wave
+// workgroup t owns 64 groups (one per lane) of row t / column_tiles.  The
+// row's operand offsets come from its two outer coordinates, (row mod e1,
+// row / e1), with one multiply-shift division in scalar registers; each lane
+// then only adds its column.  One group per lane and many short workgroups
+// measured fastest on MI355X for x[32768, 4096] + bias[4096] (steady state,
+// 1 GiB moved): with 256-lane workgroups, 168 us against 174 us for two
+// consecutive rows per workgroup, 178 us for four, and 173 / 183 us for two /
+// four column segments of one row; a minimal kernel of this shape took 161 /
+// 162 / 165 / 169 us with workgroups of 64 / 128 / 256 / 512 lanes.
+// Requires tiles and rows below 2^31.
+constexpr int kRowTileThreads = 64;
+
 struct RowTileGeometry {
   uint64_t inner;        // row length (elements), a multiple of W
   uint32_t tiles;        // column tiles x rows
-  FastDiv column_tiles;  // 256-group segments per row
+  FastDiv column_tiles;  // kRowTileThreads-group segments per row
   FastDiv outer1;        // extent of the axis above the row (1 for a single row)
   uint64_t offsets[2];
   uint64_t stride1[2];   // operand strides of that axis
@@ -224,14 +228,15 @@ struct RowTileGeometry {
 };
 
 template <typename T, int NOPS, typename F, bool NT, int MODE_A, int MODE_B>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kRowTileThreads)
     row_tile_kernel(T* out, const T* a, const T* b, RowTileGeometry rg, F f) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   for (uint32_t tile = blockIdx.x; tile < rg.tiles; tile += gridDim.x) {
     const uint32_t row = rg.column_tiles.div(tile);
     const uint64_t column =
-        (static_cast<uint64_t>(tile - row * rg.column_tiles.divisor) * kThreads + threadIdx.x) * W;
+        (static_cast<uint64_t>(tile - row * rg.column_tiles.divisor) * kRowTileThreads +
+         threadIdx.x) * W;
     const uint32_t c2 = rg.outer1.div(row);
     const uint32_t c1 = row - c2 * rg.outer1.divisor;
     const uint64_t off0 = rg.offsets[0] + c1 * rg.stride1[0] + c2 * rg.stride2[0];
@@ -628,7 +633,7 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
     const uint64_t groups = count / W;
     const uint64_t groups_per_row = inner / W;
     const uint64_t rows = count / inner;
-    const bool long_rows = groups_per_row >= kThreads / 2 && view.rank <= 3 &&
+    const bool long_rows = groups_per_row >= kRowTileThreads && view.rank <= 3 &&
                            !(NOPS == 2 && mode[0] == kSplatGroup && mode[1] == kSplatGroup);
     with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
       constexpr bool NT = decltype(nt)::value;
@@ -638,11 +643,11 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
                guard.stream>>>(out, a, b, groups, rg, f);
         return;
       }
-      // Long rows: one workgroup per 256-group row segment.
+      // Long rows: one single-wave workgroup per 64-group row segment.
       RowTileGeometry tg{};
       tg.inner = inner;
-      const uint64_t column_tiles = (groups_per_row + kThreads - 1) / kThreads;
-      tg.tiles = static_cast<uint32_t>(column_tiles * rows);  // < count / 128
+      const uint64_t column_tiles = (groups_per_row + kRowTileThreads - 1) / kRowTileThreads;
+      tg.tiles = static_cast<uint32_t>(column_tiles * rows);  // <= count / 128
       tg.column_tiles.init(static_cast<uint32_t>(column_tiles));
       // Outer axes: axis1 directly above the row, axis2 above it (rank 3).
       const int axis1 = view.rank - 2;
@@ -661,7 +666,7 @@ void launch_view(T* out, const T* a, const T* b, const MultiView& view, F f,
             return;  // never selected (see long_rows and the NOPS == 1 mode above)
           } else {
             row_tile_kernel<T, NOPS, F, NT, MA, MB>
-                <<<capped_grid(tg.tiles, 1), kThreads, 0, guard.stream>>>(out, a, b, tg, f);
+                <<<capped_grid(tg.tiles, 1), kRowTileThreads, 0, guard.stream>>>(out, a, b, tg, f);
           }
         });
       });
