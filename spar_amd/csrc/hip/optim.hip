@@ -35,10 +35,12 @@ namespace spar_hip {
 namespace {
 
 constexpr int kThreads = 256;
+// Streaming kernels use single-wave workgroups (see elementwise.hip).
+constexpr int kVectorThreads = 64;
 constexpr uint64_t kMaxGrid = uint64_t{1} << 20;
 
 uint32_t tile_grid(uint64_t vectors) {
-  uint64_t blocks = (vectors + kThreads - 1) / kThreads;
+  uint64_t blocks = (vectors + kVectorThreads - 1) / kVectorThreads;
   if (blocks == 0) blocks = 1;
   if (blocks > kMaxGrid) blocks = kMaxGrid;
   return static_cast<uint32_t>(blocks);
@@ -94,7 +96,7 @@ __device__ __forceinline__ void adamw_element(T& parameter, T gradient, T& first
 constexpr int kAdamwUnroll = 2;
 
 template <typename T, bool NT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kVectorThreads)
     adamw_vec_kernel(T* parameter, const T* gradient, T* first, T* second, uint64_t count,
                      AdamwStep step) {
   using V = typename Vec16<T>::type;
@@ -105,33 +107,33 @@ __global__ void __launch_bounds__(kThreads)
   const V* g_v = reinterpret_cast<const V*>(gradient);
   V* m_v = reinterpret_cast<V*>(first);
   V* s_v = reinterpret_cast<V*>(second);
-  const uint64_t tile = static_cast<uint64_t>(kThreads) * U;
+  const uint64_t tile = static_cast<uint64_t>(kVectorThreads) * U;
   for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile + threadIdx.x; base < vectors;
        base += static_cast<uint64_t>(gridDim.x) * tile) {
     V p[U], g[U], m[U], s[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads;
       if (i < vectors) p[u] = stream_load(p_v + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads;
       if (i < vectors) g[u] = stream_load(g_v + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads;
       if (i < vectors) m[u] = stream_load(m_v + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads;
       if (i < vectors) s[u] = stream_load(s_v + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
+      const uint64_t i = base + static_cast<uint64_t>(u) * kVectorThreads;
       if (i >= vectors) continue;
 #pragma unroll
       for (int k = 0; k < W; ++k) {
@@ -170,7 +172,8 @@ void launch_adamw(T* parameter, const T* gradient, T* first, T* second, uint64_t
     const uint64_t vectors = count / Vec16<T>::width;
     with_policy(stream_output(3 * count * sizeof(T)), [&](auto nt) {
       adamw_vec_kernel<T, decltype(nt)::value>
-          <<<tile_grid((vectors + kAdamwUnroll - 1) / kAdamwUnroll), kThreads, 0, guard.stream>>>(
+          <<<tile_grid((vectors + kAdamwUnroll - 1) / kAdamwUnroll), kVectorThreads, 0,
+             guard.stream>>>(
               parameter, gradient, first, second, count, step);
     });
   } else {
@@ -188,14 +191,14 @@ __device__ __forceinline__ T scaled(T value, double factor) {
 }
 
 template <typename T, bool NT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kVectorThreads)
     scale_vec_kernel(T* values, uint64_t count, double factor) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = count / W;
   V* v_v = reinterpret_cast<V*>(values);
-  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vectors;
-       i += static_cast<uint64_t>(gridDim.x) * kThreads) {
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kVectorThreads + threadIdx.x;
+       i < vectors; i += static_cast<uint64_t>(gridDim.x) * kVectorThreads) {
     V v = stream_load(v_v + i);
 #pragma unroll
     for (int k = 0; k < W; ++k) vec_set<T>(v, k, scaled(vec_get<T>(v, k), factor));
@@ -222,7 +225,8 @@ void launch_scale(T* values, uint64_t count, double factor, const DeviceGuard& g
   if (aligned16(values)) {
     with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
       scale_vec_kernel<T, decltype(nt)::value>
-          <<<tile_grid(count / Vec16<T>::width), kThreads, 0, guard.stream>>>(values, count, factor);
+          <<<tile_grid(count / Vec16<T>::width), kVectorThreads, 0, guard.stream>>>(values, count,
+                                                                                    factor);
     });
   } else {
     scale_scalar_kernel<T><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(

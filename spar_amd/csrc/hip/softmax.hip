@@ -1017,19 +1017,24 @@ __global__ void __launch_bounds__(kEntropyThreads)
 // backward turns it into dx = g - exp(lp) * s with s = sum of g = g_t
 // (softmax.cpp:406-444).  Here lp = (x - m) - log S is recomputed with the
 // forward's operations, so dx is that expression without either tensor
-// materialised; undefined rows are NaN.  Tiles of 256 x W columns of one row.
+// materialised; undefined rows are NaN.  Single-wave workgroups over tiles of
+// 64 x W columns of one row (single-wave workgroups stream fastest; see
+// elementwise.hip).  Tile counts below 2^31 use multiply-shift division.
+constexpr int kEntropyTileThreads = 64;
+
 template <typename T, typename I, bool VEC, bool NT>
-__global__ void __launch_bounds__(kEntropyThreads)
+__global__ void __launch_bounds__(kEntropyTileThreads)
     entropy_backward_kernel(T* dx, const T* loss_gradient, const T* logits, const T* row_max,
                             const T* row_log_sum, const int32_t* undefined, const I* targets,
                             uint64_t rows, uint64_t classes, uint64_t column_tiles,
-                            TargetMap map) {
+                            FastDiv tiles_per_row, TargetMap map) {
   constexpr int W = VEC ? Vec16<T>::width : 1;
   using V = typename Vec16<T>::type;
   const uint64_t tiles = rows * column_tiles;
+  const bool small = tiles <= kIndex32Limit;
   for (uint64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const uint64_t r = tile / column_tiles;
-    const uint64_t c = ((tile - r * column_tiles) * kEntropyThreads + threadIdx.x) * W;
+    const uint64_t r = small ? tiles_per_row.div(static_cast<uint32_t>(tile)) : tile / column_tiles;
+    const uint64_t c = ((tile - r * column_tiles) * kEntropyTileThreads + threadIdx.x) * W;
     if (c >= classes) continue;
     uint64_t target_index, output_index;
     T g_t = T(0);
@@ -1233,13 +1238,16 @@ void launch_entropy_backward(void* logits_gradient, const void* loss_gradient,
   const bool vec = classes % Vec16<T>::width == 0 && aligned16(logits) &&
                    aligned16(logits_gradient);
   const uint64_t width = vec ? Vec16<T>::width : 1;
-  const uint64_t column_tiles = (classes + kEntropyThreads * width - 1) / (kEntropyThreads * width);
+  const uint64_t column_tiles =
+      (classes + kEntropyTileThreads * width - 1) / (kEntropyTileThreads * width);
+  FastDiv tiles_per_row;
+  tiles_per_row.init(column_tiles <= kIndex32Limit ? static_cast<uint32_t>(column_tiles) : 1U);
   auto launch = [&](auto kernel) {
-    kernel<<<grid_for(rows * column_tiles), kEntropyThreads, 0, guard.stream>>>(
+    kernel<<<grid_for(rows * column_tiles), kEntropyTileThreads, 0, guard.stream>>>(
         static_cast<T*>(logits_gradient), static_cast<const T*>(loss_gradient),
         static_cast<const T*>(logits), static_cast<const T*>(row_max),
         static_cast<const T*>(row_log_sum), undefined_rows, static_cast<const I*>(targets), rows,
-        classes, column_tiles, map);
+        classes, column_tiles, tiles_per_row, map);
   };
   if (vec) {
     with_policy(stream_output(rows * classes * sizeof(T)), [&](auto nt) {

@@ -46,7 +46,8 @@ ROOT = Path(__file__).resolve().parent.parent
 # kernels such as the partial-sum combine add traffic but no launch).
 CLASSES = {
     "broadcast_binary": [(r"::row_tile_kernel<|::row_vector_kernel<", True)],
-    "column_reduction": [(r"::column_kernel<", True), (r"::combine_columns_kernel<", False)],
+    "column_reduction": [(r"::column_kernel<|::column_wide_kernel<", True),
+                         (r"::combine_columns_kernel<", False)],
 }
 COPY_PATTERN = r"CopyOp"
 CALIBRATION_BYTES = 512 << 20
