@@ -8,9 +8,11 @@
 // CDNA4 design for the last axis (inner == 1), the common case: one
 // workgroup per row holds the whole row in VGPRs (up to 32768 float32 with
 // 1024 lanes x 8 float4), so the row is read from HBM once and written once:
-//   pass over registers 1: max (first occurrence), NaN flag, +inf count;
+//   pass over registers 1: first-occurrence max;
 //   workgroup combine through wave64 shuffles and a 16-entry LDS exchange;
 //   pass 2: e = exp(x - max), sum; pass 3: p = e / sum (log: (x-max) - log sum).
+// A row's workgroup stays under 64 VGPRs per lane, so two or more rows share
+// a CU and one row's loads overlap another's reductions and stores.
 // Backward keeps g and y (or log p) in registers the same way.  Rows longer
 // than the register budget take a three-read loop, and a non-last axis
 // (inner > 1) a lane-per-slice kernel that is coalesced across `inner`.
@@ -36,9 +38,8 @@ struct SliceStats {
 
 // Barrier for the reductions' LDS exchanges: waits for this wave's LDS
 // accesses (lgkmcnt(0)) and meets the other waves at s_barrier.  Unlike
-// __syncthreads() it is not a release fence, so global loads in flight, such
-// as the next row's direct-to-LDS prefetch into a separate stage buffer, keep
-// flying across it.  The signal fences stop the compiler from moving memory
+// __syncthreads() it is not a release fence, so global stores in flight keep
+// draining across it.  The signal fences stop the compiler from moving memory
 // accesses across the barrier; they emit no instructions.
 __device__ __forceinline__ void exchange_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -173,49 +174,63 @@ __device__ __forceinline__ bool slice_undefined(const SliceStats<T>& s) {
 
 // Element j of a thread's register array maps to column col(t, j):
 // VEC: 16-byte groups interleaved across lanes; scalar: lanes interleaved.
+// Register rows hold at most 32768 elements, so columns are 32-bit and a
+// row access is a uniform row base plus a 32-bit lane offset.
 template <typename T, int THREADS, bool VEC>
-__device__ __forceinline__ uint64_t column_of(int j) {
+__device__ __forceinline__ uint32_t column_of(int j) {
   if constexpr (VEC) {
     constexpr int W = Vec16<T>::width;
-    return (static_cast<uint64_t>(j / W) * THREADS + threadIdx.x) * W + (j % W);
+    return (static_cast<uint32_t>(j / W) * THREADS + threadIdx.x) * W + (j % W);
   } else {
-    return static_cast<uint64_t>(j) * THREADS + threadIdx.x;
+    return static_cast<uint32_t>(j) * THREADS + threadIdx.x;
   }
 }
 
+// Columns grow with the register slot j, so the slots of a lane that hold
+// columns < n are a prefix j < live_slots(n) (whole 16-byte groups for VEC,
+// where n is a multiple of the vector width).  One 32-bit bound per lane
+// replaces a 64-bit column compare per slot.
+template <typename T, int THREADS, int E, bool VEC>
+__device__ __forceinline__ int live_slots(uint64_t n) {
+  constexpr int W = VEC ? Vec16<T>::width : 1;
+  const int units = static_cast<int>(n / W);  // n <= THREADS * E
+  const int lane = static_cast<int>(threadIdx.x);
+  return units > lane ? ((units - lane + THREADS - 1) / THREADS) * W : 0;
+}
+
+// Loads a row into registers; slots past the row hold `pad`.
 template <typename T, int THREADS, int E, bool VEC, bool FULL>
-__device__ __forceinline__ void load_row(T (&x)[E], const T* row, uint64_t n) {
+__device__ __forceinline__ void load_row(T (&x)[E], const T* row, int live, T pad) {
   if constexpr (VEC) {
     using V = typename Vec16<T>::type;
     constexpr int W = Vec16<T>::width;
 #pragma unroll
     for (int v = 0; v < E / W; ++v) {
-      const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
-      if (FULL || col < n) {
-        const V value = stream_load(reinterpret_cast<const V*>(row + col));
+      if (FULL || v * W < live) {
+        const V value = stream_load(reinterpret_cast<const V*>(row + column_of<T, THREADS, true>(v * W)));
 #pragma unroll
         for (int k = 0; k < W; ++k) x[v * W + k] = vec_get<T>(value, k);
+      } else {
+#pragma unroll
+        for (int k = 0; k < W; ++k) x[v * W + k] = pad;
       }
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const uint64_t col = column_of<T, THREADS, false>(j);
-      if (FULL || col < n) x[j] = row[col];
-    }
+    for (int j = 0; j < E; ++j) x[j] = FULL || j < live ? row[column_of<T, THREADS, false>(j)] : pad;
   }
 }
 
 // NT: non-temporal stores (outputs of 64 MiB or more).
 template <typename T, int THREADS, int E, bool VEC, bool FULL, bool NT>
-__device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n) {
+__device__ __forceinline__ void store_row(T* row, const T (&y)[E], int live) {
   if constexpr (VEC) {
     using V = typename Vec16<T>::type;
     constexpr int W = Vec16<T>::width;
 #pragma unroll
     for (int v = 0; v < E / W; ++v) {
-      const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
-      if (FULL || col < n) {
+      if (FULL || v * W < live) {
+        const uint32_t col = column_of<T, THREADS, true>(v * W);
         V value;
 #pragma unroll
         for (int k = 0; k < W; ++k) vec_set<T>(value, k, y[v * W + k]);
@@ -225,8 +240,7 @@ __device__ __forceinline__ void store_row(T* row, const T (&y)[E], uint64_t n) {
   } else {
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const uint64_t col = column_of<T, THREADS, false>(j);
-      if (FULL || col < n) row[col] = y[j];
+      if (FULL || j < live) row[column_of<T, THREADS, false>(j)] = y[j];
     }
   }
 }
@@ -268,10 +282,12 @@ __device__ __forceinline__ T block_max_first(T value, int32_t index) {
   return best;
 }
 
-// Forward over rows held in registers.  Each block walks rows blockIdx.x,
-// blockIdx.x + gridDim.x, ... (the grid is sized to the resident blocks) and,
-// when PREFETCH, issues the loads of its next row before computing the
-// current one, so a CU's HBM reads overlap its arithmetic.
+// Forward over rows held in registers, one row per workgroup (the launcher
+// splits the rows into grids of at most kMaxGrid workgroups).  With no row
+// loop nothing is hoisted across rows, so a lane needs E + ~30 VGPRs and
+// several workgroups share a CU: while one reduces or stores, the others'
+// loads are in flight.  The per-lane maximum tracks the register slot j
+// (an immediate) and turns it into a column once, after the scan.
 //
 // The fast path keeps no NaN or infinity bookkeeping: with m the
 // first-occurrence maximum over the non-NaN elements, S = sum exp(x - m) is
@@ -279,165 +295,47 @@ __device__ __forceinline__ T block_max_first(T value, int32_t index) {
 // maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
 // otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
 // row and apply the reference's special cases from full slice statistics.
-template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool PREFETCH, bool NT>
-__global__ void __launch_bounds__(THREADS)
-    forward_row_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n) {
-  T x[E];
-  T next[PREFETCH ? E : 1];
-  uint64_t r = blockIdx.x;
-  if constexpr (PREFETCH) {
-    if (r < rows) load_row<T, THREADS, E, VEC, FULL>(next, in + r * n, n);
-  }
-  for (; r < rows; r += gridDim.x) {
-    if constexpr (PREFETCH) {
-#pragma unroll
-      for (int j = 0; j < E; ++j) x[j] = next[j];
-      if (r + gridDim.x < rows) load_row<T, THREADS, E, VEC, FULL>(next, in + (r + gridDim.x) * n, n);
-    } else {
-      load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
-    }
-    // Lane maximum: columns reach a lane in increasing order, so a later
-    // element wins only if it is strictly larger.
-    T lane_max = -positive_infinity<T>();
-    int32_t lane_index = INT32_MAX;
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const uint64_t col = column_of<T, THREADS, VEC>(j);
-      if (FULL || col < n) {
-        const bool take = x[j] > lane_max;
-        lane_max = take ? x[j] : lane_max;
-        lane_index = take ? static_cast<int32_t>(col) : lane_index;
-      }
-    }
-    const T maximum = block_max_first<T, THREADS>(lane_max, lane_index);
-    // The results overwrite x in place so one row costs E registers per lane.
-    T local = T(0);
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const uint64_t col = column_of<T, THREADS, VEC>(j);
-      if constexpr (LOG) {
-        x[j] = x[j] - maximum;
-        if (FULL || col < n) local += math_exp(x[j]);
-      } else {
-        x[j] = math_exp(x[j] - maximum);
-        if (FULL || col < n) local += x[j];
-      }
-    }
-    const T total = block_sum<T, THREADS>(local);
-    const bool bad = total != total;
-    if (threadIdx.x == 0) undefined[r] = bad ? 1 : 0;
-    if (!bad) {
-      if constexpr (LOG) {
-        const T log_sum = math_log(total);
-#pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = x[j] - log_sum;
-      } else {
-        const RowDivisor<T> divide(total);
-#pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = divide(x[j]);
-      }
-    } else {
-      load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
-      SliceStats<T> s;
-      stats_init(s);
-#pragma unroll
-      for (int j = 0; j < E; ++j) {
-        const uint64_t col = column_of<T, THREADS, VEC>(j);
-        if (FULL || col < n) stats_add(s, x[j], static_cast<int64_t>(col));
-      }
-      s = block_stats<T, THREADS>(s);
-#pragma unroll
-      for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
-    }
-    store_row<T, THREADS, E, VEC, FULL, NT>(out + r * n, x, n);
-  }
-}
-
-// ------------------------------------------- LDS-staged rows (prefetch)
-
-// s_waitcnt immediate that waits until at most `count` vector memory
-// operations are outstanding (vmcnt in bits 3:0 and 15:14) and leaves expcnt
-// (bits 6:4) and lgkmcnt (bits 11:8) at their maxima, i.e. unconstrained.
-constexpr int vmcnt_wait(int count) {
-  return (count & 0xF) | ((count >> 4) << 14) | (0x7 << 4) | (0xF << 8);
-}
-
-// Issues direct global-to-LDS loads (global_load_lds_dwordx4) of one row
-// into `stage`, laid out in column order.  Lane i of a wave writes the 16
-// bytes at the wave's LDS base + 16 i, so the base of vector group v for
-// wave w is (v * THREADS + 64 w) * W elements.
-template <typename T, int THREADS, int E, bool FULL>
-__device__ __forceinline__ void stage_row(T* stage, const T* row, uint64_t n) {
-  constexpr int W = Vec16<T>::width;
-  const int wave_base = (threadIdx.x / kWave) * kWave;
-#pragma unroll
-  for (int v = 0; v < E / W; ++v) {
-    const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
-    if (FULL || col < n) {
-      __builtin_amdgcn_global_load_lds(
-          (__attribute__((address_space(1))) void*)(row + col),
-          (__attribute__((address_space(3))) void*)(stage + (v * THREADS + wave_base) * W), 16,
-          0, 0);
-    }
-  }
-}
-
-template <typename T, int THREADS, int E, bool FULL>
-__device__ __forceinline__ void unstage_row(T (&x)[E], const T* stage, uint64_t n) {
-  using V = typename Vec16<T>::type;
-  constexpr int W = Vec16<T>::width;
-#pragma unroll
-  for (int v = 0; v < E / W; ++v) {
-    const uint64_t col = (static_cast<uint64_t>(v) * THREADS + threadIdx.x) * W;
-    if (FULL || col < n) {
-      const V value = *reinterpret_cast<const V*>(stage + (v * THREADS + threadIdx.x) * W);
-#pragma unroll
-      for (int k = 0; k < W; ++k) x[v * W + k] = vec_get<T>(value, k);
-    }
-  }
-}
-
-// One row of the staged forward: copies the stage (row r, already landed)
-// into registers, starts staging row r + stride, computes, stores.
 //
-// The fast path keeps no NaN or infinity bookkeeping: with m the
-// first-occurrence maximum over the non-NaN elements, S = sum exp(x - m) is
-// NaN exactly when the slice is undefined (a NaN element gives NaN - m; a +inf
-// maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
-// otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
-// row and apply the reference's special cases from full slice statistics.
-template <typename T, int THREADS, int E, bool LOG, bool FULL, bool NT>
-__device__ __forceinline__ void staged_forward_row(T* out, int32_t* undefined, const T* in,
-                                                   uint64_t rows, uint64_t n, uint64_t r,
-                                                   uint64_t stride, T* stage) {
+// Waves per SIMD the register budget must allow: a row of up to 128 bytes
+// per lane fits in 64 VGPRs (8 waves, two 1024-lane workgroups per CU);
+// longer rows get 128 (4 waves).
+template <typename T, int E>
+constexpr int row_waves() {
+  return sizeof(T) * E <= 128 ? 8 : 4;
+}
+
+template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool NT>
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(row_waves<T, E>())))
+    forward_row_kernel(T* out, int32_t* undefined, const T* in, uint64_t n) {
+  const uint64_t r = blockIdx.x;
+  const int live = FULL ? E : live_slots<T, THREADS, E, VEC>(n);
+  // Slots past the row hold -inf: never a strict maximum, and exp(-inf - m)
+  // adds an exact +0 to the sum for every m that leaves the row defined.
   T x[E];
-  unstage_row<T, THREADS, E, FULL>(x, stage, n);
-  exchange_barrier();  // the stage is free for the next row
-  if (r + stride < rows) stage_row<T, THREADS, E, FULL>(stage, in + (r + stride) * n, n);
-  // Lane maximum: columns reach a lane in increasing order, so a later
+  load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, live, -positive_infinity<T>());
+  // Lane maximum: columns reach a lane in increasing order of j, so a later
   // element wins only if it is strictly larger.
   T lane_max = -positive_infinity<T>();
-  int32_t lane_index = INT32_MAX;
+  int lane_slot = E;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const uint64_t col = column_of<T, THREADS, true>(j);
-    if (FULL || col < n) {
-      const bool take = x[j] > lane_max;
-      lane_max = take ? x[j] : lane_max;
-      lane_index = take ? static_cast<int32_t>(col) : lane_index;
-    }
+    const bool take = x[j] > lane_max;
+    lane_max = take ? x[j] : lane_max;
+    lane_slot = take ? j : lane_slot;
   }
+  const int32_t lane_index =
+      lane_slot == E ? INT32_MAX : static_cast<int32_t>(column_of<T, THREADS, VEC>(lane_slot));
   const T maximum = block_max_first<T, THREADS>(lane_max, lane_index);
+  // The results overwrite x in place so one row costs E registers per lane.
   T local = T(0);
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const uint64_t col = column_of<T, THREADS, true>(j);
     if constexpr (LOG) {
       x[j] = x[j] - maximum;
-      if (FULL || col < n) local += math_exp(x[j]);
+      local += math_exp(x[j]);
     } else {
       x[j] = math_exp(x[j] - maximum);
-      if (FULL || col < n) local += x[j];
+      local += x[j];
     }
   }
   const T total = block_sum<T, THREADS>(local);
@@ -454,83 +352,45 @@ __device__ __forceinline__ void staged_forward_row(T* out, int32_t* undefined, c
       for (int j = 0; j < E; ++j) x[j] = divide(x[j]);
     }
   } else {
-    load_row<T, THREADS, E, true, FULL>(x, in + r * n, n);
+    load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, live, T(0));
     SliceStats<T> s;
     stats_init(s);
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const uint64_t col = column_of<T, THREADS, true>(j);
-      if (FULL || col < n) stats_add(s, x[j], static_cast<int64_t>(col));
+      if (FULL || j < live) stats_add(s, x[j], static_cast<int64_t>(column_of<T, THREADS, VEC>(j)));
     }
     s = block_stats<T, THREADS>(s);
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
   }
-  store_row<T, THREADS, E, true, FULL, NT>(out + r * n, x, n);
-}
-
-// Forward over rows (16-byte aligned, n a multiple of the vector width) in
-// which each block walks rows blockIdx.x, blockIdx.x + gridDim.x, ... (the
-// grid is sized to the resident blocks).  The next row streams from HBM into
-// an LDS stage while the current row is computed in registers, so a CU's
-// reads overlap its arithmetic without spending VGPRs on a second row, and
-// its stores drain while the following row is computed.
-template <typename T, int THREADS, int E, bool LOG, bool FULL, bool NT>
-__global__ void __launch_bounds__(THREADS)
-    forward_row_staged_kernel(T* out, int32_t* undefined, const T* in, uint64_t rows,
-                              uint64_t n) {
-  __shared__ __attribute__((aligned(16))) T stage[THREADS * E];
-  uint64_t r = blockIdx.x;
-  if (r >= rows) return;
-  stage_row<T, THREADS, E, FULL>(stage, in + r * n, n);
-  __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // nothing was issued after the staging loads
-  exchange_barrier();                          // every wave's staged loads have landed
-  staged_forward_row<T, THREADS, E, LOG, FULL, NT>(out, undefined, in, rows, n, r, gridDim.x,
-                                                   stage);
-  for (r += gridDim.x; r < rows; r += gridDim.x) {
-    // Vector memory operations retire in issue order on this architecture.
-    // After the staging loads of row r, a wave of a full row issued at least
-    // E / W further operations (its row stores; wave 0 also its flag store),
-    // so waiting until at most E / W remain lands the staged row while the
-    // previous row's stores keep draining.  Partial rows skip stores per
-    // wave and wait for everything.
-    if constexpr (FULL) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(E / Vec16<T>::width));
-    } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
-    }
-    exchange_barrier();  // every wave's staged loads have landed
-    staged_forward_row<T, THREADS, E, LOG, FULL, NT>(out, undefined, in, rows, n, r, gridDim.x,
-                                                     stage);
-  }
+  store_row<T, THREADS, E, VEC, FULL, NT>(out + r * n, x, live);
 }
 
 template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     backward_row_kernel(T* out, const T* gradient, const T* saved, const int32_t* undefined,
                         uint64_t rows, uint64_t n) {
+  const int live = FULL ? E : live_slots<T, THREADS, E, VEC>(n);
   for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     T* out_row = out + r * n;
     T g[E];
     if (undefined[r] != 0) {
 #pragma unroll
       for (int j = 0; j < E; ++j) g[j] = quiet_nan<T>();
-      store_row<T, THREADS, E, VEC, FULL, NT>(out_row, g, n);
+      store_row<T, THREADS, E, VEC, FULL, NT>(out_row, g, live);
       continue;
     }
+    // Slots past the row hold +0 in both, adding an exact +0 to the sum.
     T y[E];
-    load_row<T, THREADS, E, VEC, FULL>(g, gradient + r * n, n);
-    load_row<T, THREADS, E, VEC, FULL>(y, saved + r * n, n);
+    load_row<T, THREADS, E, VEC, FULL>(g, gradient + r * n, live, T(0));
+    load_row<T, THREADS, E, VEC, FULL>(y, saved + r * n, live, T(0));
     T local = T(0);
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const uint64_t col = column_of<T, THREADS, VEC>(j);
-      if (FULL || col < n) {
-        if constexpr (LOG) {
-          local += g[j];
-        } else {
-          local += g[j] * y[j];
-        }
+      if constexpr (LOG) {
+        local += g[j];
+      } else {
+        local += g[j] * y[j];
       }
     }
     const T reduced = block_sum<T, THREADS>(local);
@@ -542,7 +402,7 @@ __global__ void __launch_bounds__(THREADS)
         g[j] = y[j] * (g[j] - reduced);
       }
     }
-    store_row<T, THREADS, E, VEC, FULL, NT>(out_row, g, n);
+    store_row<T, THREADS, E, VEC, FULL, NT>(out_row, g, live);
   }
 }
 
@@ -710,24 +570,17 @@ uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
 
 // Register-row configurations (threads, elements per lane), smallest first;
 // FULL drops the bounds checks when the row exactly fills the registers.
-// The forward prefetches the next row when a second row array fits in 32
-// VGPRs per lane, with one block per resident slot walking many rows.
+// One workgroup per row, launched in grids of at most kMaxGrid rows.
 template <typename T, int THREADS, int E, bool LOG, bool VEC, bool FULL>
 void forward_rows_as(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
                      const DeviceGuard& guard) {
-  // The LDS stage holds one row of THREADS * E elements (at most 128 KiB of
-  // the CU's 160 KiB).
-  constexpr bool kStaged = VEC && THREADS * E * sizeof(T) <= (128U << 10);
   with_policy(stream_output(rows * n * sizeof(T)), [&](auto nt) {
     constexpr bool NT = decltype(nt)::value;
-    if constexpr (kStaged) {
-      auto kernel = forward_row_staged_kernel<T, THREADS, E, LOG, FULL, NT>;
-      const uint64_t resident = resident_blocks(kernel, THREADS, guard);
-      kernel<<<grid_for(rows < resident ? rows : resident), THREADS, 0, guard.stream>>>(
-          out, undefined, in, rows, n);
-    } else {
-      forward_row_kernel<T, THREADS, E, LOG, VEC, FULL, false, NT>
-          <<<grid_for(rows), THREADS, 0, guard.stream>>>(out, undefined, in, rows, n);
+    for (uint64_t first = 0; first < rows; first += kMaxGrid) {
+      const uint64_t count = rows - first < kMaxGrid ? rows - first : kMaxGrid;
+      forward_row_kernel<T, THREADS, E, LOG, VEC, FULL, NT>
+          <<<static_cast<uint32_t>(count), THREADS, 0, guard.stream>>>(
+              out + first * n, undefined + first, in + first * n, n);
     }
   });
 }
@@ -757,15 +610,19 @@ void backward_rows(T* out, const T* gradient, const T* saved, const int32_t* und
   });
 }
 
+// Row lengths up to 1024 take one wave per row (no cross-wave exchange);
+// 8192 takes 256 lanes x 32, which measured faster than 512 x 16.
 template <typename T, bool LOG, bool VEC>
 bool launch_forward_rows(T* out, int32_t* undefined, const T* in, uint64_t rows, uint64_t n,
                          const DeviceGuard& guard) {
-  if (n <= 256 * 4) {
-    forward_rows<T, 256, 4, LOG, VEC>(out, undefined, in, rows, n, guard);
+  if (n <= 64 * 4) {
+    forward_rows<T, 64, 4, LOG, VEC>(out, undefined, in, rows, n, guard);
+  } else if (n <= 64 * 16) {
+    forward_rows<T, 64, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 256 * 16) {
     forward_rows<T, 256, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
-  } else if (n <= 512 * 16) {
-    forward_rows<T, 512, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
+  } else if (n <= 256 * 32) {
+    forward_rows<T, 256, 32, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 1024 * 16) {
     forward_rows<T, 1024, 16, LOG, VEC>(out, undefined, in, rows, n, guard);
   } else if (n <= 1024 * 32) {

@@ -581,9 +581,10 @@ def softmax_backward_bound(g, y, extent, dtype, log):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,extent", [(3, 1), (5, 7), (64, 1000), (16, 1024), (8, 4096),
-                                         (4, 8192), (4, 12000), (2, 16384), (2, 32768),
-                                         (2, 32770), (1, 40000)])
+@pytest.mark.parametrize("rows,extent", [(3, 1), (5, 7), (40, 200), (64, 1000), (16, 1024),
+                                         (8, 2000), (8, 4096), (4, 6000), (4, 8192), (4, 12000),
+                                         (2, 16384), (2, 32000), (2, 32768), (2, 32770),
+                                         (1, 40000)])
 def test_softmax_rows(hip, dtype, rows, extent):
     x = (inputs(28, rows * extent, dtype, with_specials=False) * dtype(np.sqrt(2))).reshape(rows, extent)
     got, und = softmax_device(hip, x, rows, extent, 1, False, dtype)
@@ -625,6 +626,45 @@ def test_softmax_special_slices(hip, dtype):
         want, und_ref = (ref.log_softmax(x, 1) if log else ref.softmax_axis(x, 1))
         assert np.array_equal(und, und_ref.astype(np.int32))
         assert_ulp(got, want, 2, f"special log={log}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("extent", [1000, 12000, 32000, 32768, 32770])
+def test_softmax_special_long_rows(hip, dtype, extent):
+    """Undefined and +inf rows at every register-row shape, full and partial
+    (their slow path reloads the row), beside rows of equal values."""
+    inf, nan = np.inf, np.nan
+    x = np.zeros((8, extent), dtype=dtype)
+    x[0, extent // 3] = nan
+    x[1, :] = -inf
+    x[2, [5, extent - 2]] = inf
+    x[2, 7] = -inf
+    x[3, extent - 1] = inf
+    x[4, :] = 2.5
+    x[5, ::2] = -0.0
+    x[6, :] = -inf
+    x[6, extent // 2] = 1.0
+    x[7, :] = 3.0
+    x[7, extent - 1] = nan
+    rows = x.shape[0]
+    for log in (False, True):
+        got, und = softmax_device(hip, x, rows, extent, 1, log, dtype)
+        want, und_ref = (ref.log_softmax(x, 1) if log else ref.softmax_axis(x, 1))
+        assert np.array_equal(und, und_ref.astype(np.int32))
+        assert_ulp(got, want, 2, f"special long rows {extent} log={log}")
+
+
+def test_softmax_rows_beyond_one_grid(hip):
+    """More rows than one launch grid holds (2^20): the rows go out in
+    several grids at shifted offsets."""
+    rows, extent = (1 << 20) + 3, 4
+    x = inputs(32, rows * extent, F32, with_specials=False).reshape(rows, extent)
+    x[-1, 2] = np.nan
+    got, und = softmax_device(hip, x, rows, extent, 1, False, F32)
+    want, und_ref = ref.softmax_axis(x, 1)
+    assert np.array_equal(und, und_ref.astype(np.int32))
+    softmax_tolerance_check(got[:-1], want[:-1], extent, F32, "softmax beyond one grid")
+    assert np.all(np.isnan(got[-1]))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
