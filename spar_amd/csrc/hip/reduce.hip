@@ -20,6 +20,8 @@
 //     result of a sequential scan bit for bit (including -0.0 vs +0.0).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -129,6 +131,31 @@ template <typename T> struct ScanAcc<T, Kind::Max> {
   }
 };
 
+// Max without its index, for a scan whose accumulator covers one contiguous
+// range in order (a column scan's split): the first occurrence of the
+// maximum is then fixed by the compare rule alone, ties included (-0 before
+// +0 stays -0), and the range's position orders it against other ranges.
+// One compare and one select per element.
+template <typename T> struct ScanPeak {
+  T value;
+  __device__ __forceinline__ void init() { value = argmax_identity<T>().value; }
+  __device__ __forceinline__ void add(T x, uint32_t) {
+    value = !(x <= value) && value == value ? x : value;
+  }
+  __device__ __forceinline__ void add_ordered(T x, uint32_t) { value = x > value ? x : value; }
+  // The index is the range's first; only the value is kept.
+  __device__ __forceinline__ Acc<T, Kind::Max> finish(int64_t base) const {
+    Acc<T, Kind::Max> acc;
+    acc.best.value = value;
+    acc.best.index = base;
+    return acc;
+  }
+};
+
+// Column scans of a max without argmax use ScanPeak (INDEX false).
+template <typename T, Kind K, bool INDEX>
+using ColumnScan = std::conditional_t<K == Kind::Max && !INDEX, ScanPeak<T>, ScanAcc<T, K>>;
+
 // Reads one element: the input itself, or the product of two inputs that
 // share strides (each product rounded to T, as multiply() would store it).
 template <typename T, int NIN>
@@ -206,15 +233,21 @@ __device__ __forceinline__ void sink_write(const Sink<T>& sink, uint64_t slot, c
 }
 
 // Reads partial `slot` of split `split` (splits of `segment` elements).
-template <typename T, Kind K>
+// Without stored indices (INDEX false: a max of contiguous splits) the
+// split's number stands in for the index: it orders equal maxima of
+// different splits the way their first occurrences are ordered.
+template <typename T, Kind K, bool INDEX = true>
 __device__ __forceinline__ Acc<T, K> partial_read(const T* values, const uint32_t* indices,
                                                   uint64_t slot, uint64_t split, uint64_t segment) {
   Acc<T, K> acc;
   if constexpr (K == Kind::Sum) {
     acc.value = values[slot];
-  } else {
+  } else if constexpr (INDEX) {
     acc.best.value = values[slot];
     acc.best.index = static_cast<int64_t>(split * segment + indices[slot]);
+  } else {
+    acc.best.value = values[slot];
+    acc.best.index = static_cast<int64_t>(split);
   }
   return acc;
 }
@@ -462,8 +495,9 @@ __global__ void __launch_bounds__(kThreads)
 //   [8192, 4096]  axis 0            26.5 us                    25.8 us
 //
 // VPL = 4 needs the row length to be a multiple of 4 x 256 groups; other
-// wide rows take VPL = 1.
-template <typename T, Kind K, int NIN, int VPL, int R>
+// wide rows take VPL = 1.  A max without argmax (INDEX false) scans values
+// only and writes value-only partials.
+template <typename T, Kind K, int NIN, int VPL, int R, bool INDEX = true>
 __global__ void __launch_bounds__(kThreads)
     column_wide_kernel(const T* a, const T* b, uint64_t outer, uint64_t n,
                        uint64_t reduced_stride, uint64_t inner, uint64_t column_blocks,
@@ -483,7 +517,7 @@ __global__ void __launch_bounds__(kThreads)
     if (column >= inner) continue;
     const uint64_t begin = split * segment;
     const uint64_t end = begin + segment < n ? begin + segment : n;
-    ScanAcc<T, K> scan[VPL][W];
+    ColumnScan<T, K, INDEX> scan[VPL][W];
 #pragma unroll
     for (int g = 0; g < VPL; ++g) {
 #pragma unroll
@@ -589,7 +623,7 @@ __global__ void __launch_bounds__(kThreads)
           }
         }
         *reinterpret_cast<V*>(sink.values + slot) = values;
-        if constexpr (K == Kind::Max) {
+        if constexpr (K == Kind::Max && INDEX) {
           if constexpr (W == 4) {
             *reinterpret_cast<i32x4*>(sink.partial_indices + slot) =
                 i32x4{static_cast<int32_t>(indices[0]), static_cast<int32_t>(indices[1]),
@@ -619,7 +653,7 @@ constexpr int kCombineThreads = 1024;
 constexpr int kCombineWaves = kCombineThreads / kWave;
 constexpr int kCombineBatch = 8;
 
-template <typename T, Kind K, int P>
+template <typename T, Kind K, int P, bool INDEX = true>
 __global__ void __launch_bounds__(kCombineThreads)
     combine_columns_kernel(const T* part_values, const uint32_t* part_indices, uint64_t outer,
                            uint64_t splits, uint64_t segment, uint64_t inner, Sink<T> sink) {
@@ -648,8 +682,8 @@ __global__ void __launch_bounds__(kCombineThreads)
         for (int j = 0; j < kCombineBatch; ++j) {
           const uint64_t s = s0 + static_cast<uint64_t>(j) * P;
           if (s < splits) {
-            part[j] = partial_read<T, K>(part_values, part_indices, (o * splits + s) * inner + i, s,
-                                         segment);
+            part[j] = partial_read<T, K, INDEX>(part_values, part_indices,
+                                                (o * splits + s) * inner + i, s, segment);
           } else {
             part[j].init();
           }
@@ -790,13 +824,14 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     return s;
   };
 
-  // Scratch for partial results (values, plus indices for max/argmax).
-  auto with_partials = [&](uint64_t slots, auto&& body) -> hipError_t {
+  // Scratch for partial results (values, plus indices for max/argmax unless
+  // the partials are value-only).
+  auto with_partials = [&](uint64_t slots, auto&& body, bool value_only = false) -> hipError_t {
     void* values = nullptr;
     void* indices = nullptr;
     hipError_t error = scratch_allocate(&values, slots * sizeof(T), device);
     if (error != hipSuccess) return error;
-    if constexpr (K == Kind::Max) {
+    if (K == Kind::Max && !value_only) {
       error = scratch_allocate(&indices, slots * sizeof(uint32_t), device);
       if (error != hipSuccess) {
         scratch_release(values, device);
@@ -905,14 +940,28 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     if (splits < range_splits) splits = range_splits;
     const uint64_t segment = (n + splits - 1) / splits;
     splits = (n + segment - 1) / segment;
+    // A max without argmax over wide rows scans and combines values only.
+    const bool value_only = K == Kind::Max && operation == SPAR_HIP_MAX && wide;
     auto launch = [&](const Sink<T>& s) {
       const uint32_t grid = grid_for(outer * splits * column_blocks);
-      if (quad) {
-        column_wide_kernel<T, K, NIN, 4, 2><<<grid, kThreads, 0, guard.stream>>>(
-            a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
-      } else if (wide) {
-        column_wide_kernel<T, K, NIN, 1, 4><<<grid, kThreads, 0, guard.stream>>>(
-            a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
+      auto launch_wide = [&](auto index) {
+        constexpr bool INDEX = decltype(index)::value;
+        if (quad) {
+          column_wide_kernel<T, K, NIN, 4, 2, INDEX><<<grid, kThreads, 0, guard.stream>>>(
+              a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
+        } else {
+          column_wide_kernel<T, K, NIN, 1, 4, INDEX><<<grid, kThreads, 0, guard.stream>>>(
+              a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
+        }
+      };
+      if (wide) {
+        if constexpr (K == Kind::Max) {
+          if (value_only) {
+            launch_wide(std::false_type{});
+            return;
+          }
+        }
+        launch_wide(std::true_type{});
       } else if (vec) {
         column_kernel<T, K, NIN, true><<<grid, kThreads, 0, guard.stream>>>(
             a, b, outer, n, reduced_stride, inner, column_blocks, splits, segment, map, s);
@@ -933,14 +982,24 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
                  guard.stream>>>(partial.values, partial.partial_indices, outer, splits, segment,
                                  inner, final_sink());
       };
-      if (splits >= 128) {
-        combine(combine_columns_kernel<T, K, 16>, 1);
-      } else if (splits >= 16) {
-        combine(combine_columns_kernel<T, K, 4>, 4);
-      } else {
-        combine(combine_columns_kernel<T, K, 1>, 16);
+      auto combine_all = [&](auto index) {
+        constexpr bool INDEX = decltype(index)::value;
+        if (splits >= 128) {
+          combine(combine_columns_kernel<T, K, 16, INDEX>, 1);
+        } else if (splits >= 16) {
+          combine(combine_columns_kernel<T, K, 4, INDEX>, 4);
+        } else {
+          combine(combine_columns_kernel<T, K, 1, INDEX>, 16);
+        }
+      };
+      if constexpr (K == Kind::Max) {
+        if (value_only) {
+          combine_all(std::false_type{});
+          return;
+        }
       }
-    });
+      combine_all(std::true_type{});
+    }, value_only);
   }
 
   // Generic: one wave per output.

@@ -427,6 +427,34 @@ def test_max_argmax_nan_rescan(hip, dtype, shape, axes):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows", [8192, 700])
+def test_column_max_value_only_across_splits(hip, dtype, rows):
+    """A max without argmax over wide rows keeps no indices: ties between
+    splits (signed zeros, NaN payloads) must still resolve to the first
+    occurrence, ordered by split."""
+    cols = 4096
+    x = -np.abs(inputs(33, rows * cols, dtype, with_specials=False)).reshape(rows, cols) - 1
+    x[rows - 1, 0] = 0.0      # +0 last, -0 first: -0
+    x[3, 0] = -0.0
+    x[2, 1] = 0.0             # +0 first, -0 later: +0
+    x[rows - 2, 1] = -0.0
+    x[:, 2] = 5.0             # every row ties
+    x[:, 3] = -np.inf
+    quiet = np.array([0x7FC00001, 0x7FC00002], dtype=np.uint32) if dtype == F32 else \
+        np.array([0x7FF8000000000001, 0x7FF8000000000002], dtype=np.uint64)
+    nans = quiet.view(dtype)
+    x[rows // 2, 4] = nans[1]  # later NaN
+    x[rows // 4, 4] = nans[0]  # first NaN: its payload is the result
+    x[rows - 1, 5] = nans[1]
+    mx, _ = ref.axis_max(x, [0])
+    got = axis_reduce(hip, x, x, [0], "max", dtype)
+    assert_bitexact(got, mx, f"value-only max {rows}")
+    assert np.signbit(got[0]) and not np.signbit(got[1])
+    assert got[4:5].view(quiet.dtype)[0] == quiet[0]
+    assert np.isnan(got[5]) and got[2] == 5.0 and got[3] == -np.inf
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_max_argmax_negative_infinity_runs(hip, dtype):
     """Rows long enough to be split over blocks, made of -inf runs: the answer
     is the first -inf unless a NaN or a finite value appears later."""
