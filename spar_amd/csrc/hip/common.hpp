@@ -45,6 +45,17 @@ struct DeviceGuard {
 // Fills `guard`; returns hipSuccess or the failing HIP error.
 hipError_t enter(int device, DeviceGuard& guard);
 
+// Workgroups of `kernel` resident on the device at once (at least one per CU).
+template <typename K>
+uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      per_cu < 1) {
+    per_cu = 1;
+  }
+  return static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(guard.multiprocessors);
+}
+
 // Checks hipGetLastError after a launch and converts it to a status.
 SparHipStatus finish(const DeviceGuard& guard);
 

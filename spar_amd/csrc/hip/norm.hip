@@ -324,16 +324,6 @@ uint32_t grid_for(uint64_t blocks) {
   return static_cast<uint32_t>(blocks > kMaxGrid ? kMaxGrid : blocks);
 }
 
-template <typename K>
-uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-      per_cu < 1) {
-    per_cu = 1;
-  }
-  return static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(guard.multiprocessors);
-}
-
 struct NormArgs {
   void* out;
   void* mean;

@@ -557,17 +557,6 @@ uint32_t grid_for(uint64_t blocks) {
   return static_cast<uint32_t>(blocks > kMaxGrid ? kMaxGrid : blocks);
 }
 
-// Blocks of `kernel` resident on the device at once (at least one per CU).
-template <typename K>
-uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-      per_cu < 1) {
-    per_cu = 1;
-  }
-  return static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(guard.multiprocessors);
-}
-
 // Register-row configurations (threads, elements per lane), smallest first;
 // FULL drops the bounds checks when the row exactly fills the registers.
 // One workgroup per row, launched in grids of at most kMaxGrid rows.
