@@ -319,6 +319,27 @@ def test_transposed_views_vector_tiles(hip, dtype):
                         f"copy {name}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_transposed_tiles_walked_by_resident_workgroups(hip, dtype):
+    """More tiles than resident workgroups (about 512 with one transposed
+    operand, 256 with two): each workgroup walks several tiles and loads the
+    next one while storing the current, across partial edge tiles and
+    batch axes."""
+    base = inputs(47, 2600 * 4000, dtype).reshape(2600, 4000)
+    twin = inputs(48, 2600 * 4000, dtype).reshape(2600, 4000)
+    mu = inputs(49, 4000, dtype).reshape(4000, 1)
+    cube = inputs(50, 24 * 520 * 300, dtype).reshape(24, 520, 300)
+    cube2 = inputs(51, 24 * 520 * 300, dtype).reshape(24, 520, 300)
+    for name, lb, lv, rb, rv in [
+        ("T - column", base, base.T, mu, mu),
+        ("T - T", base, base.T, twin, twin.T),
+        ("batched T - T", cube, cube.transpose(0, 2, 1), cube2, cube2.transpose(0, 2, 1)),
+    ]:
+        got, want = strided_binary(hip, lb, lv, rb, rv, "subtract", dtype)
+        assert_bitexact(got, want, name)
+    assert_bitexact(strided_copy(hip, base, base.T, dtype), ref.strided_copy(base.T), "copy T")
+
+
 def test_strided_binary_odd_inner_extent(hip):
     # inner extent not a multiple of 4: row-vector path must not be taken
     x = inputs(20, 33 * 37, F32).reshape(33, 37)
