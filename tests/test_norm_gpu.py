@@ -140,6 +140,23 @@ def test_norm_forward_kernel(hip, dtype, center):
         assert_rows(got_y, want_y, n, dtype, what + " y")
 
 
+@pytest.mark.parametrize("center", [True, False])
+def test_norm_forward_rows_beyond_one_grid(hip, center):
+    """More rows than one launch grid holds (2^20): the rows go out in
+    several grids, each with its own row offset into y, mu and d."""
+    rows, n = (1 << 20) + 7, 4
+    x, w, b, _ = data(rows, n, F32, 300)
+    got_y, got_mu, got_d, _ = forward_device(hip, x, w, b, center, F32)
+    want_y, want_mu, want_d = composed_forward(x, w, b, center)
+    what = f"{'layer' if center else 'rms'} norm {rows}x{n}"
+    if center:
+        assert_red(got_mu, want_mu, n, np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=1)) / n,
+                   what + " mean")
+    assert np.all(np.abs(got_d.astype(np.float64) - want_d) <=
+                  (4e-6 * np.sqrt(n) + 4 * np.finfo(F32).eps) * want_d), what + " d"
+    assert_rows(got_y, want_y, n, F32, what + " y")
+
+
 @pytest.mark.parametrize("dtype", [F32, F64])
 @pytest.mark.parametrize("center", [True, False])
 def test_norm_backward_kernel(hip, dtype, center):
