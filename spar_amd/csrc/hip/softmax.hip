@@ -821,9 +821,17 @@ __global__ void __launch_bounds__(kEntropyThreads)
       T top = m;
 #pragma unroll
       for (int j = 0; j < U * W; ++j) top = fmax_of(top, x[j]);
+      // exp(x - top) already gives an exact 0 for x = -inf whenever top is
+      // above -inf; only a lane whose elements so far are all -inf (or NaN)
+      // needs exp_term's guard against -inf - -inf, so it alone recomputes.
       T batch = T(0);
 #pragma unroll
-      for (int j = 0; j < U * W; ++j) batch += exp_term(x[j], top);
+      for (int j = 0; j < U * W; ++j) batch += math_exp(x[j] - top);
+      if (top == -positive_infinity<T>()) {
+        batch = T(0);
+#pragma unroll
+        for (int j = 0; j < U * W; ++j) batch += exp_term(x[j], top);
+      }
       s = rescaled(s, m, top) + batch;
       m = top;
     }
