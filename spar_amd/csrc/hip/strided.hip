@@ -242,7 +242,8 @@ __global__ void __launch_bounds__(kRowTileThreads)
     const uint64_t off0 = rg.offsets[0] + c1 * rg.stride1[0] + c2 * rg.stride2[0];
     const uint64_t off1 = rg.offsets[1] + c1 * rg.stride1[1] + c2 * rg.stride2[1];
     if (column < rg.inner) {
-      V ra, rb;
+      V ra;
+      V rb{};  // unused by one-operand ops
       ra = row_group<T, MODE_A>(a, off0, column);
       if constexpr (NOPS == 2) rb = row_group<T, MODE_B>(b, off1, column);
       store_vector<NT>(reinterpret_cast<V*>(out + row * rg.inner + column),
