@@ -88,7 +88,8 @@ class Workload:
         self.zero8 = u([0] * 8)
         hip.synchronize()
 
-    # algorithmic bytes of each op
+    # algorithmic bytes of each op: every distinct input byte read once, every
+    # output byte written once, broadcast operands at their stored size
     def op_bytes(self):
         n, f = self.n, 4
         return {
