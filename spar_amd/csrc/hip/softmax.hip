@@ -94,12 +94,14 @@ __device__ __forceinline__ SliceStats<T> wave_stats(SliceStats<T> s) {
   return s;
 }
 
-template <typename T, int THREADS>
+// GUARD: wait before writing the LDS slots, which a previous call of the
+// same kernel may still be reading; a kernel that calls it once skips it.
+template <typename T, int THREADS, bool GUARD = true>
 __device__ __forceinline__ SliceStats<T> block_stats(SliceStats<T> s) {
   constexpr int kWavesPerBlock = THREADS / kWave;
   __shared__ SliceStats<T> lds[kWavesPerBlock];
   s = wave_stats(s);
-  exchange_barrier();
+  if constexpr (GUARD) exchange_barrier();
   if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = s;
   exchange_barrier();
   SliceStats<T> total = lds[0];
@@ -108,12 +110,12 @@ __device__ __forceinline__ SliceStats<T> block_stats(SliceStats<T> s) {
   return total;
 }
 
-template <typename T, int THREADS>
+template <typename T, int THREADS, bool GUARD = true>
 __device__ __forceinline__ T block_sum(T value) {
   constexpr int kWavesPerBlock = THREADS / kWave;
   __shared__ T lds[kWavesPerBlock];
   value = wave_sum(value);
-  exchange_barrier();
+  if constexpr (GUARD) exchange_barrier();
   if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = value;
   exchange_barrier();
   T total = lds[0];
@@ -250,7 +252,7 @@ __device__ __forceinline__ void store_row(T* row, const T (&y)[E], int live) {
 // Block-wide first-occurrence maximum of (value, column) pairs: the larger
 // value wins, equal values (including -0 and +0) keep the smaller column.
 // NaN never enters (a lane only takes an element that compares larger).
-template <typename T, int THREADS>
+template <typename T, int THREADS, bool GUARD = true>
 __device__ __forceinline__ T block_max_first(T value, int32_t index) {
   constexpr int kWavesPerBlock = THREADS / kWave;
   __shared__ T lds_value[kWavesPerBlock];
@@ -263,7 +265,7 @@ __device__ __forceinline__ T block_max_first(T value, int32_t index) {
     value = take ? other : value;
     index = take ? other_index : index;
   }
-  exchange_barrier();
+  if constexpr (GUARD) exchange_barrier();
   if (threadIdx.x % kWave == 0) {
     lds_value[threadIdx.x / kWave] = value;
     lds_index[threadIdx.x / kWave] = index;
@@ -325,7 +327,8 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(ro
   }
   const int32_t lane_index =
       lane_slot == E ? INT32_MAX : static_cast<int32_t>(column_of<T, THREADS, VEC>(lane_slot));
-  const T maximum = block_max_first<T, THREADS>(lane_max, lane_index);
+  // Each block reduction below runs once per kernel: no guard barriers.
+  const T maximum = block_max_first<T, THREADS, false>(lane_max, lane_index);
   // The results overwrite x in place so one row costs E registers per lane.
   T local = T(0);
 #pragma unroll
@@ -338,7 +341,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(ro
       local += x[j];
     }
   }
-  const T total = block_sum<T, THREADS>(local);
+  const T total = block_sum<T, THREADS, false>(local);
   const bool bad = total != total;
   if (threadIdx.x == 0) undefined[r] = bad ? 1 : 0;
   if (!bad) {
@@ -359,7 +362,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(ro
     for (int j = 0; j < E; ++j) {
       if (FULL || j < live) stats_add(s, x[j], static_cast<int64_t>(column_of<T, THREADS, VEC>(j)));
     }
-    s = block_stats<T, THREADS>(s);
+    s = block_stats<T, THREADS, false>(s);
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = undefined_value<T, LOG>(s, x[j]);
   }
