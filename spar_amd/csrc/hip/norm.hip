@@ -309,7 +309,18 @@ __global__ void __launch_bounds__(kCombineThreads)
     const uint64_t col = group * kWave + lane;
     T total = T(0);
     if (col < n) {
-      for (uint64_t p = wave; p < parts; p += kCombineWaves) total += partial[p * n + col];
+      // Eight loads in flight per lane, added in the same order as one at a
+      // time.
+      constexpr int kBatch = 8;
+      uint64_t p = wave;
+      for (; p + (kBatch - 1) * kCombineWaves < parts; p += kBatch * kCombineWaves) {
+        T v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = partial[(p + u * kCombineWaves) * n + col];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) total += v[u];
+      }
+      for (; p < parts; p += kCombineWaves) total += partial[p * n + col];
     }
     __syncthreads();
     lds[wave][lane] = total;
