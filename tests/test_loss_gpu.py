@@ -134,6 +134,38 @@ def test_cross_entropy_undefined_rows(sp):
         assert np.allclose(gdx[finite], wdx[finite], rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("dtype", [F32, F64])
+def test_cross_entropy_negative_infinity_runs(sp, dtype):
+    """Masked logits: long runs of -inf before, between and after finite
+    values, so that lanes see only -inf for whole batches (and some rows end
+    that way), as the forward's streaming sum must handle."""
+    rng = np.random.default_rng(83)
+    classes = 32768
+    x = (rng.standard_normal((6, classes)) * 2).astype(dtype)
+    x[0, : classes // 2] = -np.inf            # masked first half
+    x[1, :] = -np.inf
+    x[1, classes - 3] = 0.25                  # one live logit at the end
+    x[2, 1000:] = -np.inf                     # masked tail
+    x[3, ::2] = -np.inf                       # every other logit masked
+    x[4, :] = -np.inf
+    x[4, 7] = 1.5
+    x[4, classes - 1] = 1.5                   # two live logits far apart
+    x[5, 4096:28672] = -np.inf                # masked middle
+    t = np.array([classes - 1, classes - 3, 5, 1, 7, 100], np.int64)
+    got, want, gdx, wdx = run_both(sp, x, t, "none")
+    finite = np.isfinite(x).astype(np.float64)
+    lp = np.where(finite > 0, closed_lp(np.where(finite > 0, x.astype(np.float64), -1e300)),
+                  -np.inf)
+    picked = -lp[np.arange(6), t]
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= lp_bound(picked, classes, dtype)), f"losses: {err}"
+    assert np.array_equal(np.isnan(gdx), np.isnan(wdx)) and not np.isnan(gdx).any()
+    eps = np.finfo(dtype).eps
+    bound = np.exp(lp) * (lp_bound(np.where(np.isfinite(lp), lp, 0), classes, dtype) + 4 * eps) \
+        + 4 * eps * np.abs(wdx) + np.finfo(dtype).tiny
+    assert np.all(np.abs(gdx.astype(np.float64) - wdx) <= bound), "dlogits"
+
+
 def test_cross_entropy_errors(sp):
     device = sp.Device.hip(0)
     logits = sp.Tensor.from_numpy(np.zeros((2, 3), F32)).to(device)
