@@ -196,14 +196,24 @@ struct SparHipStatus spar_hip_launch_scalar(void* output, const void* input, uin
 struct SparHipStatus spar_hip_launch_unary(void* output, const void* input, uint64_t count,
                                            int dtype, int operation, int device);
 
-/* output[i] = scalar[0] / (T)divisor with scalar a device pointer to one
- * element.  Used by sum backward (divisor 1) and mean backward (divisor n).
- * Replaces spar_cuda_launch_fill_from_scalar (cuda_kernels.hpp:85-87), whose
- * `scale` argument multiplied by a rounded reciprocal; the divisor form
- * reproduces the CPU path's `g / (float)n` (src/ops/reduction.cpp:263-277). */
+/* output[i] = scalar[0] * (T)scale, with scalar a device pointer to one
+ * element: the reference's semantics.  Replaces
+ * spar_cuda_launch_fill_from_scalar (cuda_kernels.hpp:85-87,
+ * cuda_kernels.cu:249-257, :1093-1118); its callers pass scale 1 for sum
+ * backward and 1.0 / n for mean backward (src/ops/reduction.cpp:201-204,
+ * :265-268). */
 struct SparHipStatus spar_hip_launch_fill_from_scalar(void* output, const void* scalar,
-                                                      uint64_t count, int dtype, double divisor,
+                                                      uint64_t count, int dtype, double scale,
                                                       int device);
+
+/* output[i] = scalar[0] / (T)divisor, divisor > 0.  The CPU path's mean
+ * backward divides the gradient by (T)n (src/ops/reduction.cpp:263-277),
+ * which differs in the last bit from multiplying by the rounded reciprocal;
+ * this form reproduces the CPU bits.  No counterpart in the reference's
+ * C ABI; the Tensor layer's sum/mean backward calls it. */
+struct SparHipStatus spar_hip_launch_fill_from_scalar_divided(void* output, const void* scalar,
+                                                              uint64_t count, int dtype,
+                                                              double divisor, int device);
 
 /* output[i] = (T)value for a host value (ones/full on the device,
  * src/core/tensor.cppm:168-178 staged these through the host). */

@@ -172,22 +172,27 @@ void launch_map2(T* out, const T* a, const T* b, uint64_t count, F f, const Devi
 }
 
 
-// Writes one value to every element.  The value is scalar[0] when a scalar
-// is given, else `value`; with `divide` it is then divided by `divisor` in T
-// (the mean backward's g / (T)n).  The vector form stores 16 bytes per lane
-// over the aligned body and needs a 16-byte aligned output.
+// How a fill derives its value from scalar[0] (or the host value): as is,
+// times a factor (the reference's fill_from_scalar: g * scale), or divided by
+// a divisor (the CPU mean backward's g / (T)n).  All in T.
+enum class FillScale : int { kNone = 0, kMultiply = 1, kDivide = 2 };
+
+// Writes one value to every element.  The vector form stores 16 bytes per
+// lane over the aligned body and needs a 16-byte aligned output.
 template <typename T>
-__device__ __forceinline__ T fill_value(const T* scalar, T value, T divisor, bool divide) {
+__device__ __forceinline__ T fill_value(const T* scalar, T value, T factor, FillScale mode) {
   const T v = scalar != nullptr ? scalar[0] : value;
-  return divide ? v / divisor : v;
+  if (mode == FillScale::kMultiply) return v * factor;
+  if (mode == FillScale::kDivide) return v / factor;
+  return v;
 }
 
 template <typename T, bool NT>
 __global__ void __launch_bounds__(kVectorThreads)
-    fill_vec_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide) {
+    fill_vec_kernel(T* out, uint64_t count, const T* scalar, T value, T factor, FillScale mode) {
   using V = typename Vec16<T>::type;
   constexpr int W = Vec16<T>::width;
-  const T v = fill_value(scalar, value, divisor, divide);
+  const T v = fill_value(scalar, value, factor, mode);
   V o;
 #pragma unroll
   for (int k = 0; k < W; ++k) vec_set<T>(o, k, v);
@@ -206,8 +211,8 @@ __global__ void __launch_bounds__(kVectorThreads)
 
 template <typename T>
 __global__ void __launch_bounds__(kThreads)
-    fill_scalar_kernel(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide) {
-  const T v = fill_value(scalar, value, divisor, divide);
+    fill_scalar_kernel(T* out, uint64_t count, const T* scalar, T value, T factor, FillScale mode) {
+  const T v = fill_value(scalar, value, factor, mode);
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
        i += stride) {
@@ -216,18 +221,34 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 template <typename T>
-void launch_fill_values(T* out, uint64_t count, const T* scalar, T value, T divisor, bool divide,
+void launch_fill_values(T* out, uint64_t count, const T* scalar, T value, T factor, FillScale mode,
                         const DeviceGuard& guard) {
   if (aligned16(out)) {
     with_policy(stream_output(count * sizeof(T)), [&](auto nt) {
       fill_vec_kernel<T, decltype(nt)::value>
           <<<vector_grid(count, Vec16<T>::width), kVectorThreads, 0, guard.stream>>>(
-              out, count, scalar, value, divisor, divide);
+              out, count, scalar, value, factor, mode);
     });
   } else {
     fill_scalar_kernel<T><<<scalar_grid(count, guard), kThreads, 0, guard.stream>>>(
-        out, count, scalar, value, divisor, divide);
+        out, count, scalar, value, factor, mode);
   }
+}
+
+// Fills output with scalar[0] (a device element) scaled by `factor` in T.
+SparHipStatus fill_from_device_scalar(void* output, const void* scalar, uint64_t count, int dtype,
+                                      double factor, FillScale mode, int device) {
+  if (count == 0) return ok();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (dtype == SPAR_HIP_FLOAT32) {
+    launch_fill_values(static_cast<float*>(output), count, static_cast<const float*>(scalar), 0.0F,
+                       static_cast<float>(factor), mode, guard);
+  } else {
+    launch_fill_values(static_cast<double*>(output), count, static_cast<const double*>(scalar),
+                       0.0, factor, mode, guard);
+  }
+  return finish(guard);
 }
 
 // SplitMix64 draw `index` (0-based) of Random(seed): the generator adds the
@@ -352,24 +373,24 @@ extern "C" SparHipStatus spar_hip_launch_unary(void* output, const void* input, 
 }
 
 extern "C" SparHipStatus spar_hip_launch_fill_from_scalar(void* output, const void* scalar,
-                                                          uint64_t count, int dtype,
-                                                          double divisor, int device) {
+                                                          uint64_t count, int dtype, double scale,
+                                                          int device) {
+  if (!valid_float_dtype(dtype) || scalar == nullptr || (count != 0 && output == nullptr)) {
+    return invalid();
+  }
+  return fill_from_device_scalar(output, scalar, count, dtype, scale, FillScale::kMultiply, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_fill_from_scalar_divided(void* output,
+                                                                  const void* scalar,
+                                                                  uint64_t count, int dtype,
+                                                                  double divisor, int device) {
   if (!valid_float_dtype(dtype) || scalar == nullptr || (count != 0 && output == nullptr) ||
       !(divisor > 0.0)) {
     return invalid();
   }
-  if (count == 0) return ok();
-  DeviceGuard guard;
-  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
-  const bool divide = divisor != 1.0;
-  if (dtype == SPAR_HIP_FLOAT32) {
-    launch_fill_values(static_cast<float*>(output), count, static_cast<const float*>(scalar), 0.0F,
-                       static_cast<float>(divisor), divide, guard);
-  } else {
-    launch_fill_values(static_cast<double*>(output), count, static_cast<const double*>(scalar),
-                       0.0, divisor, divide, guard);
-  }
-  return finish(guard);
+  const FillScale mode = divisor == 1.0 ? FillScale::kNone : FillScale::kDivide;
+  return fill_from_device_scalar(output, scalar, count, dtype, divisor, mode, device);
 }
 
 extern "C" SparHipStatus spar_hip_launch_fill(void* output, uint64_t count, int dtype,
@@ -384,19 +405,19 @@ extern "C" SparHipStatus spar_hip_launch_fill(void* output, uint64_t count, int 
   switch (dtype) {
     case SPAR_HIP_FLOAT32:
       launch_fill_values<float>(static_cast<float*>(output), count, nullptr,
-                                static_cast<float>(value), 1.0F, false, guard);
+                                static_cast<float>(value), 1.0F, FillScale::kNone, guard);
       break;
     case SPAR_HIP_FLOAT64:
-      launch_fill_values<double>(static_cast<double*>(output), count, nullptr, value, 1.0, false,
-                                 guard);
+      launch_fill_values<double>(static_cast<double*>(output), count, nullptr, value, 1.0,
+                                 FillScale::kNone, guard);
       break;
     case SPAR_HIP_INT32:
       launch_fill_values<int32_t>(static_cast<int32_t*>(output), count, nullptr,
-                                  static_cast<int32_t>(value), 1, false, guard);
+                                  static_cast<int32_t>(value), 1, FillScale::kNone, guard);
       break;
     default:
       launch_fill_values<int64_t>(static_cast<int64_t*>(output), count, nullptr,
-                                  static_cast<int64_t>(value), 1, false, guard);
+                                  static_cast<int64_t>(value), 1, FillScale::kNone, guard);
       break;
   }
   return finish(guard);

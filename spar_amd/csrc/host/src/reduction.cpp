@@ -111,10 +111,9 @@ Tensor fill_from_gradient(const Shape& input_shape, DType dtype, const Tensor& g
   Tensor contribution{input_shape, dtype, gradient.device()};
   if (contribution.numel() == 0) return contribution;
   const Tensor scalar{gradient.is_contiguous() ? gradient : gradient.contiguous()};
-  hip::check(spar_hip_launch_fill_from_scalar(HipTensorAccess::mutable_data(contribution),
-                                              HipTensorAccess::data(scalar), contribution.numel(),
-                                              hip::dtype_tag(dtype), divisor,
-                                              gradient.device().index()),
+  hip::check(spar_hip_launch_fill_from_scalar_divided(
+                 HipTensorAccess::mutable_data(contribution), HipTensorAccess::data(scalar),
+                 contribution.numel(), hip::dtype_tag(dtype), divisor, gradient.device().index()),
              "reduction backward", gradient.device());
   return contribution;
 }

@@ -85,6 +85,7 @@ SIGNATURES = {
     "spar_hip_launch_scalar": [_P, _P, _U64, _I, _I, _D, _I],
     "spar_hip_launch_unary": [_P, _P, _U64, _I, _I, _I],
     "spar_hip_launch_fill_from_scalar": [_P, _P, _U64, _I, _D, _I],
+    "spar_hip_launch_fill_from_scalar_divided": [_P, _P, _U64, _I, _D, _I],
     "spar_hip_launch_fill": [_P, _U64, _I, _D, _I],
     "spar_hip_launch_add_in_place": [_P, _P, _U64, _I, _I],
     "spar_hip_launch_strided_copy": [_P, _P, _U64, _U64P, _U64P, _U64, _U64, _U64, _I],

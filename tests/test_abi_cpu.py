@@ -55,7 +55,8 @@ U = hip.u64_array
     ("spar_hip_launch_probability_forward", (None, None, None, 1, 0, 1, 0, 0, 0)),  # empty axis
     ("spar_hip_launch_probability_forward", (None, None, None, 1, 4, 1, 0, 2, 0)),  # log flag
     ("spar_hip_launch_probability_backward", (None, None, None, None, 1, 4, 0, 0, 0, 0)),
-    ("spar_hip_launch_fill_from_scalar", (None, None, 4, 0, 0.0, 0)),  # divisor 0
+    ("spar_hip_launch_fill_from_scalar", (None, None, 4, 0, 0.25, 0)),  # null scalar
+    ("spar_hip_launch_fill_from_scalar_divided", (None, None, 4, 0, 0.0, 0)),  # divisor 0
     ("spar_hip_random_uniform", (None, 4, 0, 1, 1.0, 1.0, 0)),         # low == high
 ])
 def test_invalid_arguments_rejected_on_host(name, args):

@@ -173,15 +173,31 @@ def test_fill_add_in_place_zero(hip, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("divisor", [1.0, 3.0, 4096.0, 67108864.0])
-def test_fill_from_scalar_divides_like_cpu(hip, dtype, divisor):
+@pytest.mark.parametrize("scale", [1.0, 0.25, 1.0 / 3.0, 1.0 / 4096.0, -2.5])
+def test_fill_from_scalar_multiplies_like_reference(hip, dtype, scale):
+    # the reference kernel writes scalar[0] * (T)scale (cuda_kernels.cu:249-257)
     g = np.array([0.7], dtype)
     n = 1000
     out = out_buf(hip, (n,), dtype)
-    hip.call("spar_hip_launch_fill_from_scalar", out.ptr, dev(hip, g).ptr, n, tag(dtype), divisor, 0)
+    hip.call("spar_hip_launch_fill_from_scalar", out.ptr, dev(hip, g).ptr, n, tag(dtype), scale, 0)
+    want = np.full(n, g[0] * dtype(scale), dtype)
+    assert_bitexact(out.to_numpy(dtype, (n,)), want, "fill_from_scalar")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("divisor", [1.0, 3.0, 1000.0, 4096.0, 67108864.0])
+def test_fill_from_scalar_divided_like_cpu(hip, dtype, divisor):
+    g = np.array([0.7], dtype)
+    n = 1000
+    out = out_buf(hip, (n,), dtype)
+    hip.call("spar_hip_launch_fill_from_scalar_divided", out.ptr, dev(hip, g).ptr, n, tag(dtype),
+             divisor, 0)
     # mean backward on the CPU: g / (T)n (ops/reduction.cpp:263-277)
     want = np.full(n, g[0] / dtype(divisor), dtype)
-    assert_bitexact(out.to_numpy(dtype, (n,)), want, "fill_from_scalar")
+    assert_bitexact(out.to_numpy(dtype, (n,)), want, "fill_from_scalar_divided")
+    if divisor == 1000.0 and dtype == np.float32:
+        # the two forms round apart here: 0.7f / 1000 != 0.7f * (float)(1 / 1000)
+        assert np.float32(0.7) * np.float32(1e-3) != want[0]
 
 
 # --------------------------------------------------------------- layouts
