@@ -93,6 +93,15 @@ enum SparHipReductionOp {
   SPAR_HIP_ARGMAX = 3,
 };
 
+/* Status code of spar_hip_launch_axis_reduction_no_alloc when the reduction
+ * needs more partial-result memory than its fixed workspace holds; nothing
+ * was enqueued.  (Codes 0-2 are listed at the top of this header.) */
+#define SPAR_HIP_STATUS_WORKSPACE_EXCEEDED 3
+
+/* Bytes of the fixed per-device workspace of
+ * spar_hip_launch_axis_reduction_no_alloc (8 MiB). */
+#define SPAR_HIP_NO_ALLOC_SCRATCH_BYTES (8u << 20)
+
 /* Replaces struct SparCudaStatus (cuda_kernels.hpp:41-44). */
 struct SparHipStatus {
   int code;
@@ -291,6 +300,31 @@ struct SparHipStatus spar_hip_launch_axis_reduction(void* output, const void* in
                                                     uint64_t storage_offset,
                                                     uint32_t reduced_mask, int dtype,
                                                     int operation, int device);
+
+/* spar_hip_launch_axis_reduction without any allocation: same arguments,
+ * same kernels, same results bit for bit.  No counterpart in the reference;
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Split reductions keep their partial results in a fixed workspace of
+ * SPAR_HIP_NO_ALLOC_SCRATCH_BYTES per device, a static device array held
+ * until the process ends, instead of allocator scratch.  A reduction whose
+ * partials do not fit (values rounded up to 256 bytes, plus 4 bytes per
+ * partial for max/argmax indices) returns SPAR_HIP_STATUS_WORKSPACE_EXCEEDED
+ * before anything is enqueued; on MI355X every [8192, 8192] float32 or
+ * float64 reduction fits.  The partials are written before they are read,
+ * so nothing needs clearing between calls.
+ *
+ * Every call on a device shares that device's workspace.  Calls issued from
+ * one host thread are ordered on the backend stream and do not interfere;
+ * calls that overlap on one device (several host threads, or captured work
+ * replayed concurrently with other calls) race on it.  The first call on a
+ * device resolves the workspace's address; the backend stream is created by
+ * the first call of any entry point on the device. */
+struct SparHipStatus spar_hip_launch_axis_reduction_no_alloc(
+    void* output, const void* input, uint64_t rank, const uint64_t* extents,
+    const uint64_t* strides, uint64_t storage_offset, uint32_t reduced_mask, int dtype,
+    int operation, int device);
 
 /* Sums a contiguous gradient of shape gradient_extents over its broadcast
  * axes into the contiguous original shape (right-aligned numpy rules).  The

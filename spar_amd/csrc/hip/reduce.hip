@@ -20,6 +20,7 @@
 //     result of a sequential scan bit for bit (including -0.0 vs +0.0).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -805,9 +806,25 @@ uint32_t grid_for(uint64_t blocks) {
   return static_cast<uint32_t>(blocks > kMaxGrid ? kMaxGrid : blocks);
 }
 
+// Where a split reduction keeps its partial results.  With `fixed` null the
+// caching allocator supplies them for the duration of the launch; otherwise
+// they are carved from the caller's fixed region of `capacity` bytes (values
+// first, then 32-bit indices at the next 256-byte boundary), and a plan that
+// needs more is refused with kWorkspaceExceeded before anything is launched.
+struct Workspace {
+  void* fixed = nullptr;
+  uint64_t capacity = 0;
+};
+
+// Returned by run_plan when the fixed workspace is too small; no kernel of
+// the reduction has been enqueued.
+constexpr hipError_t kWorkspaceExceeded = hipErrorOutOfMemory;
+
+uint64_t align256(uint64_t bytes) { return (bytes + 255) / 256 * 256; }
+
 template <typename T, Kind K, int NIN>
 hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int operation,
-                    int device, const DeviceGuard& guard) {
+                    int device, const DeviceGuard& guard, const Workspace& workspace) {
   constexpr int W = Vec16<T>::width;
   Sink<T> sink{};
   sink.operation = operation;
@@ -825,17 +842,26 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
   };
 
   // Scratch for partial results (values, plus indices for max/argmax unless
-  // the partials are value-only).
+  // the partials are value-only), from the allocator or the fixed workspace.
   auto with_partials = [&](uint64_t slots, auto&& body, bool value_only = false) -> hipError_t {
+    const bool indexed = K == Kind::Max && !value_only;
     void* values = nullptr;
     void* indices = nullptr;
-    hipError_t error = scratch_allocate(&values, slots * sizeof(T), device);
-    if (error != hipSuccess) return error;
-    if (K == Kind::Max && !value_only) {
-      error = scratch_allocate(&indices, slots * sizeof(uint32_t), device);
-      if (error != hipSuccess) {
-        scratch_release(values, device);
-        return error;
+    if (workspace.fixed != nullptr) {
+      const uint64_t value_bytes = align256(slots * sizeof(T));
+      const uint64_t needed = value_bytes + (indexed ? slots * sizeof(uint32_t) : 0);
+      if (needed > workspace.capacity) return kWorkspaceExceeded;
+      values = workspace.fixed;
+      indices = indexed ? static_cast<unsigned char*>(workspace.fixed) + value_bytes : nullptr;
+    } else {
+      hipError_t error = scratch_allocate(&values, slots * sizeof(T), device);
+      if (error != hipSuccess) return error;
+      if (indexed) {
+        error = scratch_allocate(&indices, slots * sizeof(uint32_t), device);
+        if (error != hipSuccess) {
+          scratch_release(values, device);
+          return error;
+        }
       }
     }
     Sink<T> partial = sink;
@@ -844,8 +870,10 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     partial.indices = nullptr;
     partial.partial_indices = static_cast<uint32_t*>(indices);
     body(partial);
-    scratch_release(values, device);
-    scratch_release(indices, device);
+    if (workspace.fixed == nullptr) {
+      scratch_release(values, device);
+      scratch_release(indices, device);
+    }
     return hipSuccess;
   };
 
@@ -860,7 +888,7 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     single.red_rank = 1;
     single.red_extents[0] = 1;
     single.red_strides[0] = 1;
-    return run_plan<T, K, NIN>(single, a, b, output, operation, device, guard);
+    return run_plan<T, K, NIN>(single, a, b, output, operation, device, guard, workspace);
   }
 
   if (row_case) {
@@ -1018,13 +1046,15 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
 
 template <typename T, int NIN>
 hipError_t dispatch_plan(const Plan& plan, const void* a, const void* b, void* output,
-                         int operation, int device, const DeviceGuard& guard) {
+                         int operation, int device, const DeviceGuard& guard,
+                         const Workspace& workspace) {
   const T* ta = static_cast<const T*>(a);
   const T* tb = static_cast<const T*>(b);
   if (operation == SPAR_HIP_SUM || operation == SPAR_HIP_MEAN) {
-    return run_plan<T, Kind::Sum, NIN>(plan, ta, tb, output, operation, device, guard);
+    return run_plan<T, Kind::Sum, NIN>(plan, ta, tb, output, operation, device, guard,
+                                       workspace);
   }
-  return run_plan<T, Kind::Max, NIN>(plan, ta, tb, output, operation, device, guard);
+  return run_plan<T, Kind::Max, NIN>(plan, ta, tb, output, operation, device, guard, workspace);
 }
 
 // Builds a plan from a view and a reduced-axis mask.
@@ -1050,21 +1080,48 @@ Plan make_plan(uint64_t rank, const uint64_t* extents, const uint64_t* strides, 
   return plan;
 }
 
-SparHipStatus execute(const Plan& plan, const void* a, const void* b, int nin, void* output,
-                      int dtype, int operation, int device) {
+// Runs a plan on `device`'s stream.  `fixed_workspace`, when given, returns
+// the device's fixed partial-result region (it is called with the device
+// current) and no memory is allocated.
+template <typename FixedWorkspace>
+SparHipStatus execute_with(const Plan& plan, const void* a, const void* b, int nin, void* output,
+                           int dtype, int operation, int device, FixedWorkspace&& fixed_workspace) {
   DeviceGuard guard;
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  Workspace workspace;
+  if (const hipError_t error = fixed_workspace(workspace); error != hipSuccess) {
+    return runtime(error);
+  }
   hipError_t error;
   if (dtype == SPAR_HIP_FLOAT32) {
-    error = nin == 1 ? dispatch_plan<float, 1>(plan, a, b, output, operation, device, guard)
-                     : dispatch_plan<float, 2>(plan, a, b, output, operation, device, guard);
+    error = nin == 1
+                ? dispatch_plan<float, 1>(plan, a, b, output, operation, device, guard, workspace)
+                : dispatch_plan<float, 2>(plan, a, b, output, operation, device, guard, workspace);
   } else {
-    error = nin == 1 ? dispatch_plan<double, 1>(plan, a, b, output, operation, device, guard)
-                     : dispatch_plan<double, 2>(plan, a, b, output, operation, device, guard);
+    error = nin == 1
+                ? dispatch_plan<double, 1>(plan, a, b, output, operation, device, guard, workspace)
+                : dispatch_plan<double, 2>(plan, a, b, output, operation, device, guard, workspace);
+  }
+  if (error == kWorkspaceExceeded && workspace.fixed != nullptr) {
+    return {SPAR_HIP_STATUS_WORKSPACE_EXCEEDED, static_cast<int>(hipErrorInvalidValue)};
   }
   if (error != hipSuccess) return runtime(error);
   return finish(guard);
 }
+
+SparHipStatus execute(const Plan& plan, const void* a, const void* b, int nin, void* output,
+                      int dtype, int operation, int device) {
+  return execute_with(plan, a, b, nin, output, dtype, operation, device,
+                      [](Workspace&) { return hipSuccess; });
+}
+
+// Validates an axis reduction request and builds its plan.  Returns false
+// with `status` set when the request is finished without a launch (an
+// empty output, an empty reduced domain zero-filled) or invalid.
+bool axis_reduction_plan(Plan& plan, SparHipStatus& status, void* output, const void* input,
+                         uint64_t rank, const uint64_t* extents, const uint64_t* strides,
+                         uint64_t storage_offset, uint32_t reduced_mask, int dtype, int operation,
+                         int device);
 
 bool valid_reduction(int operation) {
   return operation >= SPAR_HIP_SUM && operation <= SPAR_HIP_ARGMAX;
@@ -1141,16 +1198,18 @@ extern "C" SparHipStatus spar_hip_launch_row_reduction(void* output, const void*
   return execute(plan, input, nullptr, 1, output, dtype, operation, device);
 }
 
-extern "C" SparHipStatus spar_hip_launch_axis_reduction(void* output, const void* input,
-                                                        uint64_t rank, const uint64_t* extents,
-                                                        const uint64_t* strides,
-                                                        uint64_t storage_offset,
-                                                        uint32_t reduced_mask, int dtype,
-                                                        int operation, int device) {
+namespace spar_hip {
+namespace {
+
+bool axis_reduction_plan(Plan& plan, SparHipStatus& status, void* output, const void* input,
+                         uint64_t rank, const uint64_t* extents, const uint64_t* strides,
+                         uint64_t storage_offset, uint32_t reduced_mask, int dtype, int operation,
+                         int device) {
   if (!valid_float_dtype(dtype) || !valid_reduction(operation) || rank > kMaxRank ||
       (rank != 0 && (extents == nullptr || strides == nullptr)) ||
       (rank < 32 && (reduced_mask >> rank) != 0)) {
-    return invalid();
+    status = invalid();
+    return false;
   }
   uint64_t outputs = 1;
   uint64_t reduced = 1;
@@ -1161,15 +1220,90 @@ extern "C" SparHipStatus spar_hip_launch_axis_reduction(void* output, const void
       outputs *= extents[axis];
     }
   }
-  if (outputs == 0) return ok();
-  if (output == nullptr) return invalid();
-  if (reduced == 0) {
-    if (operation != SPAR_HIP_SUM) return invalid();
-    return spar_hip_zero(output, outputs * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8), device);
+  if (outputs == 0) {
+    status = ok();
+    return false;
   }
-  if (input == nullptr) return invalid();
-  const Plan plan = make_plan(rank, extents, strides, storage_offset, reduced_mask);
+  if (output == nullptr) {
+    status = invalid();
+    return false;
+  }
+  if (reduced == 0) {
+    status = operation != SPAR_HIP_SUM
+                 ? invalid()
+                 : spar_hip_zero(output, outputs * (dtype == SPAR_HIP_FLOAT32 ? 4 : 8), device);
+    return false;
+  }
+  if (input == nullptr) {
+    status = invalid();
+    return false;
+  }
+  plan = make_plan(rank, extents, strides, storage_offset, reduced_mask);
+  return true;
+}
+
+// The no-allocation entry point's partial results: one fixed array per
+// device, resident until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a stand-in, not device memory):
+// the first call on each device, with that device current, resolves the
+// device's own address with hipGetSymbolAddress, and launches use that.
+static __device__ __align__(256) unsigned char scratch[SPAR_HIP_NO_ALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxScratchDevices] = {};
+
+hipError_t scratch_address(int device, void** address) {
+  if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    void* resolved = nullptr;
+    const hipError_t error = hipGetSymbolAddress(&resolved, HIP_SYMBOL(scratch));
+    if (error != hipSuccess) return error;
+    if (resolved == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_address[device] = resolved;
+  }
+  *address = g_scratch_address[device];
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace spar_hip
+
+extern "C" SparHipStatus spar_hip_launch_axis_reduction(void* output, const void* input,
+                                                        uint64_t rank, const uint64_t* extents,
+                                                        const uint64_t* strides,
+                                                        uint64_t storage_offset,
+                                                        uint32_t reduced_mask, int dtype,
+                                                        int operation, int device) {
+  Plan plan;
+  SparHipStatus status{};
+  if (!axis_reduction_plan(plan, status, output, input, rank, extents, strides, storage_offset,
+                           reduced_mask, dtype, operation, device)) {
+    return status;
+  }
   return execute(plan, input, nullptr, 1, output, dtype, operation, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_axis_reduction_no_alloc(
+    void* output, const void* input, uint64_t rank, const uint64_t* extents,
+    const uint64_t* strides, uint64_t storage_offset, uint32_t reduced_mask, int dtype,
+    int operation, int device) {
+  Plan plan;
+  SparHipStatus status{};
+  if (!axis_reduction_plan(plan, status, output, input, rank, extents, strides, storage_offset,
+                           reduced_mask, dtype, operation, device)) {
+    return status;
+  }
+  return execute_with(plan, input, nullptr, 1, output, dtype, operation, device,
+                      [device](Workspace& workspace) {
+                        void* address = nullptr;
+                        const hipError_t error = scratch_address(device, &address);
+                        if (error != hipSuccess) return error;
+                        workspace.fixed = address;
+                        workspace.capacity = SPAR_HIP_NO_ALLOC_SCRATCH_BYTES;
+                        return hipSuccess;
+                      });
 }
 
 extern "C" SparHipStatus spar_hip_launch_broadcast_reduce(

@@ -95,6 +95,8 @@ SIGNATURES = {
     "spar_hip_launch_reduction": [_P, _P, _U64, _I, _I, _I],
     "spar_hip_launch_row_reduction": [_P, _P, _U64, _U64, _I, _I, _I],
     "spar_hip_launch_axis_reduction": [_P, _P, _U64, _U64P, _U64P, _U64, _U32, _I, _I, _I],
+    "spar_hip_launch_axis_reduction_no_alloc": [_P, _P, _U64, _U64P, _U64P, _U64, _U32, _I, _I,
+                                                _I],
     "spar_hip_launch_broadcast_reduce": [_P, _P, _U64, _U64P, _U64, _U64P, _U64P, _U64, _I, _I],
     "spar_hip_launch_multiply_reduce": [_P, _P, _P, _U64, _U64P, _U64, _U64P, _U64, _I, _I],
     "spar_hip_launch_probability_forward": [_P, _P, _P, _U64, _U64, _U64, _I, _I, _I],
