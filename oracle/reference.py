@@ -9,6 +9,9 @@ them: view metadata (core/tensor.cpp:237-346), broadcast rules (:549-570),
 the backward rules of every op (ops/*.cpp) and the engine
 (autograd/autograd.cpp:43-265), including its contribution clones and
 in-place accumulation order.  The product (spar_amd/) never imports it.
+
+Its backward rules are pinned against torch.autograd in float64 and central
+differences by tests/test_oracle_autograd_cpu.py.
 """
 from __future__ import annotations
 

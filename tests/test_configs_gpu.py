@@ -249,26 +249,44 @@ def test_c5_layernorm_chain(hip, view):
         outside[256:256 + rows, 512:512 + cols] = 0
         assert not outside.any(), "gradient outside the slice is zero"
 
-    # sampled rows through the oracle's restatement of the same chain
-    picked = sample_rows(30, rows, 62)
+    # Every row against the chain evaluated in float64 on the host, then
+    # sampled rows against the oracle's restatement (the reference's float32
+    # operations and order).  Bound: 1e-6 * sqrt(n) of the row's largest
+    # magnitude; the oracle's own float32 chain stays within 0.02 of that
+    # bound of the float64 values on these inputs.
     x_host = base.T if view == "transposed" else base[256:256 + rows, 512:512 + cols]
+    x64 = x_host.astype(np.float64)
+    xc64 = x64 - x64.mean(axis=1, keepdims=True)
+    sd64 = np.sqrt((xc64 * xc64).mean(axis=1, keepdims=True) + 1e-5)
+    xhat64 = xc64 / sd64
+    y64 = xhat64 * gamma + beta
+    g64 = G.astype(np.float64) * gamma
+    dx64 = (g64 - g64.mean(axis=1, keepdims=True)
+            - xhat64 * (g64 * xhat64).mean(axis=1, keepdims=True)) / sd64
+    tol = 1e-6 * np.sqrt(cols)
+    for name, got, want in (("xhat", got_xhat, xhat64), ("y", got_y, y64), ("dx", got_dx, dx64)):
+        scale = np.max(np.abs(want), axis=1, keepdims=True) + 1e-30
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= tol * scale), f"C5 {view} {name} vs float64: max rel {np.max(err / scale)}"
+
+    picked = sample_rows(128, rows, 62)
     sub = [R.RTensor.of(np.ascontiguousarray(x_host[picked]), requires_grad=True),
            R.RTensor.of(gamma, requires_grad=True), R.RTensor.of(beta, requires_grad=True),
            R.RTensor.of(np.ascontiguousarray(G[picked]))]
     want_xhat, want_y, want_loss = chain(R, sub[0], sub[1], sub[2], sub[3])
     want_loss.backward()
-    tol = 1e-6 * np.sqrt(cols) * 8
     for name, got, want in (("xhat", got_xhat[picked], want_xhat.numpy()),
                             ("y", got_y[picked], want_y.numpy()),
                             ("dx", got_dx[picked], sub[0].grad().numpy())):
         scale = np.max(np.abs(want), axis=1, keepdims=True) + 1e-30
         err = np.abs(got.astype(np.float64) - want)
-        assert np.all(err <= tol * scale), f"C5 {view} {name}: max rel {np.max(err / scale)}"
+        assert np.all(err <= tol * scale), f"C5 {view} {name} vs oracle: max rel {np.max(err / scale)}"
 
-    # d beta = sum over rows of G (closed form); d gamma = sum over rows of G * xhat
+    # d beta = sum over rows of G (closed form); d gamma = sum over rows of
+    # G * xhat with xhat from the host's float64 chain
     assert_red(got_dbeta, ref.axis_sum(G, [0]), rows, norm2(G, axis=0), "d beta")
-    want_dgamma = np.sum(G.astype(np.float64) * got_xhat.astype(np.float64), axis=0)
-    norm = norm2(G.astype(np.float64) * got_xhat, axis=0)
+    want_dgamma = np.sum(G.astype(np.float64) * xhat64, axis=0)
+    norm = norm2(G.astype(np.float64) * xhat64, axis=0)
     assert_red(got_dgamma, want_dgamma, rows, norm * 4, "d gamma")
 
 
