@@ -42,17 +42,23 @@ struct DeviceGuard {
   ~DeviceGuard();
 };
 
-// Fills `guard`; returns hipSuccess or the failing HIP error.
+// Fills `guard`; returns hipSuccess or the failing HIP error.  It also
+// clears the calling thread's last-error slot, so that finish() reports only
+// errors raised by the launches of the current call.
 hipError_t enter(int device, DeviceGuard& guard);
 
-// Workgroups of `kernel` resident on the device at once (at least one per CU).
+// Workgroups of `kernel` resident on the device at once (at least one per
+// CU), or 0 when the runtime cannot say.  A failed query's error is consumed
+// here: callers fall back to a launch shape that does not need the answer,
+// and the error must not surface later as the status of that launch.
 template <typename K>
 uint64_t resident_blocks(K kernel, int threads, const DeviceGuard& guard) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-      per_cu < 1) {
-    per_cu = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) {
+    static_cast<void>(hipGetLastError());
+    return 0;
   }
+  if (per_cu < 1) per_cu = 1;
   return static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(guard.multiprocessors);
 }
 

@@ -403,10 +403,12 @@ hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard&
   };
   // Two workgroups per CU (bounded by occupancy): enough rows in flight per
   // CU while keeping the [grid, n] partials small.
-  uint64_t grid = stream ? resident_blocks(kernel_for(Policy<true>{}), THREADS, guard)
-                         : resident_blocks(kernel_for(Policy<false>{}), THREADS, guard);
+  // The workgroups do not depend on each other, so an unknown occupancy
+  // (0) leaves the wanted count.
+  const uint64_t resident = stream ? resident_blocks(kernel_for(Policy<true>{}), THREADS, guard)
+                                   : resident_blocks(kernel_for(Policy<false>{}), THREADS, guard);
   const uint64_t wanted = static_cast<uint64_t>(guard.multiprocessors) * 2;
-  if (grid > wanted) grid = wanted;
+  uint64_t grid = resident != 0 && resident < wanted ? resident : wanted;
   if (grid > a.rows) grid = a.rows;
   const uint64_t parts = (CENTER ? 2 : 1) * grid * a.n;
   void* scratch = nullptr;

@@ -168,6 +168,7 @@ DeviceGuard::~DeviceGuard() {
 }
 
 hipError_t enter(int device, DeviceGuard& guard) {
+  static_cast<void>(hipGetLastError());
   DeviceState* state = state_for(device);
   if (state == nullptr) {
     guard.error = hipErrorInvalidDevice;

@@ -615,18 +615,17 @@ bool launch_vec_tiled(T* out, const T* a, const T* b, const MultiView& view, int
   tg.tiles_q.init(static_cast<uint32_t>(tiles_q));
   tg.tile_count = static_cast<uint32_t>(tiles);
   // One workgroup per resident slot (two per CU with one staged operand, one
-  // with two), each walking tiles.
+  // with two), each walking tiles.  Without an occupancy answer the view
+  // takes another kernel (same values).
   auto launch = [&](auto kernel) {
     const uint64_t slots = resident_blocks(kernel, kThreads, guard);
+    if (slots == 0) return false;
     kernel<<<static_cast<uint32_t>(tiles < slots ? tiles : slots), kThreads, 0, guard.stream>>>(
         out, a, b, tg, f);
+    return true;
   };
-  if (staged == 1) {
-    launch(vec_tiled_kernel<T, NOPS, 1, F>);
-  } else {
-    launch(vec_tiled_kernel<T, NOPS, 2, F>);
-  }
-  return true;
+  return staged == 1 ? launch(vec_tiled_kernel<T, NOPS, 1, F>)
+                     : launch(vec_tiled_kernel<T, NOPS, 2, F>);
 }
 
 // Chooses and launches the kernel for a coalesced view; out is contiguous.
