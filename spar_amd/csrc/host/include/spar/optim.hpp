@@ -3,8 +3,10 @@
 // spar.nn.parameter (src/nn/parameter.cppm:8-31), spar.optim.adamw
 // (src/optim/adamw.cppm:8-62) and spar.training.gradients
 // (src/training/gradients.cppm:6-26).  The per-element work runs in the
-// backend's AdamW, norm-summary and scaling kernels.  Migration between
-// devices (nn::move_to, AdamW::move_to) is not provided.
+// backend's AdamW, norm-summary and scaling kernels.  Parameters and
+// optimizer state migrate between the host and HIP devices with
+// nn::move_to and AdamW::move_to (src/nn/parameter.cpp:54-87,
+// src/optim/adamw.cpp:172-190).
 #pragma once
 
 #include <cstddef>
@@ -36,8 +38,19 @@ class Parameter {
   [[nodiscard]] Parameter clone() const;
 
  private:
+  friend void move_to(Parameter& parameter, Device target);
+  friend void move_to(std::span<Parameter> parameters, Device target);
   Tensor tensor_;
 };
+
+/// Moves a Parameter's values to `target` in place: its Tensor, autograd
+/// and Storage identities are kept (parameter.cppm:33-39).  Refused with
+/// std::logic_error while the Parameter holds a gradient.
+void move_to(Parameter& parameter, Device target);
+
+/// Moves every distinct Parameter (aliases once) to `target`.  All copies
+/// are made before any Parameter changes, so a failure changes nothing.
+void move_to(std::span<Parameter> parameters, Device target);
 
 }  // namespace spar::nn
 
@@ -89,6 +102,10 @@ class AdamW {
 
   void step();
   void zero_grad();
+  /// Moves the optimizer moments and every tracked Parameter to `target`;
+  /// the moments are copied before any Parameter moves, and committed only
+  /// after all of them have (adamw.cppm:25-26).
+  void move_to(Device target);
 
   [[nodiscard]] std::size_t parameter_count() const noexcept;
   [[nodiscard]] double learning_rate() const noexcept;
@@ -115,6 +132,13 @@ class AdamW {
     nn::Parameter parameter;
     std::optional<State> state;
   };
+
+  // The entry tracking `parameter` (same identity), or null.
+  [[nodiscard]] const Entry* entry_of(const nn::Parameter& parameter) const noexcept;
+  // Whether `entry` takes part in a step; throws if it cannot.
+  [[nodiscard]] static bool steps(const Entry& entry);
+  // One fused update of `entry`'s Parameter and moments.
+  void update(Entry& entry) const;
 
   std::vector<Entry> entries_;
   double learning_rate_;

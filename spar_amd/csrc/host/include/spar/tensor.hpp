@@ -29,12 +29,14 @@ class Tensor;
 
 namespace spar::detail {
 
-struct AutogradAccess;
-struct AutogradMeta;
+struct GradState;
 struct HipTensorAccess;
+struct TensorInternals;
 
-/// Ref-counted allocation (src/core/storage.cppm:10-33): host bytes, or a
-/// device block from the backend's caching allocator.
+/// Ref-counted allocation with the interface of src/core/storage.cppm:10-33:
+/// host bytes, or a block of a HIP device's caching allocator.  The block
+/// and its device travel together in one owner whose deleter returns the
+/// block to where it came from.
 class Storage final {
  public:
   Storage(std::size_t nbytes, Device device);
@@ -51,10 +53,14 @@ class Storage final {
   void swap_payload(Storage& other) noexcept;
 
  private:
+  struct Release {
+    Device device;
+    void operator()(void* block) const noexcept;
+  };
+  [[nodiscard]] void* block_on(DeviceType expected) const;
+
   std::size_t nbytes_;
-  Device device_;
-  std::unique_ptr<std::byte[]> host_data_;
-  void* hip_data_;
+  std::unique_ptr<void, Release> block_;
 };
 
 }  // namespace spar::detail
@@ -134,13 +140,21 @@ class Tensor {
   }
 
  private:
-  friend struct detail::AutogradAccess;
+  friend struct detail::TensorInternals;
   friend struct detail::HipTensorAccess;
   friend Tensor zeros(Shape shape, DType dtype, Device device);
   friend Tensor full_value(Shape shape, DType dtype, double value, Device device);
 
   Tensor(std::shared_ptr<detail::Storage> storage, DType dtype, Shape shape,
          std::vector<Shape::stride_type> strides, std::size_t storage_offset);
+
+  // A view on this tensor's storage with new metadata.  When this tensor is
+  // tracked, `rule` maps the view's gradient to this tensor's gradient.
+  [[nodiscard]] Tensor make_view(Shape shape, std::vector<Shape::stride_type> strides,
+                                 std::size_t storage_offset,
+                                 std::function<std::vector<Tensor>(const Tensor&)> rule) const;
+  // A view whose axis k is this tensor's axis order[k]; `order` is valid.
+  [[nodiscard]] Tensor permuted(const std::vector<std::size_t>& order) const;
 
   void initialize_autograd();
   void reset_to_empty() noexcept;
@@ -149,6 +163,7 @@ class Tensor {
   [[nodiscard]] static std::size_t checked_nbytes(std::size_t numel, DType dtype);
   [[nodiscard]] std::size_t checked_storage_byte_offset() const;
   [[nodiscard]] Tensor materialize_values(Device target) const;
+  [[nodiscard]] Tensor gathered() const;
   [[nodiscard]] std::byte* mutable_host_data();
   [[nodiscard]] const std::byte* host_data() const;
 
@@ -166,7 +181,7 @@ class Tensor {
   std::vector<Shape::stride_type> strides_;
   std::size_t storage_offset_;
   std::size_t nbytes_;
-  std::shared_ptr<detail::AutogradMeta> autograd_;
+  std::shared_ptr<detail::GradState> grad_state_;
 };
 
 void swap(Tensor& left, Tensor& right) noexcept;

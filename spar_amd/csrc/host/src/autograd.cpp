@@ -1,17 +1,26 @@
-// Reverse-mode autograd engine (src/autograd/autograd.cpp:43-265).
+// Reverse-mode autograd engine of the host library.
 //
-// Graph recording, the DFS topological order, the `ones` seed and the
-// reverse sweep are the reference's.  Two differences keep the device path
-// lean without changing any value:
-//   * contributions are not cloned: a backward rule's result is kept as is
-//     when it owns its storage outright; otherwise the first in-place
-//     accumulation into it is done out of place (same additions, same order);
-//   * a node's gradient is released once its backward rule has run.
-// Gradient accumulation is the elementwise `dst += src` of the reference
-// (add_gradient_values, :99-133), in the same order, so gradients are
-// bit-identical given identical contributions.
+// Public behaviour, messages and exception types follow Spar's engine
+// (src/autograd/autograd.cpp:43-265).  The structure is this library's own:
+// an explicit-stack graph walk, a slot per reachable identity, and gradients
+// that are moved, not cloned, through the sweep.
+//
+// Accumulation-order contract.  It fixes every gradient bit, so it is the
+// same as the reference's:
+//   1. The reachable identities are ordered by a depth-first post-order walk
+//      from the loss that visits each operation's inputs in the order they
+//      were recorded and enters each identity once.
+//   2. The sweep runs that order backwards, seeded with ones for the loss.
+//   3. An identity's first incoming gradient is kept as it is; every later
+//      one is added elementwise, `held += incoming`, in sweep order.
+//   4. A leaf keeps the gradient it is handed on its first backward() and
+//      adds later ones in place (`accumulated += incoming`).
+// Given identical contributions, the gradients are therefore identical to
+// the reference's.  The reference also cloned each contribution
+// (autograd.cpp:145, :244); the clone only copied values, so leaving it out
+// changes no bit.  A held gradient whose storage another handle still sees
+// is added out of place (same operands, same order) instead of in place.
 #include <unordered_map>
-#include <unordered_set>
 
 #include "autograd_internal.hpp"
 #include "bridge.hpp"
@@ -19,12 +28,30 @@
 #include "spar/tensor.hpp"
 
 namespace spar::detail {
+namespace {
+
+GradInput input_of(const Tensor& parent) {
+  return GradInput{TensorInternals::grad_state(parent), parent.shape(), parent.dtype(),
+                   parent.device()};
+}
+
+// Gives `output` a fresh tracked identity produced by `function`.
+void attach(Tensor& output, std::shared_ptr<GradFunction> function) {
+  auto state{std::make_shared<GradState>()};
+  state->tracked = true;
+  state->producer = std::move(function);
+  TensorInternals::grad_state(output) = std::move(state);
+}
+
+}  // namespace
 
 void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
                       BackwardFunction backward) {
   if (requiring_parents.empty()) {
     throw std::logic_error{"Cannot record an autograd operation without requiring-grad parents"};
   }
+  auto function{std::make_shared<GradFunction>()};
+  function->inputs.reserve(requiring_parents.size());
   for (const Tensor& parent : requiring_parents) {
     if (!parent.requires_grad()) {
       throw std::logic_error{"Autograd nodes may retain only requiring-grad parents"};
@@ -32,18 +59,10 @@ void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
     if (parent.device() != output.device()) {
       throw std::logic_error{"Autograd output and parent Device mismatch"};
     }
+    function->inputs.push_back(input_of(parent));
   }
-  std::vector<AutogradEdge> edges;
-  edges.reserve(requiring_parents.size());
-  for (const Tensor& parent : requiring_parents) {
-    edges.push_back(AutogradEdge{AutogradAccess::meta(parent), parent.shape(), parent.dtype(),
-                                 parent.device()});
-  }
-  auto& output_meta{AutogradAccess::meta(output)};
-  output_meta = std::make_shared<AutogradMeta>();
-  output_meta->requires_grad = true;
-  output_meta->grad_fn =
-      std::make_shared<AutogradNode>(AutogradNode{std::move(edges), std::move(backward)});
+  function->rule = std::move(backward);
+  attach(output, std::move(function));
 }
 
 void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward) {
@@ -51,77 +70,162 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
     throw std::logic_error{"Cannot record a transfer from a non-requiring parent"};
   }
   if (requiring_parent.device() == output.device()) {
-    throw std::logic_error{"Transfer autograd nodes require different source and destination Devices"};
+    throw std::logic_error{
+        "Transfer autograd nodes require different source and destination Devices"};
   }
-  std::vector<AutogradEdge> edges;
-  edges.push_back(AutogradEdge{AutogradAccess::meta(requiring_parent), requiring_parent.shape(),
-                               requiring_parent.dtype(), requiring_parent.device()});
-  auto& output_meta{AutogradAccess::meta(output)};
-  output_meta = std::make_shared<AutogradMeta>();
-  output_meta->requires_grad = true;
-  output_meta->grad_fn =
-      std::make_shared<AutogradNode>(AutogradNode{std::move(edges), std::move(backward)});
+  auto function{std::make_shared<GradFunction>()};
+  function->inputs.push_back(input_of(requiring_parent));
+  function->rule = std::move(backward);
+  attach(output, std::move(function));
 }
 
 bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept {
-  const auto& left_meta{AutogradAccess::meta(left)};
-  const auto& right_meta{AutogradAccess::meta(right)};
-  return left_meta != nullptr && left_meta == right_meta;
+  const GradState* identity{TensorInternals::grad_state(left).get()};
+  return identity != nullptr && identity == TensorInternals::grad_state(right).get();
 }
 
+namespace {
+
+void check_same_layout(const Tensor& held, const Tensor& incoming) {
+  if (held.shape() != incoming.shape() || held.dtype() != incoming.dtype() ||
+      held.device() != incoming.device()) {
+    throw std::logic_error{"Internal gradient accumulation shape, dtype, or Device mismatch"};
+  }
+  if (!is_floating(held.dtype())) throw std::logic_error{"Integer gradients are not supported"};
+}
+
+// held[i] += incoming[i] on the device, into held's own storage.
+void add_into(Tensor& held, const Tensor& incoming) {
+  require_hip(held, "gradient accumulation");
+  const Tensor source{incoming.is_contiguous() ? incoming : incoming.contiguous()};
+  hip::check(spar_hip_launch_add_in_place(HipTensorAccess::mutable_data(held),
+                                          HipTensorAccess::data(source), held.numel(),
+                                          hip::dtype_tag(held.dtype()), held.device().index()),
+             "gradient accumulation", held.device());
+}
+
+// The sweep state of one backward() call.
+class Sweep final {
+ public:
+  explicit Sweep(GradState* loss) { order_from(loss); }
+
+  void run(GradState* loss, Tensor seed) {
+    pending_[slot_.at(loss)] = std::move(seed);
+    for (std::size_t position{order_.size()}; position-- > 0;) {
+      GradState& state{*order_[position]};
+      std::optional<Tensor>& held{pending_[position]};
+      if (!held.has_value()) {
+        throw std::logic_error{"Reachable autograd identity did not receive a gradient"};
+      }
+      Tensor gradient{std::move(*held)};
+      held.reset();
+      if (state.producer == nullptr) {
+        deliver_to_leaf(state, std::move(gradient));
+        continue;
+      }
+      propagate(*state.producer, std::move(gradient));
+    }
+  }
+
+ private:
+  // Depth-first post-order over tracked identities, inputs in recording
+  // order, each identity entered once (contract, point 1).
+  void order_from(GradState* loss) {
+    struct Frame {
+      GradState* state;
+      std::size_t next_input;
+    };
+    std::vector<Frame> stack;
+    const auto enter = [this, &stack](GradState* state) {
+      if (state == nullptr || !state->tracked) return;
+      if (!slot_.emplace(state, kUnplaced).second) return;
+      stack.push_back(Frame{state, 0});
+    };
+    enter(loss);
+    while (!stack.empty()) {
+      Frame& top{stack.back()};
+      const GradFunction* producer{top.state->producer.get()};
+      if (producer != nullptr && top.next_input < producer->inputs.size()) {
+        enter(producer->inputs[top.next_input++].identity.get());
+        continue;
+      }
+      slot_[top.state] = order_.size();
+      order_.push_back(top.state);
+      stack.pop_back();
+    }
+    pending_.resize(order_.size());
+  }
+
+  // Runs one operation's rule and hands each input its gradient.
+  void propagate(const GradFunction& function, Tensor gradient) {
+    std::vector<Tensor> contributions{function.rule(gradient)};
+    if (contributions.size() != function.inputs.size()) {
+      throw std::logic_error{"Backward rule returned an incorrect number of gradients"};
+    }
+    gradient = Tensor{Shape{}, gradient.dtype(), Device::cpu()};  // free it before the adds
+    for (std::size_t k{0}; k < contributions.size(); ++k) {
+      const GradInput& input{function.inputs[k]};
+      const Tensor& produced{contributions[k]};
+      if (produced.shape() != input.shape || produced.dtype() != input.dtype ||
+          produced.device() != input.device) {
+        throw std::logic_error{
+            "Backward rule produced a gradient with incorrect shape, dtype, or Device"};
+      }
+      if (produced.requires_grad()) {
+        throw std::logic_error{"Backward rule produced a higher-order gradient"};
+      }
+      Tensor incoming{produced.detach()};
+      contributions[k] = Tensor{Shape{}, produced.dtype(), Device::cpu()};
+      const auto found{slot_.find(input.identity.get())};
+      if (found == slot_.end()) continue;  // an identity no longer tracked
+      std::optional<Tensor>& held{pending_[found->second]};
+      if (!held.has_value()) {
+        held = std::move(incoming);
+        continue;
+      }
+      check_same_layout(*held, incoming);
+      if (TensorInternals::sole_owner(*held)) {
+        add_into(*held, incoming);
+      } else {
+        held = add(held->detach(), incoming.detach());
+      }
+    }
+  }
+
+  static void deliver_to_leaf(GradState& leaf, Tensor gradient) {
+    if (leaf.accumulated.has_value()) {
+      check_same_layout(*leaf.accumulated, gradient);
+      add_into(*leaf.accumulated, gradient);  // in place: grad() handles see it
+      return;
+    }
+    leaf.accumulated = TensorInternals::sole_owner(gradient) ? gradient.detach()
+                                                             : gradient.detach().clone();
+  }
+
+  static constexpr std::size_t kUnplaced = static_cast<std::size_t>(-1);
+
+  std::vector<GradState*> order_;
+  std::unordered_map<const GradState*, std::size_t> slot_;
+  std::vector<std::optional<Tensor>> pending_;
+};
+
+}  // namespace
 }  // namespace spar::detail
 
 namespace spar {
-namespace {
 
-// destination += contribution (autograd.cpp:99-133).  An engine-internal
-// accumulator whose storage is shared with another handle is replaced by a
-// new tensor instead; a leaf gradient (`in_place`) is always updated in place
-// so handles returned by grad() observe the accumulation, as in the reference.
-void add_gradient_values(Tensor& destination, const Tensor& contribution, bool in_place = false) {
-  if (destination.shape() != contribution.shape() || destination.dtype() != contribution.dtype() ||
-      destination.device() != contribution.device()) {
-    throw std::logic_error{"Internal gradient accumulation shape, dtype, or Device mismatch"};
-  }
-  if (!is_floating(destination.dtype())) throw std::logic_error{"Integer gradients are not supported"};
-  detail::require_hip(destination, "gradient accumulation");
-  const Tensor source{contribution.is_contiguous() ? contribution : contribution.contiguous()};
-  if (!in_place && !detail::AutogradAccess::exclusively_owned(destination)) {
-    destination = add(destination.detach(), source.detach());
-    return;
-  }
-  detail::hip::check(
-      spar_hip_launch_add_in_place(detail::HipTensorAccess::mutable_data(destination),
-                                   detail::HipTensorAccess::data(source), destination.numel(),
-                                   detail::hip::dtype_tag(destination.dtype()),
-                                   destination.device().index()),
-      "gradient accumulation", destination.device());
+using detail::GradState;
+
+void Tensor::initialize_autograd() { grad_state_ = std::make_shared<GradState>(); }
+
+bool Tensor::requires_grad() const noexcept { return grad_state_ != nullptr && grad_state_->tracked; }
+
+bool Tensor::is_leaf() const noexcept {
+  return grad_state_ == nullptr || grad_state_->producer == nullptr;
 }
-
-// autograd.cpp:135-146 without the clone.
-void validate_contribution(const Tensor& contribution, const detail::AutogradEdge& parent) {
-  if (contribution.shape() != parent.expected_shape ||
-      contribution.dtype() != parent.expected_dtype ||
-      contribution.device() != parent.expected_device) {
-    throw std::logic_error{"Backward rule produced a gradient with incorrect shape, dtype, or Device"};
-  }
-  if (contribution.requires_grad()) {
-    throw std::logic_error{"Backward rule produced a higher-order gradient"};
-  }
-}
-
-}  // namespace
-
-void Tensor::initialize_autograd() { autograd_ = std::make_shared<detail::AutogradMeta>(); }
-
-bool Tensor::requires_grad() const noexcept {
-  return autograd_ != nullptr && autograd_->requires_grad;
-}
-
-bool Tensor::is_leaf() const noexcept { return autograd_ == nullptr || autograd_->grad_fn == nullptr; }
 
 bool Tensor::has_grad() const noexcept {
-  return autograd_ != nullptr && autograd_->leaf_grad.has_value();
+  return grad_state_ != nullptr && grad_state_->accumulated.has_value();
 }
 
 void Tensor::set_requires_grad(bool enabled) {
@@ -129,82 +233,35 @@ void Tensor::set_requires_grad(bool enabled) {
   if (enabled && !is_floating(dtype_)) {
     throw std::invalid_argument{"Only Float32 and Float64 tensors may require gradients"};
   }
-  if (autograd_ == nullptr) initialize_autograd();
-  autograd_->requires_grad = enabled;
-  if (!enabled) autograd_->leaf_grad.reset();
+  if (grad_state_ == nullptr) initialize_autograd();
+  grad_state_->tracked = enabled;
+  if (!enabled) grad_state_->accumulated.reset();
 }
 
 Tensor Tensor::grad() const {
   if (!is_leaf()) throw std::invalid_argument{"Gradients are retained for leaf tensors only"};
   if (!has_grad()) throw std::logic_error{"Tensor has no accumulated gradient"};
-  return autograd_->leaf_grad->detach();
+  return grad_state_->accumulated->detach();
 }
 
 void Tensor::zero_grad() {
   if (!is_leaf()) throw std::invalid_argument{"zero_grad is supported for leaf tensors only"};
-  if (autograd_ != nullptr) autograd_->leaf_grad.reset();
+  if (grad_state_ != nullptr) grad_state_->accumulated.reset();
 }
 
 void Tensor::backward() {
-  if (!requires_grad()) throw std::invalid_argument{"backward requires a Tensor that tracks gradients"};
+  if (!requires_grad()) {
+    throw std::invalid_argument{"backward requires a Tensor that tracks gradients"};
+  }
   if (numel() != 1) {
-    throw std::invalid_argument{"backward without an explicit gradient requires a one-element Tensor"};
+    throw std::invalid_argument{
+        "backward without an explicit gradient requires a one-element Tensor"};
   }
-  if (!is_floating(dtype_)) throw std::invalid_argument{"backward supports Float32 and Float64 losses only"};
-
-  std::vector<std::shared_ptr<detail::AutogradMeta>> topological_order;
-  std::unordered_set<detail::AutogradMeta*> visited;
-  const auto visit = [&topological_order, &visited](
-                         const auto& self, const std::shared_ptr<detail::AutogradMeta>& meta) -> void {
-    if (meta == nullptr || !meta->requires_grad || !visited.insert(meta.get()).second) return;
-    if (meta->grad_fn != nullptr) {
-      for (const detail::AutogradEdge& parent : meta->grad_fn->parents) self(self, parent.identity);
-    }
-    topological_order.push_back(meta);
-  };
-  visit(visit, autograd_);
-
-  std::unordered_map<detail::AutogradMeta*, Tensor> gradients;
-  gradients.emplace(autograd_.get(), ones(shape_, dtype_, device()));
-
-  for (auto iterator{topological_order.rbegin()}; iterator != topological_order.rend(); ++iterator) {
-    const auto& meta{*iterator};
-    auto gradient_iterator{gradients.find(meta.get())};
-    if (gradient_iterator == gradients.end()) {
-      throw std::logic_error{"Reachable autograd identity did not receive a gradient"};
-    }
-    Tensor gradient{std::move(gradient_iterator->second)};
-    gradients.erase(gradient_iterator);
-
-    if (meta->grad_fn == nullptr) {
-      if (meta->leaf_grad.has_value()) {
-        add_gradient_values(*meta->leaf_grad, gradient, /*in_place=*/true);
-      } else if (detail::AutogradAccess::exclusively_owned(gradient)) {
-        meta->leaf_grad = gradient.detach();
-      } else {
-        meta->leaf_grad = gradient.detach().clone();
-      }
-      continue;
-    }
-
-    auto contributions{meta->grad_fn->backward(gradient)};
-    if (contributions.size() != meta->grad_fn->parents.size()) {
-      throw std::logic_error{"Backward rule returned an incorrect number of gradients"};
-    }
-    gradient = Tensor{Shape{}, dtype_, Device::cpu()};  // release this node's gradient
-    for (std::size_t index{0}; index < contributions.size(); ++index) {
-      const detail::AutogradEdge& parent{meta->grad_fn->parents[index]};
-      validate_contribution(contributions[index], parent);
-      Tensor contribution{contributions[index].detach()};
-      contributions[index] = Tensor{Shape{}, dtype_, Device::cpu()};
-      auto existing{gradients.find(parent.identity.get())};
-      if (existing == gradients.end()) {
-        gradients.emplace(parent.identity.get(), std::move(contribution));
-      } else {
-        add_gradient_values(existing->second, contribution);
-      }
-    }
+  if (!is_floating(dtype_)) {
+    throw std::invalid_argument{"backward supports Float32 and Float64 losses only"};
   }
+  detail::Sweep sweep{grad_state_.get()};
+  sweep.run(grad_state_.get(), ones(shape_, dtype_, device()));
 }
 
 }  // namespace spar

@@ -1,4 +1,12 @@
-// Private autograd graph types (src/autograd/autograd.cpp:13-41).
+// Private autograd and tensor-internals types of the host library.
+//
+// Every Tensor handle carries a shared GradState.  Copies of a handle share
+// it (they are the same autograd identity); detach() and fresh outputs get
+// their own.  An op output that depends on tracked inputs also owns a
+// GradFunction: the inputs' identities with the shape, dtype and device each
+// gradient must have, and the rule that maps the output's gradient to one
+// gradient per input (the reference keeps the same information in its
+// AutogradMeta/AutogradNode/AutogradEdge, src/autograd/autograd.cpp:13-41).
 #pragma once
 
 #include <memory>
@@ -9,48 +17,54 @@
 
 namespace spar::detail {
 
-struct AutogradMeta;
+struct GradState;
 
-struct AutogradEdge final {
-  std::shared_ptr<AutogradMeta> identity;
-  Shape expected_shape;
-  DType expected_dtype;
-  Device expected_device;
+/// One input of a recorded operation.
+struct GradInput final {
+  std::shared_ptr<GradState> identity;
+  Shape shape;
+  DType dtype;
+  Device device;
 };
 
-struct AutogradNode final {
-  std::vector<AutogradEdge> parents;
-  BackwardFunction backward;
+/// A recorded operation: its tracked inputs, in recording order, and the
+/// rule producing one gradient per input.
+struct GradFunction final {
+  std::vector<GradInput> inputs;
+  BackwardFunction rule;
 };
 
-struct AutogradMeta final {
-  bool requires_grad{false};
-  std::shared_ptr<AutogradNode> grad_fn;
-  std::optional<Tensor> leaf_grad;
+struct GradState final {
+  bool tracked{false};
+  /// null for a leaf.
+  std::shared_ptr<GradFunction> producer;
+  /// the leaf's accumulated gradient, once backward() has reached it.
+  std::optional<Tensor> accumulated;
 };
 
-struct AutogradAccess final {
-  [[nodiscard]] static std::shared_ptr<AutogradMeta>& meta(Tensor& tensor) {
-    return tensor.autograd_;
+/// Access to Tensor internals for the engine and the layout helpers.
+struct TensorInternals final {
+  [[nodiscard]] static std::shared_ptr<GradState>& grad_state(Tensor& tensor) {
+    return tensor.grad_state_;
   }
-  [[nodiscard]] static const std::shared_ptr<AutogradMeta>& meta(const Tensor& tensor) {
-    return tensor.autograd_;
+  [[nodiscard]] static const std::shared_ptr<GradState>& grad_state(const Tensor& tensor) {
+    return tensor.grad_state_;
   }
   [[nodiscard]] static const std::shared_ptr<Storage>& storage(const Tensor& tensor) {
     return tensor.storage_;
   }
-  /// host bytes of a contiguous CPU tensor's first element
+  /// host address of a contiguous CPU tensor's first element.
   [[nodiscard]] static std::byte* host_bytes(Tensor& tensor) {
     return tensor.storage_->host_data() + tensor.storage_offset_ * size_of(tensor.dtype_);
   }
   [[nodiscard]] static const std::byte* host_bytes(const Tensor& tensor) {
     return tensor.storage_->host_data() + tensor.storage_offset_ * size_of(tensor.dtype_);
   }
-  /// true when no other Tensor handle shares this tensor's storage and the
-  /// tensor covers the whole allocation contiguously.
-  [[nodiscard]] static bool exclusively_owned(const Tensor& tensor) {
+  /// true when this handle is the only one on its storage and covers all of
+  /// it contiguously, so the engine may add into it in place.
+  [[nodiscard]] static bool sole_owner(const Tensor& tensor) {
     return tensor.storage_ != nullptr && tensor.storage_.use_count() == 1 &&
-           tensor.is_contiguous() && tensor.storage_offset_ == 0 &&
+           tensor.storage_offset_ == 0 && tensor.is_contiguous() &&
            tensor.nbytes_ == tensor.storage_->nbytes();
   }
 };

@@ -55,36 +55,36 @@ Shape::stride_type Shape::checked_extent(dimension_type dimension) {
   return static_cast<stride_type>(dimension);
 }
 
+// Row-major strides: each axis steps over the elements of the axes inside it.
+// The running product is formed over every axis, the outermost included, and
+// reports overflow as the reference does (shape.cpp:61-75).
 std::vector<Shape::stride_type> Shape::contiguous_strides() const {
   std::vector<stride_type> strides(rank());
-  stride_type running{1};
-  for (std::size_t index{rank()}; index > 0; --index) {
-    const std::size_t current{index - 1};
-    strides[current] = running;
-    const auto dimension{checked_extent(dimensions_[current])};
-    if (dimension != 0 && running > std::numeric_limits<stride_type>::max() / dimension) {
+  stride_type inside{1};
+  for (std::size_t axis{rank()}; axis-- > 0;) {
+    strides[axis] = inside;
+    if (__builtin_mul_overflow(inside, checked_extent(dimensions_[axis]), &inside)) {
       throw std::overflow_error{"Shape stride calculation overflow"};
     }
-    running *= dimension;
   }
   return strides;
 }
 
+// Number of elements.  Every extent is validated first (a negative one is an
+// invalid_argument wherever it appears); a zero extent makes the shape empty
+// whatever the other extents are; only a non-empty product can overflow.
 std::size_t Shape::compute_numel(const std::vector<dimension_type>& dimensions) {
-  bool has_zero_extent{false};
+  std::size_t count{1};
+  bool overflowed{false};
+  bool empty{false};
   for (const auto dimension : dimensions) {
-    if (checked_extent(dimension) == 0) has_zero_extent = true;
+    const stride_type extent{checked_extent(dimension)};
+    empty = empty || extent == 0;
+    overflowed = overflowed || (!empty && __builtin_mul_overflow(count, extent, &count));
   }
-  if (has_zero_extent) return 0;
-  std::size_t result{1};
-  for (const auto dimension : dimensions) {
-    const auto value{static_cast<std::size_t>(dimension)};
-    if (result > std::numeric_limits<std::size_t>::max() / value) {
-      throw std::overflow_error{"Shape element count overflow"};
-    }
-    result *= value;
-  }
-  return result;
+  if (empty) return 0;
+  if (overflowed) throw std::overflow_error{"Shape element count overflow"};
+  return count;
 }
 
 Device Device::hip(std::int32_t index) {

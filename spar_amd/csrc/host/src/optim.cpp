@@ -1,10 +1,11 @@
-// Parameters, AdamW and the global gradient norm: the host logic of
-// src/nn/parameter.cpp, src/optim/adamw.cpp and src/training/gradients.cpp
-// with their validation order and messages.  Per-element work runs on the
-// device: spar_hip_launch_adamw, spar_hip_launch_gradient_norm_summary and
-// spar_hip_launch_scale_in_place.  The norm launches every gradient's summary
-// before reading them all back with one copy per device, where the reference
-// synchronises once per gradient (gradients.cpp:119).
+// Parameters, AdamW, the global gradient norm and gradient scaling on HIP
+// tensors.  Names, validation order, messages and exception types are
+// Spar's (src/nn/parameter.cpp, src/optim/adamw.cpp,
+// src/training/gradients.cpp); the per-element work runs in the backend's
+// kernels (spar_hip_launch_adamw, spar_hip_launch_gradient_norm_summary,
+// spar_hip_launch_scale_in_place).  The norm enqueues every gradient's
+// summary before one read-back per device, where the reference synchronises
+// once per gradient (gradients.cpp:119).
 #include "spar/optim.hpp"
 
 #include <algorithm>
@@ -13,15 +14,50 @@
 #include <map>
 #include <stdexcept>
 #include <string>
+#include <unordered_set>
 #include <utility>
 
+#include "autograd_internal.hpp"
 #include "bridge.hpp"
 
 namespace spar {
+namespace {
+
+namespace hip = detail::hip;
+using detail::HipTensorAccess;
+
+// The autograd identity a Parameter and all its copies share.
+const void* identity_of(const nn::Parameter& parameter) {
+  return detail::TensorInternals::grad_state(parameter.tensor()).get();
+}
+
+// Parameters in first-occurrence order, each identity once, filtered by
+// `keep`.  A hash set of identities replaces the pairwise identity scan.
+template <typename Keep>
+std::vector<nn::Parameter*> distinct(std::span<nn::Parameter> parameters, Keep keep) {
+  std::vector<nn::Parameter*> result;
+  std::unordered_set<const void*> seen;
+  for (nn::Parameter& parameter : parameters) {
+    if (keep(parameter) && seen.insert(identity_of(parameter)).second) {
+      result.push_back(&parameter);
+    }
+  }
+  return result;
+}
+
+bool active(const nn::Parameter& parameter) {
+  return parameter.requires_grad() && parameter.has_grad();
+}
+
+bool matches(const Tensor& tensor, const Tensor& model) {
+  return tensor.shape() == model.shape() && tensor.dtype() == model.dtype() &&
+         tensor.device() == model.device();
+}
+
+}  // namespace
 
 namespace nn {
 
-// parameter.cpp:11-16
 Parameter::Parameter(Tensor initial_value) : tensor_{initial_value.detach().clone()} {
   if (!is_floating(tensor_.dtype())) {
     throw std::invalid_argument{"Parameter requires a floating-point Tensor"};
@@ -30,7 +66,6 @@ Parameter::Parameter(Tensor initial_value) : tensor_{initial_value.detach().clon
 }
 
 const Tensor& Parameter::tensor() const noexcept { return tensor_; }
-
 bool Parameter::requires_grad() const noexcept { return tensor_.requires_grad(); }
 
 bool Parameter::shares_identity_with(const Parameter& other) const noexcept {
@@ -38,75 +73,82 @@ bool Parameter::shares_identity_with(const Parameter& other) const noexcept {
 }
 
 void Parameter::set_requires_grad(bool enabled) { tensor_.set_requires_grad(enabled); }
-
 bool Parameter::has_grad() const noexcept { return tensor_.has_grad(); }
-
 Tensor Parameter::grad() const { return tensor_.grad(); }
-
 void Parameter::zero_grad() { tensor_.zero_grad(); }
-
 Parameter Parameter::clone() const { return Parameter{tensor_}; }
+
+void move_to(Parameter& parameter, Device target) {
+  move_to(std::span<Parameter>{&parameter, 1}, target);
+}
+
+// Two phases: every copy is made first (a failure leaves all Parameters as
+// they were), then each Parameter's Storage takes the copy's payload, which
+// cannot fail.  Tensor, autograd and Storage objects keep their identity.
+void move_to(std::span<Parameter> parameters, Device target) {
+  const auto movers{distinct(parameters, [target](const Parameter& parameter) {
+    return parameter.tensor_.device() != target;
+  })};
+  for (const Parameter* parameter : movers) {
+    if (parameter->has_grad()) {
+      throw std::logic_error{"Parameter Device migration requires clearing its live gradient first"};
+    }
+  }
+  std::vector<Tensor> copies;
+  copies.reserve(movers.size());
+  for (const Parameter* parameter : movers) copies.push_back(parameter->tensor_.detach().to(target));
+  for (std::size_t k{0}; k < movers.size(); ++k) {
+    detail::swap_storage_payloads(movers[k]->tensor_, copies[k]);
+  }
+}
 
 }  // namespace nn
 
 namespace training {
 namespace {
 
-namespace hip = detail::hip;
-using detail::HipTensorAccess;
-
-// gradients.cpp:14-26
-std::vector<nn::Parameter*> unique_active_parameters(std::span<nn::Parameter> parameters) {
-  std::vector<nn::Parameter*> unique;
-  unique.reserve(parameters.size());
-  for (nn::Parameter& parameter : parameters) {
-    const bool duplicate{std::any_of(unique.begin(), unique.end(),
-                                     [&parameter](const nn::Parameter* existing) {
-                                       return existing->shares_identity_with(parameter);
-                                     })};
-    if (!duplicate && parameter.requires_grad() && parameter.has_grad()) {
-      unique.push_back(&parameter);
-    }
-  }
-  return unique;
-}
-
-// The combining half of StableSumSquares (gradients.cpp:57-88); the element
-// half runs on the device and arrives as summaries.
-struct SumSquares final {
+// The running value of Spar's StableSumSquares (gradients.cpp:28-88) over
+// whole gradients: every element arrives from the device already folded
+// into a per-gradient summary, and summaries merge in Parameter order.
+struct NormTotal final {
   double scale{0.0};
   double scaled_sum_squares{1.0};
   bool has_infinity{false};
   bool has_nan{false};
-
-  void combine(const SparHipNormSummary& other) noexcept {
-    has_nan = has_nan || other.has_nan != 0;
-    has_infinity = has_infinity || other.has_infinity != 0;
-    if (other.scale == 0.0) return;
-    if (scale == 0.0) {
-      scale = other.scale;
-      scaled_sum_squares = other.scaled_sum_squares;
-      return;
-    }
-    if (scale < other.scale) {
-      const double ratio{scale / other.scale};
-      scaled_sum_squares = other.scaled_sum_squares + scaled_sum_squares * ratio * ratio;
-      scale = other.scale;
-    } else {
-      const double ratio{other.scale / scale};
-      scaled_sum_squares += other.scaled_sum_squares * ratio * ratio;
-    }
-  }
-
-  [[nodiscard]] double norm() const noexcept {
-    if (has_nan) return std::numeric_limits<double>::quiet_NaN();
-    if (has_infinity) return std::numeric_limits<double>::infinity();
-    return scale == 0.0 ? 0.0 : scale * std::sqrt(scaled_sum_squares);
-  }
 };
 
-// gradients.cpp:108-118 and :145-155: the checks on an active gradient.
-Tensor checked_gradient(const nn::Parameter& parameter, const char* operation) {
+// Merges a summary into the total.  The summary with the larger scale (the
+// total on a tie) keeps its sum; the other's sum is rescaled by the square
+// of the ratio of scales before the addition: big + (small * r) * r.
+void merge(NormTotal& total, const SparHipNormSummary& summary) {
+  total.has_nan = total.has_nan || summary.has_nan != 0;
+  total.has_infinity = total.has_infinity || summary.has_infinity != 0;
+  if (summary.scale == 0.0) return;
+  if (total.scale == 0.0) {
+    total.scale = summary.scale;
+    total.scaled_sum_squares = summary.scaled_sum_squares;
+    return;
+  }
+  const bool summary_larger{total.scale < summary.scale};
+  const double big_scale{summary_larger ? summary.scale : total.scale};
+  const double big_sum{summary_larger ? summary.scaled_sum_squares : total.scaled_sum_squares};
+  const double small_scale{summary_larger ? total.scale : summary.scale};
+  const double small_sum{summary_larger ? total.scaled_sum_squares : summary.scaled_sum_squares};
+  const double ratio{small_scale / big_scale};
+  total.scale = big_scale;
+  total.scaled_sum_squares = big_sum + small_sum * ratio * ratio;
+}
+
+double norm_of(const NormTotal& total) {
+  if (total.has_nan) return std::numeric_limits<double>::quiet_NaN();
+  if (total.has_infinity) return std::numeric_limits<double>::infinity();
+  if (total.scale == 0.0) return 0.0;
+  return total.scale * std::sqrt(total.scaled_sum_squares);
+}
+
+// An active Parameter's gradient after the reference's checks
+// (gradients.cpp:108-118, :145-155).
+Tensor checked_gradient(const nn::Parameter& parameter, std::string_view operation) {
   Tensor gradient{parameter.grad()};
   if (gradient.device() != parameter.tensor().device()) {
     throw std::logic_error{"Active Parameter gradient Device mismatch"};
@@ -121,64 +163,76 @@ Tensor checked_gradient(const nn::Parameter& parameter, const char* operation) {
   return gradient;
 }
 
-// Device buffer of `count` summaries, returned to the allocator on exit.
-class SummaryBuffer final {
+std::vector<Tensor> checked_gradients(std::span<nn::Parameter> parameters,
+                                      std::string_view operation) {
+  std::vector<Tensor> gradients;
+  for (const nn::Parameter* parameter : distinct(parameters, active)) {
+    gradients.push_back(checked_gradient(*parameter, operation));
+  }
+  return gradients;
+}
+
+// Device memory for the summaries, returned to the allocator on scope exit.
+class SummarySlots final {
  public:
-  SummaryBuffer(std::size_t count, int device) : device_{device} {
-    hip::check(spar_hip_allocate(&pointer_, count * sizeof(SparHipNormSummary), device),
+  SummarySlots(std::size_t count, int device) : device_{device} {
+    hip::check(spar_hip_allocate(&block_, count * sizeof(SparHipNormSummary), device),
                "global gradient norm", device);
   }
-  SummaryBuffer(const SummaryBuffer&) = delete;
-  SummaryBuffer& operator=(const SummaryBuffer&) = delete;
-  ~SummaryBuffer() { static_cast<void>(spar_hip_deallocate(pointer_, device_)); }
-
-  [[nodiscard]] SparHipNormSummary* data() const {
-    return static_cast<SparHipNormSummary*>(pointer_);
+  SummarySlots(const SummarySlots&) = delete;
+  SummarySlots& operator=(const SummarySlots&) = delete;
+  ~SummarySlots() { static_cast<void>(spar_hip_deallocate(block_, device_)); }
+  [[nodiscard]] SparHipNormSummary* at(std::size_t k) const {
+    return static_cast<SparHipNormSummary*>(block_) + k;
   }
 
  private:
-  void* pointer_{nullptr};
+  void* block_{nullptr};
   int device_;
 };
+
+// Summaries of the given gradients (all on `device`), computed into one
+// device array and read back with one copy.
+std::vector<SparHipNormSummary> device_summaries(const std::vector<const Tensor*>& gradients,
+                                                 int device) {
+  const SummarySlots slots{gradients.size(), device};
+  for (std::size_t k{0}; k < gradients.size(); ++k) {
+    const Tensor& gradient{*gradients[k]};
+    hip::check(spar_hip_launch_gradient_norm_summary(slots.at(k), HipTensorAccess::data(gradient),
+                                                     gradient.numel(),
+                                                     hip::dtype_tag(gradient.dtype()), device),
+               "global gradient norm", device);
+  }
+  std::vector<SparHipNormSummary> host(gradients.size());
+  hip::check(spar_hip_copy_device_to_host(host.data(), slots.at(0),
+                                          host.size() * sizeof(SparHipNormSummary), device),
+             "global gradient norm", device);
+  return host;
+}
 
 }  // namespace
 
 double global_grad_norm(std::span<nn::Parameter> parameters) {
-  std::vector<Tensor> gradients;
-  for (const nn::Parameter* parameter : unique_active_parameters(parameters)) {
-    gradients.push_back(checked_gradient(*parameter, "global gradient norm"));
-  }
+  const std::vector<Tensor> gradients{checked_gradients(parameters, "global gradient norm")};
   std::map<int, std::vector<std::size_t>> by_device;
-  for (std::size_t index{0}; index < gradients.size(); ++index) {
-    by_device[gradients[index].device().index()].push_back(index);
+  for (std::size_t k{0}; k < gradients.size(); ++k) {
+    by_device[gradients[k].device().index()].push_back(k);
   }
   std::vector<SparHipNormSummary> summaries(gradients.size());
-  for (const auto& [device, indices] : by_device) {
-    SummaryBuffer buffer{indices.size(), device};
-    for (std::size_t slot{0}; slot < indices.size(); ++slot) {
-      const Tensor& gradient{gradients[indices[slot]]};
-      hip::check(spar_hip_launch_gradient_norm_summary(
-                     buffer.data() + slot, HipTensorAccess::data(gradient), gradient.numel(),
-                     hip::dtype_tag(gradient.dtype()), device),
-                 "global gradient norm", device);
-    }
-    std::vector<SparHipNormSummary> host(indices.size());
-    hip::check(spar_hip_copy_device_to_host(host.data(), buffer.data(),
-                                            host.size() * sizeof(SparHipNormSummary), device),
-               "global gradient norm", device);
-    for (std::size_t slot{0}; slot < indices.size(); ++slot) summaries[indices[slot]] = host[slot];
+  for (const auto& [device, members] : by_device) {
+    std::vector<const Tensor*> group;
+    for (const std::size_t k : members) group.push_back(&gradients[k]);
+    const auto results{device_summaries(group, device)};
+    for (std::size_t j{0}; j < members.size(); ++j) summaries[members[j]] = results[j];
   }
-  SumSquares accumulator;
-  for (const SparHipNormSummary& summary : summaries) accumulator.combine(summary);
-  return accumulator.norm();
+  NormTotal total;
+  for (const SparHipNormSummary& summary : summaries) merge(total, summary);
+  return norm_of(total);
 }
 
 void scale_gradients(std::span<nn::Parameter> parameters, double factor) {
   if (!std::isfinite(factor)) throw std::invalid_argument{"Gradient scale factor must be finite"};
-  std::vector<Tensor> gradients;
-  for (const nn::Parameter* parameter : unique_active_parameters(parameters)) {
-    gradients.push_back(checked_gradient(*parameter, "gradient scaling"));
-  }
+  std::vector<Tensor> gradients{checked_gradients(parameters, "gradient scaling")};
   for (Tensor& gradient : gradients) {
     hip::check(spar_hip_launch_scale_in_place(HipTensorAccess::mutable_data(gradient),
                                               gradient.numel(), hip::dtype_tag(gradient.dtype()),
@@ -187,19 +241,20 @@ void scale_gradients(std::span<nn::Parameter> parameters, double factor) {
   }
 }
 
-// gradients.cpp:176-190
 ClipGradNormResult clip_grad_norm(std::span<nn::Parameter> parameters, double max_norm) {
   if (!std::isfinite(max_norm) || max_norm < 0.0) {
     throw std::invalid_argument{"Maximum gradient norm must be finite and nonnegative"};
   }
-  const double total_norm{global_grad_norm(parameters)};
-  if (!std::isfinite(total_norm)) throw std::runtime_error{"Cannot clip nonfinite gradients"};
-  if (total_norm == 0.0 || total_norm <= max_norm) {
-    return {.total_norm = total_norm, .scale = 1.0, .clipped = false};
+  ClipGradNormResult result{global_grad_norm(parameters), 1.0, false};
+  if (!std::isfinite(result.total_norm)) {
+    throw std::runtime_error{"Cannot clip nonfinite gradients"};
   }
-  const double scale{max_norm / total_norm};
-  scale_gradients(parameters, scale);
-  return {.total_norm = total_norm, .scale = scale, .clipped = true};
+  if (result.total_norm > max_norm) {  // a zero norm never exceeds max_norm >= 0
+    result.scale = max_norm / result.total_norm;
+    result.clipped = true;
+    scale_gradients(parameters, result.scale);
+  }
+  return result;
 }
 
 }  // namespace training
@@ -207,25 +262,21 @@ ClipGradNormResult clip_grad_norm(std::span<nn::Parameter> parameters, double ma
 namespace optim {
 namespace {
 
-namespace hip = detail::hip;
-using detail::HipTensorAccess;
-
-// adamw.cpp:14-35
-void validate_learning_rate(double learning_rate) {
-  if (!std::isfinite(learning_rate) || learning_rate < 0.0) {
+void check_learning_rate(double value) {
+  if (!std::isfinite(value) || value < 0.0) {
     throw std::invalid_argument{"AdamW learning_rate must be finite and nonnegative"};
   }
 }
 
-void validate_hyperparameters(double learning_rate, double beta1, double beta2, double epsilon,
-                              double weight_decay) {
-  validate_learning_rate(learning_rate);
-  if (!std::isfinite(beta1) || beta1 < 0.0 || beta1 >= 1.0) {
-    throw std::invalid_argument{"AdamW beta1 must be finite and in [0,1)"};
-  }
-  if (!std::isfinite(beta2) || beta2 < 0.0 || beta2 >= 1.0) {
-    throw std::invalid_argument{"AdamW beta2 must be finite and in [0,1)"};
-  }
+// The hyperparameter rules of adamw.cpp:14-35, in their order.
+void check_hyperparameters(double learning_rate, double beta1, double beta2, double epsilon,
+                           double weight_decay) {
+  check_learning_rate(learning_rate);
+  const auto unit_interval = [](double beta) {
+    return std::isfinite(beta) && beta >= 0.0 && beta < 1.0;
+  };
+  if (!unit_interval(beta1)) throw std::invalid_argument{"AdamW beta1 must be finite and in [0,1)"};
+  if (!unit_interval(beta2)) throw std::invalid_argument{"AdamW beta2 must be finite and in [0,1)"};
   if (!std::isfinite(epsilon) || epsilon <= 0.0) {
     throw std::invalid_argument{"AdamW epsilon must be finite and positive"};
   }
@@ -234,99 +285,114 @@ void validate_hyperparameters(double learning_rate, double beta1, double beta2, 
   }
 }
 
-bool same_layout(const Tensor& tensor, const Tensor& reference) {
-  return tensor.shape() == reference.shape() && tensor.dtype() == reference.dtype() &&
-         tensor.device() == reference.device();
-}
-
 }  // namespace
 
 AdamW::AdamW(std::vector<nn::Parameter> parameters, double learning_rate, double beta1,
              double beta2, double epsilon, double weight_decay)
-    : learning_rate_{learning_rate},
-      beta1_{beta1},
-      beta2_{beta2},
-      epsilon_{epsilon},
+    : learning_rate_{learning_rate}, beta1_{beta1}, beta2_{beta2}, epsilon_{epsilon},
       weight_decay_{weight_decay} {
-  validate_hyperparameters(learning_rate, beta1, beta2, epsilon, weight_decay);
-  entries_.reserve(parameters.size());
-  for (auto& parameter : parameters) {
-    const bool duplicate{std::any_of(entries_.begin(), entries_.end(),
-                                     [&parameter](const Entry& entry) {
-                                       return entry.parameter.shares_identity_with(parameter);
-                                     })};
-    if (!duplicate) entries_.push_back(Entry{std::move(parameter), std::nullopt});
+  check_hyperparameters(learning_rate, beta1, beta2, epsilon, weight_decay);
+  for (nn::Parameter* parameter :
+       distinct(std::span<nn::Parameter>{parameters}, [](const nn::Parameter&) { return true; })) {
+    entries_.push_back(Entry{std::move(*parameter), std::nullopt});
   }
 }
 
-// adamw.cpp:83-170: validate every active entry, stage new states, then
-// update each Parameter with one kernel.
+const AdamW::Entry* AdamW::entry_of(const nn::Parameter& parameter) const noexcept {
+  const void* identity{identity_of(parameter)};
+  if (identity == nullptr) return nullptr;
+  const auto found{std::find_if(entries_.begin(), entries_.end(), [identity](const Entry& entry) {
+    return identity_of(entry.parameter) == identity;
+  })};
+  return found == entries_.end() ? nullptr : &*found;
+}
+
+// adamw.cpp:85-124: an entry steps when its Parameter requires a gradient
+// and holds one; its gradient, state and placement are checked first.
+bool AdamW::steps(const Entry& entry) {
+  const nn::Parameter& parameter{entry.parameter};
+  if (!active(parameter)) return false;
+  const Tensor& value{parameter.tensor()};
+  const Tensor gradient{parameter.grad()};
+  if (!matches(gradient, value)) {
+    throw std::logic_error{"AdamW gradient shape, dtype, or Device does not match its Parameter"};
+  }
+  if (!is_floating(value.dtype())) {
+    throw std::logic_error{"AdamW encountered a non-floating Parameter"};
+  }
+  if (!value.is_contiguous() || !gradient.is_contiguous()) {
+    throw std::logic_error{"AdamW requires contiguous Parameters and gradients"};
+  }
+  if (const auto& state{entry.state}) {
+    for (const Tensor* moment : {&state->first_moment, &state->second_moment}) {
+      if (!matches(*moment, value) || !moment->is_contiguous()) {
+        throw std::logic_error{"AdamW state shape, dtype, or Device does not match its Parameter"};
+      }
+    }
+    if (state->step == 0) throw std::logic_error{"AdamW initialized state has an invalid zero step"};
+    if (state->step == std::numeric_limits<std::uint64_t>::max()) {
+      throw std::overflow_error{"AdamW per-Parameter step counter overflow"};
+    }
+  }
+  detail::require_hip(value, "AdamW update");
+  return true;
+}
+
+void AdamW::update(Entry& entry) const {
+  State& state{*entry.state};
+  ++state.step;
+  Tensor value{entry.parameter.tensor().detach()};
+  const Tensor gradient{entry.parameter.grad()};
+  // Bias corrections computed on the host, as the reference's device path
+  // does (cuda_ops.cppm:675-676).
+  const auto correction = [step = static_cast<double>(state.step)](double beta) {
+    return 1.0 - std::pow(beta, step);
+  };
+  hip::check(spar_hip_launch_adamw(HipTensorAccess::mutable_data(value),
+                                   HipTensorAccess::data(gradient),
+                                   HipTensorAccess::mutable_data(state.first_moment),
+                                   HipTensorAccess::mutable_data(state.second_moment),
+                                   value.numel(), hip::dtype_tag(value.dtype()), learning_rate_,
+                                   beta1_, beta2_, epsilon_, weight_decay_, correction(beta1_),
+                                   correction(beta2_), value.device().index()),
+             "AdamW update", value.device());
+}
+
+// Every stepping entry is validated before anything changes, and the zero
+// moments of first steps are all allocated before any is installed.
 void AdamW::step() {
-  std::vector<std::size_t> active;
-  active.reserve(entries_.size());
-  for (std::size_t index{0}; index < entries_.size(); ++index) {
-    const Entry& entry{entries_[index]};
-    const nn::Parameter& parameter{entry.parameter};
-    if (!parameter.requires_grad() || !parameter.has_grad()) continue;
-    const Tensor gradient{parameter.grad()};
-    if (!same_layout(gradient, parameter.tensor())) {
-      throw std::logic_error{"AdamW gradient shape, dtype, or Device does not match its Parameter"};
-    }
-    if (!is_floating(parameter.tensor().dtype())) {
-      throw std::logic_error{"AdamW encountered a non-floating Parameter"};
-    }
-    if (!parameter.tensor().is_contiguous() || !gradient.is_contiguous()) {
-      throw std::logic_error{"AdamW requires contiguous Parameters and gradients"};
-    }
-    if (entry.state) {
-      const State& state{*entry.state};
-      for (const Tensor* moment : {&state.first_moment, &state.second_moment}) {
-        if (!same_layout(*moment, parameter.tensor()) || !moment->is_contiguous()) {
-          throw std::logic_error{"AdamW state shape, dtype, or Device does not match its Parameter"};
-        }
-      }
-      if (state.step == 0) throw std::logic_error{"AdamW initialized state has an invalid zero step"};
-      if (state.step == std::numeric_limits<std::uint64_t>::max()) {
-        throw std::overflow_error{"AdamW per-Parameter step counter overflow"};
-      }
-    }
-    detail::require_hip(parameter.tensor(), "AdamW update");
-    active.push_back(index);
+  std::vector<Entry*> stepping;
+  for (Entry& entry : entries_) {
+    if (steps(entry)) stepping.push_back(&entry);
   }
+  std::vector<std::pair<Entry*, State>> first_states;
+  for (Entry* entry : stepping) {
+    if (entry->state) continue;
+    const Tensor& value{entry->parameter.tensor()};
+    first_states.emplace_back(entry, State{zeros(value.shape(), value.dtype(), value.device()),
+                                           zeros(value.shape(), value.dtype(), value.device()),
+                                           0});
+  }
+  for (auto& [entry, state] : first_states) entry->state.emplace(std::move(state));
+  for (Entry* entry : stepping) update(*entry);
+}
 
-  std::vector<std::optional<std::pair<Tensor, Tensor>>> staged(entries_.size());
-  for (const std::size_t index : active) {
-    const Tensor& value{entries_[index].parameter.tensor()};
-    if (!entries_[index].state) {
-      staged[index].emplace(zeros(value.shape(), value.dtype(), value.device()),
-                            zeros(value.shape(), value.dtype(), value.device()));
+void AdamW::move_to(Device target) {
+  std::vector<std::optional<std::pair<Tensor, Tensor>>> moved(entries_.size());
+  for (std::size_t k{0}; k < entries_.size(); ++k) {
+    if (const auto& state{entries_[k].state}) {
+      moved[k].emplace(state->first_moment.to(target), state->second_moment.to(target));
     }
   }
-  for (const std::size_t index : active) {
-    if (staged[index]) {
-      entries_[index].state.emplace(State{std::move(staged[index]->first),
-                                          std::move(staged[index]->second), 0});
+  std::vector<nn::Parameter> tracked;
+  tracked.reserve(entries_.size());
+  for (const Entry& entry : entries_) tracked.push_back(entry.parameter);
+  nn::move_to(std::span<nn::Parameter>{tracked}, target);
+  for (std::size_t k{0}; k < entries_.size(); ++k) {
+    if (moved[k]) {
+      entries_[k].state->first_moment = std::move(moved[k]->first);
+      entries_[k].state->second_moment = std::move(moved[k]->second);
     }
-  }
-
-  for (const std::size_t index : active) {
-    Entry& entry{entries_[index]};
-    const Tensor gradient{entry.parameter.grad()};
-    State& state{*entry.state};
-    ++state.step;
-    Tensor values{entry.parameter.tensor().detach()};
-    // cuda_ops.cppm:675-676: bias corrections on the host.
-    const double first_correction{1.0 - std::pow(beta1_, static_cast<double>(state.step))};
-    const double second_correction{1.0 - std::pow(beta2_, static_cast<double>(state.step))};
-    hip::check(spar_hip_launch_adamw(HipTensorAccess::mutable_data(values),
-                                     HipTensorAccess::data(gradient),
-                                     HipTensorAccess::mutable_data(state.first_moment),
-                                     HipTensorAccess::mutable_data(state.second_moment),
-                                     values.numel(), hip::dtype_tag(values.dtype()),
-                                     learning_rate_, beta1_, beta2_, epsilon_, weight_decay_,
-                                     first_correction, second_correction,
-                                     values.device().index()),
-               "AdamW update", values.device());
   }
 }
 
@@ -338,7 +404,7 @@ std::size_t AdamW::parameter_count() const noexcept { return entries_.size(); }
 double AdamW::learning_rate() const noexcept { return learning_rate_; }
 
 void AdamW::set_learning_rate(double learning_rate) {
-  validate_learning_rate(learning_rate);
+  check_learning_rate(learning_rate);
   learning_rate_ = learning_rate;
 }
 
@@ -348,49 +414,37 @@ double AdamW::epsilon() const noexcept { return epsilon_; }
 double AdamW::weight_decay() const noexcept { return weight_decay_; }
 
 bool AdamW::tracks(const nn::Parameter& parameter) const noexcept {
-  return std::any_of(entries_.begin(), entries_.end(), [&parameter](const Entry& entry) {
-    return entry.parameter.shares_identity_with(parameter);
-  });
+  return entry_of(parameter) != nullptr;
 }
 
-// adamw.cpp:230-243
 std::optional<AdamWParameterState> AdamW::parameter_state(const nn::Parameter& parameter) const {
-  const auto iterator{std::find_if(entries_.begin(), entries_.end(), [&parameter](const Entry& entry) {
-    return entry.parameter.shares_identity_with(parameter);
-  })};
-  if (iterator == entries_.end()) {
-    throw std::invalid_argument{"AdamW does not track the requested Parameter"};
-  }
-  if (!iterator->state) return std::nullopt;
-  return AdamWParameterState{iterator->state->first_moment.detach().clone(),
-                             iterator->state->second_moment.detach().clone(),
-                             iterator->state->step};
+  const Entry* entry{entry_of(parameter)};
+  if (entry == nullptr) throw std::invalid_argument{"AdamW does not track the requested Parameter"};
+  if (!entry->state) return std::nullopt;
+  const State& state{*entry->state};
+  return AdamWParameterState{state.first_moment.detach().clone(),
+                             state.second_moment.detach().clone(), state.step};
 }
 
-// adamw.cpp:245-272
 void AdamW::set_parameter_state(const nn::Parameter& parameter,
                                 std::optional<AdamWParameterState> state) {
-  const auto iterator{std::find_if(entries_.begin(), entries_.end(), [&parameter](const Entry& entry) {
-    return entry.parameter.shares_identity_with(parameter);
-  })};
-  if (iterator == entries_.end()) {
-    throw std::invalid_argument{"AdamW does not track the requested Parameter"};
-  }
+  Entry* entry{const_cast<Entry*>(entry_of(parameter))};
+  if (entry == nullptr) throw std::invalid_argument{"AdamW does not track the requested Parameter"};
   if (!state) {
-    iterator->state.reset();
+    entry->state.reset();
     return;
   }
   if (state->step == 0) throw std::invalid_argument{"AdamW restored state step must be at least one"};
   for (const Tensor* moment : {&state->first_moment, &state->second_moment}) {
-    if (!same_layout(*moment, parameter.tensor())) {
+    if (!matches(*moment, parameter.tensor())) {
       throw std::invalid_argument{"AdamW restored moment shape, dtype, or Device mismatch"};
     }
     if (!is_floating(moment->dtype())) {
       throw std::invalid_argument{"AdamW restored moments must be floating point"};
     }
   }
-  iterator->state.emplace(State{state->first_moment.detach().clone(),
-                                state->second_moment.detach().clone(), state->step});
+  entry->state.emplace(State{state->first_moment.detach().clone(),
+                             state->second_moment.detach().clone(), state->step});
 }
 
 }  // namespace optim

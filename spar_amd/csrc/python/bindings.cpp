@@ -262,6 +262,12 @@ PYBIND11_MODULE(_spar, m) {
       .def("grad", &spar::nn::Parameter::grad)
       .def("zero_grad", &spar::nn::Parameter::zero_grad)
       .def("clone", &spar::nn::Parameter::clone);
+  // Parameter copies share their Tensor and Storage, so moving the copies
+  // in this list moves the caller's Parameters.
+  nn.def("move_to", [](std::vector<spar::nn::Parameter> parameters, Device target) {
+    py::gil_scoped_release release;
+    spar::nn::move_to(std::span<spar::nn::Parameter>{parameters}, target);
+  }, py::arg("parameters"), py::arg("target"));
   auto training = m.def_submodule("training", "spar::training (src/training/gradients.cppm)");
   py::class_<spar::training::ClipGradNormResult>(training, "ClipGradNormResult")
       .def_readonly("total_norm", &spar::training::ClipGradNormResult::total_norm)
@@ -295,6 +301,8 @@ PYBIND11_MODULE(_spar, m) {
            py::arg("epsilon") = 1.0e-8, py::arg("weight_decay") = 0.01)
       .def("step", &spar::optim::AdamW::step, py::call_guard<py::gil_scoped_release>())
       .def("zero_grad", &spar::optim::AdamW::zero_grad)
+      .def("move_to", &spar::optim::AdamW::move_to, py::arg("target"),
+           py::call_guard<py::gil_scoped_release>())
       .def("parameter_count", &spar::optim::AdamW::parameter_count)
       .def("learning_rate", &spar::optim::AdamW::learning_rate)
       .def("set_learning_rate", &spar::optim::AdamW::set_learning_rate, py::arg("learning_rate"))

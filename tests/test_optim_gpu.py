@@ -358,6 +358,86 @@ def test_clip_rejects_nonfinite_before_scaling(sp):
     assert math.isnan(sp.training.global_grad_norm(params))
 
 
+def test_parameter_move_to_keeps_identity(sp):
+    """nn.move_to (parameter.cpp:54-87): values move between the host and
+    hip:0 in place; aliases, earlier Tensor handles and the autograd identity
+    follow; a live gradient refuses the move and changes nothing."""
+    rng = np.random.default_rng(108)
+    cpu, device = sp.Device.cpu(), sp.Device.hip(0)
+    values = rng.standard_normal((33, 5)).astype(F32)
+    p = sp.nn.Parameter(sp.Tensor.from_numpy(values))
+    tracked = sp.optim.AdamW([p])  # holds a C++ copy of the Parameter
+    handle = p.tensor()
+    assert handle.device == cpu
+    sp.nn.move_to([p, p], device)  # duplicates move once
+    assert p.tensor().device == device and handle.device == device
+    assert tracked.tracks(p)
+    assert_bitexact(host(sp, p.tensor()), values, "values after the move")
+    w = rng.standard_normal((33, 5)).astype(F32)
+    sp.sum(sp.multiply(p.tensor(), sp.Tensor.from_numpy(w).to(device))).backward()
+    assert p.has_grad()
+    with pytest.raises(sp.LogicError, match="live gradient"):
+        sp.nn.move_to([p], cpu)
+    assert p.tensor().device == device  # unchanged by the refused move
+    assert_bitexact(host(sp, p.grad()), w, "gradient after the refused move")
+    p.zero_grad()
+    sp.nn.move_to([p], cpu)
+    assert p.tensor().device == cpu and handle.device == cpu
+    assert_bitexact(p.tensor().numpy(), values, "values back on the host")
+    sp.nn.move_to([p], cpu)  # already there: nothing to do
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+def test_adamw_move_to_round_trip_is_bitexact(sp, dtype):
+    """AdamW.move_to: moments and Parameters go to the host and back; the
+    steps after the round trip equal those of an optimizer that never moved."""
+    rng = np.random.default_rng(109)
+    cpu, device = sp.Device.cpu(), sp.Device.hip(0)
+    shapes = [(40, 7), (129,)]
+    arrays = [rng.standard_normal(s).astype(dtype) for s in shapes]
+    grads = [[rng.standard_normal(s).astype(dtype) for s in shapes] for _ in range(3)]
+
+    def run(move):
+        params = [sp.nn.Parameter(sp.Tensor.from_numpy(a).to(device)) for a in arrays]
+        opt = sp.optim.AdamW(params, learning_rate=3e-3, weight_decay=0.1)
+        for step in range(3):
+            for param, g in zip(params, grads[step]):
+                param.zero_grad()
+                sp.sum(sp.multiply(param.tensor(), sp.Tensor.from_numpy(g).to(device))).backward()
+            opt.step()
+            if move and step == 1:
+                opt.zero_grad()
+                opt.move_to(cpu)
+                for param in params:
+                    assert param.tensor().device == cpu
+                    state = opt.parameter_state(param)
+                    assert state.first_moment.device == cpu and state.second_moment.device == cpu
+                opt.move_to(device)
+        return [host(sp, p.tensor()) for p in params], [opt.parameter_state(p) for p in params]
+
+    moved, moved_states = run(True)
+    still, still_states = run(False)
+    for k in range(len(shapes)):
+        assert_bitexact(moved[k], still[k], f"parameter {k}")
+        assert moved_states[k].step == still_states[k].step == 3
+        assert_bitexact(host(sp, moved_states[k].first_moment), host(sp, still_states[k].first_moment),
+                        f"first moment {k}")
+        assert_bitexact(host(sp, moved_states[k].second_moment),
+                        host(sp, still_states[k].second_moment), f"second moment {k}")
+
+
+def test_adamw_move_to_refused_with_gradients(sp):
+    device = sp.Device.hip(0)
+    p = sp.nn.Parameter(sp.Tensor.from_numpy(np.ones(6, F32)).to(device))
+    opt = sp.optim.AdamW([p])
+    sp.sum(sp.multiply(p.tensor(), p.tensor())).backward()
+    opt.step()
+    with pytest.raises(sp.LogicError, match="live gradient"):
+        opt.move_to(sp.Device.cpu())
+    state = opt.parameter_state(p)
+    assert state.first_moment.device == device  # nothing committed
+
+
 def test_adamw_full_size_step(hip):
     """One AdamW step over GPT-2 small's 124,439,808 fp32 parameters, bit-exact,
     and the gradient norm over the same gradient within red(N)."""
