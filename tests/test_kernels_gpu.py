@@ -463,6 +463,46 @@ def test_max_argmax_nan_rescan(hip, dtype, shape, axes):
     assert_bitexact(axis_reduce(hip, x, x, axes, "argmax", dtype), am, f"nan rescan argmax {shape}")
 
 
+STRIP_CASES = [
+    # (dtype, base shape, view slices, reduced axes): max/argmax over a
+    # contiguous kept axis wide enough for one 128-byte strip per CU
+    (F32, (1000, 8192), None, [0]),
+    (F32, (300, 8200), None, [0]),                                 # partial last strip
+    (F64, (600, 4096), None, [0]),
+    (F32, (2, 300, 8192), None, [1]),                              # two outer indices
+    (F32, (400, 8208), (slice(3, 397), slice(8, 8200)), [0]),      # offset, padded rows
+]
+
+
+@pytest.mark.parametrize("case", range(len(STRIP_CASES)))
+def test_max_argmax_column_strips(hip, case):
+    """The one-pass strip kernel: lanes scan rows 32 apart, so ties, signed
+    zeros, -inf columns and NaNs (first one wins) must resolve across lanes;
+    a NaN in the tail rows and NaNs in several lanes of one column force the
+    exact rescan."""
+    dtype, shape, window, axes = STRIP_CASES[case]
+    size = int(np.prod(shape))
+    base = (np.round(inputs(34 + case, size, dtype, with_specials=False) * 4) / 4).astype(dtype)
+    base = base.reshape(shape)
+    view = base if window is None else base[window]
+    flat = view if view.ndim == 2 else view[1]  # a view into base: writes reach it
+    n = flat.shape[0]
+    flat[:, 7] = -0.0
+    flat[33, 7] = 0.0            # +0 in another lane after -0: -0 at row 0 wins
+    flat[:, 8] = -np.inf         # all -inf: row 0
+    flat[2, 9] = np.inf
+    flat[n - 1, 9] = np.inf
+    flat[n // 5, 100] = np.nan   # two NaNs in different lanes: the first wins
+    flat[n // 2, 100] = np.nan
+    flat[n - 3, 101] = np.nan    # in the tail rows
+    flat[:, 102] = 1.0           # every row ties: row 0
+    flat[40, 103] = 3.0          # ties between two lanes: row 40 before row 71
+    flat[71, 103] = 3.0
+    mx, am = ref.axis_max(view, axes)
+    assert_bitexact(axis_reduce(hip, base, view, axes, "max", dtype), mx, f"strip max {case}")
+    assert_bitexact(axis_reduce(hip, base, view, axes, "argmax", dtype), am, f"strip argmax {case}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows", [8192, 700])
 def test_column_max_value_only_across_splits(hip, dtype, rows):
