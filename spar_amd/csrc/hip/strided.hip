@@ -348,7 +348,11 @@ __global__ void __launch_bounds__(kThreads)
 // row's granules, and 8 lanes of the store phase, which read one granule
 // index from rows W m + k of 8 consecutive m, hit 8 different bank groups.
 // Measured on MI355X for x^T - mu over x [8192, 4096] float32 (cold cache):
-// ~4.9 TB/s, against ~1.8 TB/s for the scalar 64 x 65 tile above.
+// ~4.9 TB/s, against ~1.8 TB/s for the scalar 64 x 65 tile above.  Back to
+// back over rotated inputs, the rotated tile order (see locate) and
+// non-temporal stores for outputs of 64 MiB or more took the same op from
+// 57.4 us to 46.2 us (5.8 TB/s); each alone gave 53.5 (stores) and 50.1 us
+// (order).
 //
 // The grid is the resident workgroups, each walking tiles; the staged loads
 // of a workgroup's next tile are issued right after its current tile lands in
@@ -378,7 +382,7 @@ constexpr int kAlongQ = 1;
 constexpr int kFixedQ = 2;
 constexpr int kGather = 3;
 
-template <typename T, int NOPS, int NSTAGED, typename F>
+template <typename T, int NOPS, int NSTAGED, typename F, bool NT>
 __global__ void __launch_bounds__(kThreads)
     vec_tiled_kernel(T* out, const T* a, const T* b, VecTileGeometry tg, F f) {
   using V = typename Vec16<T>::type;
@@ -396,12 +400,19 @@ __global__ void __launch_bounds__(kThreads)
     uint64_t base[2];
     uint64_t p0, q0;
   };
+  // Tiles are numbered q fastest, then p, then batch, and each q column of
+  // tiles is rotated along p by its q index (tile (tq, r) covers p tile
+  // (r + tq) mod tiles_p): workgroups running side by side then differ in both
+  // p and q, so neither the staged reads (512-byte pieces of rows 16 KiB
+  // apart in the C5 base) nor the stores gather on the same DRAM channels.
   auto locate = [&](uint32_t tile) {
     Where w;
     const uint32_t rest = tg.tiles_q.div(tile);
     const uint32_t tq = tile - rest * tg.tiles_q.divisor;
     const uint32_t batch = tg.tiles_p.div(rest);
-    const uint32_t tp = rest - batch * tg.tiles_p.divisor;
+    const uint32_t rotated = rest - batch * tg.tiles_p.divisor + tq % tg.tiles_p.divisor;
+    const uint32_t tp =
+        rotated >= tg.tiles_p.divisor ? rotated - tg.tiles_p.divisor : rotated;
     w.out_base = 0;
     w.base[0] = tg.offsets[0];
     w.base[1] = tg.offsets[1];
@@ -521,7 +532,7 @@ __global__ void __launch_bounds__(kThreads)
             vec_set<T>(o, k, f(values[0][i][k], values[1][i][k]));
           }
         }
-        *reinterpret_cast<V*>(out + out_base + (p + i) * tg.out_stride_p + q) = o;
+        store_vector<NT>(reinterpret_cast<V*>(out + out_base + (p + i) * tg.out_stride_p + q), o);
       }
     }
     if (next >= tg.tile_count) break;
@@ -624,8 +635,13 @@ bool launch_vec_tiled(T* out, const T* a, const T* b, const MultiView& view, int
         out, a, b, tg, f);
     return true;
   };
-  return staged == 1 ? launch(vec_tiled_kernel<T, NOPS, 1, F>)
-                     : launch(vec_tiled_kernel<T, NOPS, 2, F>);
+  bool launched = false;
+  with_policy(stream_output(view_numel(view) * sizeof(T)), [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    launched = staged == 1 ? launch(vec_tiled_kernel<T, NOPS, 1, F, NT>)
+                           : launch(vec_tiled_kernel<T, NOPS, 2, F, NT>);
+  });
+  return launched;
 }
 
 // Chooses and launches the kernel for a coalesced view; out is contiguous.
