@@ -15,8 +15,12 @@ with upstream gradient G ~ N(0,1).  Every op runs through the backend's C ABI
 `value` is the step's algorithmic HBM bytes (each distinct input byte read
 once, each output byte written once, broadcast operands at their stored size)
 divided by the measured time, in GB/s (1e9 B/s).  One JSON line is printed.
-`--suite` additionally measures every op of the five benchmark configurations
-and prints one JSON line per op.
+Its `suite` key holds every op of the other configurations (C1, C3, C4, C5
+and the optimizer kernels), each timed steady state, with the HBM traffic per
+launch that the committed rocprof summaries measured, and per configuration a
+roofline record for its dominant op.  `--suite` also prints one JSON line per
+op; `--suite-op CONFIG/OP --profile-launches K` runs only that op, K times,
+for the counter passes that write those summaries.
 """
 from __future__ import annotations
 
@@ -24,6 +28,7 @@ import argparse
 import ctypes
 import json
 import os
+import platform
 import statistics
 import sys
 import time
@@ -46,12 +51,20 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--suite", action="store_true", help="also measure every config op")
+    p.add_argument("--suite", action="store_true",
+                   help="also print one JSON line per suite op")
     p.add_argument("--suite-only", default=None,
                    help="comma-separated suite sections to run (C1,C3,C4,C5,optim)")
+    p.add_argument("--no-suite", action="store_true", help="leave the suite out of the line")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-loop", type=int, default=0,
                    help="run only N steps of the workload (for rocprofv3) and exit")
+    p.add_argument("--suite-op", default=None,
+                   help="CONFIG/OP: run only this suite op (for rocprofv3) and exit")
+    p.add_argument("--profile-launches", type=int, default=4,
+                   help="launches of the --suite-op op")
+    p.add_argument("--list-suite-ops", action="store_true",
+                   help="print the suite's configurations and ops as JSON and exit")
     return p.parse_args()
 
 
@@ -175,21 +188,46 @@ def cpu_baseline(hip, work: Workload, sample_batch=16, repeats=3):
         per_rep.append(time.perf_counter() - t0)
     seconds = statistics.median(per_rep)
     total = sum(nbytes.values())
+    model = cpu_model()
     return {
         "value": round(total / seconds / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"the same five ops on the first {sample_batch} of {B} batch rows "
-                   f"(x[{sample_batch},{T},{C}]), oracle C loops compiled -O2 -ffp-contract=off, "
-                   f"median of {repeats} runs of {sum(per_rep) / repeats:.2f} s; host "
-                   f"{os.cpu_count()} logical CPUs, 1 thread used"),
+        "cpu_model": model,
+        "sample": (f"the five ops of the step on the first {sample_batch} of {B} batch rows "
+                   f"(x[{sample_batch},{T},{C}], half the step's bytes, scaled by its own bytes), "
+                   f"the oracle's C loops (-O2 -ffp-contract=off) on 1 core of {model} "
+                   f"({os.cpu_count()} logical CPUs visible), median of {repeats} runs of "
+                   f"{sum(per_rep) / repeats:.2f} s"),
         "seconds_per_step_sample": round(seconds, 4),
     }
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as info:
+            for line in info:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown CPU"
+
+
+def calibration_copy(hip, work):
+    """One plain contiguous copy of x (512 MiB read, 512 MiB written), whose
+    counters calibrate bytes per counter unit in the traffic summaries."""
+    hip.call("spar_hip_launch_strided_copy", work.y1.ptr, work.x.ptr, 1, hip.u64_array([work.n]),
+             hip.u64_array([1]), 0, work.n, 4, 0)
+    hip.synchronize()
+
+
 def main():
     args = parse()
+    if args.list_suite_ops:
+        print(json.dumps(SUITE_OPS))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); this backend's "
               "benchmark is a single-device measurement", file=sys.stderr)
@@ -201,18 +239,27 @@ def main():
         print("no HIP device visible", file=sys.stderr)
         sys.exit(1)
 
-    work = Workload(hip)
-    if args.profile_loop:
-        # Workload steps, then one plain contiguous copy of x (512 MiB read,
-        # 512 MiB written) whose counters calibrate bytes per counter unit.
-        for _ in range(args.profile_loop):
-            work.step()
-        hip.call("spar_hip_launch_strided_copy", work.y1.ptr, work.x.ptr, 1, hip.u64_array([work.n]),
-                 hip.u64_array([1]), 0, work.n, 4, 0)
-        hip.synchronize()
-        print(json.dumps({"profile_loop_steps": args.profile_loop, "copy_bytes": work.n * 4}))
+    if args.suite_op:
+        config, _, op = args.suite_op.partition("/")
+        if op not in SUITE_OPS.get(config, []):
+            print(f"unknown suite op {args.suite_op!r}", file=sys.stderr)
+            sys.exit(2)
+        suite = Suite(hip, profile=(config, op, args.profile_launches))
+        suite.run([config])
+        op_bytes = suite.profile_bytes
+        del suite
+        calibration_copy(hip, Workload(hip))
+        print(json.dumps({"suite_op": args.suite_op, "launches": args.profile_launches,
+                          "bytes": op_bytes, "copy_bytes": B * T * C * 4}))
         return
 
+    work = Workload(hip)
+    if args.profile_loop:
+        for _ in range(args.profile_loop):
+            work.step()
+        calibration_copy(hip, work)
+        print(json.dumps({"profile_loop_steps": args.profile_loop, "copy_bytes": work.n * 4}))
+        return
     nbytes = work.op_bytes()
     step_bytes = sum(nbytes.values())
     for _ in range(args.warmup):
@@ -293,15 +340,52 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(hip, work)
-    print(json.dumps(result), flush=True)
-    if args.suite or args.suite_only:
+    suite = None
+    if not args.no_suite:
         del work
-        run_suite(hip, only=None if args.suite_only is None else args.suite_only.split(","))
+        suite = Suite(hip)
+        suite.run(None if args.suite_only is None else args.suite_only.split(","))
+        result["suite"] = suite.summary()
+    print(json.dumps(result), flush=True)
+    if args.suite and suite is not None:
+        for line in suite.lines:
+            print(json.dumps(line), flush=True)
 
 
 # ----------------------------------------------------------------- suite
 
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+# The suite's configurations, their workloads and their ops, in run order.
+SUITE_WORKLOADS = {
+    "C1": "contiguous fp32 elementwise on [4096, 4096] a, b ~ N(0,1)",
+    "C3": "axis reductions on [8192, 8192] ~ N(0,1); full reductions of 2^28 ~ U(-1,1)",
+    "C4": "row softmax / log-softmax (and cross entropy) on logits [8192, 32768] ~ N(0, 2)",
+    "C5": "LayerNorm chain through the Tensor API on [4096, 8192] views: a transposed "
+          "[8192, 4096] base and a block of a [4608, 9216] base",
+    "optim": "AdamW, gradient-norm summary and scaling over 124,439,808 fp32 parameters",
+}
+SUITE_OPS = {
+    "C1": ["a+b", "a*b", "gelu(a)", "exp(a)"],
+    "C3": [f"{op} axis {axis}" for axis in (1, 0) for op in ("sum", "mean", "max", "argmax")]
+          + [f"full {op} 2^28" for op in ("sum", "mean", "max")],
+    "C4": ["softmax forward", "softmax backward", "log_softmax forward", "log_softmax backward",
+           "cross_entropy forward (fused)", "cross_entropy backward (fused)",
+           "cross_entropy forward (composed, vs fused bytes)",
+           "cross_entropy backward (composed, vs fused bytes)"],
+    "C5": [f"{op} {view}" for view in ("transposed", "sliced")
+           for op in ("mu=mean(x,1)", "xc=x-mu", "square(xc)", "var=mean(sq,1)", "xhat=xc/sd",
+                      "xhat*gamma", "+beta", "y*G", "sum(y*G)")]
+          + [f"{op} {view} (vs fused minimum)" for view in ("transposed", "sliced")
+             for op in ("forward chain", "backward chain", "fused layer_norm forward",
+                        "fused layer_norm backward")],
+    "optim": ["adamw step (fp32, double math)", "gradient norm summary",
+              "scale gradients in place"],
+}
+# Ops measured against a minimum other than their own bytes (the fused
+# minimum of the C5 chain, the fused cross entropy's bytes): reported, but
+# never a configuration's roofline op.
+SUITE_REFERENCE_ONLY = ("composed", "chain", "fused layer_norm")
 
 
 def rotation(set_bytes):
@@ -310,9 +394,9 @@ def rotation(set_bytes):
     return max(3, -(-3 * MALL_BYTES // max(set_bytes, 1)) + 1)
 
 
-def run_suite(hip, reps=20, warmup=3, only=None):
-    """Times every op of the five benchmark configurations (one JSON line per
-    op), two ways:
+class Suite:
+    """Times every op of the benchmark configurations other than the default
+    workload, two ways:
 
     * steady state ("ms", "GB/s", "frac"): back-to-back launches rotating over
       input/output sets that together exceed the Infinity Cache several times,
@@ -326,43 +410,74 @@ def run_suite(hip, reps=20, warmup=3, only=None):
       launch itself leaves dirty in the cache, which flatters ordinary stores
       against non-temporal ones.
 
-    Ops that need a fresh graph per launch (the backward chains) are timed cold
-    only."""
-    F = hip.FLOAT32
-    u = hip.u64_array
-    flush = hip.DeviceBuffer(512 << 20)
-    hip.call("spar_hip_zero", flush.ptr, flush.nbytes, 0)
-    flush_sink = hip.DeviceBuffer(8)
-    start, stop = hip.Event(), hip.Event()
+    Ops that need a fresh graph per launch (the backward chains) are timed
+    cold only.
 
-    def measure(config, name, nbytes, launches, elements, prepare=None):
+    With `profile=(config, op, launches)` only that op runs, `launches`
+    times, each launch preceded by a marker dispatch (a 16-byte
+    spar_hip_touch) and the last one followed by another, so a counter pass
+    can attribute the dispatches between markers to the op (a prepare step,
+    such as building a fresh graph, runs before its marker)."""
+
+    def __init__(self, hip, reps=20, warmup=3, profile=None):
+        self.hip = hip
+        self.reps = reps
+        self.warmup = warmup
+        self.profile = profile
+        self.lines = []
+        self.results = {}
+        self.profile_bytes = None
+        self.flush = hip.DeviceBuffer(512 << 20)
+        hip.call("spar_hip_zero", self.flush.ptr, self.flush.nbytes, 0)
+        self.sink = hip.DeviceBuffer(16)
+        self.start, self.stop = hip.Event(), hip.Event()
+
+    def wanted(self, config, name):
+        return self.profile is None or (config, name) == self.profile[:2]
+
+    def measure(self, config, name, nbytes, launches, elements, prepare=None):
+        assert name in SUITE_OPS[config], (config, name)
+        if not self.wanted(config, name):
+            return
+        hip = self.hip
         if callable(launches):
             launches = [launches]
-        for _ in range(warmup):
+        if self.profile is not None:
+            self.profile_bytes = nbytes
+            hip.synchronize()
+            for k in range(self.profile[2]):
+                if prepare is not None:
+                    prepare()
+                hip.call("spar_hip_touch", self.sink.ptr, 16, 0, 0)  # marker: a launch starts
+                launches[k % len(launches)]()
+            hip.call("spar_hip_touch", self.sink.ptr, 16, 0, 0)  # marker: the last one ended
+            hip.synchronize()
+            return
+        for _ in range(self.warmup):
             for launch in launches:
                 if prepare is not None:
                     prepare()
                 launch()
         hip.synchronize()
         samples = []
-        for _ in range(reps):
+        for _ in range(self.reps):
             if prepare is not None:
                 prepare()
-            hip.call("spar_hip_touch", flush.ptr, flush.nbytes, flush_sink.ptr, 0)
-            start.record()
+            hip.call("spar_hip_touch", self.flush.ptr, self.flush.nbytes, self.sink.ptr, 0)
+            self.start.record()
             launches[0]()
-            stop.record()
-            samples.append(start.elapsed_ms(stop))
+            self.stop.record()
+            samples.append(self.start.elapsed_ms(self.stop))
         cold = statistics.median(samples)
         line = {"suite": config, "op": name}
         if prepare is None and len(launches) > 1:
-            count = max(reps, 2 * len(launches))
+            count = max(self.reps, 2 * len(launches))
             hip.synchronize()
-            start.record()
+            self.start.record()
             for k in range(count):
                 launches[k % len(launches)]()
-            stop.record()
-            ms = start.elapsed_ms(stop) / count
+            self.stop.record()
+            ms = self.start.elapsed_ms(self.stop) / count
             line["timing"] = f"steady, {len(launches)} rotated sets"
         else:
             ms = cold
@@ -373,258 +488,295 @@ def run_suite(hip, reps=20, warmup=3, only=None):
                      "elements_per_s": round(elements / (ms * 1e-3), 1),
                      "cold_ms": round(cold, 5),
                      "cold_GB/s": round(nbytes / (cold * 1e-3) / 1e9, 1)})
-        print(json.dumps(line), flush=True)
+        self.lines.append(line)
+        self.results.setdefault(config, {})[name] = line
 
-    def normal(n, seed, std=1.0):
-        buf = hip.DeviceBuffer(n * 4)
-        hip.call("spar_hip_random_normal", buf.ptr, n, F, seed, 0.0, std, 0)
-        return buf
+    def summary(self):
+        """Per configuration: every op's steady-state figures with its HBM
+        traffic per launch from the committed counter summary (null where
+        none was measured), and the roofline record of its dominant op (the
+        longest op measured against its own bytes)."""
+        from spar_amd.rocprof_summary import read_op_traffic, suite_traffic_file
 
-    def uniform(n, seed, low, high):
-        buf = hip.DeviceBuffer(n * 4)
-        hip.call("spar_hip_random_uniform", buf.ptr, n, F, seed, low, high, 0)
-        return buf
+        out = {}
+        for config, ops in self.results.items():
+            traffic = read_op_traffic(ROOT / "profiles" / suite_traffic_file(config))
+            entry = {"workload": SUITE_WORKLOADS[config], "ops": {}}
+            for name, line in ops.items():
+                entry["ops"][name] = {key: line[key] for key in ("ms", "GB/s", "frac", "bytes",
+                                                                 "timing")}
+                entry["ops"][name]["traffic"] = traffic.get(name)
+            own = {name: line for name, line in ops.items()
+                   if not any(tag in name for tag in SUITE_REFERENCE_ONLY)}
+            if own:
+                name = max(own, key=lambda op: own[op]["ms"])
+                line = own[name]
+                entry["roofline"] = {"op": name, "bound": "hbm", "achieved": line["GB/s"],
+                                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": line["frac"],
+                                     "bytes_per_launch": line["bytes"],
+                                     "avg_launch_ms": line["ms"], "traffic": traffic.get(name)}
+            out[config] = entry
+        return out
 
-    def c1():
-        # C1: contiguous elementwise on [4096, 4096]; set 0 carries the
-        # benchmark seeds, the other sets only rotate the cache.
-        n = 4096 * 4096
-        sets = [(normal(n, 1 + 100 * k), normal(n, 2 + 100 * k), hip.DeviceBuffer(n * 4))
-                for k in range(rotation(12 * n))]
-        for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
-            measure("C1", name, 12 * n, [lambda a=a, b=b, out=out, op=op: hip.call(
-                "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0) for a, b, out in sets], n)
-        measure("C1", "gelu(a)", 8 * n, [lambda a=a, out=out: hip.call(
-            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0) for a, _, out in sets], n)
-        # exp(clip(a, -10, 10)): the clip is the identity on these draws (checked here)
-        peak = hip.DeviceBuffer(8)
-        for a, _, out in sets:
-            hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
-            for source in (a, out):  # max(a) and max(-a)
-                hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
-                assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
-        measure("C1", "exp(a)", 8 * n, [lambda a=a, out=out: hip.call(
-            "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0) for a, _, out in sets], n)
-        del sets
+    def run(self, only=None):
+        for name, section in self.sections().items():
+            if (only is None or name in only) and (self.profile is None
+                                                    or self.profile[0] == name):
+                section()
 
-    def c3():
-        # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
-        R = 8192
-        n = R * R
-        sets = [(normal(n, 3 + 100 * k), hip.DeviceBuffer(R * 8)) for k in range(rotation(4 * n))]
-        codes = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}
-        for axis in (1, 0):
-            for name, code in codes.items():
-                out_bytes = R * (8 if name == "argmax" else 4)
-                measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, [
-                    lambda x=x, out=out, code=code, axis=axis: hip.call(
-                        "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
-                        1 << axis, F, code, 0) for x, out in sets], n)
-        del sets
-        n = 1 << 28
-        sets = [(uniform(n, 4 + 100 * k, -1.0, 1.0), hip.DeviceBuffer(8))
-                for k in range(rotation(4 * n))]
-        for name in ("sum", "mean", "max"):
-            measure("C3", f"full {name} 2^28", 4 * n + 4, [lambda v=v, out=out, name=name: hip.call(
-                "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0)
-                for v, out in sets], n)
-        del sets
+    def sections(self):
+        hip = self.hip
+        F = hip.FLOAT32
+        u = hip.u64_array
+        measure = self.measure
 
-    def c4():
-        # C4: row softmax / log-softmax on [8192, 32768]
-        rows, V = 8192, 32768
-        n = rows * V
-        count = rotation(16 * n)
+        def normal(n, seed, std=1.0):
+            buf = hip.DeviceBuffer(n * 4)
+            hip.call("spar_hip_random_normal", buf.ptr, n, F, seed, 0.0, std, 0)
+            return buf
 
-        class Set:
-            def __init__(self, k):
-                self.logits = normal(n, 5 + 100 * k, np.sqrt(2.0))
-                self.grad = normal(n, 6 + 100 * k)
-                self.probs = hip.DeviceBuffer(n * 4)
-                self.dx = hip.DeviceBuffer(n * 4)
-                self.undefined = hip.DeviceBuffer(rows * 4)
+        def uniform(n, seed, low, high):
+            buf = hip.DeviceBuffer(n * 4)
+            hip.call("spar_hip_random_uniform", buf.ptr, n, F, seed, low, high, 0)
+            return buf
 
-        sets = [Set(k) for k in range(count)]
-        for log in (0, 1):
-            label = "log_softmax" if log else "softmax"
-            measure("C4", f"{label} forward", 8 * n + 4 * rows, [lambda s=s, log=log: hip.call(
-                "spar_hip_launch_probability_forward", s.probs.ptr, s.undefined.ptr, s.logits.ptr,
-                rows, V, 1, F, log, 0) for s in sets], n)
-            measure("C4", f"{label} backward", 12 * n + 4 * rows, [lambda s=s, log=log: hip.call(
-                "spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
-                s.undefined.ptr, rows, V, 1, F, log, 0) for s in sets], n)
-        # C4 as a loss: cross entropy over the same logits, fused (one read of the
-        # logits forward; one read and one write backward) and composed as the
-        # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
-        # log_softmax backward), with the same targets.
-        targets = hip.DeviceBuffer(rows * 8)
-        hip.call("spar_hip_copy_host_to_device", targets.ptr,
-                 np.random.default_rng(9).integers(0, V, rows).astype(np.int64).ctypes.data,
-                 rows * 8, 0)
-        losses, row_max, row_log_sum = (hip.DeviceBuffer(rows * 4) for _ in range(3))
-        invalid = hip.DeviceBuffer(4)
-        loss_grad = uniform(rows, 10, 0.5, 1.5)
-        small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
-        measure("C4", "cross_entropy forward (fused)", 4 * n + small, [lambda s=s: hip.call(
-            "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
-            s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0)
-            for s in sets], n)
-        # the backward of each set uses that set's forward statistics
-        for s in sets:
-            s.row_max, s.row_log_sum = hip.DeviceBuffer(rows * 4), hip.DeviceBuffer(rows * 4)
-            hip.call("spar_hip_launch_cross_entropy_forward", losses.ptr, s.row_max.ptr,
-                     s.row_log_sum.ptr, s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows,
-                     V, 0, F, hip.INT64, 0, 0)
-        measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, [lambda s=s: hip.call(
-            "spar_hip_launch_cross_entropy_backward", s.dx.ptr, loss_grad.ptr, s.logits.ptr,
-            s.row_max.ptr, s.row_log_sum.ptr, s.undefined.ptr, targets.ptr, rows, V, 0, F,
-            hip.INT64, 0, 0) for s in sets], n)
+        def c1():
+            # C1: contiguous elementwise on [4096, 4096]; set 0 carries the
+            # benchmark seeds, the other sets only rotate the cache.
+            n = 4096 * 4096
+            sets = [(normal(n, 1 + 100 * k), normal(n, 2 + 100 * k), hip.DeviceBuffer(n * 4))
+                    for k in range(rotation(12 * n))]
+            for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
+                measure("C1", name, 12 * n, [lambda a=a, b=b, out=out, op=op: hip.call(
+                    "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0) for a, b, out in sets], n)
+            measure("C1", "gelu(a)", 8 * n, [lambda a=a, out=out: hip.call(
+                "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0) for a, _, out in sets], n)
+            # exp(clip(a, -10, 10)): the clip is the identity on these draws (checked here)
+            peak = hip.DeviceBuffer(8)
+            for a, _, out in sets:
+                hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
+                for source in (a, out):  # max(a) and max(-a)
+                    hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
+                    assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
+            measure("C1", "exp(a)", 8 * n, [lambda a=a, out=out: hip.call(
+                "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0) for a, _, out in sets], n)
+            del sets
 
-        def composed_forward(s):
-            hip.call("spar_hip_launch_probability_forward", s.probs.ptr, s.undefined.ptr,
-                     s.logits.ptr, rows, V, 1, F, 1, 0)
-            hip.call("spar_hip_launch_nll_forward", losses.ptr, s.probs.ptr, targets.ptr, rows, V, 0,
-                     F, hip.INT64, 0, 0)
+        def c3():
+            # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
+            R = 8192
+            n = R * R
+            sets = [(normal(n, 3 + 100 * k), hip.DeviceBuffer(R * 8)) for k in range(rotation(4 * n))]
+            codes = {"sum": hip.SUM, "mean": hip.MEAN, "max": hip.MAX, "argmax": hip.ARGMAX}
+            for axis in (1, 0):
+                for name, code in codes.items():
+                    out_bytes = R * (8 if name == "argmax" else 4)
+                    measure("C3", f"{name} axis {axis}", 4 * n + out_bytes, [
+                        lambda x=x, out=out, code=code, axis=axis: hip.call(
+                            "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
+                            1 << axis, F, code, 0) for x, out in sets], n)
+            del sets
+            n = 1 << 28
+            sets = [(uniform(n, 4 + 100 * k, -1.0, 1.0), hip.DeviceBuffer(8))
+                    for k in range(rotation(4 * n))]
+            for name in ("sum", "mean", "max"):
+                measure("C3", f"full {name} 2^28", 4 * n + 4, [lambda v=v, out=out, name=name: hip.call(
+                    "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0)
+                    for v, out in sets], n)
+            del sets
 
-        def composed_backward(s):
-            hip.call("spar_hip_zero", s.grad.ptr, n * 4, 0)
-            hip.call("spar_hip_launch_nll_backward", s.grad.ptr, loss_grad.ptr, targets.ptr, rows, V,
-                     0, F, hip.INT64, 0, 0)
-            hip.call("spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
-                     s.undefined.ptr, rows, V, 1, F, 1, 0)
+        def c4():
+            # C4: row softmax / log-softmax on [8192, 32768]
+            rows, V = 8192, 32768
+            n = rows * V
+            count = rotation(16 * n)
 
-        # reported against the fused kernels' bytes, so the ratio is the speed-up
-        measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
-                [lambda s=s: composed_forward(s) for s in sets], n)
-        measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
-                [lambda s=s: composed_backward(s) for s in sets], n)
-        del sets, targets, losses, row_max, row_log_sum, invalid, loss_grad
+            class Set:
+                def __init__(self, k):
+                    self.logits = normal(n, 5 + 100 * k, np.sqrt(2.0))
+                    self.grad = normal(n, 6 + 100 * k)
+                    self.probs = hip.DeviceBuffer(n * 4)
+                    self.dx = hip.DeviceBuffer(n * 4)
+                    self.undefined = hip.DeviceBuffer(rows * 4)
 
-    def c5():
-        # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
-        # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a
-        # [4608,9216] base, through the Tensor API: each op's time includes its
-        # host-side dispatch and allocation as well as its kernels.  Then
-        # loss = sum(y * G) and loss.backward() into base, gamma and beta.  Each
-        # rotated set has its own base, G and chain intermediates.
-        from spar_amd import spar
+            sets = [Set(k) for k in range(count)]
+            for log in (0, 1):
+                label = "log_softmax" if log else "softmax"
+                measure("C4", f"{label} forward", 8 * n + 4 * rows, [lambda s=s, log=log: hip.call(
+                    "spar_hip_launch_probability_forward", s.probs.ptr, s.undefined.ptr, s.logits.ptr,
+                    rows, V, 1, F, log, 0) for s in sets], n)
+                measure("C4", f"{label} backward", 12 * n + 4 * rows, [lambda s=s, log=log: hip.call(
+                    "spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
+                    s.undefined.ptr, rows, V, 1, F, log, 0) for s in sets], n)
+            # C4 as a loss: cross entropy over the same logits, fused (one read of the
+            # logits forward; one read and one write backward) and composed as the
+            # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
+            # log_softmax backward), with the same targets.
+            targets = hip.DeviceBuffer(rows * 8)
+            hip.call("spar_hip_copy_host_to_device", targets.ptr,
+                     np.random.default_rng(9).integers(0, V, rows).astype(np.int64).ctypes.data,
+                     rows * 8, 0)
+            losses, row_max, row_log_sum = (hip.DeviceBuffer(rows * 4) for _ in range(3))
+            invalid = hip.DeviceBuffer(4)
+            loss_grad = uniform(rows, 10, 0.5, 1.5)
+            small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
+            measure("C4", "cross_entropy forward (fused)", 4 * n + small, [lambda s=s: hip.call(
+                "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
+                s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0)
+                for s in sets], n)
+            # the backward of each set uses that set's forward statistics
+            for s in sets:
+                s.row_max, s.row_log_sum = hip.DeviceBuffer(rows * 4), hip.DeviceBuffer(rows * 4)
+                hip.call("spar_hip_launch_cross_entropy_forward", losses.ptr, s.row_max.ptr,
+                         s.row_log_sum.ptr, s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows,
+                         V, 0, F, hip.INT64, 0, 0)
+            measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, [lambda s=s: hip.call(
+                "spar_hip_launch_cross_entropy_backward", s.dx.ptr, loss_grad.ptr, s.logits.ptr,
+                s.row_max.ptr, s.row_log_sum.ptr, s.undefined.ptr, targets.ptr, rows, V, 0, F,
+                hip.INT64, 0, 0) for s in sets], n)
 
-        device = spar.Device.hip(0)
-        f32 = spar.DType.float32
-        rows, cols = 4096, 8192
-        n = rows * cols
-        T = 4 * n  # bytes of one full-tensor read or write
-        rng = spar.Random(7)
-        gamma = spar.random_uniform([cols], f32, rng, 0.5, 1.5, device)
-        beta = spar.random_uniform([cols], f32, rng, -0.1, 0.1, device)
-        count = rotation(3 * T)
-        Gs = [spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device) for _ in range(count)]
-        shapes = {"transposed": [8192, 4096], "sliced": [4608, 9216]}
-        bases = {label: [spar.random_normal(shape, f32, rng, 0.0, 1.0, device) for _ in range(count)]
-                 for label, shape in shapes.items()}
-        for leaf in (gamma, beta, *bases["transposed"], *bases["sliced"]):
-            leaf.set_requires_grad(True)
+            def composed_forward(s):
+                hip.call("spar_hip_launch_probability_forward", s.probs.ptr, s.undefined.ptr,
+                         s.logits.ptr, rows, V, 1, F, 1, 0)
+                hip.call("spar_hip_launch_nll_forward", losses.ptr, s.probs.ptr, targets.ptr, rows, V, 0,
+                         F, hip.INT64, 0, 0)
 
-        def view_of(label, k=0):
-            base = bases[label][k]
-            return base.transpose(0, 1) if label == "transposed" else base.narrow(0, 256, rows).narrow(1, 512, cols)
+            def composed_backward(s):
+                hip.call("spar_hip_zero", s.grad.ptr, n * 4, 0)
+                hip.call("spar_hip_launch_nll_backward", s.grad.ptr, loss_grad.ptr, targets.ptr, rows, V,
+                         0, F, hip.INT64, 0, 0)
+                hip.call("spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
+                         s.undefined.ptr, rows, V, 1, F, 1, 0)
 
-        def forward(x, G):
-            mu = spar.mean(x, [1], True)
-            xc = spar.subtract(x, mu)
-            var = spar.mean(spar.square(xc), [1], True)
-            xhat = spar.divide(xc, spar.sqrt(spar.add_scalar(var, 1e-5)))
-            y = spar.add(spar.multiply(xhat, gamma), beta)
-            return spar.sum(spar.multiply(y, G), None, False)
+            # reported against the fused kernels' bytes, so the ratio is the speed-up
+            measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
+                    [lambda s=s: composed_forward(s) for s in sets], n)
+            measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
+                    [lambda s=s: composed_backward(s) for s in sets], n)
+            del sets, targets, losses, row_max, row_log_sum, invalid, loss_grad
 
-        for label in bases:
-            chains = []
-            for k in range(count):
-                c = {"x": view_of(label, k), "G": Gs[k]}
-                c["mu"] = spar.mean(c["x"], [1], True)
-                c["xc"] = spar.subtract(c["x"], c["mu"])
-                c["sq"] = spar.square(c["xc"])
-                c["var"] = spar.mean(c["sq"], [1], True)
-                c["sd"] = spar.sqrt(spar.add_scalar(c["var"], 1e-5))
-                c["xhat"] = spar.divide(c["xc"], c["sd"])
-                c["yg"] = spar.multiply(c["xhat"], gamma)
-                c["y"] = spar.add(c["yg"], beta)
-                c["yG"] = spar.multiply(c["y"], c["G"])
-                chains.append(c)
+        def c5():
+            # C5: the LayerNorm chain on a transposed view (a [8192,4096] base viewed
+            # as [4096,8192]) and on a [4096,8192] block at a nonzero offset of a
+            # [4608,9216] base, through the Tensor API: each op's time includes its
+            # host-side dispatch and allocation as well as its kernels.  Then
+            # loss = sum(y * G) and loss.backward() into base, gamma and beta.  Each
+            # rotated set has its own base, G and chain intermediates.
+            from spar_amd import spar
 
-            def each(fn):
-                return [lambda c=c: fn(c) for c in chains]
+            device = spar.Device.hip(0)
+            f32 = spar.DType.float32
+            rows, cols = 4096, 8192
+            n = rows * cols
+            T = 4 * n  # bytes of one full-tensor read or write
+            rng = spar.Random(7)
+            gamma = spar.random_uniform([cols], f32, rng, 0.5, 1.5, device)
+            beta = spar.random_uniform([cols], f32, rng, -0.1, 0.1, device)
+            count = rotation(3 * T)
+            Gs = [spar.random_normal([rows, cols], f32, rng, 0.0, 1.0, device) for _ in range(count)]
+            shapes = {"transposed": [8192, 4096], "sliced": [4608, 9216]}
+            bases = {label: [spar.random_normal(shape, f32, rng, 0.0, 1.0, device) for _ in range(count)]
+                     for label, shape in shapes.items()}
+            for leaf in (gamma, beta, *bases["transposed"], *bases["sliced"]):
+                leaf.set_requires_grad(True)
 
-            measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows,
-                    each(lambda c: spar.mean(c["x"], [1], True)), n)
-            measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows,
-                    each(lambda c: spar.subtract(c["x"], c["mu"])), n)
-            measure("C5", f"square(xc) {label}", 2 * T, each(lambda c: spar.square(c["xc"])), n)
-            measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows,
-                    each(lambda c: spar.mean(c["sq"], [1], True)), n)
-            measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows,
-                    each(lambda c: spar.divide(c["xc"], c["sd"])), n)
-            measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols,
-                    each(lambda c: spar.multiply(c["xhat"], gamma)), n)
-            measure("C5", f"+beta {label}", 2 * T + 4 * cols, each(lambda c: spar.add(c["yg"], beta)), n)
-            measure("C5", f"y*G {label}", 3 * T, each(lambda c: spar.multiply(c["y"], c["G"])), n)
-            measure("C5", f"sum(y*G) {label}", T + 4, each(lambda c: spar.sum(c["yG"], None, False)), n)
-            del chains
-            # Whole forward, then backward.  Both are reported against the fused
-            # minimum: forward reads x and G once (the loss is a scalar);
-            # backward reads x and G and writes dx (gamma, beta grads are small).
-            measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T,
-                    [lambda k=k: forward(view_of(label, k), Gs[k]) for k in range(count)], n)
-            losses = []
+            def view_of(label, k=0):
+                base = bases[label][k]
+                return base.transpose(0, 1) if label == "transposed" else base.narrow(0, 256, rows).narrow(1, 512, cols)
 
-            def prepare():
-                for leaf in (gamma, beta, bases[label][0]):
-                    leaf.zero_grad()
-                losses[:] = [forward(view_of(label), Gs[0])]
+            def forward(x, G):
+                mu = spar.mean(x, [1], True)
+                xc = spar.subtract(x, mu)
+                var = spar.mean(spar.square(xc), [1], True)
+                xhat = spar.divide(xc, spar.sqrt(spar.add_scalar(var, 1e-5)))
+                y = spar.add(spar.multiply(xhat, gamma), beta)
+                return spar.sum(spar.multiply(y, G), None, False)
 
-            measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
-                    lambda: losses[0].backward(), n, prepare=prepare)
+            for label in bases:
+                chains = []
+                for k in range(count):
+                    c = {"x": view_of(label, k), "G": Gs[k]}
+                    c["mu"] = spar.mean(c["x"], [1], True)
+                    c["xc"] = spar.subtract(c["x"], c["mu"])
+                    c["sq"] = spar.square(c["xc"])
+                    c["var"] = spar.mean(c["sq"], [1], True)
+                    c["sd"] = spar.sqrt(spar.add_scalar(c["var"], 1e-5))
+                    c["xhat"] = spar.divide(c["xc"], c["sd"])
+                    c["yg"] = spar.multiply(c["xhat"], gamma)
+                    c["y"] = spar.add(c["yg"], beta)
+                    c["yG"] = spar.multiply(c["y"], c["G"])
+                    chains.append(c)
 
-            # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
-            # first made contiguous, inside the timed op.
-            measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
-                    [lambda k=k: spar.layer_norm(view_of(label, k), gamma, beta, 1e-5)
-                     for k in range(count)], n)
+                def each(fn):
+                    return [lambda c=c: fn(c) for c in chains]
 
-            def prepare_fused():
-                for leaf in (gamma, beta, bases[label][0]):
-                    leaf.zero_grad()
-                y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
-                losses[:] = [spar.sum(spar.multiply(y, Gs[0]), None, False)]
+                measure("C5", f"mu=mean(x,1) {label}", T + 4 * rows,
+                        each(lambda c: spar.mean(c["x"], [1], True)), n)
+                measure("C5", f"xc=x-mu {label}", 2 * T + 4 * rows,
+                        each(lambda c: spar.subtract(c["x"], c["mu"])), n)
+                measure("C5", f"square(xc) {label}", 2 * T, each(lambda c: spar.square(c["xc"])), n)
+                measure("C5", f"var=mean(sq,1) {label}", T + 4 * rows,
+                        each(lambda c: spar.mean(c["sq"], [1], True)), n)
+                measure("C5", f"xhat=xc/sd {label}", 2 * T + 4 * rows,
+                        each(lambda c: spar.divide(c["xc"], c["sd"])), n)
+                measure("C5", f"xhat*gamma {label}", 2 * T + 4 * cols,
+                        each(lambda c: spar.multiply(c["xhat"], gamma)), n)
+                measure("C5", f"+beta {label}", 2 * T + 4 * cols, each(lambda c: spar.add(c["yg"], beta)), n)
+                measure("C5", f"y*G {label}", 3 * T, each(lambda c: spar.multiply(c["y"], c["G"])), n)
+                measure("C5", f"sum(y*G) {label}", T + 4, each(lambda c: spar.sum(c["yG"], None, False)), n)
+                del chains
+                # Whole forward, then backward.  Both are reported against the fused
+                # minimum: forward reads x and G once (the loss is a scalar);
+                # backward reads x and G and writes dx (gamma, beta grads are small).
+                measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T,
+                        [lambda k=k: forward(view_of(label, k), Gs[k]) for k in range(count)], n)
+                losses = []
 
-            measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
-                    lambda: losses[0].backward(), n, prepare=prepare_fused)
-            del losses
+                def prepare():
+                    for leaf in (gamma, beta, bases[label][0]):
+                        leaf.zero_grad()
+                    losses[:] = [forward(view_of(label), Gs[0])]
 
-    def optim():
-        # Optimizer: one AdamW step, the gradient-norm summary and the clip scaling
-        # over GPT-2 small's 124,439,808 fp32 parameters held as one flat buffer.
-        n = 124_439_808
-        count = rotation(16 * n)
-        sets = [(normal(n, 81 + 100 * k), normal(n, 82 + 100 * k, 1e-2),
-                 normal(n, 83 + 100 * k, 1e-3), uniform(n, 84 + 100 * k, 0.0, 1e-5),
-                 hip.DeviceBuffer(64)) for k in range(count)]
-        c1, c2 = 1.0 - 0.9 ** 1000, 1.0 - 0.95 ** 1000
-        measure("optim", "adamw step (fp32, double math)", 28 * n, [
-            lambda p=p, g=g, m=m, v=v: hip.call(
-                "spar_hip_launch_adamw", p.ptr, g.ptr, m.ptr, v.ptr, n, F, 3e-4, 0.9, 0.95, 1e-8, 0.1,
-                c1, c2, 0) for p, g, m, v, _ in sets], n)
-        measure("optim", "gradient norm summary", 4 * n, [lambda g=g, summary=summary: hip.call(
-            "spar_hip_launch_gradient_norm_summary", summary.ptr, g.ptr, n, F, 0)
-            for _, g, _, _, summary in sets], n)
-        measure("optim", "scale gradients in place", 8 * n, [lambda g=g: hip.call(
-            "spar_hip_launch_scale_in_place", g.ptr, n, F, 1.0, 0) for _, g, _, _, _ in sets], n)
-        del sets
+                measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
+                        lambda: losses[0].backward(), n, prepare=prepare)
 
-    sections = {"C1": c1, "C3": c3, "C4": c4, "C5": c5, "optim": optim}
-    for name, section in sections.items():
-        if only is None or name in only:
-            section()
+                # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
+                # first made contiguous, inside the timed op.
+                measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
+                        [lambda k=k: spar.layer_norm(view_of(label, k), gamma, beta, 1e-5)
+                         for k in range(count)], n)
+
+                def prepare_fused():
+                    for leaf in (gamma, beta, bases[label][0]):
+                        leaf.zero_grad()
+                    y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
+                    losses[:] = [spar.sum(spar.multiply(y, Gs[0]), None, False)]
+
+                measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
+                        lambda: losses[0].backward(), n, prepare=prepare_fused)
+                del losses
+
+        def optim():
+            # Optimizer: one AdamW step, the gradient-norm summary and the clip scaling
+            # over GPT-2 small's 124,439,808 fp32 parameters held as one flat buffer.
+            n = 124_439_808
+            count = rotation(16 * n)
+            sets = [(normal(n, 81 + 100 * k), normal(n, 82 + 100 * k, 1e-2),
+                     normal(n, 83 + 100 * k, 1e-3), uniform(n, 84 + 100 * k, 0.0, 1e-5),
+                     hip.DeviceBuffer(64)) for k in range(count)]
+            c1, c2 = 1.0 - 0.9 ** 1000, 1.0 - 0.95 ** 1000
+            measure("optim", "adamw step (fp32, double math)", 28 * n, [
+                lambda p=p, g=g, m=m, v=v: hip.call(
+                    "spar_hip_launch_adamw", p.ptr, g.ptr, m.ptr, v.ptr, n, F, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+                    c1, c2, 0) for p, g, m, v, _ in sets], n)
+            measure("optim", "gradient norm summary", 4 * n, [lambda g=g, summary=summary: hip.call(
+                "spar_hip_launch_gradient_norm_summary", summary.ptr, g.ptr, n, F, 0)
+                for _, g, _, _, summary in sets], n)
+            measure("optim", "scale gradients in place", 8 * n, [lambda g=g: hip.call(
+                "spar_hip_launch_scale_in_place", g.ptr, n, F, 1.0, 0) for _, g, _, _, _ in sets], n)
+            del sets
+
+        return {"C1": c1, "C3": c3, "C4": c4, "C5": c5, "optim": optim}
 
 
 if __name__ == "__main__":

@@ -26,6 +26,25 @@ for its roofline ``traffic`` field.
 profiles one ``bench.py --suite-only SECTION`` run with ``--kernel-trace
 --stats`` and runs the same command without a profiler, then writes a
 per-kernel duration table next to the suite's own event-timed lines.
+
+    python3 -m spar_amd.rocprof_summary traffic --section C3 --raw DIR --out DIR
+
+measures every op of a suite section alone (``bench.py --suite-op
+SECTION/OP --profile-launches 4``): one ``--pmc FETCH_SIZE`` and one ``--pmc
+WRITE_SIZE`` pass per op, each ending with the calibration copy, and one pass
+of gfx950's request-size counters per section.  Dispatches between the
+bench's marker dispatches belong to the op; the summary gives each op's HBM
+bytes per launch, which bench.py reports as the op's ``traffic``.
+
+Why FETCH_SIZE needs the calibration factor on gfx950: rocprofv3 defines it
+(counter_defs.yaml) as (TCC_BUBBLE*128 + (TCC_EA0_RDREQ - TCC_BUBBLE -
+TCC_EA0_RDREQ_32B)*64 + TCC_EA0_RDREQ_32B*32) / 1024 KiB, where TCC_BUBBLE
+counts 128-byte read requests.  On gfx950 TCC_BUBBLE reads 0 while the
+streaming kernels' reads arrive as 128-byte requests, counted by
+TCC_EA0_RDREQ_128B: FETCH_SIZE prices each at 64 bytes and reports half the
+bytes read.  The request-size pass shows it directly: 32*RDREQ_32B +
+64*RDREQ_64B + 128*RDREQ_128B equals the algorithmic read bytes, and
+calibration against the 512 MiB copy gives the same factor, 2.0.
 """
 from __future__ import annotations
 
@@ -332,6 +351,173 @@ def read_traffic(path: Path):
     return found
 
 
+SUITE_FILES = {"C1": "c1_4096x4096", "C3": "c3_8192x8192", "C4": "c4_8192x32768",
+               "C5": "c5_4096x8192", "optim": "optim_124439808"}
+MARKER = r"touch_kernel"
+GENERATORS = r"normal_kernel<|uniform_f32_kernel|uniform_kernel<"
+REQUEST_COUNTERS = ["TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum",
+                    "TCC_BUBBLE_sum"]
+
+
+def suite_traffic_file(config: str) -> str:
+    return f"hbm_traffic_suite_{SUITE_FILES[config]}.md"
+
+
+def read_op_traffic(path: Path):
+    """{op: HBM bytes per launch} from a suite traffic summary ({} if absent)."""
+    if not path.exists():
+        return {}
+    found = {}
+    for m in re.finditer(r"^- op_hbm_bytes_per_launch\[(.+)\] = (\d+)$", path.read_text(), re.M):
+        found[m.group(1)] = int(m.group(2))
+    return found
+
+
+def dispatches(path: Path):
+    """[(dispatch id, kernel name, {counter: value})] in dispatch order."""
+    by_id = {}
+    for r in csv.DictReader(open(path)):
+        key = int(r["Dispatch_Id"])
+        entry = by_id.setdefault(key, (key, r["Kernel_Name"], {}))
+        entry[2][r["Counter_Name"]] = float(r["Counter_Value"])
+    return [by_id[k] for k in sorted(by_id)]
+
+
+def op_window(rows):
+    """Dispatches between the first and the last marker, markers excluded,
+    and the calibration copy (the last dispatch)."""
+    marks = [i for i, (_, name, _) in enumerate(rows) if re.search(MARKER, name)]
+    if len(marks) < 2:
+        raise SystemExit("expected marker dispatches around the op")
+    copy = rows[-1]
+    if not re.search(COPY_PATTERN, copy[1]):
+        raise SystemExit(f"last dispatch is not the calibration copy: {copy[1]}")
+    window = [row for row in rows[marks[0] + 1:marks[-1]] if not re.search(MARKER, row[1])]
+    return window, copy
+
+
+def bench_info(log: Path):
+    """The JSON line bench.py printed at the end of a --suite-op pass."""
+    if not log.exists():
+        return {}
+    for line in reversed(log.read_text().splitlines()):
+        line = line.strip()
+        if line.startswith('{"suite_op"'):
+            return json.loads(line)
+    return {}
+
+
+def suite_bench(op_spec: str, launches: int):
+    return [sys.executable, str(ROOT / "bench.py"), "--suite-op", op_spec,
+            "--profile-launches", str(launches)]
+
+
+def run_traffic(raw: Path, out: Path, section: str, limit: int, launches: int) -> None:
+    """Counter passes over every op of a section, then the summary."""
+    raw.mkdir(parents=True, exist_ok=True)
+    listing = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--list-suite-ops"],
+                             capture_output=True, text=True, check=True)
+    ops = json.loads(listing.stdout)[section]
+    plan = []
+    for k, op in enumerate(ops):
+        spec = f"{section}/{op}"
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            tag = f"op{k:02d}_{counter.lower()}"
+            plan.append((tag, ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d",
+                               str(raw / tag), "-o", tag, "--"] + suite_bench(spec, launches)))
+    largest = f"{section}/{ops[0]}"
+    plan.append(("requests", ["rocprofv3", "--pmc", *REQUEST_COUNTERS, "--output-format", "csv",
+                              "-d", str(raw / "requests"), "-o", "requests", "--"]
+                 + suite_bench(largest, launches)))
+    for tag, argv in plan:
+        print(f"pass {tag}: {shell(argv)}", flush=True)
+        with open(raw / f"{tag}.log", "w") as handle:
+            proc = subprocess.run(["timeout", "-s", "KILL", str(limit)] + argv, cwd="/tmp",
+                                  env=dict(os.environ, TMPDIR="/tmp"), stdout=handle,
+                                  stderr=subprocess.STDOUT)
+        if proc.returncode != 0:
+            sys.stdout.write((raw / f"{tag}.log").read_text()[-3000:])
+            raise SystemExit(f"pass {tag}: exit {proc.returncode}")
+    (raw / "plan.json").write_text(json.dumps({"section": section, "ops": ops,
+                                               "launches": launches,
+                                               "commands": {t: shell(a) for t, a in plan}}))
+    summarize_traffic(raw, out)
+
+
+def summarize_traffic(raw: Path, out: Path) -> None:
+    plan = json.loads((raw / "plan.json").read_text())
+    section, ops, launches = plan["section"], plan["ops"], plan["launches"]
+    cal_kib = CALIBRATION_BYTES / 1024
+    lines = [
+        f"# HBM traffic per launch: bench.py suite section {section}, "
+        f"{SUITE_WORKLOADS[section][1]}",
+        "",
+        "Generated (from the repository root) by",
+        "",
+        f"    python3 -m spar_amd.rocprof_summary traffic --section {section} "
+        f"--raw gpurun_out/traffic_{section} --out profiles",
+        "",
+        f"which runs two counter passes per op, for example (op `{ops[0]}`):",
+        "",
+        "    " + plan["commands"]["op00_fetch_size"],
+        "    " + plan["commands"]["op00_write_size"],
+        "",
+        f"Each pass runs the op alone {launches} times between marker dispatches and ends with",
+        "a plain contiguous copy of 512 MiB; each pass's FETCH_SIZE and WRITE_SIZE are",
+        "scaled by 512 MiB over the copy's reading, and the dispatches between the",
+        "markers (random generators excluded) are summed and divided by the launches.",
+        "",
+        "| op | kernels per launch | FETCH_SIZE scale | HBM read MB | HBM write MB | "
+        "HBM MB per launch | algorithmic MB | ratio |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    results = []
+    for k, op in enumerate(ops):
+        fetch_rows = dispatches(raw / f"op{k:02d}_fetch_size" / f"op{k:02d}_fetch_size_counter_collection.csv")
+        write_rows = dispatches(raw / f"op{k:02d}_write_size" / f"op{k:02d}_write_size_counter_collection.csv")
+        fwin, fcopy = op_window(fetch_rows)
+        wwin, wcopy = op_window(write_rows)
+        f_scale = cal_kib / fcopy[2]["FETCH_SIZE"]
+        w_scale = cal_kib / wcopy[2]["WRITE_SIZE"]
+        fwin = [r for r in fwin if not re.search(GENERATORS, r[1])]
+        wwin = [r for r in wwin if not re.search(GENERATORS, r[1])]
+        read = sum(r[2]["FETCH_SIZE"] for r in fwin) * f_scale * 1024 / launches
+        write = sum(r[2]["WRITE_SIZE"] for r in wwin) * w_scale * 1024 / launches
+        kernels = sorted({short(r[1]) for r in fwin})
+        results.append((op, round(read + write)))
+        info = bench_info(raw / f"op{k:02d}_fetch_size.log")
+        algorithmic = info.get("bytes")
+        ratio = f"{(read + write) / algorithmic:.3f}" if algorithmic else ""
+        alg_mb = f"{algorithmic / 1e6:.1f}" if algorithmic else ""
+        lines.append(f"| {op} | {'<br>'.join('`' + n + '`' for n in kernels)} | {f_scale:.3f} | "
+                     f"{read / 1e6:.1f} | {write / 1e6:.1f} | {(read + write) / 1e6:.1f} | "
+                     f"{alg_mb} | {ratio} |")
+    lines += ["", "HBM bytes per launch of each op (bench.py reads these lines):", ""]
+    lines += [f"- op_hbm_bytes_per_launch[{op}] = {value}" for op, value in results]
+    req = dispatches(raw / "requests" / "requests_counter_collection.csv")
+    rwin, rcopy = op_window(req)
+
+    def request_bytes(c):
+        return 32 * c["TCC_EA0_RDREQ_32B_sum"] + 64 * c["TCC_EA0_RDREQ_64B_sum"] + \
+            128 * c["TCC_EA0_RDREQ_128B_sum"]
+
+    lines += ["", "Read requests by size (gfx950 TCC counters; one pass, op `" + ops[0] + "`):",
+              "", "    " + plan["commands"]["requests"], "",
+              "| dispatch | 32 B | 64 B | 128 B | TCC_BUBBLE | bytes by request size |",
+              "|---|---|---|---|---|---|"]
+    for _, name, c in rwin[:6] + [rcopy]:
+        lines.append(f"| `{short(name)}` | {c['TCC_EA0_RDREQ_32B_sum']:.0f} | "
+                     f"{c['TCC_EA0_RDREQ_64B_sum']:.0f} | {c['TCC_EA0_RDREQ_128B_sum']:.0f} | "
+                     f"{c['TCC_BUBBLE_sum']:.0f} | {request_bytes(c) / 1e6:.1f} MB |")
+    lines += ["", "TCC_BUBBLE stays 0 on gfx950 while reads go out as 128-byte requests, so",
+              "FETCH_SIZE (which prices non-32-byte requests not counted by TCC_BUBBLE at 64",
+              "bytes) reads half; the request sizes give the copy's 536.9 MB directly."]
+    out.mkdir(parents=True, exist_ok=True)
+    target = out / suite_traffic_file(section)
+    target.write_text("\n".join(lines) + "\n")
+    print(f"wrote {target}", flush=True)
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     sub = p.add_subparsers(dest="mode", required=True)
@@ -347,11 +533,25 @@ def main():
     q.add_argument("--raw", type=Path, required=True)
     q.add_argument("--out", type=Path, required=True)
     q.add_argument("--limit", type=int, default=240, help="seconds per pass")
+    t = sub.add_parser("traffic")
+    t.add_argument("--section", required=True, choices=sorted(SUITE_FILES))
+    t.add_argument("--raw", type=Path, required=True)
+    t.add_argument("--out", type=Path, required=True)
+    t.add_argument("--limit", type=int, default=120, help="seconds per pass")
+    t.add_argument("--launches", type=int, default=4)
+    ts = sub.add_parser("summarize-traffic")
+    ts.add_argument("--raw", type=Path, required=True)
+    ts.add_argument("--out", type=Path, required=True)
     args = p.parse_args()
     if args.mode == "run":
         run(args.raw.resolve(), args.out.resolve(), args.limit)
     elif args.mode == "suite":
         run_suite(args.raw.resolve(), args.out.resolve(), args.section, args.limit)
+    elif args.mode == "traffic":
+        run_traffic(args.raw.resolve(), args.out.resolve(), args.section, args.limit,
+                    args.launches)
+    elif args.mode == "summarize-traffic":
+        summarize_traffic(args.raw.resolve(), args.out.resolve())
     else:
         summarize(args.raw.resolve(), args.out.resolve())
 
