@@ -54,6 +54,7 @@ import csv
 import json
 import os
 import re
+import shlex
 import subprocess
 import sys
 from pathlib import Path
@@ -111,7 +112,7 @@ def commands(raw: Path):
 
 def shell(argv) -> str:
     """The command as typed from the repository root."""
-    text = " ".join(argv)
+    text = " ".join(shlex.quote(str(a)) for a in argv)
     text = text.replace(sys.executable, "python3").replace(str(ROOT) + "/", "")
     return text
 
