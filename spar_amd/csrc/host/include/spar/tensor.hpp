@@ -245,4 +245,16 @@ void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
 void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward);
 [[nodiscard]] bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept;
 
+/// Process-wide tallies of the autograd engine: backward() calls, leaf
+/// gradients copied because their storage was shared, and gradient
+/// accumulations done in place or out of place.  The engine never copies an
+/// intermediate gradient.
+struct AutogradCounters final {
+  std::uint64_t backward_calls;
+  std::uint64_t leaf_copies;
+  std::uint64_t in_place_adds;
+  std::uint64_t out_of_place_adds;
+};
+[[nodiscard]] AutogradCounters autograd_counters() noexcept;
+
 }  // namespace spar::detail

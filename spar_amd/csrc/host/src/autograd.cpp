@@ -20,6 +20,7 @@
 // (autograd.cpp:145, :244); the clone only copied values, so leaving it out
 // changes no bit.  A held gradient whose storage another handle still sees
 // is added out of place (same operands, same order) instead of in place.
+#include <atomic>
 #include <unordered_map>
 
 #include "autograd_internal.hpp"
@@ -29,6 +30,12 @@
 
 namespace spar::detail {
 namespace {
+
+// Process-wide tallies of what backward() did with gradients.
+std::atomic<std::uint64_t> g_backward_calls{0};
+std::atomic<std::uint64_t> g_leaf_copies{0};
+std::atomic<std::uint64_t> g_in_place_adds{0};
+std::atomic<std::uint64_t> g_out_of_place_adds{0};
 
 GradInput input_of(const Tensor& parent) {
   return GradInput{TensorInternals::grad_state(parent), parent.shape(), parent.dtype(),
@@ -77,6 +84,11 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
   function->inputs.push_back(input_of(requiring_parent));
   function->rule = std::move(backward);
   attach(output, std::move(function));
+}
+
+AutogradCounters autograd_counters() noexcept {
+  return AutogradCounters{g_backward_calls.load(), g_leaf_copies.load(), g_in_place_adds.load(),
+                          g_out_of_place_adds.load()};
 }
 
 bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept {
@@ -186,8 +198,10 @@ class Sweep final {
       check_same_layout(*held, incoming);
       if (TensorInternals::sole_owner(*held)) {
         add_into(*held, incoming);
+        g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
       } else {
         held = add(held->detach(), incoming.detach());
+        g_out_of_place_adds.fetch_add(1, std::memory_order_relaxed);
       }
     }
   }
@@ -196,10 +210,15 @@ class Sweep final {
     if (leaf.accumulated.has_value()) {
       check_same_layout(*leaf.accumulated, gradient);
       add_into(*leaf.accumulated, gradient);  // in place: grad() handles see it
+      g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
       return;
     }
-    leaf.accumulated = TensorInternals::sole_owner(gradient) ? gradient.detach()
-                                                             : gradient.detach().clone();
+    if (TensorInternals::sole_owner(gradient)) {
+      leaf.accumulated = gradient.detach();
+    } else {
+      leaf.accumulated = gradient.detach().clone();
+      g_leaf_copies.fetch_add(1, std::memory_order_relaxed);
+    }
   }
 
   static constexpr std::size_t kUnplaced = static_cast<std::size_t>(-1);
@@ -260,6 +279,7 @@ void Tensor::backward() {
   if (!is_floating(dtype_)) {
     throw std::invalid_argument{"backward supports Float32 and Float64 losses only"};
   }
+  detail::g_backward_calls.fetch_add(1, std::memory_order_relaxed);
   detail::Sweep sweep{grad_state_.get()};
   sweep.run(grad_state_.get(), ones(shape_, dtype_, device()));
 }

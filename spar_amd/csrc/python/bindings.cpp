@@ -329,4 +329,13 @@ PYBIND11_MODULE(_spar, m) {
   });
   m.def("synchronize", &spar::synchronize, py::arg("device") = Device::hip(0));
   m.def("hip_device_count", &spar::hip_device_count);
+  m.def("autograd_counters", [] {
+    const auto c = spar::detail::autograd_counters();
+    py::dict d;
+    d["backward_calls"] = c.backward_calls;
+    d["leaf_copies"] = c.leaf_copies;
+    d["in_place_adds"] = c.in_place_adds;
+    d["out_of_place_adds"] = c.out_of_place_adds;
+    return d;
+  });
 }

@@ -404,3 +404,57 @@ def test_autograd_api_errors(sp):
         y.grad()
     with pytest.raises(ValueError):
         hip_tensor(sp, np.arange(3, dtype=np.int64)).set_requires_grad(True)
+
+
+def memory_stats():
+    import ctypes
+
+    from spar_amd import hip
+
+    stats = hip.MemoryStats()
+    hip.call("spar_hip_memory_stats", ctypes.byref(stats), 0)
+    return stats
+
+
+def test_layernorm_chain_second_run_allocates_nothing_and_copies_no_gradient(sp):
+    """A C5-shaped LayerNorm chain on a transposed view, forward and backward,
+    twice: the second run takes every block from the caching allocator (no
+    hipMalloc, cache hits > 0), and the engine neither copies a leaf gradient
+    nor adds out of place, because every gradient it holds owns its storage
+    (the reference cloned every contribution, autograd.cpp:145, :244)."""
+    device = sp.Device.hip(0)
+    rng = np.random.default_rng(71)
+    base = sp.Tensor.from_numpy(rng.standard_normal((2048, 1024)).astype(np.float32)).to(device)
+    gamma = sp.Tensor.from_numpy(rng.uniform(0.5, 1.5, 2048).astype(np.float32)).to(device)
+    beta = sp.Tensor.from_numpy(rng.uniform(-0.1, 0.1, 2048).astype(np.float32)).to(device)
+    G = sp.Tensor.from_numpy(rng.standard_normal((1024, 2048)).astype(np.float32)).to(device)
+    for leaf in (base, gamma, beta):
+        leaf.set_requires_grad(True)
+
+    def run():
+        for leaf in (base, gamma, beta):
+            leaf.zero_grad()
+        x = base.transpose(0, 1)
+        mu = sp.mean(x, [1], True)
+        xc = sp.subtract(x, mu)
+        var = sp.mean(sp.square(xc), [1], True)
+        y = sp.add(sp.multiply(sp.divide(xc, sp.sqrt(sp.add_scalar(var, 1e-5))), gamma), beta)
+        sp.sum(sp.multiply(y, G), None, False).backward()
+        sp.synchronize(device)
+        return [leaf.grad().to(sp.Device.cpu()).numpy() for leaf in (base, gamma, beta)]
+
+    first = run()
+    stats_before = memory_stats()
+    counters_before = sp.autograd_counters()
+    second = run()
+    stats_after = memory_stats()
+    counters_after = sp.autograd_counters()
+    assert stats_after.device_allocations == stats_before.device_allocations
+    assert stats_after.cache_hits > stats_before.cache_hits
+    assert counters_after["backward_calls"] == counters_before["backward_calls"] + 1
+    assert counters_after["leaf_copies"] == counters_before["leaf_copies"]
+    assert counters_after["out_of_place_adds"] == counters_before["out_of_place_adds"]
+    # x feeds mean and subtract, xc feeds square and divide: in-place adds
+    assert counters_after["in_place_adds"] > counters_before["in_place_adds"]
+    for a, b in zip(first, second):
+        assert_bitexact(b, a, "second run")

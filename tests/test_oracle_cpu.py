@@ -1,7 +1,7 @@
 """Pins the oracle (the C restatement of Spar's CPU loops) on the CPU.
 
 The reference ships no tests, fixtures or golden vectors and cannot be built
-here (oracle/build_reference.py), so each oracle function is checked against
+here (its sources need C++23 `import std`), so each oracle function is checked against
 something independent of its own code, chosen so a plausible restatement
 mistake (wrong loop order, transposed stride, dropped term, wrong rounding
 step) fails:
