@@ -23,6 +23,7 @@ INCLUDE = ROOT / "include"
 HIP_DIR = PACKAGE / "csrc" / "hip"
 HOST_DIR = PACKAGE / "csrc" / "host"
 PY_DIR = PACKAGE / "csrc" / "python"
+MODULE_DIR = PACKAGE / "csrc" / "module"
 LIB_DIR = PACKAGE / "lib"
 OBJ_DIR = ROOT / "_build" / "spar_amd"
 
@@ -115,12 +116,34 @@ def build_python_binding() -> Path:
     return target
 
 
+def build_module_binding() -> Path:
+    """Compiles spar.hip_ops (the C ABI as a C++23 named module, with
+    spar_hip.h in its global module fragment) and a consumer that imports
+    it, linked against libspar_hip.so: the binding Spar's own modules would
+    use.  Returns the consumer executable."""
+    clang = os.environ.get("CLANGXX", "/opt/rocm/llvm/bin/clang++")
+    flags = ["-std=c++23", "-O2", f"-I{INCLUDE}"]
+    pcm = OBJ_DIR / "spar_hip_ops.pcm"
+    _run([clang, *flags, "--precompile", str(MODULE_DIR / "spar_hip_ops.cppm"), "-o", str(pcm)])
+    module_obj = OBJ_DIR / "spar_hip_ops.o"
+    _run([clang, "-std=c++23", "-O2", "-c", str(pcm), "-o", str(module_obj)])
+    check_obj = OBJ_DIR / "module_check.o"
+    _run([clang, *flags, f"-fmodule-file=spar.hip_ops={pcm}", "-c",
+          str(MODULE_DIR / "module_check.cpp"), "-o", str(check_obj)])
+    target = LIB_DIR / "spar_hip_module_check"
+    _run([clang, str(check_obj), str(module_obj), f"-L{LIB_DIR}", "-lspar_hip",
+          "-Wl,-rpath,$ORIGIN", "-o", str(target)])
+    return target
+
+
 def build(jobs: int = 8) -> None:
     build_hip_library(jobs)
     if (HOST_DIR / "src").exists() and any((HOST_DIR / "src").glob("*.cpp")):
         build_host_library(jobs)
         if (PY_DIR / "bindings.cpp").exists():
             build_python_binding()
+    if MODULE_DIR.exists():
+        build_module_binding()
 
 
 def clean() -> None:

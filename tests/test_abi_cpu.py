@@ -80,3 +80,19 @@ def test_error_string():
     lib = hip.load()
     assert lib.spar_hip_error_string(0)
     assert lib.spar_hip_error_string(1)
+
+
+def test_module_binding_compiles_and_calls_the_abi():
+    """spar.hip_ops (spar_amd/csrc/module/spar_hip_ops.cppm) is a C++23 named
+    module with spar_hip.h in its global module fragment, as Spar's backend
+    modules include the CUDA header (src/backend/cuda_ops.cppm:1-5); build()
+    compiles it with clang++ --precompile and links a consumer that imports
+    it.  The consumer calls launchers through the module: an empty launch
+    succeeds and an invalid dtype becomes std::invalid_argument."""
+    import subprocess
+
+    binary = ROOT / "spar_amd" / "lib" / "spar_hip_module_check"
+    assert binary.exists(), "build() did not produce the module consumer"
+    run = subprocess.run([str(binary)], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "empty launch ok, invalid dtype rejected" in run.stdout
