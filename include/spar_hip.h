@@ -374,28 +374,33 @@ struct SparHipStatus spar_hip_launch_probability_backward(
 uint64_t spar_hip_norm_max_extent(int dtype);
 
 /* LayerNorm (center = 1) or RMSNorm (center = 0) over the last axis of a
- * contiguous [rows, extent] input, fused:
+ * [rows, extent] input whose rows start input_row_stride >= extent elements
+ * apart (extent for a contiguous input; larger for a block of a wider
+ * tensor), fused:
  *   LayerNorm: mu = sum(x)/n, xc = x - mu, d = sqrt(sum(xc*xc)/n + eps),
  *              y = (xc / d) * weight + bias
  *   RMSNorm:   d = sqrt(sum(x*x)/n + eps), y = (x / d) * weight
- * Writes y [rows, extent], d [rows] and, for LayerNorm, mu [rows] (`mean`
- * and `bias` are ignored and may be NULL for RMSNorm).  Replaces the composed
- * forward of RMSNorm, multiply(divide(x, sqrt(add_scalar(mean(square(x), -1,
- * true), eps))), weight) (src/nn/rmsnorm.cpp:50-52), and the same chain with
- * centring and a bias; the reference has no fused kernel for it. */
+ * Writes y [rows, extent] (contiguous), d [rows] and, for LayerNorm, mu
+ * [rows] (`mean` and `bias` are ignored and may be NULL for RMSNorm).
+ * Replaces the composed forward of RMSNorm, multiply(divide(x,
+ * sqrt(add_scalar(mean(square(x), -1, true), eps))), weight)
+ * (src/nn/rmsnorm.cpp:50-52), and the same chain with centring and a bias;
+ * the reference has no fused kernel for it. */
 struct SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void* denominator,
-                                                  const void* input, const void* weight,
-                                                  const void* bias, uint64_t rows, uint64_t extent,
-                                                  double epsilon, int center, int dtype,
-                                                  int device);
+                                                  const void* input, uint64_t input_row_stride,
+                                                  const void* weight, const void* bias,
+                                                  uint64_t rows, uint64_t extent, double epsilon,
+                                                  int center, int dtype, int device);
 
-/* Backward of the above from the saved mu and d: writes dx [rows, extent],
- * d weight [extent] and, for LayerNorm, d bias [extent] (sums over rows in a
- * fixed order).  Replaces the autograd backward of the composed chain. */
+/* Backward of the above from the saved mu and d: writes dx [rows, extent]
+ * (contiguous), d weight [extent] and, for LayerNorm, d bias [extent] (sums
+ * over rows in a fixed order).  The input rows start input_row_stride
+ * elements apart, as in the forward.  Replaces the autograd backward of the
+ * composed chain. */
 struct SparHipStatus spar_hip_launch_norm_backward(
     void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
-    const void* input, const void* weight, const void* mean, const void* denominator,
-    uint64_t rows, uint64_t extent, int center, int dtype, int device);
+    const void* input, uint64_t input_row_stride, const void* weight, const void* mean,
+    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device);
 
 /* --------------------------------------------- cross entropy (log-softmax + NLL) */
 

@@ -176,13 +176,13 @@ template <> __device__ __forceinline__ double norm_sqrt<double>(double x) { retu
 // grid-stride loop on [4096, 8192] and [8192, 8192] (bitwise equal).
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
-    norm_forward_kernel(T* out, T* mean_out, T* denominator_out, const T* in, const T* weight,
-                        const T* bias, uint64_t n, T eps) {
+    norm_forward_kernel(T* out, T* mean_out, T* denominator_out, const T* in, uint64_t in_stride,
+                        const T* weight, const T* bias, uint64_t n, T eps) {
   const T count = static_cast<T>(n);
   {
     const uint64_t r = blockIdx.x;
     T x[E];
-    norm_load<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
+    norm_load<T, THREADS, E, VEC, FULL>(x, in + r * in_stride, n);
     T mu = T(0);
     if constexpr (CENTER) {
       T local = T(0);
@@ -228,8 +228,8 @@ __global__ void __launch_bounds__(THREADS)
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     norm_backward_kernel(T* dx, T* partial_weight, T* partial_bias, const T* dy, const T* in,
-                         const T* weight, const T* mean, const T* denominator, uint64_t rows,
-                         uint64_t n) {
+                         uint64_t in_stride, const T* weight, const T* mean,
+                         const T* denominator, uint64_t rows, uint64_t n) {
   const T count = static_cast<T>(n);
   T acc_w[E];
   T acc_b[CENTER ? E : 1];
@@ -242,7 +242,7 @@ __global__ void __launch_bounds__(THREADS)
   for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     T x[E];
     T g[E];
-    norm_load<T, THREADS, E, VEC, FULL>(x, in + r * n, n);
+    norm_load<T, THREADS, E, VEC, FULL>(x, in + r * in_stride, n);
     norm_load<T, THREADS, E, VEC, FULL>(g, dy + r * n, n);
     const T mu = CENTER ? mean[r] : T(0);
     const Divisor<T> divide(denominator[r]);
@@ -344,6 +344,7 @@ struct NormArgs {
   void* mean;
   void* denominator;
   const void* input;
+  uint64_t input_stride;  // elements between the starts of two input rows
   const void* weight;
   const void* bias;
   uint64_t rows;
@@ -362,8 +363,8 @@ void forward_as(const NormArgs& a, const DeviceGuard& guard) {
       T* mean = a.mean != nullptr ? static_cast<T*>(a.mean) + first : nullptr;  // null for RMSNorm
       kernel<<<static_cast<uint32_t>(count), THREADS, 0, guard.stream>>>(
           static_cast<T*>(a.out) + first * a.n, mean, static_cast<T*>(a.denominator) + first,
-          static_cast<const T*>(a.input) + first * a.n, static_cast<const T*>(a.weight),
-          static_cast<const T*>(a.bias), a.n, eps);
+          static_cast<const T*>(a.input) + first * a.input_stride, a.input_stride,
+          static_cast<const T*>(a.weight), static_cast<const T*>(a.bias), a.n, eps);
     }
   };
   with_policy(stream_output(a.rows * a.n * sizeof(T)), [&](auto nt) {
@@ -382,6 +383,7 @@ struct NormBackwardArgs {
   void* dbias;
   const void* dy;
   const void* input;
+  uint64_t input_stride;
   const void* weight;
   const void* mean;
   const void* denominator;
@@ -419,7 +421,7 @@ hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard&
   with_policy(stream, [&](auto nt) {
     kernel_for(nt)<<<static_cast<uint32_t>(grid), THREADS, 0, guard.stream>>>(
         static_cast<T*>(a.dx), partial_weight, partial_bias, static_cast<const T*>(a.dy),
-        static_cast<const T*>(a.input), static_cast<const T*>(a.weight),
+        static_cast<const T*>(a.input), a.input_stride, static_cast<const T*>(a.weight),
         static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n);
   });
   const uint32_t combine_grid = grid_for((a.n + kWave - 1) / kWave);
@@ -500,12 +502,14 @@ extern "C" uint64_t spar_hip_norm_max_extent(int dtype) {
 }
 
 extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void* denominator,
-                                                      const void* input, const void* weight,
-                                                      const void* bias, uint64_t rows,
-                                                      uint64_t extent, double epsilon, int center,
-                                                      int dtype, int device) {
+                                                      const void* input, uint64_t input_row_stride,
+                                                      const void* weight, const void* bias,
+                                                      uint64_t rows, uint64_t extent,
+                                                      double epsilon, int center, int dtype,
+                                                      int device) {
   if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
       extent > spar_hip_norm_max_extent(dtype) || !(epsilon >= 0.0) ||
+      input_row_stride < extent ||
       (rows != 0 && (output == nullptr || denominator == nullptr || input == nullptr ||
                      weight == nullptr || (center && (mean == nullptr || bias == nullptr))))) {
     return invalid();
@@ -513,10 +517,12 @@ extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, 
   if (rows == 0) return ok();
   DeviceGuard guard;
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
-  const NormArgs a{output, mean, denominator, input, weight, bias, rows, extent, epsilon,
+  const NormArgs a{output,  mean, denominator, input,   input_row_stride,
+                   weight,  bias, rows,        extent,  epsilon,
                    center != 0};
   const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
-  const bool vec = aligned_rows(output, extent, width) && aligned_rows(input, extent, width) &&
+  const bool vec = aligned_rows(output, extent, width) &&
+                   aligned_rows(input, input_row_stride, width) && extent % width == 0 &&
                    aligned_rows(weight, extent, width) && aligned_rows(bias, extent, width);
   bool done = false;
   if (dtype == SPAR_HIP_FLOAT32) {
@@ -542,10 +548,10 @@ extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, 
 
 extern "C" SparHipStatus spar_hip_launch_norm_backward(
     void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
-    const void* input, const void* weight, const void* mean, const void* denominator,
-    uint64_t rows, uint64_t extent, int center, int dtype, int device) {
+    const void* input, uint64_t input_row_stride, const void* weight, const void* mean,
+    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device) {
   if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
-      extent > spar_hip_norm_max_extent(dtype) ||
+      extent > spar_hip_norm_max_extent(dtype) || input_row_stride < extent ||
       (rows != 0 &&
        (input_gradient == nullptr || weight_gradient == nullptr || output_gradient == nullptr ||
         input == nullptr || weight == nullptr || denominator == nullptr ||
@@ -561,12 +567,14 @@ extern "C" SparHipStatus spar_hip_launch_norm_backward(
     if (status.code == 0 && center) status = spar_hip_zero(bias_gradient, bytes, device);
     return status;
   }
-  const NormBackwardArgs a{input_gradient, weight_gradient, bias_gradient, output_gradient,
-                           input, weight, mean, denominator, rows, extent, center != 0};
+  const NormBackwardArgs a{input_gradient, weight_gradient,  bias_gradient, output_gradient,
+                           input,          input_row_stride, weight,        mean,
+                           denominator,    rows,             extent,        center != 0};
   const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
   const bool vec = aligned_rows(input_gradient, extent, width) &&
                    aligned_rows(output_gradient, extent, width) &&
-                   aligned_rows(input, extent, width) && aligned_rows(weight, extent, width);
+                   aligned_rows(input, input_row_stride, width) && extent % width == 0 &&
+                   aligned_rows(weight, extent, width);
   bool handled = false;
   hipError_t error = hipSuccess;
   if (dtype == SPAR_HIP_FLOAT32) {

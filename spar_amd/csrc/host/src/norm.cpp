@@ -60,6 +60,52 @@ Tensor composed(const Tensor& input, const Tensor& weight, const Tensor* bias, d
   return add(multiply(divide(centred, denominator), weight), *bias);
 }
 
+// Rows of `input` as the fused kernels read them: when the last axis is
+// contiguous and the leading axes step uniformly from row to row (a
+// contiguous tensor, or a block of a wider one such as a narrowed view), the
+// kernels read the rows in place, `stride` elements apart; otherwise the
+// input is made contiguous first.
+struct Rows {
+  Tensor source;        // the tensor whose storage the kernels read
+  const void* first;    // its first element
+  std::size_t stride;   // elements between row starts
+};
+
+std::optional<std::size_t> uniform_row_stride(const Tensor& input) {
+  const std::size_t rank{input.rank()};
+  if (input.strides()[rank - 1] != 1 && input.shape()[rank - 1] != 1) return std::nullopt;
+  std::optional<std::size_t> stride;
+  std::size_t inner_rows{1};  // rows spanned by the axes inside the current one
+  for (std::size_t axis{rank - 1}; axis-- > 0;) {
+    const auto extent{static_cast<std::size_t>(input.shape()[axis])};
+    if (extent == 1) continue;
+    if (!stride) {
+      stride = input.strides()[axis];
+    } else if (input.strides()[axis] != *stride * inner_rows) {
+      return std::nullopt;
+    }
+    inner_rows *= extent;
+  }
+  const auto extent{static_cast<std::size_t>(input.shape()[rank - 1])};
+  if (!stride) return extent;  // one row
+  if (*stride < extent) return std::nullopt;
+  return stride;
+}
+
+Rows rows_of(const Tensor& input) {
+  if (input.is_contiguous()) {
+    return Rows{input, HipTensorAccess::data(input),
+                static_cast<std::size_t>(input.shape()[input.rank() - 1])};
+  }
+  if (const auto stride{uniform_row_stride(input)}) {
+    const auto* base{static_cast<const std::byte*>(HipTensorAccess::storage_base(input))};
+    return Rows{input, base + input.storage_offset() * size_of(input.dtype()), *stride};
+  }
+  Tensor packed{input.contiguous()};
+  const void* first{HipTensorAccess::data(packed)};
+  return Rows{packed, first, static_cast<std::size_t>(input.shape()[input.rank() - 1])};
+}
+
 Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
              const char* name) {
   const bool center{bias != nullptr};
@@ -68,7 +114,7 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
     return composed(input, weight, bias, epsilon);
   }
   const std::size_t rows{input.numel() / extent};
-  const Tensor x{input.is_contiguous() ? input : input.contiguous()};
+  const Rows x{rows_of(input)};
   const Tensor w{weight.is_contiguous() ? weight : weight.contiguous()};
   std::optional<Tensor> b;
   if (center) b = bias->is_contiguous() ? *bias : bias->contiguous();
@@ -81,34 +127,40 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
   hip::check(spar_hip_launch_norm_forward(
                  HipTensorAccess::mutable_data(output),
                  center ? HipTensorAccess::mutable_data(*mean_rows) : nullptr,
-                 HipTensorAccess::mutable_data(denominator), HipTensorAccess::data(x),
+                 HipTensorAccess::mutable_data(denominator), x.first, x.stride,
                  HipTensorAccess::data(w), center ? HipTensorAccess::data(*b) : nullptr, rows,
                  extent, epsilon, center ? 1 : 0, hip::dtype_tag(input.dtype()), device),
              name, input.device());
 
-  const bool grad_x{x.requires_grad()}, grad_w{weight.requires_grad()};
+  // The parent is x.source: the input itself when its rows are read in
+  // place (its gradient then has the input's shape, contiguous), else its
+  // contiguous copy, whose node passes the gradient on to the input.
+  const bool grad_x{x.source.requires_grad()}, grad_w{weight.requires_grad()};
   const bool grad_b{center && bias->requires_grad()};
   if (grad_x || grad_w || grad_b) {
     std::vector<Tensor> parents;
-    if (grad_x) parents.push_back(x);
+    if (grad_x) parents.push_back(x.source);
     if (grad_w) parents.push_back(weight);
     if (grad_b) parents.push_back(*bias);
-    const Tensor saved_x{x.detach()}, saved_w{w.detach()};
+    const Tensor saved_x{x.source.detach()}, saved_w{w.detach()};
+    const std::size_t saved_stride{x.stride};
     const Shape weight_shape{weight.shape()};
     detail::record_operation(
         output, std::move(parents),
-        [saved_x, saved_w, mean_rows, denominator, rows, extent, center, grad_x, grad_w, grad_b,
-         weight_shape, name](const Tensor& gradient) {
+        [saved_x, saved_stride, saved_w, mean_rows, denominator, rows, extent, center, grad_x,
+         grad_w, grad_b, weight_shape, name](const Tensor& gradient) {
           const Tensor dy{gradient.is_contiguous() ? gradient.detach()
                                                    : gradient.detach().contiguous()};
           Tensor dx{saved_x.shape(), saved_x.dtype(), saved_x.device()};
           Tensor dw{weight_shape, saved_x.dtype(), saved_x.device()};
           std::optional<Tensor> db;
           if (center) db.emplace(weight_shape, saved_x.dtype(), saved_x.device());
+          const auto* base{static_cast<const std::byte*>(HipTensorAccess::storage_base(saved_x))};
+          const void* first{base + saved_x.storage_offset() * size_of(saved_x.dtype())};
           hip::check(spar_hip_launch_norm_backward(
                          HipTensorAccess::mutable_data(dx), HipTensorAccess::mutable_data(dw),
                          center ? HipTensorAccess::mutable_data(*db) : nullptr,
-                         HipTensorAccess::data(dy), HipTensorAccess::data(saved_x),
+                         HipTensorAccess::data(dy), first, saved_stride,
                          HipTensorAccess::data(saved_w),
                          center ? HipTensorAccess::data(*mean_rows) : nullptr,
                          HipTensorAccess::data(denominator), rows, extent, center ? 1 : 0,

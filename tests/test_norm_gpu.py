@@ -17,7 +17,7 @@ import pytest
 
 import oracle.reference as R
 from oracle import ops as ref
-from tests.helpers import assert_red
+from tests.helpers import assert_bitexact, assert_red
 
 pytestmark = pytest.mark.gpu
 
@@ -110,7 +110,7 @@ def forward_device(hip, x, w, b, center, dtype):
     rows, n = x.shape
     y, mu, d = out_buf(hip, rows * n, dtype), out_buf(hip, rows, dtype), out_buf(hip, rows, dtype)
     dx = dev(hip, x)
-    hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr, dx.ptr,
+    hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr, dx.ptr, n,
              dev(hip, w).ptr, dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center),
              tag(dtype), 0)
     return (y.to_numpy(dtype, (rows, n)), mu.to_numpy(dtype, (rows,)) if center else None,
@@ -165,8 +165,8 @@ def test_norm_backward_kernel(hip, dtype, center):
         _, _, _, (dx_in, mu, d) = forward_device(hip, x, w, b, center, dtype)
         dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
         hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
-                 dev(hip, g).ptr, dx_in.ptr, dev(hip, w).ptr, mu.ptr if center else None, d.ptr,
-                 rows, n, int(center), tag(dtype), 0)
+                 dev(hip, g).ptr, dx_in.ptr, n, dev(hip, w).ptr, mu.ptr if center else None,
+                 d.ptr, rows, n, int(center), tag(dtype), 0)
         tx = R.RTensor.of(x, requires_grad=True)
         tw = R.RTensor.of(w, requires_grad=True)
         tb = R.RTensor.of(b, requires_grad=True)
@@ -194,22 +194,24 @@ def test_norm_entry_points_reject_bad_arguments(hip):
     lib = hip.load()
     p = out_buf(hip, 64, F32).ptr
     bad = [
-        (p, p, p, p, p, p, 4, 0, EPSILON, 1, 0, 0),           # extent 0
-        (p, p, p, p, p, p, 4, 16385, EPSILON, 1, 0, 0),       # beyond the float32 limit
-        (p, p, p, p, p, p, 4, 8193, EPSILON, 1, 1, 0),        # beyond the float64 limit
-        (p, None, p, p, p, p, 4, 8, EPSILON, 1, 0, 0),        # LayerNorm without mean
-        (p, p, p, p, p, None, 4, 8, EPSILON, 1, 0, 0),        # LayerNorm without bias
-        (p, p, p, p, p, p, 4, 8, EPSILON, 2, 0, 0),           # center flag
-        (p, p, p, p, p, p, 4, 8, EPSILON, 1, 2, 0),           # integer dtype
-        (p, p, p, p, p, p, 4, 8, -1.0, 1, 0, 0),              # negative epsilon
+        (p, p, p, p, 8, p, p, 4, 0, EPSILON, 1, 0, 0),            # extent 0
+        (p, p, p, p, 16385, p, p, 4, 16385, EPSILON, 1, 0, 0),    # beyond the float32 limit
+        (p, p, p, p, 8193, p, p, 4, 8193, EPSILON, 1, 1, 0),      # beyond the float64 limit
+        (p, None, p, p, 8, p, p, 4, 8, EPSILON, 1, 0, 0),         # LayerNorm without mean
+        (p, p, p, p, 8, p, None, 4, 8, EPSILON, 1, 0, 0),         # LayerNorm without bias
+        (p, p, p, p, 8, p, p, 4, 8, EPSILON, 2, 0, 0),            # center flag
+        (p, p, p, p, 8, p, p, 4, 8, EPSILON, 1, 2, 0),            # integer dtype
+        (p, p, p, p, 8, p, p, 4, 8, -1.0, 1, 0, 0),               # negative epsilon
+        (p, p, p, p, 7, p, p, 4, 8, EPSILON, 1, 0, 0),            # rows overlap
     ]
     for args in bad:
         assert lib.spar_hip_launch_norm_forward(*args).code == 1, args
-    assert lib.spar_hip_launch_norm_backward(p, p, None, p, p, p, p, p, 4, 8, 1, 0, 0).code == 1
+    assert lib.spar_hip_launch_norm_backward(p, p, None, p, p, 8, p, p, p, 4, 8, 1, 0, 0).code == 1
+    assert lib.spar_hip_launch_norm_backward(p, p, p, p, p, 6, p, p, p, 4, 8, 1, 0, 0).code == 1
     # zero rows: parameter gradients are zero, nothing else is touched
     dw, db = out_buf(hip, 8, F32), out_buf(hip, 8, F32)
-    hip.call("spar_hip_launch_norm_backward", None, dw.ptr, db.ptr, None, None, p, None, None, 0,
-             8, 1, 0, 0)
+    hip.call("spar_hip_launch_norm_backward", None, dw.ptr, db.ptr, None, None, 8, p, None, None,
+             0, 8, 1, 0, 0)
     assert not dw.to_numpy(F32, (8,)).any() and not db.to_numpy(F32, (8,)).any()
 
 
@@ -254,15 +256,34 @@ def test_rms_norm_rejects_views_like_the_composition(sp):
 
 
 # (RMSNorm on a transposed view is an error, tested above.)
+# "narrowed" and "shifted" read the rows of a wider tensor in place (rows
+# 536 elements apart, starting at element 4 or 1 of the row: vector and
+# scalar paths).
+LAYOUT_VIEW = {
+    "contiguous": lambda t: t,
+    "transposed": lambda t: t.transpose(0, 1),
+    "narrowed": lambda t: t.narrow(1, 4, 520),
+    "shifted": lambda t: t.narrow(1, 1, 520),
+}
+
+
 @pytest.mark.parametrize("center,layout", [(True, "contiguous"), (True, "transposed"),
-                                           (False, "contiguous")])
+                                           (False, "contiguous"), (True, "narrowed"),
+                                           (True, "shifted")])
 def test_norm_api_forward_backward(sp, center, layout):
     rows, n = 96, 520
     x, w, b, g = data(rows, n, F32, 300)
-    base = np.ascontiguousarray(x.T) if layout == "transposed" else x
+    if layout == "transposed":
+        base = np.ascontiguousarray(x.T)
+    elif layout in ("narrowed", "shifted"):
+        start = 4 if layout == "narrowed" else 1
+        base = np.random.default_rng(303).standard_normal((rows, n + 16)).astype(F32)
+        base[:, start:start + n] = x
+    else:
+        base = x
 
     def build(lib, t):
-        xv = t[0].transpose(0, 1) if layout == "transposed" else t[0]
+        xv = LAYOUT_VIEW[layout](t[0])
         y = lib.layer_norm(xv, t[1], t[2], EPSILON) if center else lib.rms_norm(xv, t[1], EPSILON)
         loss = lib.sum(lib.multiply(y, t[3]))
         loss.backward()
@@ -274,6 +295,12 @@ def test_norm_api_forward_backward(sp, center, layout):
     dx_got, dx_want = td[0].grad().to(cpu).numpy(), tr[0].grad().numpy()
     if layout == "transposed":
         dx_got, dx_want = dx_got.T, dx_want.T
+    elif layout in ("narrowed", "shifted"):
+        start = 4 if layout == "narrowed" else 1
+        outside = np.ones(n + 16, bool)
+        outside[start:start + n] = False
+        assert not dx_got[:, outside].any() and not dx_want[:, outside].any()
+        dx_got, dx_want = dx_got[:, start:start + n], dx_want[:, start:start + n]
     # both gradients are back in [rows, n] orientation here
     assert_rows(dx_got, dx_want, n, F32, f"api dx {layout}", 16.0, dx_terms(g, w, x, center))
     for i in (1, 2) if center else (1,):
@@ -316,3 +343,55 @@ def test_norm_api_errors(sp):
         sp.rms_norm(x, sp.Tensor.from_numpy(np.ones(8, F64)).to(device))
     with pytest.raises(RuntimeError):
         sp.rms_norm(sp.Tensor.from_numpy(np.ones((4, 8), F32)), w)
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
+@pytest.mark.parametrize("rows,n,pitch,first", [(64, 1024, 1040, 4), (33, 4096, 4100, 0),
+                                                 (9, 1000, 1003, 3), (5, 8192, 8200, 8)])
+def test_norm_row_stride_matches_contiguous(hip, dtype, center, rows, n, pitch, first):
+    """Rows of a wider tensor (a sliced view's rows, `pitch` apart, starting
+    `first` elements in).  Where every row start stays 16-byte aligned the
+    kernels take the same vector path as for the rows made contiguous and
+    must give the same bits, forward and backward; otherwise they take the
+    scalar path, whose sums run in another order, and are held to the row
+    tolerance against the contiguous results."""
+    x, w, b, g = data(rows, n, dtype, 400 + n)
+    wide = np.zeros((rows + 1) * pitch, dtype)
+    for r in range(rows):
+        wide[first + r * pitch:first + r * pitch + n] = x[r]
+    y_ref, mu_ref, d_ref, (x_dev, mu, d) = forward_device(hip, x, w, b, center, dtype)
+    wide_dev = dev(hip, wide)
+    item = np.dtype(dtype).itemsize
+    y, mu2, d2 = out_buf(hip, rows * n, dtype), out_buf(hip, rows, dtype), out_buf(hip, rows, dtype)
+    hip.call("spar_hip_launch_norm_forward", y.ptr, mu2.ptr if center else None, d2.ptr,
+             wide_dev.address(first * item), pitch, dev(hip, w).ptr,
+             dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center), tag(dtype), 0)
+    item_aligned = (first * item) % 16 == 0 and (pitch * item) % 16 == 0
+
+    def same(got, want, what):
+        if item_aligned:
+            assert_bitexact(got, want, what)
+        elif got.ndim == 2:
+            assert_rows(got, want, n, dtype, what)
+        else:
+            bound = 1e-6 * np.sqrt(rows * n) * 8 * np.max(np.abs(want))
+            assert np.max(np.abs(got - want)) <= bound, what
+
+    same(y.to_numpy(dtype, (rows, n)), y_ref, "strided forward")
+    same(d2.to_numpy(dtype, (rows,)), d_ref, "strided denominator")
+    if center:
+        same(mu2.to_numpy(dtype, (rows,)), mu_ref, "strided mean")
+    outs = []
+    for source, stride in ((x_dev.ptr, n), (wide_dev.address(first * item), pitch)):
+        dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
+        hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
+                 dev(hip, g).ptr, source, stride, dev(hip, w).ptr, mu.ptr if center else None,
+                 d.ptr, rows, n, int(center), tag(dtype), 0)
+        outs.append([dx.to_numpy(dtype, (rows, n)), dw.to_numpy(dtype, (n,))] +
+                    ([db.to_numpy(dtype, (n,))] if center else []))
+    for a, c in zip(*outs):
+        if item_aligned or a.ndim == 1:
+            same(c, a, "strided backward")
+        else:
+            assert_rows(c, a, n, dtype, "strided backward dx", 16.0, dx_terms(g, w, x, center))
