@@ -374,12 +374,17 @@ struct SparHipStatus spar_hip_launch_probability_backward(
 uint64_t spar_hip_norm_max_extent(int dtype);
 
 /* LayerNorm (center = 1) or RMSNorm (center = 0) over the last axis of a
- * [rows, extent] input whose rows start input_row_stride >= extent elements
- * apart (extent for a contiguous input; larger for a block of a wider
- * tensor), fused:
+ * [rows, extent] strided input, fused:
  *   LayerNorm: mu = sum(x)/n, xc = x - mu, d = sqrt(sum(xc*xc)/n + eps),
  *              y = (xc / d) * weight + bias
  *   RMSNorm:   d = sqrt(sum(x*x)/n + eps), y = (x / d) * weight
+ * Element x[r][c] is input[r * input_row_stride + c * input_column_stride],
+ * in one of two layouts:
+ *   rows:    input_column_stride == 1 and input_row_stride >= extent (extent
+ *            for a contiguous input, more for a block of a wider tensor);
+ *   columns: input_row_stride == 1 and input_column_stride >= rows (the
+ *            transpose of a row-major [extent, input_column_stride] block);
+ *            a statistics pass and a tiled apply pass, no transposing copy.
  * Writes y [rows, extent] (contiguous), d [rows] and, for LayerNorm, mu
  * [rows] (`mean` and `bias` are ignored and may be NULL for RMSNorm).
  * Replaces the composed forward of RMSNorm, multiply(divide(x,
@@ -388,15 +393,16 @@ uint64_t spar_hip_norm_max_extent(int dtype);
  * the reference has no fused kernel for it. */
 struct SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void* denominator,
                                                   const void* input, uint64_t input_row_stride,
+                                                  uint64_t input_column_stride,
                                                   const void* weight, const void* bias,
                                                   uint64_t rows, uint64_t extent, double epsilon,
                                                   int center, int dtype, int device);
 
 /* Backward of the above from the saved mu and d: writes dx [rows, extent]
  * (contiguous), d weight [extent] and, for LayerNorm, d bias [extent] (sums
- * over rows in a fixed order).  The input rows start input_row_stride
- * elements apart, as in the forward.  Replaces the autograd backward of the
- * composed chain. */
+ * over rows in a fixed order).  The input is in the row layout of the
+ * forward: rows start input_row_stride >= extent elements apart, elements of
+ * a row adjacent.  Replaces the autograd backward of the composed chain. */
 struct SparHipStatus spar_hip_launch_norm_backward(
     void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
     const void* input, uint64_t input_row_stride, const void* weight, const void* mean,

@@ -16,6 +16,8 @@
 // order of the row sums differs (a tree instead of a sequential scan).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace spar_hip {
@@ -154,6 +156,8 @@ struct Divisor {
   T d;
   T r;
   __device__ __forceinline__ explicit Divisor(T value) : d(value), r(T(1) / value) {}
+  // `reciprocal` must be T(1) / value, computed once for many Divisors.
+  __device__ __forceinline__ Divisor(T value, T reciprocal) : d(value), r(reciprocal) {}
   __device__ __forceinline__ T operator()(T q) const {
     const T q0 = q * r;
     return __builtin_fma(__builtin_fma(-q0, d, q), r, q0);
@@ -215,6 +219,343 @@ __global__ void __launch_bounds__(THREADS)
       for (int j = 0; j < E; ++j) x[j] = x[j] + w[j];
     }
     norm_store<T, THREADS, E, VEC, FULL, NT>(out + r * n, x, n);
+  }
+}
+
+// ------------------------------------------------ rows down storage columns
+//
+// The same forward over a view whose rows run down the columns of its
+// storage: x[p][q] = in[p + q * pitch] for p < rows, q < n, with pitch >=
+// rows (x.transpose(0, 1) of a row-major [n, pitch] block).  A row of x is
+// then a column of the storage, and reading it as a row would take one
+// 4-byte piece of n different storage rows.  Two passes over x replace the
+// transposing copy and the row kernel (four passes):
+//
+//  1. norm_column_stats_kernel.  A workgroup owns a strip of kStatGroups
+//     16-byte groups of adjacent p (128 bytes of each storage row) and one of
+//     `splits` ranges of q.  Lane t takes group t % kStatGroups and q rows
+//     t / kStatGroups, + kStatRows, ..., R rows in flight, and sums in double
+//     s1 = sum(x - k) and s2 = sum((x - k)^2) with the shift k = x[p][0]
+//     (RMSNorm: k = 0 and only s2).  The kStatRows lanes of a group are
+//     added by a fixed LDS tree; the result is the pair partial[split][p].
+//  2. norm_apply_columns_kernel.  Tiles of 32 W values of p by 32 W values
+//     of q, staged through LDS as in the transposing elementwise path (XOR
+//     swizzle, the next tile's loads in flight during the stores, rotated
+//     tile order).  Before its stores a tile adds the partials of its p in
+//     split order: mean = k + s1 / n and var = (s2 - s1^2 / n) / n in double,
+//     rounded to T, then d = sqrt(var + eps) in T; the tiles of the first q
+//     column also write mean and d.  Each element is then computed as the
+//     row kernel computes it: y = (x - mean) / d * weight + bias, with the
+//     same quotient and the same order of float operations.
+//
+// The statistics are summed around a shift in double, so they are at least
+// as accurate as the row kernel's float sums; the two layouts agree within
+// rounding of the statistics, not bit for bit.
+constexpr int kStatThreads = 256;
+constexpr int kStatGroups = 8;
+constexpr int kStatRows = kStatThreads / kStatGroups;
+constexpr int kStatBatch = 8;        // q rows in flight per lane
+constexpr int kMaxStatSplits = 4;    // partials a tile adds (held in registers)
+constexpr int kApplyThreads = 256;
+constexpr int kApplyGranules = 32;   // tile side in 16-byte granules
+
+// The W elements of x[p .. p + W - 1][q] (zero past the last row).
+template <typename T, bool VEC>
+__device__ __forceinline__ typename Vec16<T>::type load_column_group(const T* in, uint64_t p,
+                                                                    uint64_t q, uint64_t pitch,
+                                                                    uint64_t rows) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  V v{};
+  if constexpr (VEC) {
+    // rows is a multiple of W: a group is wholly present or wholly absent
+    if (p < rows) v = stream_load(reinterpret_cast<const V*>(in + p + q * pitch));
+  } else {
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      if (p + k < rows) vec_set<T>(v, k, in[p + k + q * pitch]);
+    }
+  }
+  return v;
+}
+
+template <typename T, bool CENTER, bool VEC, int R>
+__global__ void __launch_bounds__(kStatThreads)
+    norm_column_stats_kernel(double2* partial, const T* in, uint64_t pitch, uint64_t rows,
+                             uint64_t n, uint64_t splits, uint64_t segment) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  constexpr int kColumns = kStatGroups * W;
+  constexpr int kSums = CENTER ? 2 : 1;
+  __shared__ double lds[kSums][kStatRows][kColumns];
+  const int group = threadIdx.x % kStatGroups;
+  const uint64_t lane_row = threadIdx.x / kStatGroups;
+  const uint64_t strips = (rows + kColumns - 1) / kColumns;
+  const uint64_t items = strips * splits;
+  for (uint64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    // strips fastest: workgroups side by side read neighbouring strips of
+    // the same storage rows
+    const uint64_t split = item / strips;
+    const uint64_t strip = item - split * strips;
+    const uint64_t p = strip * kColumns + static_cast<uint64_t>(group) * W;
+    const uint64_t begin = split * segment;
+    const uint64_t end = begin + segment < n ? begin + segment : n;
+    double shift[W];
+    double s1[W];
+    double s2[W];
+    {
+      const V first = CENTER ? load_column_group<T, VEC>(in, p, 0, pitch, rows) : V{};
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        shift[k] = static_cast<double>(vec_get<T>(first, k));
+        s1[k] = 0.0;
+        s2[k] = 0.0;
+      }
+    }
+    auto add = [&](const V& v) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const double d = static_cast<double>(vec_get<T>(v, k)) - shift[k];
+        if constexpr (CENTER) s1[k] += d;
+        s2[k] = __builtin_fma(d, d, s2[k]);
+      }
+    };
+    // Whether a lane's group has any element is fixed for the whole strip,
+    // so it is checked once, not per load, and the rows are walked with a
+    // pointer: no 64-bit multiply and no branch around each load, which kept
+    // the loads from issuing back to back.
+    const uint64_t first_q = begin + lane_row;
+    if (p < rows) {
+      const uint64_t step = static_cast<uint64_t>(kStatRows) * pitch;
+      const T* at = in + p + first_q * pitch;
+      uint64_t q = first_q;
+      for (; q + static_cast<uint64_t>(R - 1) * kStatRows < end; q += R * kStatRows) {
+        V v[R];
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          if constexpr (VEC) {
+            v[u] = stream_load(reinterpret_cast<const V*>(at + u * step));
+          } else {
+            v[u] = load_column_group<T, false>(in, p, q + u * kStatRows, pitch, rows);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // all R loads in flight first
+#pragma unroll
+        for (int u = 0; u < R; ++u) add(v[u]);
+        at += R * step;
+      }
+      for (; q < end; q += kStatRows) add(load_column_group<T, VEC>(in, p, q, pitch, rows));
+    }
+    __syncthreads();  // the previous item's readers are done with lds
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      lds[0][lane_row][group * W + k] = s2[k];
+      if constexpr (CENTER) lds[kSums - 1][lane_row][group * W + k] = s1[k];
+    }
+    __syncthreads();
+    for (int half = kStatRows / 2; half > 0; half /= 2) {
+      for (int e = threadIdx.x; e < half * kColumns; e += kStatThreads) {
+        const int row = e / kColumns;
+        const int c = e % kColumns;
+#pragma unroll
+        for (int s = 0; s < kSums; ++s) lds[s][row][c] += lds[s][row + half][c];
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x < kColumns) {
+      const uint64_t column = strip * kColumns + threadIdx.x;
+      if (column < rows) {
+        partial[split * rows + column] =
+            double2{CENTER ? lds[kSums - 1][0][threadIdx.x] : 0.0, lds[0][0][threadIdx.x]};
+      }
+    }
+  }
+}
+
+template <typename T, bool CENTER, bool VEC, bool NT>
+__global__ void __launch_bounds__(kApplyThreads)
+    norm_apply_columns_kernel(T* out, T* mean_out, T* denominator_out, const T* in,
+                              uint64_t pitch, const T* weight, const T* bias,
+                              const double2* partial, uint32_t splits, uint64_t rows, uint64_t n,
+                              T eps, FastDiv tiles_q, FastDiv tiles_p, uint32_t tile_count) {
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  constexpr int G = kApplyGranules;
+  constexpr int TP = G * W;
+  constexpr int TQ = G * W;
+  constexpr int kLoads = TQ * G / kApplyThreads;             // granules staged per lane
+  constexpr int kBlocks = (TQ / W) * G / kApplyThreads;      // W x W blocks stored per lane
+  static_assert(kApplyThreads % (TQ / W) == 0, "a lane keeps one q granule");
+  static_assert(kApplyThreads % G == 0, "a lane keeps its p granule for all its loads");
+  __shared__ V lds[TQ][G];
+  __shared__ T stat_mean[TP];
+  __shared__ T stat_d[TP];
+  __shared__ T stat_r[TP];
+  const double count = static_cast<double>(n);
+  struct Where {
+    uint64_t p0, q0;
+    bool first_column;
+  };
+  // q tiles fastest, each q column of tiles rotated along p by its index, so
+  // that workgroups side by side differ in both p and q.
+  auto locate = [&](uint32_t tile) {
+    const uint32_t rest = tiles_q.div(tile);
+    const uint32_t tq = tile - rest * tiles_q.divisor;
+    const uint32_t rotated = rest + tq % tiles_p.divisor;
+    const uint32_t tp = rotated >= tiles_p.divisor ? rotated - tiles_p.divisor : rotated;
+    return Where{static_cast<uint64_t>(tp) * TP, static_cast<uint64_t>(tq) * TQ, tq == 0};
+  };
+  V staged[kLoads];
+  double2 parts[kMaxStatSplits];
+  T shift = T(0);
+  // A lane's staged granules within a tile: p offset (lane % G) W, q offsets
+  // lane / G + it * kApplyThreads / G.
+  const uint64_t lane_offset = static_cast<uint64_t>(threadIdx.x % G) * W +
+                               static_cast<uint64_t>(threadIdx.x / G) * pitch;
+  const uint64_t load_step = static_cast<uint64_t>(kApplyThreads / G) * pitch;
+  auto load_tile = [&](const Where& w) {
+    if (VEC && w.p0 + TP <= rows && w.q0 + TQ <= n) {
+      // a whole tile: no bounds checks, pointer steps only
+      const T* at = in + w.p0 + w.q0 * pitch + lane_offset;
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        staged[it] = stream_load(reinterpret_cast<const V*>(at + it * load_step));
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const int index = it * kApplyThreads + threadIdx.x;
+        const uint64_t p = w.p0 + static_cast<uint64_t>(index % G) * W;
+        const uint64_t q = w.q0 + index / G;
+        staged[it] = q < n ? load_column_group<T, VEC>(in, p, q, pitch, rows) : V{};
+      }
+    }
+    const uint64_t p = w.p0 + threadIdx.x;
+    if (threadIdx.x < TP && p < rows) {
+#pragma unroll
+      for (int s = 0; s < kMaxStatSplits; ++s) {
+        if (static_cast<uint32_t>(s) < splits) parts[s] = partial[s * rows + p];
+      }
+      if constexpr (CENTER) shift = in[p];
+    }
+  };
+  uint32_t tile = blockIdx.x;
+  if (tile >= tile_count) return;
+  Where cur = locate(tile);
+  load_tile(cur);
+  while (true) {
+    const uint32_t next = tile + gridDim.x;
+    __syncthreads();  // the previous tile's LDS readers are done
+#pragma unroll
+    for (int it = 0; it < kLoads; ++it) {
+      const int index = it * kApplyThreads + threadIdx.x;
+      const int row = index / G;
+      lds[row][(index % G) ^ ((row / W) & 7)] = staged[it];
+    }
+    {
+      const uint64_t p = cur.p0 + threadIdx.x;
+      if (threadIdx.x < TP && p < rows) {
+        double s1 = 0.0;
+        double s2 = 0.0;
+#pragma unroll
+        for (int s = 0; s < kMaxStatSplits; ++s) {
+          if (static_cast<uint32_t>(s) < splits) {
+            s1 += parts[s].x;
+            s2 += parts[s].y;
+          }
+        }
+        double variance = CENTER ? (s2 - s1 * s1 / count) / count : s2 / count;
+        variance = variance > 0.0 ? variance : 0.0;
+        const T mu = CENTER ? static_cast<T>(static_cast<double>(shift) + s1 / count) : T(0);
+        const T d = norm_sqrt<T>(static_cast<T>(variance) + eps);
+        stat_mean[threadIdx.x] = mu;
+        stat_d[threadIdx.x] = d;
+        stat_r[threadIdx.x] = T(1) / d;
+        if (cur.first_column) {
+          if constexpr (CENTER) mean_out[p] = mu;
+          denominator_out[p] = d;
+        }
+      }
+    }
+    __syncthreads();
+    // A lane keeps one q granule m for all its blocks: its weight and bias
+    // groups are loaded once per tile, before the next tile's loads are
+    // issued (the wait counter retires vector loads in issue order, so a
+    // load issued after them would wait for them too).
+    const int m = threadIdx.x % (TQ / W);
+    const uint64_t q = cur.q0 + static_cast<uint64_t>(m) * W;
+    T w[W];
+    T b[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      w[k] = T(0);
+      b[k] = T(0);
+    }
+    if constexpr (VEC) {
+      if (q < n) {
+        const V wv = *reinterpret_cast<const V*>(weight + q);
+#pragma unroll
+        for (int k = 0; k < W; ++k) w[k] = vec_get<T>(wv, k);
+        if constexpr (CENTER) {
+          const V bv = *reinterpret_cast<const V*>(bias + q);
+#pragma unroll
+          for (int k = 0; k < W; ++k) b[k] = vec_get<T>(bv, k);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        if (q + k < n) {
+          w[k] = weight[q + k];
+          if constexpr (CENTER) b[k] = bias[q + k];
+        }
+      }
+    }
+    Where following = cur;
+    if (next < tile_count) {
+      following = locate(next);
+      load_tile(following);  // in flight during this tile's stores
+    }
+#pragma unroll
+    for (int it = 0; it < kBlocks; ++it) {
+      const int index = it * kApplyThreads + threadIdx.x;
+      const int g = index / (TQ / W);  // p granule within the tile
+      const uint64_t p = cur.p0 + static_cast<uint64_t>(g) * W;
+      if (q >= n || p >= rows) continue;
+      T values[W][W];  // [p offset][q offset]
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const V block = lds[m * W + k][g ^ (m & 7)];
+#pragma unroll
+        for (int i = 0; i < W; ++i) values[i][k] = vec_get<T>(block, i);
+      }
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        if (!VEC && p + i >= rows) break;
+        const T mu = stat_mean[g * W + i];
+        const Divisor<T> divide(stat_d[g * W + i], stat_r[g * W + i]);
+        V o;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          const T centred = CENTER ? values[i][k] - mu : values[i][k];
+          T y = divide(centred) * w[k];
+          if constexpr (CENTER) y = y + b[k];
+          vec_set<T>(o, k, y);
+        }
+        T* row = out + (p + i) * n + q;
+        if constexpr (VEC) {
+          store_vector<NT>(reinterpret_cast<V*>(row), o);
+        } else {
+#pragma unroll
+          for (int k = 0; k < W; ++k) {
+            if (q + k < n) row[k] = vec_get<T>(o, k);
+          }
+        }
+      }
+    }
+    if (next >= tile_count) break;
+    tile = next;
+    cur = following;
   }
 }
 
@@ -377,6 +718,63 @@ void forward_as(const NormArgs& a, const DeviceGuard& guard) {
   });
 }
 
+// Rows down storage columns: statistics pass, then the tiled apply pass.
+// The [splits, rows] partials come from the stream-ordered scratch pool.
+template <typename T, bool CENTER, bool VEC>
+hipError_t forward_columns_as(const NormArgs& a, uint64_t pitch, int device,
+                              const DeviceGuard& guard) {
+  constexpr int W = Vec16<T>::width;
+  constexpr uint64_t kColumns = static_cast<uint64_t>(kStatGroups) * W;
+  constexpr uint64_t kTile = static_cast<uint64_t>(kApplyGranules) * W;
+  const uint64_t tiles_p = (a.rows + kTile - 1) / kTile;
+  const uint64_t tiles_q = (a.n + kTile - 1) / kTile;
+  const uint64_t tiles = tiles_p * tiles_q;
+  // Splits of q: about one strip workgroup per CU, at most kMaxStatSplits,
+  // and at least one full batch of rows per lane.  On x^T for x [8192,
+  // 4096] float32 (128 strips) the statistics pass took 23.9 us with 2
+  // splits (one workgroup per CU), 26.5 us with 4 and 35.1 us with 1.
+  const uint64_t strips = (a.rows + kColumns - 1) / kColumns;
+  const uint64_t cus = static_cast<uint64_t>(guard.multiprocessors);
+  const uint64_t wanted = cus * 2;
+  uint64_t splits = (cus + strips / 2) / strips;
+  const uint64_t most = a.n / (static_cast<uint64_t>(kStatRows) * kStatBatch);
+  if (splits > most) splits = most;
+  if (splits > static_cast<uint64_t>(kMaxStatSplits)) splits = kMaxStatSplits;
+  if (splits < 1) splits = 1;
+  const uint64_t segment = (a.n + splits - 1) / splits;
+  splits = (a.n + segment - 1) / segment;
+  void* scratch = nullptr;
+  hipError_t error = scratch_allocate(&scratch, splits * a.rows * sizeof(double2), device);
+  if (error != hipSuccess) return error;
+  auto* partial = static_cast<double2*>(scratch);
+  const T* in = static_cast<const T*>(a.input);
+  norm_column_stats_kernel<T, CENTER, VEC, kStatBatch>
+      <<<grid_for(strips * splits), kStatThreads, 0, guard.stream>>>(partial, in, pitch, a.rows,
+                                                                    a.n, splits, segment);
+  FastDiv divide_q;
+  FastDiv divide_p;
+  divide_q.init(static_cast<uint32_t>(tiles_q));
+  divide_p.init(static_cast<uint32_t>(tiles_p));
+  with_policy(stream_output(a.rows * a.n * sizeof(T)), [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    const auto kernel = norm_apply_columns_kernel<T, CENTER, VEC, NT>;
+    // One workgroup per resident slot, each walking tiles; they do not
+    // depend on each other, so an unknown occupancy (0) takes two per CU.
+    uint64_t slots = resident_blocks(kernel, kApplyThreads, guard);
+    if (slots == 0) slots = wanted;
+    kernel<<<static_cast<uint32_t>(tiles < slots ? tiles : slots), kApplyThreads, 0,
+             guard.stream>>>(static_cast<T*>(a.out), static_cast<T*>(a.mean),
+                             static_cast<T*>(a.denominator), in, pitch,
+                             static_cast<const T*>(a.weight), static_cast<const T*>(a.bias),
+                             partial, static_cast<uint32_t>(splits), a.rows, a.n,
+                             static_cast<T>(a.eps), divide_q, divide_p,
+                             static_cast<uint32_t>(tiles));
+  });
+  error = hipGetLastError();
+  scratch_release(scratch, device);  // stream-ordered reuse
+  return error;
+}
+
 struct NormBackwardArgs {
   void* dx;
   void* dweight;
@@ -503,27 +901,71 @@ extern "C" uint64_t spar_hip_norm_max_extent(int dtype) {
 
 extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void* denominator,
                                                       const void* input, uint64_t input_row_stride,
+                                                      uint64_t input_column_stride,
                                                       const void* weight, const void* bias,
                                                       uint64_t rows, uint64_t extent,
                                                       double epsilon, int center, int dtype,
                                                       int device) {
+  // Row layout: elements of a row adjacent, rows input_row_stride >= extent
+  // apart.  Column layout: rows adjacent (row stride 1), a row's elements
+  // input_column_stride >= rows apart.
+  const bool row_layout = input_column_stride == 1 && input_row_stride >= extent;
+  const bool column_layout =
+      input_column_stride != 1 && input_row_stride == 1 && input_column_stride >= rows;
   if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
       extent > spar_hip_norm_max_extent(dtype) || !(epsilon >= 0.0) ||
-      input_row_stride < extent ||
+      !(row_layout || column_layout) ||
       (rows != 0 && (output == nullptr || denominator == nullptr || input == nullptr ||
                      weight == nullptr || (center && (mean == nullptr || bias == nullptr))))) {
     return invalid();
   }
   if (rows == 0) return ok();
+  const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
+  if (column_layout) {
+    const uint64_t tile = static_cast<uint64_t>(kApplyGranules) * width;
+    const uint64_t tiles = ((rows + tile - 1) / tile) * ((extent + tile - 1) / tile);
+    if (tiles > kIndex32Limit) return invalid();
+  }
   DeviceGuard guard;
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
   const NormArgs a{output,  mean, denominator, input,   input_row_stride,
                    weight,  bias, rows,        extent,  epsilon,
                    center != 0};
-  const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
-  const bool vec = aligned_rows(output, extent, width) &&
-                   aligned_rows(input, input_row_stride, width) && extent % width == 0 &&
-                   aligned_rows(weight, extent, width) && aligned_rows(bias, extent, width);
+  const bool parameters_vec = aligned_rows(output, extent, width) && extent % width == 0 &&
+                              aligned_rows(weight, extent, width) &&
+                              aligned_rows(bias, extent, width);
+  if (column_layout) {
+    const bool vec = parameters_vec && aligned_rows(input, input_column_stride, width) &&
+                     rows % static_cast<uint64_t>(width) == 0;
+    hipError_t error = hipSuccess;
+    auto run = [&](auto tag, auto center_tag, auto vec_tag) {
+      using T = decltype(tag);
+      error = forward_columns_as<T, decltype(center_tag)::value, decltype(vec_tag)::value>(
+          a, input_column_stride, device, guard);
+    };
+    auto with_vec = [&](auto tag, auto center_tag) {
+      if (vec) {
+        run(tag, center_tag, std::true_type{});
+      } else {
+        run(tag, center_tag, std::false_type{});
+      }
+    };
+    auto with_center = [&](auto tag) {
+      if (center) {
+        with_vec(tag, std::true_type{});
+      } else {
+        with_vec(tag, std::false_type{});
+      }
+    };
+    if (dtype == SPAR_HIP_FLOAT32) {
+      with_center(float{});
+    } else {
+      with_center(double{});
+    }
+    if (error != hipSuccess) return runtime(error);
+    return finish(guard);
+  }
+  const bool vec = parameters_vec && aligned_rows(input, input_row_stride, width);
   bool done = false;
   if (dtype == SPAR_HIP_FLOAT32) {
     if (center) {

@@ -391,6 +391,7 @@ __global__ void __launch_bounds__(kThreads)
   constexpr int TP = G * W;
   constexpr int TQ = G * W;
   constexpr int kLoads = TQ * G / kThreads;       // granules staged per lane
+  static_assert(kThreads % G == 0, "a lane keeps its p granule for all its loads");
   constexpr int kBlocks = (TQ / W) * G / kThreads;  // W x W blocks stored per lane
   __shared__ V lds[NSTAGED][TQ][G];
   const T* operands[2] = {a, b};
@@ -431,10 +432,24 @@ __global__ void __launch_bounds__(kThreads)
   // Staged operands in registers; with two, operand op uses slot op.
   V staged[NSTAGED][kLoads];
   auto load_tile = [&](const Where& w) {
+    const bool whole = w.p0 + TP <= tg.extent_p && w.q0 + TQ <= tg.extent_q;
 #pragma unroll
     for (int op = 0; op < NOPS; ++op) {
       if (tg.mode[op] != kStaged) continue;
       const int s = NSTAGED == 1 ? 0 : op;
+      if (whole) {
+        // a whole tile: no bounds checks; lane offset (lane % G) W along p,
+        // lane / G + it * kThreads / G along q
+        const T* at = operands[op] + w.base[op] + w.p0 + w.q0 * tg.stride_q[op] +
+                      static_cast<uint64_t>(threadIdx.x % G) * W +
+                      static_cast<uint64_t>(threadIdx.x / G) * tg.stride_q[op];
+        const uint64_t step = static_cast<uint64_t>(kThreads / G) * tg.stride_q[op];
+#pragma unroll
+        for (int it = 0; it < kLoads; ++it) {
+          staged[s][it] = stream_load(reinterpret_cast<const V*>(at + it * step));
+        }
+        continue;
+      }
 #pragma unroll
       for (int it = 0; it < kLoads; ++it) {
         const int index = it * kThreads + threadIdx.x;
@@ -467,15 +482,43 @@ __global__ void __launch_bounds__(kThreads)
       }
     }
     __syncthreads();
+    const uint64_t out_base = cur.out_base;
+    const uint64_t base[2] = {cur.base[0], cur.base[1]};
+    const uint64_t p0 = cur.p0;
+    const uint64_t q0 = cur.q0;
+    // An operand fixed along q (x^T - mu's mu) is read into registers before
+    // the next tile's staged loads are issued.  Vector memory operations
+    // complete in issue order as far as the wait counter goes, so a read
+    // issued after those loads could only be waited for together with them,
+    // and the store phase would stall until the next tile had landed.  Other
+    // direct operands are read in the store phase: holding their W x W
+    // blocks as well would take the kernel past 128 VGPRs, to one wave per
+    // SIMD.
+    constexpr bool kDirect = NOPS == 2 && NSTAGED == 1;
+    const int direct_op = tg.mode[0] == kStaged ? 1 : 0;
+    const bool fixed_direct = kDirect && tg.mode[direct_op] == kFixedQ;
+    T fixed[kDirect ? kBlocks : 1][W];
+    if constexpr (kDirect) {
+      if (fixed_direct) {
+        const int op = direct_op;
+#pragma unroll
+        for (int it = 0; it < kBlocks; ++it) {
+          const int index = it * kThreads + threadIdx.x;
+          const int m = index % (TQ / W);
+          const int g = index / (TQ / W);
+          const uint64_t q = q0 + static_cast<uint64_t>(m) * W;
+          const uint64_t p = p0 + static_cast<uint64_t>(g) * W;
+          if (q >= tg.extent_q || p >= tg.extent_p) continue;
+#pragma unroll
+          for (int i = 0; i < W; ++i) fixed[it][i] = operands[op][base[op] + (p + i) * tg.stride_p[op]];
+        }
+      }
+    }
     Where following = cur;
     if (next < tg.tile_count) {
       following = locate(next);
       load_tile(following);  // in flight during this tile's store phase
     }
-    const uint64_t out_base = cur.out_base;
-    const uint64_t base[2] = {cur.base[0], cur.base[1]};
-    const uint64_t p0 = cur.p0;
-    const uint64_t q0 = cur.q0;
 
 #pragma unroll
     for (int it = 0; it < kBlocks; ++it) {
@@ -495,6 +538,14 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
             for (int i = 0; i < W; ++i) values[op][i][k] = vec_get<T>(block, i);
           }
+        } else if (tg.mode[op] == kFixedQ) {
+          if constexpr (kDirect) {
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+#pragma unroll
+              for (int k = 0; k < W; ++k) values[op][i][k] = fixed[it][i];
+            }
+          }
         } else if (tg.mode[op] == kAlongQ) {
 #pragma unroll
           for (int i = 0; i < W; ++i) {
@@ -502,13 +553,6 @@ __global__ void __launch_bounds__(kThreads)
                                                        (p + i) * tg.stride_p[op] + q);
 #pragma unroll
             for (int k = 0; k < W; ++k) values[op][i][k] = vec_get<T>(row, k);
-          }
-        } else if (tg.mode[op] == kFixedQ) {
-#pragma unroll
-          for (int i = 0; i < W; ++i) {
-            const T value = operands[op][base[op] + (p + i) * tg.stride_p[op]];
-#pragma unroll
-            for (int k = 0; k < W; ++k) values[op][i][k] = value;
           }
         } else {
 #pragma unroll

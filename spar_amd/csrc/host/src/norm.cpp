@@ -60,15 +60,20 @@ Tensor composed(const Tensor& input, const Tensor& weight, const Tensor* bias, d
   return add(multiply(divide(centred, denominator), weight), *bias);
 }
 
-// Rows of `input` as the fused kernels read them: when the last axis is
-// contiguous and the leading axes step uniformly from row to row (a
-// contiguous tensor, or a block of a wider one such as a narrowed view), the
-// kernels read the rows in place, `stride` elements apart; otherwise the
-// input is made contiguous first.
+// Rows of `input` as the fused kernels read them, in place where the view
+// allows:
+//   row layout: the last axis contiguous and the leading axes stepping
+//     uniformly from row to row (a contiguous tensor, or a block of a wider
+//     one such as a narrowed view): rows `row_stride` elements apart;
+//   column layout: the leading axes contiguous among themselves and the
+//     last axis `column_stride` >= rows elements apart (a transposed matrix):
+//     the forward reads x without a transposing copy;
+// otherwise the input is made contiguous first.
 struct Rows {
-  Tensor source;        // the tensor whose storage the kernels read
-  const void* first;    // its first element
-  std::size_t stride;   // elements between row starts
+  Tensor source;              // the tensor whose storage the kernels read
+  const void* first;          // its first element
+  std::size_t row_stride;     // elements between row starts
+  std::size_t column_stride;  // elements between neighbours in a row
 };
 
 std::optional<std::size_t> uniform_row_stride(const Tensor& input) {
@@ -92,18 +97,38 @@ std::optional<std::size_t> uniform_row_stride(const Tensor& input) {
   return stride;
 }
 
-Rows rows_of(const Tensor& input) {
-  if (input.is_contiguous()) {
-    return Rows{input, HipTensorAccess::data(input),
-                static_cast<std::size_t>(input.shape()[input.rank() - 1])};
+std::optional<std::size_t> column_stride_of(const Tensor& input) {
+  const std::size_t rank{input.rank()};
+  if (rank < 2 || input.shape()[rank - 1] == 1) return std::nullopt;
+  std::size_t rows{1};  // row-major over the leading axes, innermost stride 1
+  for (std::size_t axis{rank - 1}; axis-- > 0;) {
+    const auto extent{static_cast<std::size_t>(input.shape()[axis])};
+    if (extent == 1) continue;
+    if (input.strides()[axis] != rows) return std::nullopt;
+    rows *= extent;
   }
+  const std::size_t stride{input.strides()[rank - 1]};
+  if (stride == 1 || stride < rows) return std::nullopt;
+  return stride;
+}
+
+const void* first_element(const Tensor& tensor) {
+  const auto* base{static_cast<const std::byte*>(HipTensorAccess::storage_base(tensor))};
+  return base + tensor.storage_offset() * size_of(tensor.dtype());
+}
+
+Rows rows_of(const Tensor& input) {
+  const auto extent{static_cast<std::size_t>(input.shape()[input.rank() - 1])};
+  if (input.is_contiguous()) return Rows{input, HipTensorAccess::data(input), extent, 1};
   if (const auto stride{uniform_row_stride(input)}) {
-    const auto* base{static_cast<const std::byte*>(HipTensorAccess::storage_base(input))};
-    return Rows{input, base + input.storage_offset() * size_of(input.dtype()), *stride};
+    return Rows{input, first_element(input), *stride, 1};
+  }
+  if (const auto stride{column_stride_of(input)}) {
+    return Rows{input, first_element(input), 1, *stride};
   }
   Tensor packed{input.contiguous()};
   const void* first{HipTensorAccess::data(packed)};
-  return Rows{packed, first, static_cast<std::size_t>(input.shape()[input.rank() - 1])};
+  return Rows{packed, first, extent, 1};
 }
 
 Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
@@ -127,7 +152,8 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
   hip::check(spar_hip_launch_norm_forward(
                  HipTensorAccess::mutable_data(output),
                  center ? HipTensorAccess::mutable_data(*mean_rows) : nullptr,
-                 HipTensorAccess::mutable_data(denominator), x.first, x.stride,
+                 HipTensorAccess::mutable_data(denominator), x.first, x.row_stride,
+                 x.column_stride,
                  HipTensorAccess::data(w), center ? HipTensorAccess::data(*b) : nullptr, rows,
                  extent, epsilon, center ? 1 : 0, hip::dtype_tag(input.dtype()), device),
              name, input.device());
@@ -143,24 +169,28 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
     if (grad_w) parents.push_back(weight);
     if (grad_b) parents.push_back(*bias);
     const Tensor saved_x{x.source.detach()}, saved_w{w.detach()};
-    const std::size_t saved_stride{x.stride};
+    const std::size_t saved_stride{x.row_stride};
+    const bool saved_columns{x.column_stride != 1};
     const Shape weight_shape{weight.shape()};
     detail::record_operation(
         output, std::move(parents),
-        [saved_x, saved_stride, saved_w, mean_rows, denominator, rows, extent, center, grad_x,
-         grad_w, grad_b, weight_shape, name](const Tensor& gradient) {
+        [saved_x, saved_stride, saved_columns, saved_w, mean_rows, denominator, rows, extent,
+         center, grad_x, grad_w, grad_b, weight_shape, name](const Tensor& gradient) {
           const Tensor dy{gradient.is_contiguous() ? gradient.detach()
                                                    : gradient.detach().contiguous()};
           Tensor dx{saved_x.shape(), saved_x.dtype(), saved_x.device()};
           Tensor dw{weight_shape, saved_x.dtype(), saved_x.device()};
           std::optional<Tensor> db;
           if (center) db.emplace(weight_shape, saved_x.dtype(), saved_x.device());
-          const auto* base{static_cast<const std::byte*>(HipTensorAccess::storage_base(saved_x))};
-          const void* first{base + saved_x.storage_offset() * size_of(saved_x.dtype())};
+          // The backward kernel reads rows: an input saved in the column
+          // layout is made contiguous here, once, instead of in the forward.
+          const Tensor x_rows{saved_columns ? saved_x.contiguous() : saved_x};
+          const void* first{first_element(x_rows)};
+          const std::size_t row_stride{saved_columns ? extent : saved_stride};
           hip::check(spar_hip_launch_norm_backward(
                          HipTensorAccess::mutable_data(dx), HipTensorAccess::mutable_data(dw),
                          center ? HipTensorAccess::mutable_data(*db) : nullptr,
-                         HipTensorAccess::data(dy), first, saved_stride,
+                         HipTensorAccess::data(dy), first, row_stride,
                          HipTensorAccess::data(saved_w),
                          center ? HipTensorAccess::data(*mean_rows) : nullptr,
                          HipTensorAccess::data(denominator), rows, extent, center ? 1 : 0,

@@ -110,7 +110,7 @@ def forward_device(hip, x, w, b, center, dtype):
     rows, n = x.shape
     y, mu, d = out_buf(hip, rows * n, dtype), out_buf(hip, rows, dtype), out_buf(hip, rows, dtype)
     dx = dev(hip, x)
-    hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr, dx.ptr, n,
+    hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr, dx.ptr, n, 1,
              dev(hip, w).ptr, dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center),
              tag(dtype), 0)
     return (y.to_numpy(dtype, (rows, n)), mu.to_numpy(dtype, (rows,)) if center else None,
@@ -194,15 +194,17 @@ def test_norm_entry_points_reject_bad_arguments(hip):
     lib = hip.load()
     p = out_buf(hip, 64, F32).ptr
     bad = [
-        (p, p, p, p, 8, p, p, 4, 0, EPSILON, 1, 0, 0),            # extent 0
-        (p, p, p, p, 16385, p, p, 4, 16385, EPSILON, 1, 0, 0),    # beyond the float32 limit
-        (p, p, p, p, 8193, p, p, 4, 8193, EPSILON, 1, 1, 0),      # beyond the float64 limit
-        (p, None, p, p, 8, p, p, 4, 8, EPSILON, 1, 0, 0),         # LayerNorm without mean
-        (p, p, p, p, 8, p, None, 4, 8, EPSILON, 1, 0, 0),         # LayerNorm without bias
-        (p, p, p, p, 8, p, p, 4, 8, EPSILON, 2, 0, 0),            # center flag
-        (p, p, p, p, 8, p, p, 4, 8, EPSILON, 1, 2, 0),            # integer dtype
-        (p, p, p, p, 8, p, p, 4, 8, -1.0, 1, 0, 0),               # negative epsilon
-        (p, p, p, p, 7, p, p, 4, 8, EPSILON, 1, 0, 0),            # rows overlap
+        (p, p, p, p, 8, 1, p, p, 4, 0, EPSILON, 1, 0, 0),            # extent 0
+        (p, p, p, p, 16385, 1, p, p, 4, 16385, EPSILON, 1, 0, 0),    # beyond the float32 limit
+        (p, p, p, p, 8193, 1, p, p, 4, 8193, EPSILON, 1, 1, 0),      # beyond the float64 limit
+        (p, None, p, p, 8, 1, p, p, 4, 8, EPSILON, 1, 0, 0),         # LayerNorm without mean
+        (p, p, p, p, 8, 1, p, None, 4, 8, EPSILON, 1, 0, 0),         # LayerNorm without bias
+        (p, p, p, p, 8, 1, p, p, 4, 8, EPSILON, 2, 0, 0),            # center flag
+        (p, p, p, p, 8, 1, p, p, 4, 8, EPSILON, 1, 2, 0),            # integer dtype
+        (p, p, p, p, 8, 1, p, p, 4, 8, -1.0, 1, 0, 0),               # negative epsilon
+        (p, p, p, p, 7, 1, p, p, 4, 8, EPSILON, 1, 0, 0),            # rows overlap
+        (p, p, p, p, 1, 3, p, p, 4, 8, EPSILON, 1, 0, 0),            # columns overlap
+        (p, p, p, p, 8, 2, p, p, 4, 8, EPSILON, 1, 0, 0),            # neither layout
     ]
     for args in bad:
         assert lib.spar_hip_launch_norm_forward(*args).code == 1, args
@@ -365,7 +367,7 @@ def test_norm_row_stride_matches_contiguous(hip, dtype, center, rows, n, pitch, 
     item = np.dtype(dtype).itemsize
     y, mu2, d2 = out_buf(hip, rows * n, dtype), out_buf(hip, rows, dtype), out_buf(hip, rows, dtype)
     hip.call("spar_hip_launch_norm_forward", y.ptr, mu2.ptr if center else None, d2.ptr,
-             wide_dev.address(first * item), pitch, dev(hip, w).ptr,
+             wide_dev.address(first * item), pitch, 1, dev(hip, w).ptr,
              dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center), tag(dtype), 0)
     item_aligned = (first * item) % 16 == 0 and (pitch * item) % 16 == 0
 
@@ -395,3 +397,49 @@ def test_norm_row_stride_matches_contiguous(hip, dtype, center, rows, n, pitch, 
             same(c, a, "strided backward")
         else:
             assert_rows(c, a, n, dtype, "strided backward dx", 16.0, dx_terms(g, w, x, center))
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
+@pytest.mark.parametrize("rows,n,pitch,first", [
+    (512, 1024, 512, 0),     # a transposed contiguous matrix: vector path, 2 splits
+    (200, 520, 264, 4),      # a transposed block of a wider matrix
+    (37, 300, 41, 3),        # unaligned: scalar loads and stores
+    (8, 8192, 8, 0),         # few rows, long rows: 4 splits
+    (130, 12, 130, 0),       # partial tiles in both directions, one split
+    (3, 5, 7, 1),            # tiny and ragged
+])
+def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
+    """Rows that run down storage columns (x[p][q] = in[p + q * pitch]) against
+    the row kernel on the same rows made contiguous.  The column path sums its
+    statistics around a shift in double, the row kernel in T, so the two agree
+    within the statistics' rounding: y within the row tolerance, mean and d
+    within a few ulp of the row's scale."""
+    x, w, b, g = data(rows, n, dtype, 500 + rows + n)
+    store = np.zeros(first + n * pitch, dtype)
+    store[first:].reshape(n, pitch)[:, :rows] = x.T
+    # highest element read: first + (rows - 1) + (n - 1) * pitch < store.size
+    assert first + rows - 1 + (n - 1) * pitch < store.size
+    y_ref, mu_ref, d_ref, _ = forward_device(hip, x, w, b, center, dtype)
+    store_dev = dev(hip, store)
+    item = np.dtype(dtype).itemsize
+    y, mu, d = out_buf(hip, rows * n, dtype), out_buf(hip, rows, dtype), out_buf(hip, rows, dtype)
+    hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr,
+             store_dev.address(first * item), 1, pitch, dev(hip, w).ptr,
+             dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center), tag(dtype), 0)
+    assert_rows(y.to_numpy(dtype, (rows, n)), y_ref, n, dtype, "column layout y")
+    eps = np.finfo(dtype).eps
+    scale = np.max(np.abs(x.astype(np.float64)), axis=1)
+    got_d = d.to_numpy(dtype, (rows,)).astype(np.float64)
+    assert np.all(np.abs(got_d - d_ref) <= 8 * eps * np.sqrt(n) * d_ref), "column layout d"
+    if center:
+        got_mu = mu.to_numpy(dtype, (rows,)).astype(np.float64)
+        assert np.all(np.abs(got_mu - mu_ref) <= 8 * eps * np.sqrt(n) * scale), "column layout mean"
+    # and against float64 statistics computed here
+    x64 = x.astype(np.float64)
+    mean64 = x64.mean(axis=1) if center else np.zeros(rows)
+    d64 = np.sqrt(((x64 - mean64[:, None]) ** 2).mean(axis=1) + EPSILON)
+    # float32: the double sums are exact to well below an ulp of T; float64:
+    # they carry their own rounding, a random walk over the row
+    allowance = 4.0 if dtype == F32 else 8.0 * np.sqrt(n)
+    assert np.all(np.abs(got_d - d64) <= allowance * eps * d64), "column layout d vs float64"
