@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
+#include "gelu_table.hpp"
 #include "spar_hip.h"
 
 namespace spar_hip {
@@ -152,21 +153,30 @@ __device__ __forceinline__ double gelu_derivative_double(double x) {
   return cdf + x * pdf;
 }
 
-// fp32 inputs need the double value only to within 2^-24 relative for the
-// rounded float32 result to stay within 1 ulp of the definition's, which a
-// short dedicated evaluation gives at a fraction of a full double erfc's
-// cost (the library erfc made GELU compute-bound at 29% of HBM bandwidth).
-// The normal upper tail Q(a) = 0.5 erfc(a / sqrt 2), 0 <= a <= 15, is
-// exp(-a^2/2) * M(a) with M(a) = 0.5 erfcx(a / sqrt 2) a degree-10
-// polynomial in t = s - mid, s = 1 / (1 + a / 3.5), relative error 2.0e-9
-// (coefficients from fit_normal_tail.py).  a^2 / 2 is exact in double for a
-// float a; its exp uses a Cody-Waite reduction by ln 2 and a degree-8 Taylor
-// polynomial on |r| <= ln(2)/2 (error 2.0e-10).  The reciprocal is
-// v_rcp_f64 (measured 2^-24.4) with one Newton step.  Checked on every
-// float32 input against the double definition: GELU within 1 ulp (0.23% of
-// inputs differ by 1 ulp, mostly ties of subnormal results); the derivative
-// within 1 ulp except for x in [-0.7576, -0.7473], where Phi(x) + x phi(x)
-// cancels near its root and the error stays below 2.4e-10 absolute.
+// fp32 inputs need the double value of the definition only to within 2^-25
+// relative for the rounded float32 result to stay within 1 ulp of the
+// correctly rounded one, which short dedicated evaluations give at a
+// fraction of a full double erfc's cost (the library erfc made GELU
+// compute-bound at 29% of HBM bandwidth).
+//
+// GELU reads Q(a) = 0.5 erfc(a / sqrt 2), 0 <= a <= 15, from a table of
+// piecewise polynomials (gelu_table.hpp, fit_gelu_table.py): the piece is
+// i = floor(g) for g = 2a + a^2/2, and a degree-6 polynomial in fract(g)
+// gives Q to 1.0e-8 relative, about 23 VALU instructions per element against
+// about 50 for an exp and a global polynomial.  The contiguous kernel holds
+// the table in LDS; other layouts read it from global memory.
+//
+// The derivative needs the density exp(-a^2/2) as well, and keeps the
+// direct evaluation: the normal upper tail Q(a) is exp(-a^2/2) * M(a) with
+// M(a) = 0.5 erfcx(a / sqrt 2) a degree-10 polynomial in t = s - mid,
+// s = 1 / (1 + a / 3.5), relative error 2.0e-9 (coefficients from
+// fit_normal_tail.py).  a^2 / 2 is exact in double for a float a; its exp
+// uses a Cody-Waite reduction by ln 2 and a degree-8 Taylor polynomial on
+// |r| <= ln(2)/2 (error 2.0e-10).  The reciprocal is v_rcp_f64 (measured
+// 2^-24.4) with one Newton step.  Checked on every float32 input against
+// the double definition: the derivative within 1 ulp except for x in
+// [-0.7576, -0.7473], where Phi(x) + x phi(x) cancels near its root and the
+// error stays below 2.4e-10 absolute.
 constexpr double kTailInvKappa = 0x1.2492492492492p-2;
 constexpr double kTailMid = 0x1.306eb3e45306fp-1;
 constexpr double kTailCoefficient[11] = {
@@ -223,23 +233,33 @@ __device__ __forceinline__ NormalTail normal_tail(double a) {
   return NormalTail{density, density * m};
 }
 
-// Any input, without branches: |x| is clamped to 15, and the results
-// outside [-15, 15] are patched.  There the exact GELU and derivative round
-// to -0 in float32 below -15; above 15, GELU rounds to x and the derivative
-// to 1, which the clamped evaluation already gives for finite x.  +inf maps
-// to +inf (GELU) and -inf to NaN, as (0.5 x) erfc(-x / sqrt 2) does, and both
-// infinities give a NaN derivative (x exp(-x^2/2) = inf * 0).  NaN inputs
-// propagate through the arithmetic.
-__device__ __forceinline__ float gelu_float(float value) {
+// GELU of a float32 from the tail table at `table` (global memory or an LDS
+// copy: the same values, so the same bits).  No branches and no patched
+// results: x is clamped to [-15, 15] inside the product, where Q(15) = 3.7e-51
+// already makes GELU round to -0 below -15 and to x above 15, and +inf stays
+// +inf (inf - 15 Q(15)).  Below 0 the product gains x - x, which is 0 for a
+// finite x and NaN for -inf, as (0.5 x) erfc(-x / sqrt 2) is; NaN inputs
+// take the x >= 0 form and propagate through it.
+__device__ __forceinline__ float gelu_float(float value, const double* table) {
   const double x = value;
-  const NormalTail tail = normal_tail(fmin(__builtin_fabs(x), 15.0));
-  const double xq = x * tail.upper;
-  float out = static_cast<float>(x < 0.0 ? xq : x - xq);
-  out = value < -15.0f ? -0.0f : out;
-  out = __builtin_isinf(value) ? (value > 0.0f ? value : __builtin_nanf("")) : out;
-  return out;
+  const double clamped = fmin(fmax(x, -kGeluTailLimit), kGeluTailLimit);
+  const double a = __builtin_fabs(clamped);
+  const double g = a * __builtin_fma(kGeluBeta, a, kGeluAlpha);
+  const double* c = table + static_cast<int>(g) * kGeluStride;
+  const double t = __builtin_amdgcn_fract(g);
+  double q = c[kGeluDegree];
+#pragma unroll
+  for (int k = kGeluDegree - 1; k >= 0; --k) q = __builtin_fma(q, t, c[k]);
+  const double negative = clamped * q + (x - x);
+  const double positive = __builtin_fma(-clamped, q, x);
+  return static_cast<float>(x < 0.0 ? negative : positive);
 }
 
+// The derivative: |x| is clamped to 15 and the results outside [-15, 15]
+// are patched.  There the exact derivative rounds to -0 in float32 below
+// -15 and to 1 above 15, which the clamped evaluation already gives for
+// finite x; both infinities give NaN (x exp(-x^2/2) = inf * 0).  NaN inputs
+// propagate through the arithmetic.
 __device__ __forceinline__ float gelu_derivative_float(float value) {
   const double x = value;
   const NormalTail tail = normal_tail(fmin(__builtin_fabs(x), 15.0));
@@ -255,7 +275,7 @@ __device__ __forceinline__ float gelu_derivative_float(float value) {
 template <typename F> struct VectorsPerLane { static constexpr int value = 1; };
 
 struct GeluOp {
-  __device__ __forceinline__ float operator()(float x) const { return gelu_float(x); }
+  __device__ __forceinline__ float operator()(float x) const { return gelu_float(x, kGeluTable); }
   __device__ __forceinline__ double operator()(double x) const { return gelu_double(x); }
 };
 

@@ -157,6 +157,27 @@ def test_unaligned_pointers_take_scalar_path(hip):
     assert_bitexact(got, ref.binary(a[1:], b[1:], "add"), "unaligned add")
 
 
+@pytest.mark.parametrize("n", [1, 3, 1027, 4099, 2 * 512 * 2 * 4 + 13, 1 << 20])
+def test_gelu_layouts_agree(hip, n):
+    """GELU float32 reads its tail table from LDS in the contiguous kernel
+    (whole tiles, leftover vectors, leftover elements) and from global memory
+    on the unaligned scalar path and on strided views: the same bits, within
+    1 ulp of the double definition."""
+    x = np.random.default_rng(n).standard_normal(n + 1).astype(F32) * 4
+    x[: min(n, 8)] = np.array([0.0, -0.0, 15.0, -15.0, 15.5, -15.5, np.inf, -np.inf], F32)[: min(n, 8)]
+    d = dev(hip, x)
+    aligned, shifted = out_buf(hip, (n + 1,), F32), out_buf(hip, (n + 1,), F32)
+    hip.call("spar_hip_launch_unary", aligned.ptr, d.ptr, n, 0, hip.GELU, 0)
+    hip.call("spar_hip_launch_unary", shifted.address(4), d.address(4), n, 0, hip.GELU, 0)
+    got = aligned.to_numpy(F32, (n + 1,))[:n]
+    got_shifted = shifted.to_numpy(F32, (n + 1,))[1:]
+    want = ref.unary(x, "gelu")
+    assert_ulp(got, want[:n], 1, "gelu contiguous")
+    assert_ulp(got_shifted, want[1:], 1, "gelu unaligned")
+    # the element both calls computed from x[k] for 1 <= k < n: same bits
+    assert_bitexact(got[1:], got_shifted[: n - 1], "gelu LDS table vs global table")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_fill_add_in_place_zero(hip, dtype):
     n = 12345
