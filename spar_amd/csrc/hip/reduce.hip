@@ -482,85 +482,93 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// Max/argmax in one pass when the kept axis is contiguous and wide enough
-// to give every CU its own strip of columns: a workgroup owns the 128 bytes
-// (kStripGroups 16-byte groups) of adjacent columns of one strip and every
-// row.  Lane t takes group t % kStripGroups and rows t / kStripGroups,
+// Max/argmax in one pass when the kept axis is contiguous and wide enough to
+// give every CU its own strip of columns (the kernel also sums, but slower
+// than the split scan): a workgroup owns the 128
+// bytes (kStripGroups 16-byte groups) of adjacent columns of one strip and
+// every row.  Lane t takes group t % kStripGroups and rows t / kStripGroups,
 // + kStripRows, ... in increasing order, R rows in flight, so each lane's
 // accumulators see their elements in index order; the lanes of a column then
-// merge through LDS under the full (NaN, value, index) rule, whose result
-// does not depend on the merge order.  No partials and no second kernel: on
-// [8192, 8192] over axis 0 the 256 strips read 128-byte pieces of every row
-// side by side, and the argmax took 42.0 us against 50.2 us for the split
-// scan plus combine (steady state, MI355X).  Lanes that saw a NaN rescan
-// their rows with the exact rule, as the other scans do.
+// merge through a fixed LDS tree (for max/argmax under the full (NaN, value,
+// index) rule, whose result does not depend on the merge order).  No
+// partials and no second kernel: on [8192, 8192] over axis 0 the 256 strips
+// read 128-byte pieces of every row side by side, and the argmax took 42.0
+// us against 50.2 us for the split scan plus combine (steady state, MI355X).
+// Lanes that saw a NaN rescan their rows with the exact rule, as the other
+// scans do.  The rows are walked with a pointer (no 64-bit multiply per
+// load).
 constexpr int kStripGroups = 8;
 constexpr int kStripRows = kThreads / kStripGroups;
 
-template <typename T, int NIN, int R>
+template <typename T, Kind K, int NIN, int R>
 __global__ void __launch_bounds__(kThreads)
     column_strip_kernel(const T* a, const T* b, uint64_t outer, uint64_t n,
                         uint64_t reduced_stride, uint64_t inner, RowMap map, Sink<T> sink) {
   constexpr int W = Vec16<T>::width;
   constexpr int kColumns = kStripGroups * W;
   using V = typename Vec16<T>::type;
-  __shared__ Acc<T, Kind::Max> lds[kStripRows][kColumns];
+  __shared__ Acc<T, K> lds[kStripRows][kColumns];
   const int group = threadIdx.x % kStripGroups;
   const uint32_t first_row = threadIdx.x / kStripGroups;
   const uint64_t strips_per_outer = (inner + kColumns - 1) / kColumns;
   const uint64_t strips = outer * strips_per_outer;
+  const uint64_t step = static_cast<uint64_t>(kStripRows) * reduced_stride;
   for (uint64_t strip = blockIdx.x; strip < strips; strip += gridDim.x) {
     const uint64_t o = strip / strips_per_outer;
     const uint64_t column = (strip - o * strips_per_outer) * kColumns + group * W;
     const bool present = column < inner;  // inner is a multiple of W
     const uint64_t base = row_offset(map, o) + column;
-    ScanAcc<T, Kind::Max> scan[W];
+    ScanAcc<T, K> scan[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) scan[k].init();
     bool unordered = false;
     if (present) {
+      uint64_t offset = base + first_row * reduced_stride;
       uint64_t r = first_row;
       for (; r + static_cast<uint64_t>(R - 1) * kStripRows < n; r += R * kStripRows) {
         V v[R];
 #pragma unroll
-        for (int u = 0; u < R; ++u) {
-          v[u] = load_vector<T, NIN>(a, b, base + (r + u * kStripRows) * reduced_stride);
-        }
-        // All R loads in flight before the first compare.
+        for (int u = 0; u < R; ++u) v[u] = load_vector<T, NIN>(a, b, offset + u * step);
+        offset += R * step;
+        // All R loads in flight before the first add or compare.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < R; ++u) {
 #pragma unroll
           for (int k = 0; k < W; ++k) {
             scan[k].add_ordered(vec_get<T>(v[u], k), static_cast<uint32_t>(r + u * kStripRows));
-            if (u % 2 == 1) {
-              unordered |= __builtin_isunordered(vec_get<T>(v[u], k), vec_get<T>(v[u - 1], k));
+            if constexpr (K == Kind::Max) {
+              if (u % 2 == 1) {
+                unordered |= __builtin_isunordered(vec_get<T>(v[u], k), vec_get<T>(v[u - 1], k));
+              }
             }
           }
         }
       }
-      for (; r < n; r += kStripRows) {
-        const V v = load_vector<T, NIN>(a, b, base + r * reduced_stride);
+      for (; r < n; r += kStripRows, offset += step) {
+        const V v = load_vector<T, NIN>(a, b, offset);
 #pragma unroll
         for (int k = 0; k < W; ++k) {
           scan[k].add_ordered(vec_get<T>(v, k), static_cast<uint32_t>(r));
-          unordered |= __builtin_isunordered(vec_get<T>(v, k), T(0));
+          if constexpr (K == Kind::Max) unordered |= __builtin_isunordered(vec_get<T>(v, k), T(0));
         }
       }
-      if (unordered) {
+      if constexpr (K == Kind::Max) {
+        if (unordered) {
 #pragma unroll
-        for (int k = 0; k < W; ++k) scan[k].init();
-        for (uint64_t row = first_row; row < n; row += kStripRows) {
-          const V v = load_vector<T, NIN>(a, b, base + row * reduced_stride);
+          for (int k = 0; k < W; ++k) scan[k].init();
+          for (uint64_t row = first_row; row < n; row += kStripRows) {
+            const V v = load_vector<T, NIN>(a, b, base + row * reduced_stride);
 #pragma unroll
-          for (int k = 0; k < W; ++k) scan[k].add(vec_get<T>(v, k), static_cast<uint32_t>(row));
+            for (int k = 0; k < W; ++k) scan[k].add(vec_get<T>(v, k), static_cast<uint32_t>(row));
+          }
         }
       }
     }
     __syncthreads();  // the previous strip's readers are done with lds
 #pragma unroll
     for (int k = 0; k < W; ++k) {
-      Acc<T, Kind::Max> acc = scan[k].finish(0);
+      Acc<T, K> acc = scan[k].finish(0);
       if (first_row < n) acc.seal(static_cast<int64_t>(first_row));
       lds[first_row][group * W + k] = acc;
     }
@@ -569,7 +577,7 @@ __global__ void __launch_bounds__(kThreads)
       for (int e = threadIdx.x; e < half * kColumns; e += kThreads) {
         const int row = e / kColumns;
         const int c = e % kColumns;
-        Acc<T, Kind::Max> acc = lds[row][c];
+        Acc<T, K> acc = lds[row][c];
         acc.merge(lds[row + half][c]);
         lds[row][c] = acc;
       }
@@ -577,7 +585,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     if (threadIdx.x < kColumns) {
       const uint64_t c = column - group * W + threadIdx.x;
-      if (c < inner) sink_write<T, Kind::Max>(sink, o * inner + c, lds[0][threadIdx.x], 0);
+      if (c < inner) sink_write<T, K>(sink, o * inner + c, lds[0][threadIdx.x], 0);
     }
   }
 }
@@ -1046,13 +1054,15 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
       if (plan.kept_strides[k] % W != 0) vec = false;
     }
     // Max/argmax over rows wide enough for a 128-byte strip per CU: one pass
-    // with no partials.
+    // with no partials.  (Sums stay on the split scan: on [8192, 8192] over
+    // axis 0 strips took 47.0 us against 45.5 us, while the strip max took
+    // 44.2 us.)
     if constexpr (K == Kind::Max) {
       constexpr uint64_t kStripColumns = static_cast<uint64_t>(kStripGroups) * W;
       const uint64_t strips = outer * ((inner + kStripColumns - 1) / kStripColumns);
       if (vec && n < kMaxScanRange && n >= static_cast<uint64_t>(kStripRows) * 8 &&
           strips >= static_cast<uint64_t>(cus)) {
-        column_strip_kernel<T, NIN, 8><<<grid_for(strips), kThreads, 0, guard.stream>>>(
+        column_strip_kernel<T, K, NIN, 8><<<grid_for(strips), kThreads, 0, guard.stream>>>(
             a, b, outer, n, reduced_stride, inner, map, final_sink());
         return hipSuccess;
       }
