@@ -257,6 +257,20 @@ struct SparHipStatus spar_hip_launch_strided_assign(void* destination, uint64_t 
                                                     uint64_t storage_offset, const void* source,
                                                     uint64_t element_size, int device);
 
+/* The gradient of a narrowed view, scattered into a fresh tensor of the
+ * base's shape in one pass: for the row-major output [outer, extent, inner]
+ * and the contiguous window input [outer, length, inner] (the narrowed axis
+ * has `extent` elements, the window starts at `start`),
+ *   output[o][e][i] = start <= e < start + length ? input[o][e - start][i] : 0.
+ * Elements are copied as bits (element_size 4 or 8).  No reference
+ * counterpart: narrow is this library's addition to the view model, and its
+ * backward would otherwise take a zero fill plus the window's strided copy,
+ * writing the window twice.  Outputs up to 2^31 - 1 elements. */
+struct SparHipStatus spar_hip_launch_window_embed(void* output, const void* input, uint64_t outer,
+                                                  uint64_t extent, uint64_t inner, uint64_t start,
+                                                  uint64_t length, uint64_t element_size,
+                                                  int device);
+
 /* Binary op over the broadcast shape `extents` (rank dims) without
  * materialising either operand: each operand is read through its own strides
  * (0 on broadcast axes) and storage offset; output is contiguous row-major.

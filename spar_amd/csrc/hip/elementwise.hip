@@ -375,6 +375,74 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// ---------------------------------------------------------------- window embed
+//
+// output[o][e][i] = e in [start, start + length) ? input[o][e - start][i] : 0
+// for the row-major output [outer, extent, inner] and the contiguous window
+// input [outer, length, inner]: narrow's gradient scattered into a zeroed
+// tensor of the base's shape in one pass (the zero fill and the window's
+// strided assign wrote the window twice).  Each lane handles G elements at a
+// time, G = 16 / sizeof(element) when every group lies inside one window row
+// or outside it and the input groups stay 16-byte aligned (VEC), else 1;
+// one 32-bit invariant-divisor division pair per group.
+template <typename E, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+    window_embed_kernel(E* output, const E* input, uint64_t groups, uint32_t length,
+                        uint32_t start, FastDiv inner, FastDiv extent) {
+  constexpr int G = VEC ? static_cast<int>(16 / sizeof(E)) : 1;
+  using V = typename Vec16<E>::type;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t group = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+       group < groups; group += stride) {
+    const uint32_t element = static_cast<uint32_t>(group) * G;
+    const uint32_t row = inner.div(element);
+    const uint32_t i = element - row * inner.divisor;
+    const uint32_t o = extent.div(row);
+    const uint32_t e = row - o * extent.divisor;
+    const bool inside = e >= start && e - start < length;
+    const uint64_t from = (static_cast<uint64_t>(o) * length + (e - start)) * inner.divisor + i;
+    if constexpr (VEC) {
+      V value{};
+      if (inside) value = stream_load(reinterpret_cast<const V*>(input + from));
+      *reinterpret_cast<V*>(output + element) = value;
+    } else {
+      output[element] = inside ? input[from] : E(0);
+    }
+  }
+}
+
+template <typename E>
+void launch_window_embed(E* output, const E* input, uint64_t outer, uint64_t extent,
+                         uint64_t inner, uint64_t start, uint64_t length,
+                         const DeviceGuard& guard) {
+  constexpr uint64_t G = 16 / sizeof(E);
+  const uint64_t count = outer * extent * inner;
+  // Groups of G elements stay in one row and keep the input aligned when
+  // rows are multiples of G, or when the narrowed axis is the last one and
+  // its window starts and ends on group boundaries.
+  const bool vec = aligned16(output) && aligned16(input) &&
+                   (inner % G == 0 || (inner == 1 && extent % G == 0 && start % G == 0 &&
+                                       length % G == 0));
+  FastDiv divide_inner;
+  FastDiv divide_extent;
+  divide_inner.init(static_cast<uint32_t>(inner));
+  divide_extent.init(static_cast<uint32_t>(extent));
+  const uint64_t groups = vec ? count / G : count;
+  uint64_t blocks = (groups + kThreads - 1) / kThreads;
+  const uint64_t cap = static_cast<uint64_t>(guard.multiprocessors) * 16;
+  if (blocks > cap) blocks = cap;
+  if (blocks == 0) blocks = 1;
+  if (vec) {
+    window_embed_kernel<E, true><<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(
+        output, input, groups, static_cast<uint32_t>(length), static_cast<uint32_t>(start),
+        divide_inner, divide_extent);
+  } else {
+    window_embed_kernel<E, false><<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(
+        output, input, groups, static_cast<uint32_t>(length), static_cast<uint32_t>(start),
+        divide_inner, divide_extent);
+  }
+}
+
 }  // namespace
 }  // namespace spar_hip
 
@@ -465,6 +533,36 @@ extern "C" SparHipStatus spar_hip_launch_fill_from_scalar_divided(void* output,
   }
   const FillScale mode = divisor == 1.0 ? FillScale::kNone : FillScale::kDivide;
   return fill_from_device_scalar(output, scalar, count, dtype, divisor, mode, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_window_embed(void* output, const void* input,
+                                                      uint64_t outer, uint64_t extent,
+                                                      uint64_t inner, uint64_t start,
+                                                      uint64_t length, uint64_t element_size,
+                                                      int device) {
+  if ((element_size != 4 && element_size != 8) || start > extent || length > extent - start) {
+    return invalid();
+  }
+  uint64_t count = 0;
+  if (__builtin_mul_overflow(outer, extent, &count) ||
+      __builtin_mul_overflow(count, inner, &count)) {
+    return invalid();
+  }
+  if (count == 0) return ok();
+  // 32-bit element indices inside the kernel
+  if (count > kIndex32Limit || output == nullptr || (length != 0 && input == nullptr)) {
+    return invalid();
+  }
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (element_size == 4) {
+    launch_window_embed(static_cast<int32_t*>(output), static_cast<const int32_t*>(input),
+                        outer, extent, inner, start, length, guard);
+  } else {
+    launch_window_embed(static_cast<int64_t*>(output), static_cast<const int64_t*>(input),
+                        outer, extent, inner, start, length, guard);
+  }
+  return finish(guard);
 }
 
 extern "C" SparHipStatus spar_hip_launch_fill(void* output, uint64_t count, int dtype,

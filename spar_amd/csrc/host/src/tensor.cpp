@@ -354,9 +354,32 @@ Tensor Tensor::narrow(std::size_t axis, std::size_t start, std::size_t length) c
   auto dimensions{dimensions_of(shape_)};
   dimensions[axis] = static_cast<Shape::dimension_type>(length);
   const std::size_t offset{length == 0 ? storage_offset_ : storage_offset_ + start * strides_[axis]};
-  // The gradient of a narrowed view is zero outside the window.
+  // The gradient of a narrowed view is zero outside the window.  On a HIP
+  // device a contiguous gradient is embedded in one pass; otherwise the
+  // window of a zero tensor is assigned.
   return make_view(Shape{std::move(dimensions)}, strides_, offset,
                    [original = shape_, axis, start, length](const Tensor& gradient) {
+                     if (gradient.device().is_hip() && gradient.is_contiguous()) {
+                       std::size_t outer{1}, inner{1};
+                       for (std::size_t k{0}; k < axis; ++k) {
+                         outer *= static_cast<std::size_t>(original[k]);
+                       }
+                       for (std::size_t k{axis + 1}; k < original.rank(); ++k) {
+                         inner *= static_cast<std::size_t>(original[k]);
+                       }
+                       Tensor result{original, gradient.dtype(), gradient.device()};
+                       const auto status{spar_hip_launch_window_embed(
+                           detail::HipTensorAccess::mutable_data(result),
+                           detail::HipTensorAccess::data(gradient), outer,
+                           static_cast<std::size_t>(original[axis]), inner, start, length,
+                           size_of(gradient.dtype()), gradient.device().index())};
+                       if (status.code == 0) return std::vector<Tensor>{result};
+                       // status 1 (a shape the one-pass kernel does not take)
+                       // falls through to the two-pass form
+                       if (status.code != 1) {
+                         detail::hip::check(status, "narrow backward", gradient.device());
+                       }
+                     }
                      Tensor result{zeros(original, gradient.dtype(), gradient.device())};
                      Tensor window{result.narrow(axis, start, length)};
                      detail::copy_tensor_values(window, gradient);

@@ -101,6 +101,7 @@ SIGNATURES = {
     "spar_hip_launch_multiply_reduce": [_P, _P, _P, _U64, _U64P, _U64, _U64P, _U64, _I, _I],
     "spar_hip_launch_probability_forward": [_P, _P, _P, _U64, _U64, _U64, _I, _I, _I],
     "spar_hip_launch_probability_backward": [_P, _P, _P, _P, _U64, _U64, _U64, _I, _I, _I],
+    "spar_hip_launch_window_embed": [_P, _P, _U64, _U64, _U64, _U64, _U64, _U64, _I],
     "spar_hip_launch_norm_forward": [_P, _P, _P, _P, _U64, _U64, _P, _P, _U64, _U64, _D, _I, _I,
                                      _I],
     "spar_hip_launch_norm_backward": [_P, _P, _P, _P, _P, _U64, _P, _P, _P, _U64, _U64, _I, _I,

@@ -179,6 +179,41 @@ def test_gelu_layouts_agree(hip, n):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("outer,extent,inner,start,length", [
+    (3, 10, 1, 2, 5),        # last axis, unaligned window: element path
+    (4, 16, 1, 4, 8),        # last axis, aligned window: 16-byte groups (float32)
+    (5, 7, 8, 2, 3),         # inner rows of 8
+    (2, 9, 3, 0, 9),         # the whole axis
+    (6, 5, 4, 5, 0),         # an empty window at the end: all zeros
+    (64, 1000, 36, 100, 800),
+    (512, 9216, 1, 512, 8192),
+])
+def test_window_embed(hip, dtype, outer, extent, inner, start, length):
+    """narrow's gradient scattered into a zeroed tensor of the base's shape in
+    one pass, against numpy (bit copies, so exact)."""
+    rng = np.random.default_rng(outer + extent + inner)
+    window = rng.standard_normal((outer, length, inner)).astype(dtype)
+    want = np.zeros((outer, extent, inner), dtype)
+    want[:, start:start + length, :] = window
+    out = out_buf(hip, want.shape, dtype)
+    hip.call("spar_hip_launch_fill", out.ptr, want.size, tag(dtype), 7.0, 0)  # not zero beforehand
+    src = dev(hip, window) if window.size else None
+    hip.call("spar_hip_launch_window_embed", out.ptr, src.ptr if src else None, outer, extent,
+             inner, start, length, np.dtype(dtype).itemsize, 0)
+    assert_bitexact(out.to_numpy(dtype, want.shape), want, "window embed")
+
+
+def test_window_embed_rejects_bad_arguments(hip):
+    lib = hip.load()
+    p = out_buf(hip, (64,), F32).ptr
+    for args in [(p, p, 2, 4, 1, 5, 0, 4, 0),     # start past the axis
+                 (p, p, 2, 4, 1, 2, 3, 4, 0),     # window past the axis
+                 (p, p, 2, 4, 1, 0, 4, 2, 0),     # element size 2
+                 (p, p, 1 << 20, 1 << 12, 1, 0, 1, 4, 0)]:  # more than 2^31 - 1 elements
+        assert lib.spar_hip_launch_window_embed(*args).code == 1, args
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_fill_add_in_place_zero(hip, dtype):
     n = 12345
     d = out_buf(hip, (n,), dtype)

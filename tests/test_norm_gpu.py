@@ -443,3 +443,36 @@ def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
     # they carry their own rounding, a random walk over the row
     allowance = 4.0 if dtype == F32 else 8.0 * np.sqrt(n)
     assert np.all(np.abs(got_d - d64) <= allowance * eps * d64), "column layout d vs float64"
+
+
+@pytest.mark.parametrize("shape", [(12, 8, 300), (5, 7, 64)])
+def test_layer_norm_api_batched_column_layout(sp, shape):
+    """A rank-3 view whose rows run down storage columns: base [n, A, B]
+    permuted to [A, B, n] has leading axes contiguous among themselves and
+    the last axis A*B apart, so the fused forward reads it in the column
+    layout.  Forward and backward against the oracle's composition."""
+    a, b, n = shape
+    rng = np.random.default_rng(sum(shape))
+    base = rng.standard_normal((n, a, b)).astype(F32)
+    w = rng.uniform(0.5, 1.5, n).astype(F32)
+    bias = rng.uniform(-0.1, 0.1, n).astype(F32)
+    g = rng.standard_normal((a, b, n)).astype(F32)
+
+    def build(lib, t):
+        y = lib.layer_norm(t[0].permute([1, 2, 0]), t[1], t[2], EPSILON)
+        lib.sum(lib.multiply(y, t[3])).backward()
+        return y
+
+    got_y, want_y, td, tr = api_both(sp, [base, w, bias, g], build)
+    rows_got, rows_want = got_y.reshape(-1, n), want_y.reshape(-1, n)
+    assert_rows(rows_got, rows_want, n, F32, "batched column y")
+    cpu = sp.Device.cpu()
+    dx_got = td[0].grad().to(cpu).numpy().transpose(1, 2, 0).reshape(-1, n)
+    dx_want = tr[0].grad().numpy().transpose(1, 2, 0).reshape(-1, n)
+    x_rows = base.transpose(1, 2, 0).reshape(-1, n)
+    assert_rows(dx_got, dx_want, n, F32, "batched column dx", 16.0,
+                dx_terms(g.reshape(-1, n), w, x_rows, True))
+    for i in (1, 2):
+        got, want = td[i].grad().to(cpu).numpy(), tr[i].grad().numpy()
+        scale = np.max(np.abs(want))
+        assert np.max(np.abs(got - want)) <= 1e-6 * np.sqrt(a * b * n) * 8 * scale, f"grad {i}"
