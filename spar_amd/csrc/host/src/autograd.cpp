@@ -17,9 +17,14 @@
 //      adds later ones in place (`accumulated += incoming`).
 // Given identical contributions, the gradients are therefore identical to
 // the reference's.  The reference also cloned each contribution
-// (autograd.cpp:145, :244); the clone only copied values, so leaving it out
-// changes no bit.  A held gradient whose storage another handle still sees
-// is added out of place (same operands, same order) instead of in place.
+// (autograd.cpp:145, :244), which copied values into a dense tensor.  Here a
+// gradient is copied only where that copy is observable or needed: a leaf
+// keeps a dense, contiguous gradient of its own (a gradient that is a view,
+// or a tensor another handle still sees, is copied first), and a held
+// gradient that is a view or whose storage another handle still sees is
+// added out of place (same operands, same order) instead of in place.  The
+// view rules return dense gradients themselves (transpose's is made
+// contiguous), so on their paths nothing is copied.
 #include <atomic>
 #include <unordered_map>
 
@@ -196,7 +201,7 @@ class Sweep final {
         continue;
       }
       check_same_layout(*held, incoming);
-      if (TensorInternals::sole_owner(*held)) {
+      if (TensorInternals::sole_owner(*held) && held->is_contiguous()) {
         add_into(*held, incoming);
         g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
       } else {
@@ -213,10 +218,10 @@ class Sweep final {
       g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
       return;
     }
-    if (TensorInternals::sole_owner(gradient)) {
+    if (TensorInternals::sole_owner(gradient) && gradient.is_contiguous()) {
       leaf.accumulated = gradient.detach();
     } else {
-      leaf.accumulated = gradient.detach().clone();
+      leaf.accumulated = gradient.detach().clone();  // dense and contiguous
       g_leaf_copies.fetch_add(1, std::memory_order_relaxed);
     }
   }

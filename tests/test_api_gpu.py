@@ -406,6 +406,41 @@ def test_autograd_api_errors(sp):
         hip_tensor(sp, np.arange(3, dtype=np.int64)).set_requires_grad(True)
 
 
+def test_autograd_view_gradients_are_dense(sp):
+    """Leaf gradients are dense, as the reference's clones made them
+    (autograd.cpp:145, :244): through a transpose a leaf's gradient is
+    contiguous, adds into it across backward calls pair the right elements,
+    an identity that receives a gradient through a view and one directly
+    adds them elementwise, and AdamW accepts the gradient of a Parameter
+    used through a transpose."""
+    x = normal(81, (3, 4))
+    c = normal(82, (4, 3))
+    d = normal(83, (3, 4))
+
+    def build(lib, t):
+        through_view = lib.sum(lib.multiply(t[0].transpose(0, 1), t[1]))
+        direct = lib.sum(lib.multiply(t[0], t[2]))
+        return lib.add(through_view, direct)
+
+    dev = [hip_tensor(sp, a, requires_grad=True) for a in (x, c, d)]
+    ref = [R.RTensor.of(a, requires_grad=True) for a in (x, c, d)]
+    for _ in range(2):  # two backward calls accumulate into the leaves
+        build(sp, dev).backward()
+        build(R, ref).backward()
+    got = dev[0].grad()
+    assert got.is_contiguous()
+    assert_bitexact(host(sp, got), ref[0].grad().numpy(), "x grad, two calls")
+    assert_bitexact(host(sp, dev[1].grad()), ref[1].grad().numpy(), "c grad")
+
+    # a Parameter used only through a transpose: AdamW takes its gradient
+    w = sp.nn.Parameter(hip_tensor(sp, x))
+    opt = sp.optim.AdamW([w], 1e-3)
+    sp.sum(sp.multiply(w.tensor().transpose(0, 1), hip_tensor(sp, c))).backward()
+    assert w.grad().is_contiguous()
+    assert_bitexact(host(sp, w.grad()), c.T.copy(), "parameter grad through a transpose")
+    opt.step()
+
+
 def memory_stats():
     import ctypes
 
@@ -421,7 +456,9 @@ def test_layernorm_chain_second_run_allocates_nothing_and_copies_no_gradient(sp)
     twice: the second run takes every block from the caching allocator (no
     hipMalloc, cache hits > 0), and the engine neither copies a leaf gradient
     nor adds out of place, because every gradient it holds owns its storage
-    (the reference cloned every contribution, autograd.cpp:145, :244)."""
+    and is dense (transpose's backward already returns a contiguous
+    gradient; the reference cloned every contribution, autograd.cpp:145,
+    :244)."""
     device = sp.Device.hip(0)
     rng = np.random.default_rng(71)
     base = sp.Tensor.from_numpy(rng.standard_normal((2048, 1024)).astype(np.float32)).to(device)
