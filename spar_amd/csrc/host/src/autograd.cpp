@@ -22,9 +22,10 @@
 // keeps a dense, contiguous gradient of its own (a gradient that is a view,
 // or a tensor another handle still sees, is copied first), and a held
 // gradient that is a view or whose storage another handle still sees is
-// added out of place (same operands, same order) instead of in place.  The
-// view rules return dense gradients themselves (transpose's is made
-// contiguous), so on their paths nothing is copied.
+// added out of place (same operands, same order) instead of in place, as is
+// an incoming view.  The view rules return dense gradients themselves
+// (transpose's is made contiguous); the reductions return their gradient as
+// a stride-0 broadcast view, which the rules that follow read in place.
 #include <atomic>
 #include <unordered_map>
 
@@ -201,7 +202,11 @@ class Sweep final {
         continue;
       }
       check_same_layout(*held, incoming);
-      if (TensorInternals::sole_owner(*held) && held->is_contiguous()) {
+      // In place when the held gradient is dense and its own, and the
+      // incoming one dense too (a broadcast view would first be filled out);
+      // otherwise out of place, which reads views as they are.
+      if (TensorInternals::sole_owner(*held) && held->is_contiguous() &&
+          incoming.is_contiguous()) {
         add_into(*held, incoming);
         g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
       } else {

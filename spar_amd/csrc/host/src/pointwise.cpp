@@ -69,6 +69,12 @@ Tensor binary_device(const Tensor& a, const Tensor& b, const Shape& output_shape
   return output;
 }
 
+// An incoming gradient may be a view (a reduction's gradient is a stride-0
+// broadcast); the scalar ops, like the reference's, take contiguous inputs.
+Tensor dense_gradient(const Tensor& gradient) {
+  return gradient.is_contiguous() ? gradient.detach() : gradient.detach().contiguous();
+}
+
 bool full_contiguous(const Tensor& t, const Shape& shape) {
   return t.shape() == shape && t.is_contiguous();
 }
@@ -197,7 +203,7 @@ Tensor subtract(const Tensor& a, const Tensor& b) {
           std::vector<Tensor> contributions;
           if (grad_a) contributions.push_back(detail::reduce_gradient_to_shape(gradient, shape_a));
           if (grad_b) {
-            const auto negative{multiply_scalar(gradient.is_contiguous() ? gradient : gradient.contiguous(), -1.0)};
+            const auto negative{multiply_scalar(dense_gradient(gradient), -1.0)};
             contributions.push_back(detail::reduce_gradient_to_shape(negative, shape_b));
           }
           return contributions;
@@ -293,7 +299,7 @@ Tensor multiply_scalar(const Tensor& input, double value) {
   Tensor output{dispatch_scalar(input, value, SPAR_HIP_MULTIPLY)};
   if (input.requires_grad()) {
     detail::record_operation(output, {input}, [value](const Tensor& gradient) {
-      return std::vector<Tensor>{multiply_scalar(gradient, value)};
+      return std::vector<Tensor>{multiply_scalar(dense_gradient(gradient), value)};
     });
   }
   return output;
@@ -303,7 +309,7 @@ Tensor divide_scalar(const Tensor& input, double value) {
   Tensor output{dispatch_scalar(input, value, SPAR_HIP_DIVIDE)};
   if (input.requires_grad()) {
     detail::record_operation(output, {input}, [value](const Tensor& gradient) {
-      return std::vector<Tensor>{divide_scalar(gradient, value)};
+      return std::vector<Tensor>{divide_scalar(dense_gradient(gradient), value)};
     });
   }
   return output;
@@ -315,7 +321,7 @@ Tensor negate(const Tensor& input) {
   Tensor output{dispatch_unary(input, SPAR_HIP_NEGATE, "negate")};
   if (input.requires_grad()) {
     detail::record_operation(output, {input}, [](const Tensor& gradient) {
-      return std::vector<Tensor>{multiply_scalar(gradient, -1.0)};
+      return std::vector<Tensor>{multiply_scalar(dense_gradient(gradient), -1.0)};
     });
   }
   return output;

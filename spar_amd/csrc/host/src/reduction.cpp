@@ -5,6 +5,7 @@
 // NaN-first rule of reduce_max.
 #include <algorithm>
 #include <limits>
+#include <optional>
 
 #include "autograd_internal.hpp"
 #include "bridge.hpp"
@@ -104,24 +105,31 @@ Tensor full_reduce(const Tensor& input, int operation, const char* name) {
   return output;
 }
 
-// Fills the input shape with gradient[0] / divisor (reduction.cpp:200-212,
-// :263-277: the CPU path divides by (T)n).
-Tensor fill_from_gradient(const Shape& input_shape, DType dtype, const Tensor& gradient,
-                          double divisor) {
-  Tensor contribution{input_shape, dtype, gradient.device()};
-  if (contribution.numel() == 0) return contribution;
-  const Tensor scalar{gradient.is_contiguous() ? gradient : gradient.contiguous()};
-  hip::check(spar_hip_launch_fill_from_scalar_divided(
-                 HipTensorAccess::mutable_data(contribution), HipTensorAccess::data(scalar),
-                 contribution.numel(), hip::dtype_tag(dtype), divisor, gradient.device().index()),
-             "reduction backward", gradient.device());
-  return contribution;
+// The gradient of a reduction is the output gradient broadcast back over the
+// reduced axes (reduction.cpp:147-165, :200-212, :263-277).  It is returned
+// as a stride-0 view of the output gradient instead of a filled tensor: the
+// values are the same, and no pass over the input's extent is made here.
+// Consumers read views in place (an elementwise product then reads one value
+// per row instead of a filled tensor), and the engine makes a leaf's gradient
+// dense.  A mean's gradient is divided by (T)n on the reduced tensor before
+// the broadcast, which gives each element the same quotient as dividing the
+// broadcast values one by one (the CPU path's g / (T)n, reduction.cpp:271).
+Tensor dense(const Tensor& tensor) {
+  return tensor.is_contiguous() ? tensor.detach() : tensor.detach().contiguous();
+}
+
+Tensor broadcast_full_gradient(const Shape& input_shape, const Tensor& gradient,
+                               std::optional<double> divisor) {
+  Tensor value{dense(gradient)};
+  if (divisor) value = divide_scalar(value, *divisor);
+  return value.expand(input_shape);
 }
 
 // reduction.cpp:147-165
 Tensor restore_and_expand_gradient(const Tensor& gradient, const Shape& input_shape,
-                                   std::span<const std::size_t> axes, bool keepdim) {
-  Tensor restored{gradient};
+                                   std::span<const std::size_t> axes, bool keepdim,
+                                   std::optional<double> divisor) {
+  Tensor restored{dense(gradient)};
   if (!keepdim) {
     std::vector<bool> reduced(input_shape.rank(), false);
     for (const std::size_t axis : axes) reduced[axis] = true;
@@ -130,9 +138,10 @@ Tensor restore_and_expand_gradient(const Tensor& gradient, const Shape& input_sh
     for (std::size_t axis{0}; axis < input_shape.rank(); ++axis) {
       if (!reduced[axis]) dimensions[axis] = gradient.shape()[gradient_axis++];
     }
-    restored = gradient.reshape(Shape{std::move(dimensions)});
+    restored = restored.reshape(Shape{std::move(dimensions)});
   }
-  return restored.expand(input_shape).contiguous();
+  if (divisor) restored = divide_scalar(restored, *divisor);
+  return restored.expand(input_shape);
 }
 
 }  // namespace
@@ -142,9 +151,8 @@ Tensor sum(const Tensor& input) {
   Tensor output{full_reduce(input, SPAR_HIP_SUM, "sum")};
   if (input.requires_grad()) {
     const Shape input_shape{input.shape()};
-    const DType input_dtype{input.dtype()};
-    detail::record_operation(output, {input}, [input_shape, input_dtype](const Tensor& gradient) {
-      return std::vector<Tensor>{fill_from_gradient(input_shape, input_dtype, gradient, 1.0)};
+    detail::record_operation(output, {input}, [input_shape](const Tensor& gradient) {
+      return std::vector<Tensor>{broadcast_full_gradient(input_shape, gradient, std::nullopt)};
     });
   }
   return output;
@@ -160,7 +168,8 @@ Tensor sum(const Tensor& input, std::span<const std::size_t> axes, bool keepdim)
     detail::record_operation(output, {input},
                              [input_shape, normalized_axes, keepdim](const Tensor& gradient) {
                                return std::vector<Tensor>{restore_and_expand_gradient(
-                                   gradient, input_shape, normalized_axes, keepdim)};
+                                   gradient, input_shape, normalized_axes, keepdim,
+                                   std::nullopt)};
                              });
   }
   return output;
@@ -180,12 +189,11 @@ Tensor mean(const Tensor& input) {
   Tensor output{full_reduce(input, SPAR_HIP_MEAN, "mean")};
   if (input.requires_grad()) {
     const Shape input_shape{input.shape()};
-    const DType input_dtype{input.dtype()};
     const std::size_t input_numel{input.numel()};
     detail::record_operation(
-        output, {input}, [input_shape, input_dtype, input_numel](const Tensor& gradient) {
-          return std::vector<Tensor>{fill_from_gradient(input_shape, input_dtype, gradient,
-                                                        static_cast<double>(input_numel))};
+        output, {input}, [input_shape, input_numel](const Tensor& gradient) {
+          return std::vector<Tensor>{broadcast_full_gradient(
+              input_shape, gradient, static_cast<double>(input_numel))};
         });
   }
   return output;
@@ -205,9 +213,9 @@ Tensor mean(const Tensor& input, std::span<const std::size_t> axes, bool keepdim
     detail::record_operation(
         output, {input},
         [input_shape, normalized_axes, keepdim, element_count](const Tensor& gradient) {
-          const auto expanded{
-              restore_and_expand_gradient(gradient, input_shape, normalized_axes, keepdim)};
-          return std::vector<Tensor>{divide_scalar(expanded, static_cast<double>(element_count))};
+          return std::vector<Tensor>{restore_and_expand_gradient(
+              gradient, input_shape, normalized_axes, keepdim,
+              static_cast<double>(element_count))};
         });
   }
   return output;

@@ -274,7 +274,9 @@ Tensor Tensor::reshape(Shape new_shape) const {
   auto strides{new_shape.contiguous_strides()};
   return make_view(std::move(new_shape), std::move(strides), storage_offset_,
                    [original = shape_](const Tensor& gradient) {
-                     return std::vector<Tensor>{gradient.reshape(original)};
+                     // an incoming view (a reduction's broadcast gradient)
+                     // is made contiguous first, as reshape requires
+                     return std::vector<Tensor>{gradient.contiguous().reshape(original)};
                    });
 }
 
