@@ -412,15 +412,22 @@ struct SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void
                                                   uint64_t rows, uint64_t extent, double epsilon,
                                                   int center, int dtype, int device);
 
-/* Backward of the above from the saved mu and d: writes dx [rows, extent]
- * (contiguous), d weight [extent] and, for LayerNorm, d bias [extent] (sums
- * over rows in a fixed order).  The input is in the row layout of the
- * forward: rows start input_row_stride >= extent elements apart, elements of
- * a row adjacent.  Replaces the autograd backward of the composed chain. */
+/* Backward of the above from the saved mu and d: writes dx, d weight
+ * [extent] and, for LayerNorm, d bias [extent] (sums over rows in a fixed
+ * order).  The input is in one of the forward's layouts: rows
+ * input_row_stride >= extent apart with a row's elements adjacent
+ * (input_column_stride 1), dx then written contiguous [rows, extent]; or rows
+ * adjacent (input_row_stride 1) with a row's elements input_column_stride >=
+ * rows apart, dx then written packed in that layout, element (p, q) at
+ * input_gradient[p + q * rows] (a contiguous [extent, rows] block, whose
+ * transpose is the gradient of a transposed view).  output_gradient is
+ * contiguous [rows, extent] in both.  Replaces the autograd backward of the
+ * composed chain. */
 struct SparHipStatus spar_hip_launch_norm_backward(
     void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
-    const void* input, uint64_t input_row_stride, const void* weight, const void* mean,
-    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device);
+    const void* input, uint64_t input_row_stride, uint64_t input_column_stride,
+    const void* weight, const void* mean, const void* denominator, uint64_t rows,
+    uint64_t extent, int center, int dtype, int device);
 
 /* --------------------------------------------- cross entropy (log-softmax + NLL) */
 

@@ -727,39 +727,585 @@ __global__ void __launch_bounds__(THREADS)
 constexpr int kCombineThreads = 1024;
 constexpr int kCombineWaves = kCombineThreads / kWave;
 
+// Column group `group` (64 columns) of [parts, n] partials into out.
+template <typename T>
+__device__ __forceinline__ void combine_group(T* out, const T* partial, uint64_t parts,
+                                              uint64_t n, uint64_t group,
+                                              T (&lds)[kCombineWaves][kWave]) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const uint64_t col = group * kWave + lane;
+  T total = T(0);
+  if (col < n) {
+    // Eight loads in flight per lane, added in the same order as one at a
+    // time.
+    constexpr int kBatch = 8;
+    uint64_t p = wave;
+    for (; p + (kBatch - 1) * kCombineWaves < parts; p += kBatch * kCombineWaves) {
+      T v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = partial[(p + u * kCombineWaves) * n + col];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) total += v[u];
+    }
+    for (; p < parts; p += kCombineWaves) total += partial[p * n + col];
+  }
+  __syncthreads();
+  lds[wave][lane] = total;
+  __syncthreads();
+  if (wave == 0 && col < n) {
+    T sum = lds[0][lane];
+#pragma unroll
+    for (int w = 1; w < kCombineWaves; ++w) sum += lds[w][lane];
+    out[col] = sum;
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kCombineThreads)
     norm_combine_kernel(T* out, const T* partial, uint64_t parts, uint64_t n) {
   __shared__ T lds[kCombineWaves][kWave];
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
   const uint64_t groups = (n + kWave - 1) / kWave;
   for (uint64_t group = blockIdx.x; group < groups; group += gridDim.x) {
-    const uint64_t col = group * kWave + lane;
-    T total = T(0);
-    if (col < n) {
-      // Eight loads in flight per lane, added in the same order as one at a
-      // time.
-      constexpr int kBatch = 8;
-      uint64_t p = wave;
-      for (; p + (kBatch - 1) * kCombineWaves < parts; p += kBatch * kCombineWaves) {
-        T v[kBatch];
+    combine_group<T>(out, partial, parts, n, group, lds);
+  }
+}
+
+// ------------------------------------- backward, rows down storage columns
+//
+// The backward over the forward's column layout, x[p][q] = in[p + q * pitch],
+// with dy in rows (dy[p * n + q]).  dx is written in x's layout, packed:
+// dx[p + q * rows], the storage of a contiguous [n, rows] tensor whose
+// transpose is the gradient of the transposed view.  Three launches take the
+// place of a transposing copy of x, the row kernel and a transposing copy of
+// dx:
+//
+//  1. norm_backward_columns_sums_kernel.  Tiles of 32 W values of p by 32 W
+//     values of q; x goes through LDS as in the forward's apply pass (XOR
+//     swizzle, the next tile's loads in flight while the current one is
+//     used) and dy is read along its rows.  A workgroup owns one p tile and a
+//     run of q tiles (a split of q).  Each lane keeps the sums of g = dy * w
+//     and g * xhat for its 4 W values of p in registers over the whole run;
+//     at the end the 32 lanes of each p are added through LDS in lane order.
+//     Every tile adds dy * xhat and dy over its p for each q (the 8 lanes of
+//     a q through LDS, in order).  Results: [2, splits, rows] row sums and
+//     [tiles_p, n] weight / bias partials.
+//  2. norm_backward_columns_finish_kernel: the weight and bias gradients (the
+//     partials added in p-tile order, as norm_combine_kernel does) and each
+//     row's mean(g) and mean(g * xhat) (splits added in order, then divided
+//     by (T)n).
+//  3. norm_backward_columns_apply_kernel.  Tiles in the transposed frame: dy
+//     goes through LDS, x is read and dx written along p.  Each element is
+//     computed with the row kernel's operations in the same order.
+//
+// Only the order of the sums differs from the row kernel, so the two layouts
+// agree within the sums' rounding.  On an input that fits the Infinity Cache
+// the sums pass reads x with cached loads and the apply pass finds it there.
+constexpr int kBackwardGroups = kApplyThreads / kApplyGranules;  // lanes per q granule
+
+// Butterfly reduce-scatter over the 32 lanes of a half wave: on entry each
+// lane holds NV values, on exit lane c holds in v[0] the sum over the 32
+// lanes of value c * NV / 32 (lanes c and c ^ 1 alike when NV is 16).  Step b
+// pairs lanes c and c ^ b; the lane with bit b set keeps the upper half.
+template <typename T, int NV, int B = 16>
+__device__ __forceinline__ void half_wave_reduce_scatter(T (&v)[NV], int c) {
+  if constexpr (B >= 1) {
+    if constexpr (NV > 1) {
+      constexpr int kHalf = NV / 2;
+      const bool upper = (c & B) != 0;
+      T kept[kHalf];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) v[u] = partial[(p + u * kCombineWaves) * n + col];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) total += v[u];
+      for (int j = 0; j < kHalf; ++j) {
+        const T send = upper ? v[j] : v[j + kHalf];
+        const T keep = upper ? v[j + kHalf] : v[j];
+        kept[j] = keep + __shfl_xor(send, B);
       }
-      for (; p < parts; p += kCombineWaves) total += partial[p * n + col];
+      half_wave_reduce_scatter<T, kHalf, B / 2>(kept, c);
+      v[0] = kept[0];
+    } else {
+      v[0] = v[0] + __shfl_xor(v[0], B);
+      half_wave_reduce_scatter<T, 1, B / 2>(v, c);
     }
-    __syncthreads();
-    lds[wave][lane] = total;
-    __syncthreads();
-    if (wave == 0 && col < n) {
-      T sum = lds[0][lane];
+  }
+}
+
+// Tile modes of the column backward kernels: scalar loads with per-element
+// bounds (any layout), 16-byte granules with per-granule presence (rows and n
+// multiples of W), and 16-byte granules of tiles all whole (rows and n
+// multiples of the tile side: no presence tests at all).
+constexpr int kScalarTiles = 0;
+constexpr int kVectorTiles = 1;
+constexpr int kWholeTiles = 2;
+
+template <typename T, bool CENTER, int MODE, bool CACHED>
+__global__ void __launch_bounds__(kApplyThreads)
+    norm_backward_columns_sums_kernel(T* row_partial, T* partial_weight, T* partial_bias,
+                                      const T* dy, const T* in, uint64_t pitch, const T* weight,
+                                      const T* mean, const T* denominator, uint64_t rows,
+                                      uint64_t n, uint32_t tiles_q, uint32_t splits,
+                                      uint32_t split_tiles) {
+  constexpr bool VEC = MODE != kScalarTiles;
+  constexpr bool WHOLE = MODE == kWholeTiles;
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  constexpr int G = kApplyGranules;
+  constexpr int TP = G * W;
+  constexpr int TQ = G * W;
+  constexpr int kLoads = TP * G / kApplyThreads;             // dy granules staged per lane
+  constexpr int kBlocks = (TP / W) * G / kApplyThreads;      // W x W blocks per lane
+  constexpr int kGroups = kBackwardGroups;
+  constexpr int kValues = W * 2;                              // column partials per block
+  constexpr int kWaves = kApplyThreads / kWave;
+  static_assert(kApplyThreads % G == 0 && kGroups * (TP / W) == kApplyThreads, "lane layout");
+  static_assert(TP / W == 32 && 32 % kValues == 0, "half-wave reduce-scatter");
+  static_assert(kWaves * (TP / W) * 2 * W * sizeof(T) <= sizeof(V) * TP * G, "row sums fit");
+  __shared__ V lds[TP][G];
+  __shared__ V tile_weight[TQ / W];
+  const uint32_t split = blockIdx.x % splits;
+  const uint32_t tp = blockIdx.x / splits;
+  const uint32_t first_tile = split * split_tiles;
+  if (first_tile >= tiles_q) return;  // the whole workgroup
+  const uint32_t run = tiles_q - first_tile < split_tiles ? tiles_q - first_tile : split_tiles;
+  const uint64_t p0 = static_cast<uint64_t>(tp) * TP;
+  // A lane keeps p granule c (W rows) for the whole run and takes q granules
+  // g0, g0 + kGroups, ... (one per block) of each tile.
+  const int c = threadIdx.x % (TP / W);
+  const int g0 = threadIdx.x / (TP / W);
+  const uint64_t p = p0 + static_cast<uint64_t>(c) * W;
+  T mu[W];
+  T d[W];
+  T r[W];
 #pragma unroll
-      for (int w = 1; w < kCombineWaves; ++w) sum += lds[w][lane];
-      out[col] = sum;
+  for (int i = 0; i < W; ++i) {
+    const bool present = p + i < rows;
+    mu[i] = CENTER && present ? mean[p + i] : T(0);
+    d[i] = present ? denominator[p + i] : T(1);
+    r[i] = T(1) / d[i];
+  }
+  T sum_g[W];
+  T sum_gx[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    sum_g[i] = T(0);
+    sum_gx[i] = T(0);
+  }
+  // Staged dy granules: q offset (lane % G) W, p offsets lane / G + it *
+  // kApplyThreads / G.
+  const uint64_t lane_offset = static_cast<uint64_t>(threadIdx.x % G) * W +
+                               static_cast<uint64_t>(threadIdx.x / G) * n;
+  const uint64_t load_step = static_cast<uint64_t>(kApplyThreads / G) * n;
+  V staged[kLoads];
+  auto load_tile = [&](uint64_t q0) {
+    if constexpr (VEC) {
+      // Granules are wholly present or absent (rows and n are multiples of
+      // W).  Absent ones load the first element instead and are zeroed, so
+      // every load issues unconditionally, back to back.
+      const T* at = dy + p0 * n + q0 + lane_offset;
+      const bool q_present = q0 + static_cast<uint64_t>(threadIdx.x % G) * W < n;
+      const uint64_t first_p = p0 + threadIdx.x / G;
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const bool present =
+            WHOLE ||
+            (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
+        const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
+        staged[it] = present ? v : V{};
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const int index = it * kApplyThreads + threadIdx.x;
+        const uint64_t pr = p0 + index / G;
+        const uint64_t q = q0 + static_cast<uint64_t>(index % G) * W;
+        V v{};
+        if (pr < rows) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) {
+            if (q + k < n) vec_set<T>(v, k, dy[pr * n + q + k]);
+          }
+        }
+        staged[it] = v;
+      }
     }
+  };
+  // The run starts at a tile rotated by the p tile, so that workgroups side
+  // by side read different q.
+  uint32_t offset = tp % run;
+  load_tile(static_cast<uint64_t>(first_tile + offset) * TQ);
+  for (uint32_t step = 0; step < run; ++step) {
+    const uint64_t q0 = static_cast<uint64_t>(first_tile + offset) * TQ;
+    offset = offset + 1 == run ? 0 : offset + 1;
+    __syncthreads();  // the previous tile's LDS readers are done
+#pragma unroll
+    for (int it = 0; it < kLoads; ++it) {
+      const int index = it * kApplyThreads + threadIdx.x;
+      const int row = index / G;
+      lds[row][(index % G) ^ ((row / W) & 7)] = staged[it];
+    }
+    // the tile's weight, one granule per lane of the first TQ / W
+    if (threadIdx.x < TQ / W) {
+      const uint64_t q = q0 + static_cast<uint64_t>(threadIdx.x) * W;
+      V wv{};
+      if constexpr (VEC) {
+        if (WHOLE || q < n) wv = *reinterpret_cast<const V*>(weight + q);
+      } else {
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          if (q + k < n) vec_set<T>(wv, k, weight[q + k]);
+        }
+      }
+      tile_weight[threadIdx.x] = wv;
+    }
+    __syncthreads();
+    // This tile's x, issued before the next tile's dy loads (the wait counter
+    // retires vector loads in issue order).
+    const uint64_t first_q = q0 + static_cast<uint64_t>(g0) * W;
+    V x[kBlocks][W];  // [block][q offset], W values of p each
+    if constexpr (VEC) {
+      const T* at = in + p + first_q * pitch;
+#pragma unroll
+      for (int it = 0; it < kBlocks; ++it) {
+        const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
+        const bool present = WHOLE || (p < rows && q < n);
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          const V* source = reinterpret_cast<const V*>(
+              present ? at + (static_cast<uint64_t>(it) * kGroups * W + k) * pitch : in);
+          const V v = CACHED ? *source : stream_load(source);
+          x[it][k] = present ? v : V{};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kBlocks; ++it) {
+        const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          x[it][k] = q + k < n ? load_column_group<T, false>(in, p, q + k, pitch, rows) : V{};
+        }
+      }
+    }
+    if (step + 1 < run) load_tile(static_cast<uint64_t>(first_tile + offset) * TQ);
+    // Column partials, block by block: value k * 2 + s is the sum over the
+    // lane's W rows of dy * xhat (s = 0) or dy (s = 1) at q row k of the
+    // block, then over the 32 lanes of the half wave (the tile's p), after
+    // which lane c holds value c / (32 / kValues).  Absent rows and columns
+    // hold zero dy and add nothing.
+#pragma unroll
+    for (int it = 0; it < kBlocks; ++it) {
+      const int g = g0 + it * kGroups;
+      T grad[W][W];  // [p offset][q offset]
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const V block = lds[c * W + i][g ^ (c & 7)];
+#pragma unroll
+        for (int k = 0; k < W; ++k) grad[i][k] = vec_get<T>(block, k);
+      }
+      const V wv = tile_weight[g];  // zero past the last column
+      T column[kValues];
+      T block_g[W];
+      T block_gx[W];
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        T dw = T(0);
+        T db = T(0);
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          const Divisor<T> divide(d[i], r[i]);
+          const T xhat = divide(vec_get<T>(x[it][k], i) - mu[i]);
+          dw += grad[i][k] * xhat;
+          if constexpr (CENTER) db += grad[i][k];
+          const T gw = grad[i][k] * vec_get<T>(wv, k);
+          if (k == 0) {
+            block_g[i] = gw;
+            block_gx[i] = gw * xhat;
+          } else {
+            block_g[i] += gw;
+            block_gx[i] += gw * xhat;
+          }
+        }
+        column[k * 2] = dw;
+        column[k * 2 + 1] = db;
+      }
+      // The row sums gather the block's W columns first.  The empty asm
+      // pins each sum here: otherwise the compiler sinks these adds to the
+      // loop's end and keeps the block's xhat and g * w live until then.
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        if constexpr (CENTER) {
+          sum_g[i] += block_g[i];
+          asm volatile("" : "+v"(sum_g[i]));
+        }
+        sum_gx[i] += block_gx[i];
+        asm volatile("" : "+v"(sum_gx[i]));
+      }
+      half_wave_reduce_scatter<T, kValues>(column, c);
+      constexpr int kLanesPerValue = 32 / kValues;
+      const int j = c / kLanesPerValue;
+      const int s = j % 2;
+      const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W + j / 2;
+      if (c % kLanesPerValue == 0 && (WHOLE || q < n) && (CENTER || s == 0)) {
+        (s == 0 ? partial_weight : partial_bias)[static_cast<uint64_t>(tp) * n + q] = column[0];
+      }
+    }
+  }
+  // The row sums over the run: lanes c and c + 32 of a wave, then the waves
+  // in order through LDS.
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    if constexpr (CENTER) sum_g[i] += __shfl_xor(sum_g[i], 32);
+    sum_gx[i] += __shfl_xor(sum_gx[i], 32);
+  }
+  __syncthreads();  // the last tile's LDS readers are done
+  T* red = reinterpret_cast<T*>(&lds[0][0]);  // [kWaves][TP][2]
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave < TP / W) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      red[(wave * TP + c * W + i) * 2] = sum_g[i];
+      red[(wave * TP + c * W + i) * 2 + 1] = sum_gx[i];
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < 2 * TP; t += kApplyThreads) {
+    const int s = t / TP;
+    const int pl = t % TP;
+    const uint64_t row = p0 + pl;
+    if (row < rows && (CENTER || s == 1)) {
+      T total = red[pl * 2 + s];
+#pragma unroll
+      for (int v = 1; v < kWaves; ++v) total += red[(v * TP + pl) * 2 + s];
+      row_partial[(static_cast<uint64_t>(s) * splits + split) * rows + row] = total;
+    }
+  }
+}
+
+// Weight / bias gradients and the rows' means, in one launch: blocks
+// [0, column_blocks) combine the weight partials, the next column_blocks
+// (LayerNorm) the bias partials, the rest finish kCombineThreads rows each.
+template <typename T, bool CENTER>
+__global__ void __launch_bounds__(kCombineThreads)
+    norm_backward_columns_finish_kernel(T* weight_gradient, T* bias_gradient, T* row_means,
+                                        const T* partial_weight, const T* partial_bias,
+                                        uint64_t parts, const T* row_partial, uint64_t splits,
+                                        uint64_t rows, uint64_t n, uint64_t column_blocks) {
+  __shared__ T lds[kCombineWaves][kWave];
+  const uint64_t block = blockIdx.x;
+  if (block < column_blocks) {
+    combine_group<T>(weight_gradient, partial_weight, parts, n, block, lds);
+    return;
+  }
+  uint64_t rest = block - column_blocks;
+  if constexpr (CENTER) {
+    if (rest < column_blocks) {
+      combine_group<T>(bias_gradient, partial_bias, parts, n, rest, lds);
+      return;
+    }
+    rest -= column_blocks;
+  }
+  const uint64_t p = rest * kCombineThreads + threadIdx.x;
+  if (p >= rows) return;
+  const T count = static_cast<T>(n);
+  T sum_g = T(0);
+  T sum_gx = T(0);
+  for (uint64_t s = 0; s < splits; ++s) {
+    if constexpr (CENTER) sum_g += row_partial[s * rows + p];
+    sum_gx += row_partial[(splits + s) * rows + p];
+  }
+  row_means[p] = CENTER ? sum_g / count : T(0);
+  row_means[rows + p] = sum_gx / count;
+}
+
+template <typename T, bool CENTER, int MODE, bool NT>
+__global__ void __launch_bounds__(kApplyThreads)
+    norm_backward_columns_apply_kernel(T* dx, const T* dy, const T* in, uint64_t pitch,
+                                       const T* weight, const T* mean, const T* denominator,
+                                       const T* row_means, uint64_t rows, uint64_t n,
+                                       FastDiv tiles_p, FastDiv tiles_q, uint32_t tile_count) {
+  constexpr bool VEC = MODE != kScalarTiles;
+  constexpr bool WHOLE = MODE == kWholeTiles;
+  using V = typename Vec16<T>::type;
+  constexpr int W = Vec16<T>::width;
+  constexpr int G = kApplyGranules;
+  constexpr int TP = G * W;
+  constexpr int TQ = G * W;
+  constexpr int kLoads = TP * G / kApplyThreads;             // dy granules staged per lane
+  constexpr int kBlocks = (TP / W) * G / kApplyThreads;      // W x W blocks per lane
+  constexpr int kGroups = kBackwardGroups;
+  static_assert(kApplyThreads % G == 0 && kGroups * (TP / W) == kApplyThreads, "lane layout");
+  __shared__ V lds[TP][G];
+  // p tiles fastest, each p column of tiles rotated along q by its index.
+  auto locate = [&](uint32_t tile, uint64_t& p0, uint64_t& q0) {
+    const uint32_t rest = tiles_p.div(tile);
+    const uint32_t tp = tile - rest * tiles_p.divisor;
+    const uint32_t rotated = rest + tp % tiles_q.divisor;
+    const uint32_t tq = rotated >= tiles_q.divisor ? rotated - tiles_q.divisor : rotated;
+    p0 = static_cast<uint64_t>(tp) * TP;
+    q0 = static_cast<uint64_t>(tq) * TQ;
+  };
+  V staged[kLoads];
+  // Staged dy granules: q offset (lane % G) W, p offsets lane / G + it *
+  // kApplyThreads / G.
+  const uint64_t lane_offset = static_cast<uint64_t>(threadIdx.x % G) * W +
+                               static_cast<uint64_t>(threadIdx.x / G) * n;
+  const uint64_t load_step = static_cast<uint64_t>(kApplyThreads / G) * n;
+  auto load_tile = [&](uint64_t p0, uint64_t q0) {
+    if constexpr (VEC) {
+      // whole granules; absent ones load the first element and are zeroed
+      const T* at = dy + p0 * n + q0 + lane_offset;
+      const bool q_present = q0 + static_cast<uint64_t>(threadIdx.x % G) * W < n;
+      const uint64_t first_p = p0 + threadIdx.x / G;
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const bool present =
+            WHOLE ||
+            (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
+        const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
+        staged[it] = present ? v : V{};
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const int index = it * kApplyThreads + threadIdx.x;
+        const uint64_t p = p0 + index / G;
+        const uint64_t q = q0 + static_cast<uint64_t>(index % G) * W;
+        V v{};
+        if (p < rows) {
+#pragma unroll
+          for (int k = 0; k < W; ++k) {
+            if (q + k < n) vec_set<T>(v, k, dy[p * n + q + k]);
+          }
+        }
+        staged[it] = v;
+      }
+    }
+  };
+  // Store-phase layout: a lane keeps p granule c and takes q granules g0,
+  // g0 + kGroups, ... (one per block).
+  const int c = threadIdx.x % (TP / W);
+  const int g0 = threadIdx.x / (TP / W);
+  uint32_t tile = blockIdx.x;
+  if (tile >= tile_count) return;
+  uint64_t p0 = 0;
+  uint64_t q0 = 0;
+  locate(tile, p0, q0);
+  load_tile(p0, q0);
+  while (true) {
+    const uint32_t next = tile + gridDim.x;
+    __syncthreads();  // the previous tile's LDS readers are done
+#pragma unroll
+    for (int it = 0; it < kLoads; ++it) {
+      const int index = it * kApplyThreads + threadIdx.x;
+      const int row = index / G;
+      lds[row][(index % G) ^ ((row / W) & 7)] = staged[it];
+    }
+    __syncthreads();
+    // This tile's x, weight and row statistics, issued before the next
+    // tile's dy loads.
+    const uint64_t p = p0 + static_cast<uint64_t>(c) * W;
+    T mu[W];
+    T d[W];
+    T mean_g[W];
+    T mean_gx[W];
+    V x[kBlocks][W];  // [block][q offset], W values of p each
+    T w[kBlocks][W];
+    if constexpr (VEC) {
+      // whole granules; absent ones load the first element instead
+      const bool p_present = WHOLE || p < rows;
+      const uint64_t at_p = p_present ? p : 0;
+      const V dv = *reinterpret_cast<const V*>(denominator + at_p);
+      const V gv = *reinterpret_cast<const V*>(row_means + at_p);
+      const V xv = *reinterpret_cast<const V*>(row_means + rows + at_p);
+      V mv{};
+      if constexpr (CENTER) mv = *reinterpret_cast<const V*>(mean + at_p);
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        mu[i] = vec_get<T>(mv, i);
+        d[i] = p_present ? vec_get<T>(dv, i) : T(1);
+        mean_g[i] = vec_get<T>(gv, i);
+        mean_gx[i] = vec_get<T>(xv, i);
+      }
+      const uint64_t first_q = q0 + static_cast<uint64_t>(g0) * W;
+      const T* at = in + p + first_q * pitch;
+#pragma unroll
+      for (int it = 0; it < kBlocks; ++it) {
+        const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
+        const bool present = WHOLE || (p_present && q < n);
+        const V wv = *reinterpret_cast<const V*>(present ? weight + q : weight);
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          w[it][k] = vec_get<T>(wv, k);
+          const V* source = reinterpret_cast<const V*>(
+              present ? at + (static_cast<uint64_t>(it) * kGroups * W + k) * pitch : in);
+          x[it][k] = *source;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const bool present = p + i < rows;
+        mu[i] = CENTER && present ? mean[p + i] : T(0);
+        d[i] = present ? denominator[p + i] : T(1);
+        mean_g[i] = present ? row_means[p + i] : T(0);
+        mean_gx[i] = present ? row_means[rows + p + i] : T(0);
+      }
+#pragma unroll
+      for (int it = 0; it < kBlocks; ++it) {
+        const uint64_t q = q0 + static_cast<uint64_t>(g0 + it * kGroups) * W;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          w[it][k] = q + k < n ? weight[q + k] : T(0);
+          x[it][k] = q + k < n ? load_column_group<T, false>(in, p, q + k, pitch, rows) : V{};
+        }
+      }
+    }
+    uint64_t next_p0 = p0;
+    uint64_t next_q0 = q0;
+    if (next < tile_count) {
+      locate(next, next_p0, next_q0);
+      load_tile(next_p0, next_q0);  // in flight during this tile's stores
+    }
+    T r[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) r[i] = T(1) / d[i];
+#pragma unroll
+    for (int it = 0; it < kBlocks; ++it) {
+      const int g = g0 + it * kGroups;
+      const uint64_t q = q0 + static_cast<uint64_t>(g) * W;
+      if (!WHOLE && (q >= n || p >= rows)) continue;
+      T grad[W][W];  // [p offset][q offset]
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const V block = lds[c * W + i][g ^ (c & 7)];
+#pragma unroll
+        for (int k = 0; k < W; ++k) grad[i][k] = vec_get<T>(block, k);
+      }
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        if (!WHOLE && q + k >= n) break;
+        V o;
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          const Divisor<T> divide(d[i], r[i]);
+          const T xhat = divide(vec_get<T>(x[it][k], i) - mu[i]);
+          const T gw = grad[i][k] * w[it][k];
+          vec_set<T>(o, i, divide(gw - mean_g[i] - xhat * mean_gx[i]));
+        }
+        T* column = dx + p + (q + k) * rows;
+        if constexpr (VEC) {
+          store_vector<NT>(reinterpret_cast<V*>(column), o);
+        } else {
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            if (p + i < rows) column[i] = vec_get<T>(o, i);
+          }
+        }
+      }
+    }
+    if (next >= tile_count) break;
+    tile = next;
+    p0 = next_p0;
+    q0 = next_q0;
   }
 }
 
@@ -884,6 +1430,90 @@ struct NormBackwardArgs {
   uint64_t n;
   bool center;
 };
+
+// Rows down storage columns: sums pass, finish, tiled apply pass.  The
+// partials come from the stream-ordered scratch pool.
+template <typename T, bool CENTER, int MODE>
+hipError_t backward_columns_as(const NormBackwardArgs& a, uint64_t pitch, int device,
+                               const DeviceGuard& guard) {
+  constexpr int W = Vec16<T>::width;
+  constexpr uint64_t kTile = static_cast<uint64_t>(kApplyGranules) * W;
+  const uint64_t tiles_p = (a.rows + kTile - 1) / kTile;
+  const uint64_t tiles_q = (a.n + kTile - 1) / kTile;
+  const uint64_t tiles = tiles_p * tiles_q;
+  // Splits of q for the sums pass: about one workgroup per resident slot.
+  const uint64_t cus = static_cast<uint64_t>(guard.multiprocessors);
+  uint64_t sums_slots =
+      resident_blocks(norm_backward_columns_sums_kernel<T, CENTER, MODE, true>, kApplyThreads,
+                      guard);
+  if (sums_slots == 0) sums_slots = cus;
+  uint64_t splits = (sums_slots + tiles_p - 1) / tiles_p;
+  if (splits > tiles_q) splits = tiles_q;
+  if (splits < 1) splits = 1;
+  const uint64_t split_tiles = (tiles_q + splits - 1) / splits;
+  splits = (tiles_q + split_tiles - 1) / split_tiles;
+  const uint64_t row_partials = 2 * splits * a.rows;
+  const uint64_t column_partials = (CENTER ? 2 : 1) * tiles_p * a.n;
+  const uint64_t row_means = 2 * a.rows;
+  void* scratch = nullptr;
+  hipError_t error = scratch_allocate(
+      &scratch, (row_partials + column_partials + row_means) * sizeof(T) + 512, device);
+  if (error != hipSuccess) return error;
+  // three 256-byte aligned pieces
+  auto piece = [](void* base, uint64_t offset) {
+    return reinterpret_cast<T*>((reinterpret_cast<uintptr_t>(base) + offset + 255) /
+                                256 * 256);
+  };
+  T* row_partial = static_cast<T*>(scratch);
+  T* partial_weight = piece(scratch, row_partials * sizeof(T));
+  T* partial_bias = CENTER ? partial_weight + tiles_p * a.n : nullptr;
+  T* means = piece(partial_weight, column_partials * sizeof(T));
+  const T* dy = static_cast<const T*>(a.dy);
+  const T* in = static_cast<const T*>(a.input);
+  const T* weight = static_cast<const T*>(a.weight);
+  const T* mean = static_cast<const T*>(a.mean);
+  const T* denominator = static_cast<const T*>(a.denominator);
+  const uint32_t sums_grid = static_cast<uint32_t>(tiles_p * splits);
+  if (a.rows * a.n * sizeof(T) <= kCacheReuseBytes) {
+    norm_backward_columns_sums_kernel<T, CENTER, MODE, true>
+        <<<sums_grid, kApplyThreads, 0, guard.stream>>>(
+            row_partial, partial_weight, partial_bias, dy, in, pitch, weight, mean, denominator,
+            a.rows, a.n, static_cast<uint32_t>(tiles_q), static_cast<uint32_t>(splits),
+            static_cast<uint32_t>(split_tiles));
+  } else {
+    norm_backward_columns_sums_kernel<T, CENTER, MODE, false>
+        <<<sums_grid, kApplyThreads, 0, guard.stream>>>(
+            row_partial, partial_weight, partial_bias, dy, in, pitch, weight, mean, denominator,
+            a.rows, a.n, static_cast<uint32_t>(tiles_q), static_cast<uint32_t>(splits),
+            static_cast<uint32_t>(split_tiles));
+  }
+  const uint64_t column_blocks = (a.n + kWave - 1) / kWave;
+  const uint64_t row_blocks = (a.rows + kCombineThreads - 1) / kCombineThreads;
+  norm_backward_columns_finish_kernel<T, CENTER>
+      <<<static_cast<uint32_t>((CENTER ? 2 : 1) * column_blocks + row_blocks), kCombineThreads,
+         0, guard.stream>>>(static_cast<T*>(a.dweight), static_cast<T*>(a.dbias), means,
+                            partial_weight, partial_bias, tiles_p, row_partial, splits, a.rows,
+                            a.n, column_blocks);
+  FastDiv divide_p;
+  FastDiv divide_q;
+  divide_p.init(static_cast<uint32_t>(tiles_p));
+  divide_q.init(static_cast<uint32_t>(tiles_q));
+  with_policy(stream_output(a.rows * a.n * sizeof(T)), [&](auto nt) {
+    constexpr bool NT = decltype(nt)::value;
+    const auto kernel = norm_backward_columns_apply_kernel<T, CENTER, MODE, NT>;
+    // One workgroup per resident slot, each walking tiles; they do not
+    // depend on each other, so an unknown occupancy (0) takes two per CU.
+    uint64_t slots = resident_blocks(kernel, kApplyThreads, guard);
+    if (slots == 0) slots = 2 * cus;
+    kernel<<<static_cast<uint32_t>(tiles < slots ? tiles : slots), kApplyThreads, 0,
+             guard.stream>>>(static_cast<T*>(a.dx), dy, in, pitch, weight, mean, denominator,
+                             means, a.rows, a.n, divide_p, divide_q,
+                             static_cast<uint32_t>(tiles));
+  });
+  error = hipGetLastError();
+  scratch_release(scratch, device);  // stream-ordered reuse
+  return error;
+}
 
 template <typename T, int THREADS, int E, bool CENTER, bool VEC>
 hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard& guard) {
@@ -1096,15 +1726,27 @@ extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, 
 
 extern "C" SparHipStatus spar_hip_launch_norm_backward(
     void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
-    const void* input, uint64_t input_row_stride, const void* weight, const void* mean,
-    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device) {
+    const void* input, uint64_t input_row_stride, uint64_t input_column_stride,
+    const void* weight, const void* mean, const void* denominator, uint64_t rows,
+    uint64_t extent, int center, int dtype, int device) {
+  // The forward's two layouts; in the column layout dx is written packed in
+  // that layout (dx[p + q * rows]).
+  const bool row_layout = input_column_stride == 1 && input_row_stride >= extent;
+  const bool column_layout =
+      input_column_stride != 1 && input_row_stride == 1 && input_column_stride >= rows;
   if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
-      extent > spar_hip_norm_max_extent(dtype) || input_row_stride < extent ||
+      extent > spar_hip_norm_max_extent(dtype) || !(row_layout || column_layout) ||
       (rows != 0 &&
        (input_gradient == nullptr || weight_gradient == nullptr || output_gradient == nullptr ||
         input == nullptr || weight == nullptr || denominator == nullptr ||
         (center && (mean == nullptr || bias_gradient == nullptr))))) {
     return invalid();
+  }
+  const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
+  if (column_layout) {
+    const uint64_t tile = static_cast<uint64_t>(kApplyGranules) * width;
+    const uint64_t tiles = ((rows + tile - 1) / tile) * ((extent + tile - 1) / tile);
+    if (tiles > kIndex32Limit) return invalid();
   }
   DeviceGuard guard;
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
@@ -1118,7 +1760,46 @@ extern "C" SparHipStatus spar_hip_launch_norm_backward(
   const NormBackwardArgs a{input_gradient, weight_gradient,  bias_gradient, output_gradient,
                            input,          input_row_stride, weight,        mean,
                            denominator,    rows,             extent,        center != 0};
-  const int width = dtype == SPAR_HIP_FLOAT32 ? 4 : 2;
+  if (column_layout) {
+    const bool vec = aligned_rows(output_gradient, extent, width) && extent % width == 0 &&
+                     aligned_rows(weight, extent, width) &&
+                     aligned_rows(input, input_column_stride, width) &&
+                     aligned_rows(input_gradient, rows, width) &&
+                     rows % static_cast<uint64_t>(width) == 0 &&
+                     aligned16(denominator) && (!center || aligned16(mean));
+    // every tile whole: rows and extent multiples of the tile side
+    const uint64_t tile = static_cast<uint64_t>(kApplyGranules) * width;
+    const bool whole = vec && rows % tile == 0 && extent % tile == 0;
+    hipError_t error = hipSuccess;
+    auto run = [&](auto tag, auto center_tag, auto mode_tag) {
+      using T = decltype(tag);
+      error = backward_columns_as<T, decltype(center_tag)::value, decltype(mode_tag)::value>(
+          a, input_column_stride, device, guard);
+    };
+    auto with_vec = [&](auto tag, auto center_tag) {
+      if (whole) {
+        run(tag, center_tag, std::integral_constant<int, kWholeTiles>{});
+      } else if (vec) {
+        run(tag, center_tag, std::integral_constant<int, kVectorTiles>{});
+      } else {
+        run(tag, center_tag, std::integral_constant<int, kScalarTiles>{});
+      }
+    };
+    auto with_center = [&](auto tag) {
+      if (center) {
+        with_vec(tag, std::true_type{});
+      } else {
+        with_vec(tag, std::false_type{});
+      }
+    };
+    if (dtype == SPAR_HIP_FLOAT32) {
+      with_center(float{});
+    } else {
+      with_center(double{});
+    }
+    if (error != hipSuccess) return runtime(error);
+    return finish(guard);
+  }
   const bool vec = aligned_rows(input_gradient, extent, width) &&
                    aligned_rows(output_gradient, extent, width) &&
                    aligned_rows(input, input_row_stride, width) && extent % width == 0 &&

@@ -67,7 +67,7 @@ Tensor composed(const Tensor& input, const Tensor& weight, const Tensor* bias, d
 //     one such as a narrowed view): rows `row_stride` elements apart;
 //   column layout: the leading axes contiguous among themselves and the
 //     last axis `column_stride` >= rows elements apart (a transposed matrix):
-//     the forward reads x without a transposing copy;
+//     forward and backward read x without a transposing copy;
 // otherwise the input is made contiguous first.
 struct Rows {
   Tensor source;              // the tensor whose storage the kernels read
@@ -131,6 +131,35 @@ Rows rows_of(const Tensor& input) {
   return Rows{packed, first, extent, 1};
 }
 
+// Storage for a gradient of `shape` in the packed column layout: a
+// contiguous [last, leading...] block viewed with the last axis moved back
+// to the end (for a matrix, the transpose of a contiguous [n, rows] block).
+struct PackedColumns {
+  Tensor storage;  // contiguous: the kernels write here
+  Tensor view;     // `shape`, the gradient handed to autograd
+};
+
+PackedColumns packed_columns(const Shape& shape, DType dtype, const Device& device) {
+  const std::size_t rank{shape.rank()};
+  std::vector<Shape::dimension_type> outer{shape[rank - 1]};
+  std::vector<std::size_t> order;
+  for (std::size_t axis{0}; axis + 1 < rank; ++axis) {
+    outer.push_back(shape[axis]);
+    order.push_back(axis + 1);
+  }
+  order.push_back(0);
+  Tensor storage{Shape{std::move(outer)}, dtype, device};
+  Tensor view{storage.permute(std::span<const std::size_t>{order})};
+  return PackedColumns{std::move(storage), std::move(view)};
+}
+
+PackedColumns input_gradient(const Tensor& input, bool columns) {
+  if (columns) return packed_columns(input.shape(), input.dtype(), input.device());
+  Tensor storage{input.shape(), input.dtype(), input.device()};
+  Tensor view{storage};
+  return PackedColumns{std::move(storage), std::move(view)};
+}
+
 Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
              const char* name) {
   const bool center{bias != nullptr};
@@ -169,35 +198,35 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
     if (grad_w) parents.push_back(weight);
     if (grad_b) parents.push_back(*bias);
     const Tensor saved_x{x.source.detach()}, saved_w{w.detach()};
-    const std::size_t saved_stride{x.row_stride};
-    const bool saved_columns{x.column_stride != 1};
+    const std::size_t saved_row_stride{x.row_stride};
+    const std::size_t saved_column_stride{x.column_stride};
     const Shape weight_shape{weight.shape()};
     detail::record_operation(
         output, std::move(parents),
-        [saved_x, saved_stride, saved_columns, saved_w, mean_rows, denominator, rows, extent,
-         center, grad_x, grad_w, grad_b, weight_shape, name](const Tensor& gradient) {
+        [saved_x, saved_row_stride, saved_column_stride, saved_w, mean_rows, denominator, rows,
+         extent, center, grad_x, grad_w, grad_b, weight_shape, name](const Tensor& gradient) {
           const Tensor dy{gradient.is_contiguous() ? gradient.detach()
                                                    : gradient.detach().contiguous()};
-          Tensor dx{saved_x.shape(), saved_x.dtype(), saved_x.device()};
+          // An input read in the column layout gets its gradient in that
+          // layout, packed (the gradient of a transposed view is then the
+          // transpose of a contiguous block, passed on without a copy); one
+          // read in rows gets a contiguous gradient.
+          PackedColumns dx{input_gradient(saved_x, saved_column_stride != 1)};
           Tensor dw{weight_shape, saved_x.dtype(), saved_x.device()};
           std::optional<Tensor> db;
           if (center) db.emplace(weight_shape, saved_x.dtype(), saved_x.device());
-          // The backward kernel reads rows: an input saved in the column
-          // layout is made contiguous here, once, instead of in the forward.
-          const Tensor x_rows{saved_columns ? saved_x.contiguous() : saved_x};
-          const void* first{first_element(x_rows)};
-          const std::size_t row_stride{saved_columns ? extent : saved_stride};
           hip::check(spar_hip_launch_norm_backward(
-                         HipTensorAccess::mutable_data(dx), HipTensorAccess::mutable_data(dw),
+                         HipTensorAccess::mutable_data(dx.storage),
+                         HipTensorAccess::mutable_data(dw),
                          center ? HipTensorAccess::mutable_data(*db) : nullptr,
-                         HipTensorAccess::data(dy), first, row_stride,
-                         HipTensorAccess::data(saved_w),
+                         HipTensorAccess::data(dy), first_element(saved_x), saved_row_stride,
+                         saved_column_stride, HipTensorAccess::data(saved_w),
                          center ? HipTensorAccess::data(*mean_rows) : nullptr,
                          HipTensorAccess::data(denominator), rows, extent, center ? 1 : 0,
                          hip::dtype_tag(saved_x.dtype()), saved_x.device().index()),
                      std::string{name} + " backward", saved_x.device());
           std::vector<Tensor> contributions;
-          if (grad_x) contributions.push_back(dx);
+          if (grad_x) contributions.push_back(dx.view);
           if (grad_w) contributions.push_back(dw);
           if (grad_b) contributions.push_back(*db);
           return contributions;

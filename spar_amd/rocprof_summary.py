@@ -283,7 +283,7 @@ def suite_commands(raw: Path, section: str):
     return {
         "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d",
                   str(raw / "trace"), "-o", "trace", "--"] + bench,
-        "plain": bench,
+        "plain": bench + ["--suite"],
     }
 
 
@@ -335,7 +335,8 @@ def summarize_suite(raw: Path, out: Path, section: str) -> None:
     suite_lines = [line for line in (raw / "plain.log").read_text().splitlines()
                    if line.startswith('{"suite"')]
     lines += ["", "The suite's own lines without a profiler (`" + shell(cmds["plain"]) + "`),",
-              "each op timed cold with HIP events (median of 20):", "", "```"]
+              "each op timed with HIP events (`timing` says how: back to back over rotated",
+              "input sets, or cold single launches, median of 20):", "", "```"]
     lines += suite_lines
     lines += ["```"]
     (out / suite_file(section)).write_text("\n".join(lines) + "\n")

@@ -165,7 +165,7 @@ def test_norm_backward_kernel(hip, dtype, center):
         _, _, _, (dx_in, mu, d) = forward_device(hip, x, w, b, center, dtype)
         dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
         hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
-                 dev(hip, g).ptr, dx_in.ptr, n, dev(hip, w).ptr, mu.ptr if center else None,
+                 dev(hip, g).ptr, dx_in.ptr, n, 1, dev(hip, w).ptr, mu.ptr if center else None,
                  d.ptr, rows, n, int(center), tag(dtype), 0)
         tx = R.RTensor.of(x, requires_grad=True)
         tw = R.RTensor.of(w, requires_grad=True)
@@ -208,12 +208,18 @@ def test_norm_entry_points_reject_bad_arguments(hip):
     ]
     for args in bad:
         assert lib.spar_hip_launch_norm_forward(*args).code == 1, args
-    assert lib.spar_hip_launch_norm_backward(p, p, None, p, p, 8, p, p, p, 4, 8, 1, 0, 0).code == 1
-    assert lib.spar_hip_launch_norm_backward(p, p, p, p, p, 6, p, p, p, 4, 8, 1, 0, 0).code == 1
+    backward_bad = [
+        (p, p, None, p, p, 8, 1, p, p, p, 4, 8, 1, 0, 0),  # LayerNorm without a bias gradient
+        (p, p, p, p, p, 6, 1, p, p, p, 4, 8, 1, 0, 0),     # rows overlap
+        (p, p, p, p, p, 1, 3, p, p, p, 4, 8, 1, 0, 0),     # columns overlap
+        (p, p, p, p, p, 8, 2, p, p, p, 4, 8, 1, 0, 0),     # neither layout
+    ]
+    for args in backward_bad:
+        assert lib.spar_hip_launch_norm_backward(*args).code == 1, args
     # zero rows: parameter gradients are zero, nothing else is touched
     dw, db = out_buf(hip, 8, F32), out_buf(hip, 8, F32)
-    hip.call("spar_hip_launch_norm_backward", None, dw.ptr, db.ptr, None, None, 8, p, None, None,
-             0, 8, 1, 0, 0)
+    hip.call("spar_hip_launch_norm_backward", None, dw.ptr, db.ptr, None, None, 8, 1, p, None,
+             None, 0, 8, 1, 0, 0)
     assert not dw.to_numpy(F32, (8,)).any() and not db.to_numpy(F32, (8,)).any()
 
 
@@ -388,7 +394,7 @@ def test_norm_row_stride_matches_contiguous(hip, dtype, center, rows, n, pitch, 
     for source, stride in ((x_dev.ptr, n), (wide_dev.address(first * item), pitch)):
         dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
         hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
-                 dev(hip, g).ptr, source, stride, dev(hip, w).ptr, mu.ptr if center else None,
+                 dev(hip, g).ptr, source, stride, 1, dev(hip, w).ptr, mu.ptr if center else None,
                  d.ptr, rows, n, int(center), tag(dtype), 0)
         outs.append([dx.to_numpy(dtype, (rows, n)), dw.to_numpy(dtype, (n,))] +
                     ([db.to_numpy(dtype, (n,))] if center else []))
@@ -443,6 +449,79 @@ def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
     # they carry their own rounding, a random walk over the row
     allowance = 4.0 if dtype == F32 else 8.0 * np.sqrt(n)
     assert np.all(np.abs(got_d - d64) <= allowance * eps * d64), "column layout d vs float64"
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
+@pytest.mark.parametrize("rows,n,pitch,first", [
+    (512, 1024, 512, 0),     # a transposed contiguous matrix: whole tiles
+    (200, 520, 264, 4),      # a transposed block of a wider matrix: partial tiles
+    (37, 300, 41, 3),        # unaligned: scalar loads and stores
+    (8, 8192, 8, 0),         # few rows, long rows: one p tile, many q splits
+    (1000, 12, 1000, 0),     # many rows, short rows: one q tile
+    (3, 5, 7, 1),            # tiny and ragged
+])
+def test_norm_backward_column_layout(hip, dtype, center, rows, n, pitch, first):
+    """The backward over rows that run down storage columns writes dx packed
+    in that layout (dx[p + q * rows]).  Against the row kernel on the same
+    rows made contiguous, with the same saved statistics: the two sum in
+    different orders, so dx within the dx row tolerance and the parameter
+    gradients within red(rows) of their terms."""
+    x, w, b, g = data(rows, n, dtype, 700 + rows + n)
+    store = np.zeros(first + n * pitch, dtype)
+    store[first:].reshape(n, pitch)[:, :rows] = x.T
+    assert first + rows - 1 + (n - 1) * pitch < store.size
+    _, _, _, (x_dev, mu, d) = forward_device(hip, x, w, b, center, dtype)
+    store_dev = dev(hip, store)
+    item = np.dtype(dtype).itemsize
+    g_dev, w_dev = dev(hip, g), dev(hip, w)
+    outs = []
+    for source, row_stride, column_stride in ((x_dev.ptr, n, 1),
+                                              (store_dev.address(first * item), 1, pitch)):
+        dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
+        hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
+                 g_dev.ptr, source, row_stride, column_stride, w_dev.ptr,
+                 mu.ptr if center else None, d.ptr, rows, n, int(center), tag(dtype), 0)
+        got = dx.to_numpy(dtype, (rows * n,))
+        got = got.reshape(rows, n) if column_stride == 1 else got.reshape(n, rows).T
+        outs.append((got, dw.to_numpy(dtype, (n,)), db.to_numpy(dtype, (n,)) if center else None))
+    (dx_rows, dw_rows, db_rows), (dx_cols, dw_cols, db_cols) = outs
+    what = f"column backward {rows}x{n} {np.dtype(dtype).name} center={center}"
+    assert_rows(dx_cols, dx_rows, n, dtype, what + " dx", 16.0, dx_terms(g, w, x, center))
+    x64 = x.astype(np.float64)
+    xc = x64 - (x64.mean(axis=1, keepdims=True) if center else 0)
+    xhat = xc / np.sqrt(np.mean(xc * xc, axis=1, keepdims=True) + EPSILON)
+    terms = np.abs(g.astype(np.float64) * xhat)
+    bound = 8e-6 * np.sqrt(max(rows, n)) * np.sum(terms, axis=0) + 1e-30
+    assert np.all(np.abs(dw_cols.astype(np.float64) - dw_rows) <= bound), what + " d weight"
+    if center:
+        bound = 8e-6 * np.sqrt(rows) * np.sum(np.abs(g.astype(np.float64)), axis=0) + 1e-30
+        assert np.all(np.abs(db_cols.astype(np.float64) - db_rows) <= bound), what + " d bias"
+
+
+def test_layer_norm_transposed_gradient_is_packed(sp):
+    """The gradient of a transposed view's LayerNorm reaches the base as a
+    contiguous [n, rows] tensor: the norm's backward writes it packed in the
+    column layout, and transpose's backward passes it on without a copy."""
+    rows, n = 96, 160
+    rng = np.random.default_rng(5)
+    base = rng.standard_normal((n, rows)).astype(F32)
+    w = rng.uniform(0.5, 1.5, n).astype(F32)
+    bias = rng.uniform(-0.1, 0.1, n).astype(F32)
+    g = rng.standard_normal((rows, n)).astype(F32)
+
+    def build(lib, t):
+        y = lib.layer_norm(t[0].transpose(0, 1), t[1], t[2], EPSILON)
+        lib.sum(lib.multiply(y, t[3])).backward()
+        return y
+
+    got_y, want_y, td, tr = api_both(sp, [base, w, bias, g], build)
+    assert_rows(got_y, want_y, n, F32, "transposed y")
+    cpu = sp.Device.cpu()
+    grad = td[0].grad()
+    assert grad.is_contiguous() and tuple(grad.shape) == (n, rows)
+    assert_rows(grad.to(cpu).numpy().T, tr[0].grad().numpy().T, n, F32, "transposed dx", 16.0,
+                dx_terms(g, w, base.T, True))
 
 
 @pytest.mark.parametrize("shape", [(12, 8, 300), (5, 7, 64)])
