@@ -271,6 +271,18 @@ struct SparHipStatus spar_hip_launch_window_embed(void* output, const void* inpu
                                                   uint64_t length, uint64_t element_size,
                                                   int device);
 
+/* The same for a box of several axes at once: output (contiguous, `rank`
+ * extents) = zeros except the box starts[a] <= c[a] < starts[a] + lengths[a]
+ * on every axis, which holds input (contiguous, extents `lengths`).  The
+ * gradient of a chain of narrows in one pass; no reference counterpart.
+ * element_size 4 or 8; outputs of at most 2^31 - 1 elements; after dropping
+ * axes of extent 1 and merging neighbouring whole axes, at most 4 axes.
+ * Status 1 for other shapes and for an empty box (length 0 on some axis). */
+struct SparHipStatus spar_hip_launch_box_embed(void* output, const void* input, int rank,
+                                               const uint64_t* extents, const uint64_t* starts,
+                                               const uint64_t* lengths, uint64_t element_size,
+                                               int device);
+
 /* Binary op over the broadcast shape `extents` (rank dims) without
  * materialising either operand: each operand is read through its own strides
  * (0 on broadcast axes) and storage offset; output is contiguous row-major.

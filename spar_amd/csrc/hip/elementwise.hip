@@ -443,6 +443,94 @@ void launch_window_embed(E* output, const E* input, uint64_t outer, uint64_t ext
   }
 }
 
+// A box of a contiguous tensor embedded in zeros: the output (contiguous,
+// extents E[0..R-1]) takes the input (contiguous, extents L) at coordinates
+// c with S[a] <= c[a] < S[a] + L[a] on every axis, zero elsewhere -- the
+// gradient of a chain of narrows, in one pass.  Axes are coalesced on the
+// host (R <= kMaxBoxAxes); indices are 32-bit.  VEC: groups of G elements
+// along the innermost axis, whose extent, start and length are multiples of
+// G, so a group is wholly inside or outside and its input stays aligned.
+constexpr int kMaxBoxAxes = 4;
+
+struct BoxGeometry {
+  FastDiv extent[kMaxBoxAxes];    // output extents, outermost first
+  uint32_t start[kMaxBoxAxes];
+  uint32_t length[kMaxBoxAxes];
+  uint32_t in_stride[kMaxBoxAxes];  // input elements per step along the axis
+};
+
+template <typename E, bool VEC, int R>
+__global__ void __launch_bounds__(kThreads)
+    box_embed_kernel(E* output, const E* input, uint64_t groups, BoxGeometry box) {
+  constexpr int G = VEC ? static_cast<int>(16 / sizeof(E)) : 1;
+  using V = typename Vec16<E>::type;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t group = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+       group < groups; group += stride) {
+    const uint32_t element = static_cast<uint32_t>(group) * G;
+    uint32_t rest = element;
+    bool inside = true;
+    uint32_t from = 0;
+#pragma unroll
+    for (int a = R - 1; a >= 0; --a) {
+      const uint32_t outer = box.extent[a].div(rest);
+      const uint32_t c = rest - outer * box.extent[a].divisor;
+      rest = outer;
+      inside = inside && c >= box.start[a] && c - box.start[a] < box.length[a];
+      from += (c - box.start[a]) * box.in_stride[a];
+    }
+    if constexpr (VEC) {
+      V value{};
+      if (inside) value = stream_load(reinterpret_cast<const V*>(input + from));
+      *reinterpret_cast<V*>(output + element) = value;
+    } else {
+      output[element] = inside ? input[from] : E(0);
+    }
+  }
+}
+
+template <typename E>
+void launch_box_embed(E* output, const E* input, int rank, const uint64_t* extents,
+                      const uint64_t* starts, const uint64_t* lengths, uint64_t count,
+                      const DeviceGuard& guard) {
+  constexpr uint64_t G = 16 / sizeof(E);
+  BoxGeometry box{};
+  uint32_t in_stride = 1;
+  for (int a = rank - 1; a >= 0; --a) {
+    box.extent[a].init(static_cast<uint32_t>(extents[a]));
+    box.start[a] = static_cast<uint32_t>(starts[a]);
+    box.length[a] = static_cast<uint32_t>(lengths[a]);
+    box.in_stride[a] = in_stride;
+    in_stride *= static_cast<uint32_t>(lengths[a]);
+  }
+  const int last = rank - 1;
+  const bool vec = aligned16(output) && aligned16(input) && extents[last] % G == 0 &&
+                   starts[last] % G == 0 && lengths[last] % G == 0;
+  const uint64_t groups = vec ? count / G : count;
+  uint64_t blocks = (groups + kThreads - 1) / kThreads;
+  const uint64_t cap = static_cast<uint64_t>(guard.multiprocessors) * 16;
+  if (blocks > cap) blocks = cap;
+  if (blocks == 0) blocks = 1;
+  auto launch = [&](auto kernel) {
+    kernel<<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(output, input, groups,
+                                                                          box);
+  };
+  auto with_rank = [&](auto vec_tag) {
+    constexpr bool VEC = decltype(vec_tag)::value;
+    switch (rank) {
+      case 1: launch(box_embed_kernel<E, VEC, 1>); break;
+      case 2: launch(box_embed_kernel<E, VEC, 2>); break;
+      case 3: launch(box_embed_kernel<E, VEC, 3>); break;
+      default: launch(box_embed_kernel<E, VEC, 4>); break;
+    }
+  };
+  if (vec) {
+    with_rank(std::true_type{});
+  } else {
+    with_rank(std::false_type{});
+  }
+}
+
 }  // namespace
 }  // namespace spar_hip
 
@@ -561,6 +649,68 @@ extern "C" SparHipStatus spar_hip_launch_window_embed(void* output, const void* 
   } else {
     launch_window_embed(static_cast<int64_t*>(output), static_cast<const int64_t*>(input),
                         outer, extent, inner, start, length, guard);
+  }
+  return finish(guard);
+}
+
+extern "C" SparHipStatus spar_hip_launch_box_embed(void* output, const void* input, int rank,
+                                                   const uint64_t* extents,
+                                                   const uint64_t* starts,
+                                                   const uint64_t* lengths,
+                                                   uint64_t element_size, int device) {
+  if ((element_size != 4 && element_size != 8) || rank < 1 || rank > SPAR_HIP_MAX_RANK ||
+      extents == nullptr || starts == nullptr || lengths == nullptr) {
+    return invalid();
+  }
+  uint64_t count = 1;
+  uint64_t inside = 1;
+  for (int a = 0; a < rank; ++a) {
+    if (starts[a] > extents[a] || lengths[a] > extents[a] - starts[a] ||
+        __builtin_mul_overflow(count, extents[a], &count)) {
+      return invalid();
+    }
+    inside *= lengths[a];  // <= count
+  }
+  if (count == 0) return ok();
+  // 32-bit element indices inside the kernel
+  if (count > kIndex32Limit || output == nullptr || (inside != 0 && input == nullptr)) {
+    return invalid();
+  }
+  // Coalesce: drop axes of extent 1 and merge neighbours that are both whole.
+  uint64_t e[SPAR_HIP_MAX_RANK];
+  uint64_t st[SPAR_HIP_MAX_RANK];
+  uint64_t len[SPAR_HIP_MAX_RANK];
+  int r = 0;
+  for (int a = 0; a < rank; ++a) {
+    if (extents[a] == 1) continue;
+    const bool whole = starts[a] == 0 && lengths[a] == extents[a];
+    if (r > 0 && whole && st[r - 1] == 0 && len[r - 1] == e[r - 1]) {
+      e[r - 1] *= extents[a];
+      len[r - 1] = e[r - 1];
+      continue;
+    }
+    e[r] = extents[a];
+    st[r] = starts[a];
+    len[r] = lengths[a];
+    ++r;
+  }
+  if (r == 0) {  // a single element
+    e[0] = 1;
+    st[0] = 0;
+    len[0] = 1;
+    r = 1;
+  }
+  // status 1: more box axes than the kernel takes, or an empty box (the
+  // caller fills zeros itself)
+  if (r > kMaxBoxAxes || inside == 0) return invalid();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  if (element_size == 4) {
+    launch_box_embed(static_cast<int32_t*>(output), static_cast<const int32_t*>(input), r, e, st,
+                     len, count, guard);
+  } else {
+    launch_box_embed(static_cast<int64_t*>(output), static_cast<const int64_t*>(input), r, e,
+                     st, len, count, guard);
   }
   return finish(guard);
 }

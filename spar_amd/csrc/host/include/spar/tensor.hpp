@@ -246,14 +246,16 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
 [[nodiscard]] bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept;
 
 /// Process-wide tallies of the autograd engine: backward() calls, leaf
-/// gradients copied because their storage was shared, and gradient
-/// accumulations done in place or out of place.  The engine never copies an
-/// intermediate gradient.
+/// gradients copied because their storage was shared, gradient
+/// accumulations done in place or out of place, and narrows whose gradient
+/// was handed to the narrow below them unembedded (a chain of narrows is
+/// embedded once).  The engine never copies an intermediate gradient.
 struct AutogradCounters final {
   std::uint64_t backward_calls;
   std::uint64_t leaf_copies;
   std::uint64_t in_place_adds;
   std::uint64_t out_of_place_adds;
+  std::uint64_t window_fusions;
 };
 [[nodiscard]] AutogradCounters autograd_counters() noexcept;
 

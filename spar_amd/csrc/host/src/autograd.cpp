@@ -15,6 +15,10 @@
 //      one is added elementwise, `held += incoming`, in sweep order.
 //   4. A leaf keeps the gradient it is handed on its first backward() and
 //      adds later ones in place (`accumulated += incoming`).
+//   5. A narrow whose input is a narrow with no other incoming gradient
+//      hands its gradient down unembedded, with the composed box; the first
+//      narrow below that does not embeds it once, at its own turn, so the
+//      identities above receive the same values in the same order.
 // Given identical contributions, the gradients are therefore identical to
 // the reference's.  The reference also cloned each contribution
 // (autograd.cpp:145, :244), which copied values into a dense tensor.  Here a
@@ -42,6 +46,7 @@ std::atomic<std::uint64_t> g_backward_calls{0};
 std::atomic<std::uint64_t> g_leaf_copies{0};
 std::atomic<std::uint64_t> g_in_place_adds{0};
 std::atomic<std::uint64_t> g_out_of_place_adds{0};
+std::atomic<std::uint64_t> g_window_fusions{0};
 
 GradInput input_of(const Tensor& parent) {
   return GradInput{TensorInternals::grad_state(parent), parent.shape(), parent.dtype(),
@@ -94,7 +99,7 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
 
 AutogradCounters autograd_counters() noexcept {
   return AutogradCounters{g_backward_calls.load(), g_leaf_copies.load(), g_in_place_adds.load(),
-                          g_out_of_place_adds.load()};
+                          g_out_of_place_adds.load(), g_window_fusions.load()};
 }
 
 bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept {
@@ -122,6 +127,38 @@ void add_into(Tensor& held, const Tensor& incoming) {
              "gradient accumulation", held.device());
 }
 
+// `gradient` (contiguous, the box's lengths) embedded in zeros of `shape` at
+// `box`: one pass on a HIP device, else a zero tensor whose box is assigned.
+Tensor embed_box(const Tensor& gradient, const Shape& shape, const std::vector<WindowAxis>& box) {
+  if (gradient.device().is_hip() && gradient.is_contiguous() &&
+      shape.rank() <= static_cast<std::size_t>(SPAR_HIP_MAX_RANK)) {
+    std::uint64_t extents[SPAR_HIP_MAX_RANK];
+    std::uint64_t starts[SPAR_HIP_MAX_RANK];
+    std::uint64_t lengths[SPAR_HIP_MAX_RANK];
+    for (std::size_t k{0}; k < shape.rank(); ++k) {
+      extents[k] = static_cast<std::uint64_t>(shape[k]);
+      starts[k] = box[k].start;
+      lengths[k] = box[k].length;
+    }
+    Tensor result{shape, gradient.dtype(), gradient.device()};
+    const auto status{spar_hip_launch_box_embed(
+        HipTensorAccess::mutable_data(result), HipTensorAccess::data(gradient),
+        static_cast<int>(shape.rank()), extents, starts, lengths, size_of(gradient.dtype()),
+        gradient.device().index())};
+    if (status.code == 0) return result;
+    // status 1 (more box axes than the one-pass kernel takes, or an empty
+    // box) falls through to the assignment
+    if (status.code != 1) hip::check(status, "narrow backward", gradient.device());
+  }
+  Tensor result{zeros(shape, gradient.dtype(), gradient.device())};
+  Tensor window{result};
+  for (std::size_t k{0}; k < shape.rank(); ++k) {
+    window = window.narrow(k, box[k].start, box[k].length);
+  }
+  copy_tensor_values(window, gradient);
+  return result;
+}
+
 // The sweep state of one backward() call.
 class Sweep final {
  public:
@@ -139,6 +176,10 @@ class Sweep final {
       held.reset();
       if (state.producer == nullptr) {
         deliver_to_leaf(state, std::move(gradient));
+        continue;
+      }
+      std::vector<WindowAxis> box{std::move(deferred_[position])};
+      if (!state.producer->window.empty() && narrow_chain(*state.producer, gradient, box)) {
         continue;
       }
       propagate(*state.producer, std::move(gradient));
@@ -172,6 +213,49 @@ class Sweep final {
       stack.pop_back();
     }
     pending_.resize(order_.size());
+    deferred_.resize(order_.size());
+    incoming_.assign(order_.size(), 0);
+    for (const GradState* state : order_) {
+      if (state->producer == nullptr) continue;
+      for (const GradInput& input : state->producer->inputs) {
+        const auto found{slot_.find(input.identity.get())};
+        if (found != slot_.end()) ++incoming_[found->second];
+      }
+    }
+  }
+
+  // A narrowed view's node (window W of its input v) holding `gradient`,
+  // which covers `box` of the node's own shape (all of it when `box` is
+  // empty).  When v is itself a narrowed view whose only incoming gradient
+  // is this one, the gradient is handed on unchanged with the composed box
+  // (start W + box start, length box length), to be embedded once, at v's
+  // own turn in the sweep, so that every other identity receives its
+  // gradients in the same order as without the composition.  Returns false
+  // when the node's own rule should run instead (no box to apply).
+  bool narrow_chain(const GradFunction& function, Tensor& gradient,
+                    const std::vector<WindowAxis>& box) {
+    const GradInput& input{function.inputs.front()};
+    std::vector<WindowAxis> composed{function.window};
+    for (std::size_t k{0}; k < composed.size() && !box.empty(); ++k) {
+      composed[k].start += box[k].start;
+      composed[k].length = box[k].length;
+    }
+    const auto found{slot_.find(input.identity.get())};
+    if (found == slot_.end()) return true;  // an identity no longer tracked
+    const std::size_t next{found->second};
+    const GradState& parent{*order_[next]};
+    const bool chain{parent.producer != nullptr && !parent.producer->window.empty() &&
+                     incoming_[next] == 1 && !pending_[next].has_value() &&
+                     gradient.device().is_hip() && gradient.is_contiguous()};
+    if (chain) {
+      pending_[next] = std::move(gradient);
+      deferred_[next] = std::move(composed);
+      g_window_fusions.fetch_add(1, std::memory_order_relaxed);
+      return true;
+    }
+    if (box.empty()) return false;
+    accumulate(input, embed_box(gradient, input.shape, composed));
+    return true;
   }
 
   // Runs one operation's rule and hands each input its gradient.
@@ -194,25 +278,30 @@ class Sweep final {
       }
       Tensor incoming{produced.detach()};
       contributions[k] = Tensor{Shape{}, produced.dtype(), Device::cpu()};
-      const auto found{slot_.find(input.identity.get())};
-      if (found == slot_.end()) continue;  // an identity no longer tracked
-      std::optional<Tensor>& held{pending_[found->second]};
-      if (!held.has_value()) {
-        held = std::move(incoming);
-        continue;
-      }
-      check_same_layout(*held, incoming);
-      // In place when the held gradient is dense and its own, and the
-      // incoming one dense too (a broadcast view would first be filled out);
-      // otherwise out of place, which reads views as they are.
-      if (TensorInternals::sole_owner(*held) && held->is_contiguous() &&
-          incoming.is_contiguous()) {
-        add_into(*held, incoming);
-        g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
-      } else {
-        held = add(held->detach(), incoming.detach());
-        g_out_of_place_adds.fetch_add(1, std::memory_order_relaxed);
-      }
+      accumulate(input, std::move(incoming));
+    }
+  }
+
+  // Hands `incoming` to the identity of `input` (contract, point 3).
+  void accumulate(const GradInput& input, Tensor incoming) {
+    const auto found{slot_.find(input.identity.get())};
+    if (found == slot_.end()) return;  // an identity no longer tracked
+    std::optional<Tensor>& held{pending_[found->second]};
+    if (!held.has_value()) {
+      held = std::move(incoming);
+      return;
+    }
+    check_same_layout(*held, incoming);
+    // In place when the held gradient is dense and its own, and the
+    // incoming one dense too (a broadcast view would first be filled out);
+    // otherwise out of place, which reads views as they are.
+    if (TensorInternals::sole_owner(*held) && held->is_contiguous() &&
+        incoming.is_contiguous()) {
+      add_into(*held, incoming);
+      g_in_place_adds.fetch_add(1, std::memory_order_relaxed);
+    } else {
+      held = add(held->detach(), incoming.detach());
+      g_out_of_place_adds.fetch_add(1, std::memory_order_relaxed);
     }
   }
 
@@ -236,6 +325,10 @@ class Sweep final {
   std::vector<GradState*> order_;
   std::unordered_map<const GradState*, std::size_t> slot_;
   std::vector<std::optional<Tensor>> pending_;
+  // per identity: the box its pending gradient covers when a narrow handed
+  // it on (empty: all of it), and the number of gradients it will receive
+  std::vector<std::vector<WindowAxis>> deferred_;
+  std::vector<std::size_t> incoming_;
 };
 
 }  // namespace

@@ -27,11 +27,22 @@ struct GradInput final {
   Device device;
 };
 
+/// One axis of the box a narrowed view takes of its input.
+struct WindowAxis final {
+  std::size_t start;
+  std::size_t length;
+};
+
 /// A recorded operation: its tracked inputs, in recording order, and the
 /// rule producing one gradient per input.
 struct GradFunction final {
   std::vector<GradInput> inputs;
   BackwardFunction rule;
+  /// Set (one entry per input axis) when the output is a narrowed view of
+  /// its one input, inputs[0] restricted to this box: the rule then embeds
+  /// the gradient in zeros of the input's shape, and the engine may compose
+  /// a chain of such nodes into one embedding.
+  std::vector<WindowAxis> window;
 };
 
 struct GradState final {

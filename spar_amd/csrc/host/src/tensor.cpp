@@ -358,8 +358,9 @@ Tensor Tensor::narrow(std::size_t axis, std::size_t start, std::size_t length) c
   const std::size_t offset{length == 0 ? storage_offset_ : storage_offset_ + start * strides_[axis]};
   // The gradient of a narrowed view is zero outside the window.  On a HIP
   // device a contiguous gradient is embedded in one pass; otherwise the
-  // window of a zero tensor is assigned.
-  return make_view(Shape{std::move(dimensions)}, strides_, offset,
+  // window of a zero tensor is assigned.  The node also records its box, so
+  // that the engine can embed the gradient of a chain of narrows at once.
+  Tensor view{make_view(Shape{std::move(dimensions)}, strides_, offset,
                    [original = shape_, axis, start, length](const Tensor& gradient) {
                      if (gradient.device().is_hip() && gradient.is_contiguous()) {
                        std::size_t outer{1}, inner{1};
@@ -386,7 +387,17 @@ Tensor Tensor::narrow(std::size_t axis, std::size_t start, std::size_t length) c
                      Tensor window{result.narrow(axis, start, length)};
                      detail::copy_tensor_values(window, gradient);
                      return std::vector<Tensor>{result};
-                   });
+                   })};
+  if (view.requires_grad()) {
+    std::vector<detail::WindowAxis> box;
+    box.reserve(rank());
+    for (std::size_t k{0}; k < rank(); ++k) {
+      box.push_back(k == axis ? detail::WindowAxis{start, length}
+                              : detail::WindowAxis{0, static_cast<std::size_t>(shape_[k])});
+    }
+    detail::TensorInternals::grad_state(view)->producer->window = std::move(box);
+  }
+  return view;
 }
 
 Tensor Tensor::detach() const { return Tensor{storage_, dtype_, shape_, strides_, storage_offset_}; }

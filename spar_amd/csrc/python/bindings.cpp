@@ -336,6 +336,7 @@ PYBIND11_MODULE(_spar, m) {
     d["leaf_copies"] = c.leaf_copies;
     d["in_place_adds"] = c.in_place_adds;
     d["out_of_place_adds"] = c.out_of_place_adds;
+    d["window_fusions"] = c.window_fusions;
     return d;
   });
 }

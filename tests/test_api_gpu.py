@@ -388,6 +388,56 @@ def test_autograd_layernorm_chain_on_views(sp, view):
         assert err <= 1e-6 * np.sqrt(rows * cols) * scale * 8, f"{name}: {err} vs scale {scale}"
 
 
+def test_autograd_narrow_chains_embed_once(sp):
+    """A chain of narrows is embedded into its base once: each narrow whose
+    input is a narrow with no other consumer hands its gradient down with
+    the composed box.  The gradients are bit-exact against the oracle, which
+    embeds one narrow at a time; an intermediate view with a second consumer
+    breaks the chain there, and a chain that ends on a computed tensor
+    embeds into it before that op's rule runs."""
+    base = normal(91, (13, 17, 9))
+    G = normal(92, (5, 10, 6))
+    H = normal(93, (8, 17, 9))
+
+    def chain(t):
+        return t.narrow(0, 2, 8).narrow(2, 1, 6).narrow(1, 3, 10).narrow(0, 1, 5)
+
+    def build(lib, t):
+        return weighted_sum(lib, chain(t[0]), t[1])
+
+    before = sp.autograd_counters()
+    loss_d, loss_r, gd, gr = run_both(sp, build, [base, G])
+    after = sp.autograd_counters()
+    assert after["window_fusions"] == before["window_fusions"] + 3
+    assert_bitexact(gd[0], gr[0], "base through four narrows")
+    want = np.zeros_like(base)
+    want[3:8, 3:13, 1:7] = G  # every element of G times the ones of the sum
+    assert_bitexact(gd[0], want, "embedded box")
+
+    # v = base.narrow(0, 2, 8) also feeds a second product: the chain stops
+    # above v, which adds the two gradients before its own embedding
+    def build_shared(lib, t):
+        v = t[0].narrow(0, 2, 8)
+        first = weighted_sum(lib, v.narrow(1, 3, 10).narrow(2, 1, 6), t[1])
+        return lib.add(first, weighted_sum(lib, v, t[2]))
+
+    G8 = normal(94, (8, 10, 6))
+    before = sp.autograd_counters()
+    _, _, gd, gr = run_both(sp, build_shared, [base, G8, H])
+    after = sp.autograd_counters()
+    assert after["window_fusions"] == before["window_fusions"] + 1
+    assert_bitexact(gd[0], gr[0], "base with a shared intermediate view")
+
+    # the chain ends on a product, not a leaf
+    def build_computed(lib, t):
+        u = lib.multiply_scalar(t[0], 3.0)
+        return weighted_sum(lib, u.narrow(1, 2, 12).narrow(0, 4, 6), t[1])
+
+    G6 = normal(95, (6, 12, 9))
+    _, _, gd, gr = run_both(sp, build_computed, [base, G6])
+    assert_bitexact(gd[0], gr[0], "base through a product and two narrows")
+
+
 def test_autograd_api_errors(sp):
     x = hip_tensor(sp, normal(1, (3,)), requires_grad=True)
     y = sp.multiply(x, x)

@@ -214,6 +214,48 @@ def test_window_embed_rejects_bad_arguments(hip):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("extents,box", [
+    ((4608, 9216), ((256, 4096), (512, 8192))),      # a block of a matrix, 16-byte groups
+    ((13, 17, 9), ((3, 5), (3, 10), (1, 6))),         # three boxed axes, element path
+    ((6, 1, 8, 12), ((1, 4), (0, 1), (0, 8), (4, 8))),  # unit and whole axes coalesced
+    ((5, 7), ((0, 5), (0, 7))),                       # the whole tensor
+    ((2, 3, 4, 5, 6), ((1, 1), (0, 3), (0, 4), (0, 5), (2, 3))),  # three whole axes merged
+])
+def test_box_embed(hip, dtype, extents, box):
+    """A box of several axes scattered into zeros in one pass (a chain of
+    narrows' gradient), against numpy (bit copies, so exact)."""
+    lengths = tuple(length for _, length in box)
+    rng = np.random.default_rng(sum(extents))
+    inner = rng.standard_normal(lengths).astype(dtype)
+    want = np.zeros(extents, dtype)
+    want[tuple(slice(start, start + length) for start, length in box)] = inner
+    out = out_buf(hip, want.shape, dtype)
+    hip.call("spar_hip_launch_fill", out.ptr, want.size, tag(dtype), 7.0, 0)  # not zero beforehand
+    src = dev(hip, inner)
+    arrays = [np.array(v, dtype=np.uint64) for v in (extents, [b[0] for b in box], lengths)]
+    hip.call("spar_hip_launch_box_embed", out.ptr, src.ptr, len(extents),
+             *[a.ctypes.data for a in arrays], np.dtype(dtype).itemsize, 0)
+    assert_bitexact(out.to_numpy(dtype, want.shape), want, "box embed")
+
+
+def test_box_embed_rejects_bad_arguments(hip):
+    lib = hip.load()
+    p = out_buf(hip, (4096,), F32).ptr
+
+    def call(extents, starts, lengths, size=4):
+        arrays = [np.array(v, dtype=np.uint64) for v in (extents, starts, lengths)]
+        return lib.spar_hip_launch_box_embed(p, p, len(extents), *[a.ctypes.data for a in arrays],
+                                             size, 0).code
+
+    assert call((4, 8), (0, 6), (4, 3)) == 1                  # box past the axis
+    assert call((4, 8), (0, 2), (4, 3), size=2) == 1          # element size 2
+    assert call((4, 8), (0, 2), (0, 3)) == 1                  # empty box: caller fills zeros
+    assert call((4, 4, 4, 4, 4), (1,) * 5, (2,) * 5) == 1     # five boxed axes
+    assert call((1 << 16, 1 << 16), (0, 0), (1, 1)) == 1      # more than 2^31 - 1 elements
+    assert call((4, 8), (1, 2), (2, 3)) == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_fill_add_in_place_zero(hip, dtype):
     n = 12345
     d = out_buf(hip, (n,), dtype)
