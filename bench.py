@@ -205,14 +205,21 @@ def cpu_baseline(hip, work: Workload, sample_batch=16, repeats=3):
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with its family, model and
+    stepping numbers (a virtual machine may report only a vendor name)."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as info:
             for line in info:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, value = line.partition(":")
+                fields[key.strip()] = value.strip()
     except OSError:
         pass
-    return platform.processor() or "unknown CPU"
+    name = fields.get("model name") or platform.processor() or "unknown CPU"
+    numbers = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(numbers)})" if numbers else name
 
 
 def calibration_copy(hip, work):

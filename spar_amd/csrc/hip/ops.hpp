@@ -234,18 +234,19 @@ __device__ __forceinline__ NormalTail normal_tail(double a) {
 }
 
 // GELU of a float32 from the tail table at `table` (global memory or an LDS
-// copy: the same values, so the same bits).  No branches and no patched
+// copy: the same values, so the same bits), pieces STRIDE doubles apart.  No branches and no patched
 // results: x is clamped to [-15, 15] inside the product, where Q(15) = 3.7e-51
 // already makes GELU round to -0 below -15 and to x above 15, and +inf stays
 // +inf (inf - 15 Q(15)).  Below 0 the product gains x - x, which is 0 for a
 // finite x and NaN for -inf, as (0.5 x) erfc(-x / sqrt 2) is; NaN inputs
 // take the x >= 0 form and propagate through it.
+template <int STRIDE = kGeluStride>
 __device__ __forceinline__ float gelu_float(float value, const double* table) {
   const double x = value;
   const double clamped = fmin(fmax(x, -kGeluTailLimit), kGeluTailLimit);
   const double a = __builtin_fabs(clamped);
   const double g = a * __builtin_fma(kGeluBeta, a, kGeluAlpha);
-  const double* c = table + static_cast<int>(g) * kGeluStride;
+  const double* c = table + static_cast<int>(g) * STRIDE;
   const double t = __builtin_amdgcn_fract(g);
   double q = c[kGeluDegree];
 #pragma unroll
