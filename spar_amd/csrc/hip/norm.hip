@@ -781,15 +781,17 @@ __global__ void __launch_bounds__(kCombineThreads)
 // dx:
 //
 //  1. norm_backward_columns_sums_kernel.  Tiles of 32 W values of p by 32 W
-//     values of q; x goes through LDS as in the forward's apply pass (XOR
-//     swizzle, the next tile's loads in flight while the current one is
-//     used) and dy is read along its rows.  A workgroup owns one p tile and a
-//     run of q tiles (a split of q).  Each lane keeps the sums of g = dy * w
-//     and g * xhat for its 4 W values of p in registers over the whole run;
-//     at the end the 32 lanes of each p are added through LDS in lane order.
-//     Every tile adds dy * xhat and dy over its p for each q (the 8 lanes of
-//     a q through LDS, in order).  Results: [2, splits, rows] row sums and
-//     [tiles_p, n] weight / bias partials.
+//     values of q in the transposed frame: dy goes through LDS (XOR swizzle,
+//     the next tile's dy in flight while the current one is used) and x is
+//     read along p, before that prefetch.  A workgroup owns one p tile and a
+//     run of q tiles (a split of q); each lane keeps one granule of W rows
+//     for the run and the sums of g = dy * w and g * xhat over its columns,
+//     which at the end the 8 lanes of each granule add (two per wave by a
+//     lane exchange, then the waves in order through LDS).  Per block of W
+//     columns the lane's partials of dy * xhat and dy over its rows are
+//     added across the 32 lanes of its half wave (the tile's p) by a
+//     butterfly.  Results: [2, splits, rows] row sums and [tiles_p, n]
+//     weight / bias partials.
 //  2. norm_backward_columns_finish_kernel: the weight and bias gradients (the
 //     partials added in p-tile order, as norm_combine_kernel does) and each
 //     row's mean(g) and mean(g * xhat) (splits added in order, then divided
@@ -801,12 +803,14 @@ __global__ void __launch_bounds__(kCombineThreads)
 // Only the order of the sums differs from the row kernel, so the two layouts
 // agree within the sums' rounding.  On an input that fits the Infinity Cache
 // the sums pass reads x with cached loads and the apply pass finds it there.
-constexpr int kBackwardGroups = kApplyThreads / kApplyGranules;  // lanes per q granule
+// lanes that share one p granule (and take every kBackwardGroups-th q granule)
+constexpr int kBackwardGroups = kApplyThreads / kApplyGranules;
 
 // Butterfly reduce-scatter over the 32 lanes of a half wave: on entry each
-// lane holds NV values, on exit lane c holds in v[0] the sum over the 32
-// lanes of value c * NV / 32 (lanes c and c ^ 1 alike when NV is 16).  Step b
-// pairs lanes c and c ^ b; the lane with bit b set keeps the upper half.
+// lane holds NV values (NV divides 32), on exit lane c holds in v[0] the sum
+// over the 32 lanes of value c * NV / 32, the 32 / NV lanes that share it
+// alike.  Step b pairs lanes c and c ^ b; while more than one value is left
+// the lane with bit b set keeps the upper half, after that both add.
 template <typename T, int NV, int B = 16>
 __device__ __forceinline__ void half_wave_reduce_scatter(T (&v)[NV], int c) {
   if constexpr (B >= 1) {
