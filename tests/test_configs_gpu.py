@@ -290,10 +290,12 @@ def test_c5_layernorm_chain(hip, view):
     assert_red(got_dgamma, want_dgamma, rows, norm * 4, "d gamma")
 
 
-def test_c5_fused_layernorm_matches_chain(hip):
-    """The fused LayerNorm on the C5 transposed view against the composed
-    chain (validated against the oracle above), forward and backward, at
-    full size."""
+@pytest.mark.parametrize("view", ["transposed", "sliced"])
+def test_c5_fused_layernorm_matches_chain(hip, view):
+    """The fused LayerNorm on the C5 views against the composed chain
+    (validated against the oracle above), forward and backward, at full size:
+    the transposed view takes the column-layout passes, the block of a wider
+    base the row kernels and one embedding of the two narrows' gradient."""
     from spar_amd import spar
 
     from tests.test_norm_gpu import assert_rows, dx_terms
@@ -301,7 +303,10 @@ def test_c5_fused_layernorm_matches_chain(hip):
     rows, cols = 4096, 8192
     device, cpu = spar.Device.hip(0), spar.Device.cpu()
     rng = np.random.default_rng(63)
-    base = rng.standard_normal((cols, rows)).astype(F32)
+    if view == "transposed":
+        base = rng.standard_normal((cols, rows)).astype(F32)
+    else:
+        base = rng.standard_normal((rows + 512, cols + 1024)).astype(F32)
     gamma = rng.uniform(0.5, 1.5, cols).astype(F32)
     beta = rng.uniform(-0.1, 0.1, cols).astype(F32)
     G = rng.standard_normal((rows, cols)).astype(F32)
@@ -312,7 +317,8 @@ def test_c5_fused_layernorm_matches_chain(hip):
             t = spar.Tensor.from_numpy(array).to(device)
             t.set_requires_grad(True)
             ts.append(t)
-        x = ts[0].transpose(0, 1)
+        x = (ts[0].transpose(0, 1) if view == "transposed"
+             else ts[0].narrow(0, 256, rows).narrow(1, 512, cols))
         if fused:
             y = spar.layer_norm(x, ts[1], ts[2], 1e-5)
         else:
@@ -325,8 +331,17 @@ def test_c5_fused_layernorm_matches_chain(hip):
 
     fused, chain = run(True), run(False)
     assert_rows(fused[0], chain[0], cols, F32, "C5 fused y", 16.0)
-    assert_rows(fused[1].T, chain[1].T, cols, F32, "C5 fused dx", 32.0,
-                dx_terms(G, gamma, base.T, True))
+    if view == "transposed":
+        x_rows, dx_fused, dx_chain = base.T, fused[1].T, chain[1].T
+    else:
+        x_rows = base[256:256 + rows, 512:512 + cols]
+        dx_fused = fused[1][256:256 + rows, 512:512 + cols]
+        dx_chain = chain[1][256:256 + rows, 512:512 + cols]
+        outside = np.ones(base.shape, bool)
+        outside[256:256 + rows, 512:512 + cols] = False
+        assert not fused[1][outside].any(), "gradient outside the block"
+    assert_rows(dx_fused, dx_chain, cols, F32, "C5 fused dx", 32.0,
+                dx_terms(G, gamma, x_rows, True))
     for i, name in ((2, "d gamma"), (3, "d beta")):
         scale = np.max(np.abs(chain[i]))
         err = np.max(np.abs(fused[i].astype(np.float64) - chain[i]))
