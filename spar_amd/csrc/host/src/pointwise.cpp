@@ -255,9 +255,13 @@ Tensor divide(const Tensor& a, const Tensor& b) {
             contributions.push_back(detail::reduce_gradient_to_shape(local, shape_a));
           }
           if (grad_b) {
-            const auto denominator{multiply(saved_b, saved_b)};
+            // -(g a / (b b)), negated through the denominator: x / -y is
+            // -(x / y) bit for bit (division rounds symmetrically), and the
+            // denominator has b's shape, which a broadcast b keeps small, where
+            // the reference negates the full quotient.
+            const auto denominator{multiply_scalar(multiply(saved_b, saved_b), -1.0)};
             const auto numerator{multiply(gradient, *saved_a)};
-            const auto local{multiply_scalar(divide(numerator, denominator), -1.0)};
+            const auto local{divide(numerator, denominator)};
             contributions.push_back(detail::reduce_gradient_to_shape(local, shape_b));
           }
           return contributions;
