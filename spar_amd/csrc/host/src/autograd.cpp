@@ -15,10 +15,11 @@
 //      one is added elementwise, `held += incoming`, in sweep order.
 //   4. A leaf keeps the gradient it is handed on its first backward() and
 //      adds later ones in place (`accumulated += incoming`).
-//   5. A narrow whose input is a narrow with no other incoming gradient
-//      hands its gradient down unembedded, with the composed box; the first
-//      narrow below that does not embeds it once, at its own turn, so the
-//      identities above receive the same values in the same order.
+//   5. A narrow whose input is itself a narrow with no other incoming
+//      gradient hands its gradient down unembedded, with the composed box.
+//      The last narrow of such a chain embeds it once, at its own turn, so
+//      every identity the chain feeds receives the same values in the same
+//      order as if each narrow had embedded its own.
 // Given identical contributions, the gradients are therefore identical to
 // the reference's.  The reference also cloned each contribution
 // (autograd.cpp:145, :244), which copied values into a dense tensor.  Here a
