@@ -395,9 +395,13 @@ constexpr int kCombineBatch = 16;
 // Combines `parts` partials in a fixed order and writes the summary in the
 // reference's form (SparCudaNormSummary): scale = the largest finite
 // magnitude, scaled_sum_squares = sum of (x / scale)^2; {0, 1} when no finite
-// nonzero element was seen, as the reference's initial state.  Two passes:
-// the common exponent, maximum and flags first, then every partial's sum
-// rescaled to that exponent, so neither pass is a chain of dependent merges.
+// nonzero element was seen, as the reference's initial state.  RESCALE (fp64
+// partials): two passes, the common exponent, maximum and flags first, then
+// every partial's sum rescaled to that exponent, so neither pass is a chain
+// of dependent merges.  fp32 partials all have exponent 0 (or hold nothing),
+// so the rescale is the identity and one pass adds the same values in the
+// same order: the same bits, one round trip to the partials instead of two.
+template <bool RESCALE>
 __global__ void __launch_bounds__(kCombineThreads)
     norm_combine_kernel(SparHipNormSummary* summary, PartialArrays partials, uint64_t parts) {
   __shared__ int32_t wave_top[kCombineWaves];
@@ -406,27 +410,32 @@ __global__ void __launch_bounds__(kCombineThreads)
   __shared__ double wave_total[kCombineWaves];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  int32_t top = kNoExponent;
+  // fp32 partials that hold elements all have exponent 0, so theirs is 0
+  int32_t top = RESCALE ? kNoExponent : 0;
   int32_t flags = 0;
   double maximum = 0.0;
+  double sum = 0.0;
   // The partials come from every XCD: each batch issues all of a thread's
   // loads before using any, so a pass costs about one round trip.
   for (uint64_t base = threadIdx.x; base < parts; base += kCombineThreads * kCombineBatch) {
     int32_t e[kCombineBatch], f[kCombineBatch];
     double m[kCombineBatch];
+    double v[RESCALE ? 1 : kCombineBatch];
 #pragma unroll
     for (int k = 0; k < kCombineBatch; ++k) {
       const uint64_t i = base + static_cast<uint64_t>(k) * kCombineThreads;
       const bool in = i < parts;
-      e[k] = in ? partials.exponent[i] : kNoExponent;
+      if constexpr (RESCALE) e[k] = in ? partials.exponent[i] : kNoExponent;
       m[k] = in ? partials.maximum[i] : 0.0;
       f[k] = in ? partials.flags[i] : 0;
+      if constexpr (!RESCALE) v[k] = in ? partials.sum[i] : 0.0;
     }
 #pragma unroll
     for (int k = 0; k < kCombineBatch; ++k) {
-      top = max(top, e[k]);
+      if constexpr (RESCALE) top = max(top, e[k]);
       maximum = fmax(maximum, m[k]);
       flags |= f[k];
+      if constexpr (!RESCALE) sum += v[k];
     }
   }
 #pragma unroll
@@ -450,19 +459,20 @@ __global__ void __launch_bounds__(kCombineThreads)
     maximum = fmax(maximum, wave_maximum[w]);
     flags |= wave_flags[w];
   }
-  double sum = 0.0;
-  for (uint64_t base = threadIdx.x; base < parts; base += kCombineThreads * kCombineBatch) {
-    int32_t e[kCombineBatch];
-    double v[kCombineBatch];
+  if constexpr (RESCALE) {
+    for (uint64_t base = threadIdx.x; base < parts; base += kCombineThreads * kCombineBatch) {
+      int32_t e[kCombineBatch];
+      double v[kCombineBatch];
 #pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k) {
-      const uint64_t i = base + static_cast<uint64_t>(k) * kCombineThreads;
-      const bool in = i < parts;
-      e[k] = in ? partials.exponent[i] : top;
-      v[k] = in ? partials.sum[i] : 0.0;
+      for (int k = 0; k < kCombineBatch; ++k) {
+        const uint64_t i = base + static_cast<uint64_t>(k) * kCombineThreads;
+        const bool in = i < parts;
+        e[k] = in ? partials.exponent[i] : top;
+        v[k] = in ? partials.sum[i] : 0.0;
+      }
+#pragma unroll
+      for (int k = 0; k < kCombineBatch; ++k) sum += ldexp(v[k], 2 * (e[k] - top));
     }
-#pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k) sum += ldexp(v[k], 2 * (e[k] - top));
   }
   sum = wave_sum(sum);
   if (lane == 0) wave_total[wave] = sum;
@@ -515,7 +525,8 @@ hipError_t launch_norm_summary(SparHipNormSummary* device_summary, const T* grad
                          reinterpret_cast<int32_t*>(bytes + 20 * blocks)};
   norm_partial_kernel<T><<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(
       partials, gradient, count, segment);
-  norm_combine_kernel<<<1, kCombineThreads, 0, guard.stream>>>(device_summary, partials, blocks);
+  norm_combine_kernel<(sizeof(T) > 4)>
+      <<<1, kCombineThreads, 0, guard.stream>>>(device_summary, partials, blocks);
   scratch_release(scratch, device);  // stream-ordered reuse
   return hipGetLastError();
 }
@@ -587,7 +598,7 @@ extern "C" SparHipStatus spar_hip_launch_gradient_norm_summary(SparHipNormSummar
   DeviceGuard guard;
   if (enter(device, guard) != hipSuccess) return runtime(guard.error);
   if (count == 0) {
-    norm_combine_kernel<<<1, kCombineThreads, 0, guard.stream>>>(
+    norm_combine_kernel<true><<<1, kCombineThreads, 0, guard.stream>>>(
         summary, PartialArrays{nullptr, nullptr, nullptr, nullptr}, 0);
     return finish(guard);
   }
