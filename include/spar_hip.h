@@ -275,6 +275,8 @@ struct SparHipStatus spar_hip_launch_window_embed(void* output, const void* inpu
  * extents) = zeros except the box starts[a] <= c[a] < starts[a] + lengths[a]
  * on every axis, which holds input (contiguous, extents `lengths`).  The
  * gradient of a chain of narrows in one pass; no reference counterpart.
+ * With input NULL only the zeros are written and the box is left as it is
+ * (the border of a gradient whose box a producer writes in place).
  * element_size 4 or 8; outputs of at most 2^31 - 1 elements; after dropping
  * axes of extent 1 and merging neighbouring whole axes, at most 4 axes.
  * Status 1 for other shapes and for an empty box (length 0 on some axis). */
@@ -426,19 +428,25 @@ struct SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, void
 
 /* Backward of the above from the saved mu and d: writes dx, d weight
  * [extent] and, for LayerNorm, d bias [extent] (sums over rows in a fixed
- * order).  The input is in one of the forward's layouts: rows
- * input_row_stride >= extent apart with a row's elements adjacent
- * (input_column_stride 1), dx then written contiguous [rows, extent]; or rows
- * adjacent (input_row_stride 1) with a row's elements input_column_stride >=
- * rows apart, dx then written packed in that layout, element (p, q) at
- * input_gradient[p + q * rows] (a contiguous [extent, rows] block, whose
- * transpose is the gradient of a transposed view).  output_gradient is
- * contiguous [rows, extent] in both.  Replaces the autograd backward of the
- * composed chain. */
+ * order).  The input is in one of the forward's layouts, and dx is written
+ * in the same one:
+ *   - rows input_row_stride >= extent apart with a row's elements adjacent
+ *     (input_column_stride 1): dx row p starts at
+ *     input_gradient[p * input_gradient_stride], input_gradient_stride >=
+ *     extent (extent: contiguous [rows, extent]; larger: a block of a wider
+ *     tensor, such as the gradient of a narrowed view written in place);
+ *   - rows adjacent (input_row_stride 1) with a row's elements
+ *     input_column_stride >= rows apart: element (p, q) of dx at
+ *     input_gradient[p + q * input_gradient_stride], input_gradient_stride >=
+ *     rows (rows: a contiguous [extent, rows] block, whose transpose is the
+ *     gradient of a transposed view).
+ * output_gradient is contiguous [rows, extent] in both.  Replaces the
+ * autograd backward of the composed chain. */
 struct SparHipStatus spar_hip_launch_norm_backward(
-    void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
-    const void* input, uint64_t input_row_stride, uint64_t input_column_stride,
-    const void* weight, const void* mean, const void* denominator, uint64_t rows,
+    void* input_gradient, uint64_t input_gradient_stride, void* weight_gradient,
+    void* bias_gradient, const void* output_gradient, const void* input,
+    uint64_t input_row_stride, uint64_t input_column_stride, const void* weight,
+    const void* mean, const void* denominator, uint64_t rows,
     uint64_t extent, int center, int dtype, int device);
 
 /* --------------------------------------------- cross entropy (log-softmax + NLL) */

@@ -481,7 +481,9 @@ struct BoxGeometry {
   uint32_t in_stride[kMaxBoxAxes];  // input elements per step along the axis
 };
 
-template <typename E, bool VEC, int R>
+// BORDER: write only the zeros outside the box (input unused), leaving the
+// box to a producer that writes it in place.
+template <typename E, bool VEC, int R, bool BORDER>
 __global__ void __launch_bounds__(kThreads)
     box_embed_kernel(E* output, const E* input, uint64_t groups, BoxGeometry box) {
   constexpr int G = VEC ? static_cast<int>(16 / sizeof(E)) : 1;
@@ -501,7 +503,15 @@ __global__ void __launch_bounds__(kThreads)
       inside = inside && c >= box.start[a] && c - box.start[a] < box.length[a];
       from += (c - box.start[a]) * box.in_stride[a];
     }
-    if constexpr (VEC) {
+    if constexpr (BORDER) {
+      if (!inside) {
+        if constexpr (VEC) {
+          *reinterpret_cast<V*>(output + element) = V{};
+        } else {
+          output[element] = E(0);
+        }
+      }
+    } else if constexpr (VEC) {
       V value{};
       if (inside) value = stream_load(reinterpret_cast<const V*>(input + from));
       *reinterpret_cast<V*>(output + element) = value;
@@ -526,6 +536,8 @@ void launch_box_embed(E* output, const E* input, int rank, const uint64_t* exten
     in_stride *= static_cast<uint32_t>(lengths[a]);
   }
   const int last = rank - 1;
+  // (with input null, border only, every 16-byte group lies wholly inside
+  // or outside the box under the same conditions)
   const bool vec = aligned16(output) && aligned16(input) && extents[last] % G == 0 &&
                    starts[last] % G == 0 && lengths[last] % G == 0;
   const uint64_t groups = vec ? count / G : count;
@@ -537,19 +549,27 @@ void launch_box_embed(E* output, const E* input, int rank, const uint64_t* exten
     kernel<<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(output, input, groups,
                                                                           box);
   };
-  auto with_rank = [&](auto vec_tag) {
+  auto with_rank = [&](auto vec_tag, auto border_tag) {
     constexpr bool VEC = decltype(vec_tag)::value;
+    constexpr bool BORDER = decltype(border_tag)::value;
     switch (rank) {
-      case 1: launch(box_embed_kernel<E, VEC, 1>); break;
-      case 2: launch(box_embed_kernel<E, VEC, 2>); break;
-      case 3: launch(box_embed_kernel<E, VEC, 3>); break;
-      default: launch(box_embed_kernel<E, VEC, 4>); break;
+      case 1: launch(box_embed_kernel<E, VEC, 1, BORDER>); break;
+      case 2: launch(box_embed_kernel<E, VEC, 2, BORDER>); break;
+      case 3: launch(box_embed_kernel<E, VEC, 3, BORDER>); break;
+      default: launch(box_embed_kernel<E, VEC, 4, BORDER>); break;
+    }
+  };
+  auto with_border = [&](auto vec_tag) {
+    if (input == nullptr) {
+      with_rank(vec_tag, std::true_type{});
+    } else {
+      with_rank(vec_tag, std::false_type{});
     }
   };
   if (vec) {
-    with_rank(std::true_type{});
+    with_border(std::true_type{});
   } else {
-    with_rank(std::false_type{});
+    with_border(std::false_type{});
   }
 }
 
@@ -695,9 +715,8 @@ extern "C" SparHipStatus spar_hip_launch_box_embed(void* output, const void* inp
   }
   if (count == 0) return ok();
   // 32-bit element indices inside the kernel
-  if (count > kIndex32Limit || output == nullptr || (inside != 0 && input == nullptr)) {
-    return invalid();
-  }
+  // (input null: the zeros around the box only)
+  if (count > kIndex32Limit || output == nullptr) return invalid();
   // Coalesce: drop axes of extent 1 and merge neighbours that are both whole.
   uint64_t e[SPAR_HIP_MAX_RANK];
   uint64_t st[SPAR_HIP_MAX_RANK];

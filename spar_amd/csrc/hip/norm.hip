@@ -577,9 +577,9 @@ __global__ void __launch_bounds__(kApplyThreads)
 // blockIdx.x of the [gridDim.x, n] partial arrays.
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
-    norm_backward_kernel(T* dx, T* partial_weight, T* partial_bias, const T* dy, const T* in,
-                         uint64_t in_stride, const T* weight, const T* mean,
-                         const T* denominator, uint64_t rows, uint64_t n) {
+    norm_backward_kernel(T* dx, uint64_t dx_stride, T* partial_weight, T* partial_bias,
+                         const T* dy, const T* in, uint64_t in_stride, const T* weight,
+                         const T* mean, const T* denominator, uint64_t rows, uint64_t n) {
   const T count = static_cast<T>(n);
   T acc_w[E];
   T acc_b[CENTER ? E : 1];
@@ -634,7 +634,7 @@ __global__ void __launch_bounds__(THREADS)
     const T mean_gx = sum_gx / count;
 #pragma unroll
     for (int j = 0; j < E; ++j) g[j] = divide(g[j] - mean_g - x[j] * mean_gx);
-    norm_store<T, THREADS, E, VEC, FULL, NT>(dx + r * n, g, n);
+    norm_store<T, THREADS, E, VEC, FULL, NT>(dx + r * dx_stride, g, n);
   }
   norm_store<T, THREADS, E, VEC, FULL, false>(partial_weight + blockIdx.x * n, acc_w, n);
   if constexpr (CENTER) {
@@ -650,10 +650,10 @@ __global__ void __launch_bounds__(THREADS)
 // per CU without the prefetch, and half the weight / bias partials.
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
-    norm_backward_pipelined_kernel(T* dx, T* partial_weight, T* partial_bias, const T* dy,
-                                   const T* in, uint64_t in_stride, const T* weight,
-                                   const T* mean, const T* denominator, uint64_t rows,
-                                   uint64_t n) {
+    norm_backward_pipelined_kernel(T* dx, uint64_t dx_stride, T* partial_weight,
+                                   T* partial_bias, const T* dy, const T* in, uint64_t in_stride,
+                                   const T* weight, const T* mean, const T* denominator,
+                                   uint64_t rows, uint64_t n) {
   const T count = static_cast<T>(n);
   T acc_w[E];
   T acc_b[CENTER ? E : 1];
@@ -706,7 +706,7 @@ __global__ void __launch_bounds__(THREADS)
     const T mean_gx = sum_gx / count;
 #pragma unroll
     for (int j = 0; j < E; ++j) g[j] = divide(g[j] - mean_g - x[j] * mean_gx);
-    norm_store<T, THREADS, E, VEC, FULL, NT>(dx + r * n, g, n);
+    norm_store<T, THREADS, E, VEC, FULL, NT>(dx + r * dx_stride, g, n);
     if (next < rows) {
 #pragma unroll
       for (int j = 0; j < E; ++j) {
@@ -774,9 +774,10 @@ __global__ void __launch_bounds__(kCombineThreads)
 // ------------------------------------- backward, rows down storage columns
 //
 // The backward over the forward's column layout, x[p][q] = in[p + q * pitch],
-// with dy in rows (dy[p * n + q]).  dx is written in x's layout, packed:
-// dx[p + q * rows], the storage of a contiguous [n, rows] tensor whose
-// transpose is the gradient of the transposed view.  Three launches take the
+// with dy in rows (dy[p * n + q]).  dx is written in x's layout,
+// dx[p + q * stride]; with stride == rows, the storage of a contiguous
+// [n, rows] tensor whose transpose is the gradient of the transposed view.
+// Three launches take the
 // place of a transposing copy of x, the row kernel and a transposing copy of
 // dx:
 //
@@ -1122,7 +1123,8 @@ __global__ void __launch_bounds__(kCombineThreads)
 
 template <typename T, bool CENTER, int MODE, bool NT>
 __global__ void __launch_bounds__(kApplyThreads)
-    norm_backward_columns_apply_kernel(T* dx, const T* dy, const T* in, uint64_t pitch,
+    norm_backward_columns_apply_kernel(T* dx, uint64_t dx_stride, const T* dy, const T* in,
+                                       uint64_t pitch,
                                        const T* weight, const T* mean, const T* denominator,
                                        const T* row_means, uint64_t rows, uint64_t n,
                                        FastDiv tiles_p, FastDiv tiles_q, uint32_t tile_count) {
@@ -1295,7 +1297,7 @@ __global__ void __launch_bounds__(kApplyThreads)
           const T gw = grad[i][k] * w[it][k];
           vec_set<T>(o, i, divide(gw - mean_g[i] - xhat * mean_gx[i]));
         }
-        T* column = dx + p + (q + k) * rows;
+        T* column = dx + p + (q + k) * dx_stride;
         if constexpr (VEC) {
           store_vector<NT>(reinterpret_cast<V*>(column), o);
         } else {
@@ -1422,6 +1424,7 @@ hipError_t forward_columns_as(const NormArgs& a, uint64_t pitch, int device,
 
 struct NormBackwardArgs {
   void* dx;
+  uint64_t dx_stride;  // row layout: elements between dx rows; column layout: between q
   void* dweight;
   void* dbias;
   const void* dy;
@@ -1510,8 +1513,8 @@ hipError_t backward_columns_as(const NormBackwardArgs& a, uint64_t pitch, int de
     uint64_t slots = resident_blocks(kernel, kApplyThreads, guard);
     if (slots == 0) slots = 2 * cus;
     kernel<<<static_cast<uint32_t>(tiles < slots ? tiles : slots), kApplyThreads, 0,
-             guard.stream>>>(static_cast<T*>(a.dx), dy, in, pitch, weight, mean, denominator,
-                             means, a.rows, a.n, divide_p, divide_q,
+             guard.stream>>>(static_cast<T*>(a.dx), a.dx_stride, dy, in, pitch, weight, mean,
+                             denominator, means, a.rows, a.n, divide_p, divide_q,
                              static_cast<uint32_t>(tiles));
   });
   error = hipGetLastError();
@@ -1558,7 +1561,8 @@ hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard&
   T* partial_bias = CENTER ? partial_weight + grid * a.n : nullptr;
   with_policy(stream, [&](auto nt) {
     kernel_for(nt)<<<static_cast<uint32_t>(grid), THREADS, 0, guard.stream>>>(
-        static_cast<T*>(a.dx), partial_weight, partial_bias, static_cast<const T*>(a.dy),
+        static_cast<T*>(a.dx), a.dx_stride, partial_weight, partial_bias,
+        static_cast<const T*>(a.dy),
         static_cast<const T*>(a.input), a.input_stride, static_cast<const T*>(a.weight),
         static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n);
   });
@@ -1729,15 +1733,17 @@ extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, 
 }
 
 extern "C" SparHipStatus spar_hip_launch_norm_backward(
-    void* input_gradient, void* weight_gradient, void* bias_gradient, const void* output_gradient,
-    const void* input, uint64_t input_row_stride, uint64_t input_column_stride,
-    const void* weight, const void* mean, const void* denominator, uint64_t rows,
-    uint64_t extent, int center, int dtype, int device) {
-  // The forward's two layouts; in the column layout dx is written packed in
-  // that layout (dx[p + q * rows]).
-  const bool row_layout = input_column_stride == 1 && input_row_stride >= extent;
-  const bool column_layout =
-      input_column_stride != 1 && input_row_stride == 1 && input_column_stride >= rows;
+    void* input_gradient, uint64_t input_gradient_stride, void* weight_gradient,
+    void* bias_gradient, const void* output_gradient, const void* input,
+    uint64_t input_row_stride, uint64_t input_column_stride, const void* weight, const void* mean,
+    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device) {
+  // The forward's two layouts.  dx takes the input's layout: rows
+  // input_gradient_stride apart (row layout), or dx[p + q * stride] (column
+  // layout; stride == rows packs it).
+  const bool row_layout = input_column_stride == 1 && input_row_stride >= extent &&
+                          input_gradient_stride >= extent;
+  const bool column_layout = input_column_stride != 1 && input_row_stride == 1 &&
+                             input_column_stride >= rows && input_gradient_stride >= rows;
   if (!valid_float_dtype(dtype) || (center != 0 && center != 1) || extent == 0 ||
       extent > spar_hip_norm_max_extent(dtype) || !(row_layout || column_layout) ||
       (rows != 0 &&
@@ -1761,14 +1767,16 @@ extern "C" SparHipStatus spar_hip_launch_norm_backward(
     if (status.code == 0 && center) status = spar_hip_zero(bias_gradient, bytes, device);
     return status;
   }
-  const NormBackwardArgs a{input_gradient, weight_gradient,  bias_gradient, output_gradient,
-                           input,          input_row_stride, weight,        mean,
-                           denominator,    rows,             extent,        center != 0};
+  const NormBackwardArgs a{input_gradient, input_gradient_stride, weight_gradient,
+                           bias_gradient,  output_gradient,       input,
+                           input_row_stride, weight,              mean,
+                           denominator,    rows,                  extent,
+                           center != 0};
   if (column_layout) {
     const bool vec = aligned_rows(output_gradient, extent, width) && extent % width == 0 &&
                      aligned_rows(weight, extent, width) &&
                      aligned_rows(input, input_column_stride, width) &&
-                     aligned_rows(input_gradient, rows, width) &&
+                     aligned_rows(input_gradient, input_gradient_stride, width) &&
                      rows % static_cast<uint64_t>(width) == 0 &&
                      aligned16(denominator) && (!center || aligned16(mean));
     // every tile whole: rows and extent multiples of the tile side
@@ -1804,7 +1812,7 @@ extern "C" SparHipStatus spar_hip_launch_norm_backward(
     if (error != hipSuccess) return runtime(error);
     return finish(guard);
   }
-  const bool vec = aligned_rows(input_gradient, extent, width) &&
+  const bool vec = aligned_rows(input_gradient, input_gradient_stride, width) &&
                    aligned_rows(output_gradient, extent, width) &&
                    aligned_rows(input, input_row_stride, width) && extent % width == 0 &&
                    aligned_rows(weight, extent, width);

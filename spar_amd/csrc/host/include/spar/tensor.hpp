@@ -240,22 +240,39 @@ void swap_storage_payloads(Tensor& original, Tensor& staged) noexcept;
 
 using BackwardFunction = std::function<std::vector<Tensor>(const Tensor&)>;
 
+/// A second form of a backward rule, for ops that can write their first
+/// parent's gradient into storage the engine provides: when that parent is a
+/// chain of narrowed views, the engine offers a view of the gradient of the
+/// chain's base (its border already zero) instead of embedding the gradient
+/// afterwards.  `accepts` says whether `rule` can write into a destination
+/// of that layout; `rule` then returns the contributions with the
+/// destination, written, in the first parent's place.
+struct PlacedBackward final {
+  std::function<bool(const Tensor& destination)> accepts;
+  std::function<std::vector<Tensor>(const Tensor& gradient, const Tensor& destination)> rule;
+};
+
 void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
                       BackwardFunction backward);
+void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
+                      BackwardFunction backward, PlacedBackward placed);
 void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward);
 [[nodiscard]] bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept;
 
 /// Process-wide tallies of the autograd engine: backward() calls, leaf
 /// gradients copied because their storage was shared, gradient
-/// accumulations done in place or out of place, and narrows whose gradient
-/// was handed to the narrow below them unembedded (a chain of narrows is
-/// embedded once).  The engine never copies an intermediate gradient.
+/// accumulations done in place or out of place, narrows whose gradient was
+/// handed to the narrow below them unembedded (a chain of narrows is
+/// embedded once), and gradients a rule wrote straight into the gradient of
+/// a narrow chain's base (no embedding pass at all).  The engine never
+/// copies an intermediate gradient.
 struct AutogradCounters final {
   std::uint64_t backward_calls;
   std::uint64_t leaf_copies;
   std::uint64_t in_place_adds;
   std::uint64_t out_of_place_adds;
   std::uint64_t window_fusions;
+  std::uint64_t placed_gradients;
 };
 [[nodiscard]] AutogradCounters autograd_counters() noexcept;
 

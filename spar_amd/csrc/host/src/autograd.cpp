@@ -19,7 +19,11 @@
 //      gradient hands its gradient down unembedded, with the composed box.
 //      The last narrow of such a chain embeds it once, at its own turn, so
 //      every identity the chain feeds receives the same values in the same
-//      order as if each narrow had embedded its own.
+//      order as if each narrow had embedded its own.  A rule with a placed
+//      form (the fused norms) whose first input heads such a chain writes
+//      that gradient straight into the box of a buffer shaped like the
+//      chain's base, its border zeroed; the buffer travels down the same
+//      chain and is delivered at the same turn, with the same values.
 // Given identical contributions, the gradients are therefore identical to
 // the reference's.  The reference also cloned each contribution
 // (autograd.cpp:145, :244), which copied values into a dense tensor.  Here a
@@ -48,6 +52,7 @@ std::atomic<std::uint64_t> g_leaf_copies{0};
 std::atomic<std::uint64_t> g_in_place_adds{0};
 std::atomic<std::uint64_t> g_out_of_place_adds{0};
 std::atomic<std::uint64_t> g_window_fusions{0};
+std::atomic<std::uint64_t> g_placed_gradients{0};
 
 GradInput input_of(const Tensor& parent) {
   return GradInput{TensorInternals::grad_state(parent), parent.shape(), parent.dtype(),
@@ -84,6 +89,12 @@ void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
   attach(output, std::move(function));
 }
 
+void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
+                      BackwardFunction backward, PlacedBackward placed) {
+  record_operation(output, std::move(requiring_parents), std::move(backward));
+  TensorInternals::grad_state(output)->producer->placed = std::move(placed);
+}
+
 void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward) {
   if (!requiring_parent.requires_grad()) {
     throw std::logic_error{"Cannot record a transfer from a non-requiring parent"};
@@ -100,7 +111,8 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
 
 AutogradCounters autograd_counters() noexcept {
   return AutogradCounters{g_backward_calls.load(), g_leaf_copies.load(), g_in_place_adds.load(),
-                          g_out_of_place_adds.load(), g_window_fusions.load()};
+                          g_out_of_place_adds.load(), g_window_fusions.load(),
+                          g_placed_gradients.load()};
 }
 
 bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept {
@@ -160,6 +172,32 @@ Tensor embed_box(const Tensor& gradient, const Shape& shape, const std::vector<W
   return result;
 }
 
+// Zeros over all of `buffer` except `box`, which a producer writes itself.
+void zero_border(Tensor& buffer, const std::vector<WindowAxis>& box) {
+  const Shape& shape{buffer.shape()};
+  void* data{HipTensorAccess::mutable_data(buffer)};
+  if (shape.rank() <= static_cast<std::size_t>(SPAR_HIP_MAX_RANK)) {
+    std::uint64_t extents[SPAR_HIP_MAX_RANK];
+    std::uint64_t starts[SPAR_HIP_MAX_RANK];
+    std::uint64_t lengths[SPAR_HIP_MAX_RANK];
+    for (std::size_t k{0}; k < shape.rank(); ++k) {
+      extents[k] = static_cast<std::uint64_t>(shape[k]);
+      starts[k] = box[k].start;
+      lengths[k] = box[k].length;
+    }
+    const auto status{spar_hip_launch_box_embed(data, nullptr, static_cast<int>(shape.rank()),
+                                                extents, starts, lengths,
+                                                size_of(buffer.dtype()),
+                                                buffer.device().index())};
+    if (status.code == 0) return;
+    // status 1 (more box axes than the one-pass kernel takes): zero it all
+    if (status.code != 1) hip::check(status, "narrow backward", buffer.device());
+  }
+  hip::check(spar_hip_zero(data, buffer.numel() * size_of(buffer.dtype()),
+                           buffer.device().index()),
+             "narrow backward", buffer.device());
+}
+
 // The sweep state of one backward() call.
 class Sweep final {
  public:
@@ -180,9 +218,11 @@ class Sweep final {
         continue;
       }
       std::vector<WindowAxis> box{std::move(deferred_[position])};
-      if (!state.producer->window.empty() && narrow_chain(*state.producer, gradient, box)) {
+      if (placed_[position].has_value()) {
+        hand_placed(position, std::move(gradient));
         continue;
       }
+      if (!state.producer->window.empty() && narrow_chain(position, gradient, box)) continue;
       propagate(*state.producer, std::move(gradient));
     }
   }
@@ -215,6 +255,7 @@ class Sweep final {
     }
     pending_.resize(order_.size());
     deferred_.resize(order_.size());
+    placed_.resize(order_.size());
     incoming_.assign(order_.size(), 0);
     for (const GradState* state : order_) {
       if (state->producer == nullptr) continue;
@@ -225,32 +266,43 @@ class Sweep final {
     }
   }
 
-  // A narrowed view's node (window W of its input v) holding `gradient`,
-  // which covers `box` of the node's own shape (all of it when `box` is
+  // The slot of the identity below the narrow at `position` when a gradient
+  // may be handed to it down a chain of narrows: it is a narrowed view itself
+  // and this narrow's gradient is the only one it receives (none pending).
+  std::optional<std::size_t> chain_parent(std::size_t position) const {
+    const GradFunction& function{*order_[position]->producer};
+    const auto found{slot_.find(function.inputs.front().identity.get())};
+    if (found == slot_.end()) return std::nullopt;
+    const std::size_t next{found->second};
+    const GradState& parent{*order_[next]};
+    if (parent.producer == nullptr || parent.producer->window.empty() || incoming_[next] != 1 ||
+        pending_[next].has_value()) {
+      return std::nullopt;
+    }
+    return next;
+  }
+
+  // The narrow at `position` (window W of its input v) holding `gradient`,
+  // which covers `box` of the narrow's own shape (all of it when `box` is
   // empty).  When v is itself a narrowed view whose only incoming gradient
   // is this one, the gradient is handed on unchanged with the composed box
   // (start W + box start, length box length), to be embedded once, at v's
   // own turn in the sweep, so that every other identity receives its
   // gradients in the same order as without the composition.  Returns false
   // when the node's own rule should run instead (no box to apply).
-  bool narrow_chain(const GradFunction& function, Tensor& gradient,
-                    const std::vector<WindowAxis>& box) {
+  bool narrow_chain(std::size_t position, Tensor& gradient, const std::vector<WindowAxis>& box) {
+    const GradFunction& function{*order_[position]->producer};
     const GradInput& input{function.inputs.front()};
     std::vector<WindowAxis> composed{function.window};
     for (std::size_t k{0}; k < composed.size() && !box.empty(); ++k) {
       composed[k].start += box[k].start;
       composed[k].length = box[k].length;
     }
-    const auto found{slot_.find(input.identity.get())};
-    if (found == slot_.end()) return true;  // an identity no longer tracked
-    const std::size_t next{found->second};
-    const GradState& parent{*order_[next]};
-    const bool chain{parent.producer != nullptr && !parent.producer->window.empty() &&
-                     incoming_[next] == 1 && !pending_[next].has_value() &&
-                     gradient.device().is_hip() && gradient.is_contiguous()};
-    if (chain) {
-      pending_[next] = std::move(gradient);
-      deferred_[next] = std::move(composed);
+    if (slot_.find(input.identity.get()) == slot_.end()) return true;  // no longer tracked
+    const auto next{chain_parent(position)};
+    if (next && gradient.device().is_hip() && gradient.is_contiguous()) {
+      pending_[*next] = std::move(gradient);
+      deferred_[*next] = std::move(composed);
       g_window_fusions.fetch_add(1, std::memory_order_relaxed);
       return true;
     }
@@ -259,11 +311,78 @@ class Sweep final {
     return true;
   }
 
+  // A narrow whose gradient a rule wrote straight into the gradient of its
+  // chain's base (placed_[position], whose border is zero): the base's
+  // gradient is handed down the same chain narrow_chain composes and
+  // delivered at the last narrow's turn, where that chain would embed it,
+  // so every identity receives the same values in the same order.
+  void hand_placed(std::size_t position, Tensor gradient) {
+    Tensor buffer{std::move(*placed_[position])};
+    placed_[position].reset();
+    if (const auto next{chain_parent(position)}) {
+      pending_[*next] = std::move(gradient);
+      placed_[*next] = std::move(buffer);
+      return;
+    }
+    gradient = Tensor{Shape{}, buffer.dtype(), Device::cpu()};  // drop the view of buffer
+    accumulate(order_[position]->producer->inputs.front(), std::move(buffer));
+  }
+
+  struct Placement {
+    std::size_t slot;    // the first input's identity (the top narrow)
+    Tensor buffer;       // the chain base's gradient, border zeroed
+    Tensor destination;  // the top narrow's box of it
+  };
+
+  // Where a rule with a placed form may write its first input's gradient:
+  // that input is a narrow fed by this rule alone, so its gradient would go
+  // down the chain narrow_chain composes and be embedded in zeros of the
+  // base's shape.  The buffer of that shape is made here, its border zeroed
+  // once the rule accepts the box's layout.
+  std::optional<Placement> placement(const GradFunction& function) {
+    if (!function.placed.rule || !function.placed.accepts || function.inputs.empty()) {
+      return std::nullopt;
+    }
+    const GradInput& input{function.inputs.front()};
+    const auto found{slot_.find(input.identity.get())};
+    if (found == slot_.end() || !input.device.is_hip()) return std::nullopt;
+    std::size_t position{found->second};
+    const GradState& top{*order_[position]};
+    if (top.producer == nullptr || top.producer->window.empty() || incoming_[position] != 1 ||
+        pending_[position].has_value()) {
+      return std::nullopt;
+    }
+    std::vector<WindowAxis> box{top.producer->window};
+    while (const auto next{chain_parent(position)}) {
+      std::vector<WindowAxis> composed{order_[*next]->producer->window};
+      for (std::size_t k{0}; k < composed.size(); ++k) {
+        composed[k].start += box[k].start;
+        composed[k].length = box[k].length;
+      }
+      box = std::move(composed);
+      position = *next;
+    }
+    Tensor buffer{order_[position]->producer->inputs.front().shape, input.dtype, input.device};
+    Tensor destination{buffer};
+    for (std::size_t k{0}; k < box.size(); ++k) {
+      destination = destination.narrow(k, box[k].start, box[k].length);
+    }
+    if (destination.numel() == 0 || !function.placed.accepts(destination)) return std::nullopt;
+    zero_border(buffer, box);
+    return Placement{found->second, std::move(buffer), std::move(destination)};
+  }
+
   // Runs one operation's rule and hands each input its gradient.
   void propagate(const GradFunction& function, Tensor gradient) {
-    std::vector<Tensor> contributions{function.rule(gradient)};
+    std::optional<Placement> placed{placement(function)};
+    std::vector<Tensor> contributions{placed ? function.placed.rule(gradient, placed->destination)
+                                             : function.rule(gradient)};
     if (contributions.size() != function.inputs.size()) {
       throw std::logic_error{"Backward rule returned an incorrect number of gradients"};
+    }
+    if (placed) {
+      placed_[placed->slot] = std::move(placed->buffer);
+      g_placed_gradients.fetch_add(1, std::memory_order_relaxed);
     }
     gradient = Tensor{Shape{}, gradient.dtype(), Device::cpu()};  // free it before the adds
     for (std::size_t k{0}; k < contributions.size(); ++k) {
@@ -330,6 +449,9 @@ class Sweep final {
   // it on (empty: all of it), and the number of gradients it will receive
   std::vector<std::vector<WindowAxis>> deferred_;
   std::vector<std::size_t> incoming_;
+  // per identity: the gradient of its narrow chain's base, when a rule wrote
+  // this identity's gradient into it (the pending gradient is then a view)
+  std::vector<std::optional<Tensor>> placed_;
 };
 
 }  // namespace

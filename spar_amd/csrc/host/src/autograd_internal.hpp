@@ -43,6 +43,9 @@ struct GradFunction final {
   /// the gradient in zeros of the input's shape, and the engine may compose
   /// a chain of such nodes into one embedding.
   std::vector<WindowAxis> window;
+  /// Optional: the rule's form that writes inputs[0]'s gradient into a
+  /// destination the engine provides (empty functions when absent).
+  PlacedBackward placed;
 };
 
 struct GradState final {

@@ -4,6 +4,7 @@
 // (spar_hip_launch_norm_forward / _backward); rows longer than the fused
 // kernels accept take the composed ops, which compute the same function.
 #include <cmath>
+#include <memory>
 #include <optional>
 #include <stdexcept>
 #include <string>
@@ -160,6 +161,50 @@ PackedColumns input_gradient(const Tensor& input, bool columns) {
   return PackedColumns{std::move(storage), std::move(view)};
 }
 
+// What the backward keeps of a fused forward.
+struct SavedNorm {
+  Tensor x;  // the tensor whose rows the forward read (detached)
+  std::size_t row_stride;
+  std::size_t column_stride;
+  Tensor w;
+  std::optional<Tensor> mean_rows;  // LayerNorm only
+  Tensor denominator;
+  std::size_t rows;
+  std::size_t extent;
+  bool center;
+  bool grad_x;
+  bool grad_w;
+  bool grad_b;
+  Shape weight_shape;
+  const char* name;
+};
+
+// The backward kernels with dx written at `dx` (rows `dx_stride` elements
+// apart in the row layout; element (p, q) at dx[p + q * dx_stride] in the
+// column layout); `dx_view` is the gradient handed to autograd for x.
+std::vector<Tensor> norm_backward(const SavedNorm& saved, const Tensor& gradient, void* dx,
+                                  std::size_t dx_stride, const Tensor& dx_view) {
+  const Tensor dy{gradient.is_contiguous() ? gradient.detach() : gradient.detach().contiguous()};
+  Tensor dw{saved.weight_shape, saved.x.dtype(), saved.x.device()};
+  std::optional<Tensor> db;
+  if (saved.center) db.emplace(saved.weight_shape, saved.x.dtype(), saved.x.device());
+  hip::check(spar_hip_launch_norm_backward(
+                 dx, dx_stride, HipTensorAccess::mutable_data(dw),
+                 saved.center ? HipTensorAccess::mutable_data(*db) : nullptr,
+                 HipTensorAccess::data(dy), first_element(saved.x), saved.row_stride,
+                 saved.column_stride, HipTensorAccess::data(saved.w),
+                 saved.center ? HipTensorAccess::data(*saved.mean_rows) : nullptr,
+                 HipTensorAccess::data(saved.denominator), saved.rows, saved.extent,
+                 saved.center ? 1 : 0, hip::dtype_tag(saved.x.dtype()),
+                 saved.x.device().index()),
+             std::string{saved.name} + " backward", saved.x.device());
+  std::vector<Tensor> contributions;
+  if (saved.grad_x) contributions.push_back(dx_view);
+  if (saved.grad_w) contributions.push_back(dw);
+  if (saved.grad_b) contributions.push_back(*db);
+  return contributions;
+}
+
 Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
              const char* name) {
   const bool center{bias != nullptr};
@@ -197,40 +242,39 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
     if (grad_x) parents.push_back(x.source);
     if (grad_w) parents.push_back(weight);
     if (grad_b) parents.push_back(*bias);
-    const Tensor saved_x{x.source.detach()}, saved_w{w.detach()};
-    const std::size_t saved_row_stride{x.row_stride};
-    const std::size_t saved_column_stride{x.column_stride};
-    const Shape weight_shape{weight.shape()};
-    detail::record_operation(
-        output, std::move(parents),
-        [saved_x, saved_row_stride, saved_column_stride, saved_w, mean_rows, denominator, rows,
-         extent, center, grad_x, grad_w, grad_b, weight_shape, name](const Tensor& gradient) {
-          const Tensor dy{gradient.is_contiguous() ? gradient.detach()
-                                                   : gradient.detach().contiguous()};
-          // An input read in the column layout gets its gradient in that
-          // layout, packed (the gradient of a transposed view is then the
-          // transpose of a contiguous block, passed on without a copy); one
-          // read in rows gets a contiguous gradient.
-          PackedColumns dx{input_gradient(saved_x, saved_column_stride != 1)};
-          Tensor dw{weight_shape, saved_x.dtype(), saved_x.device()};
-          std::optional<Tensor> db;
-          if (center) db.emplace(weight_shape, saved_x.dtype(), saved_x.device());
-          hip::check(spar_hip_launch_norm_backward(
-                         HipTensorAccess::mutable_data(dx.storage),
-                         HipTensorAccess::mutable_data(dw),
-                         center ? HipTensorAccess::mutable_data(*db) : nullptr,
-                         HipTensorAccess::data(dy), first_element(saved_x), saved_row_stride,
-                         saved_column_stride, HipTensorAccess::data(saved_w),
-                         center ? HipTensorAccess::data(*mean_rows) : nullptr,
-                         HipTensorAccess::data(denominator), rows, extent, center ? 1 : 0,
-                         hip::dtype_tag(saved_x.dtype()), saved_x.device().index()),
-                     std::string{name} + " backward", saved_x.device());
-          std::vector<Tensor> contributions;
-          if (grad_x) contributions.push_back(dx.view);
-          if (grad_w) contributions.push_back(dw);
-          if (grad_b) contributions.push_back(*db);
-          return contributions;
-        });
+    auto saved{std::make_shared<const SavedNorm>(SavedNorm{
+        x.source.detach(), x.row_stride, x.column_stride, w.detach(), mean_rows, denominator,
+        rows, extent, center, grad_x, grad_w, grad_b, weight.shape(), name})};
+    detail::BackwardFunction rule{[saved](const Tensor& gradient) {
+      // An input read in the column layout gets its gradient in that layout,
+      // packed (the gradient of a transposed view is then the transpose of a
+      // contiguous block, passed on without a copy); one read in rows gets a
+      // contiguous gradient.
+      const bool columns{saved->column_stride != 1};
+      PackedColumns dx{input_gradient(saved->x, columns)};
+      return norm_backward(*saved, gradient, HipTensorAccess::mutable_data(dx.storage),
+                           columns ? saved->rows : saved->extent, dx.view);
+    }};
+    if (!grad_x || x.column_stride != 1) {
+      detail::record_operation(output, std::move(parents), std::move(rule));
+    } else {
+      // Rows read in place may also write their gradient in place, into a
+      // block of a wider gradient whose rows are a uniform stride apart (the
+      // gradient of a narrowed view's base).
+      detail::PlacedBackward placed{
+          [saved](const Tensor& destination) {
+            return destination.device() == saved->x.device() &&
+                   destination.dtype() == saved->x.dtype() &&
+                   destination.shape() == saved->x.shape() &&
+                   uniform_row_stride(destination).has_value();
+          },
+          [saved](const Tensor& gradient, const Tensor& destination) {
+            void* first{const_cast<void*>(first_element(destination))};
+            return norm_backward(*saved, gradient, first, *uniform_row_stride(destination),
+                                 destination);
+          }};
+      detail::record_operation(output, std::move(parents), std::move(rule), std::move(placed));
+    }
   }
   return output;
 }

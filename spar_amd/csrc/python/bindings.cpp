@@ -337,6 +337,7 @@ PYBIND11_MODULE(_spar, m) {
     d["in_place_adds"] = c.in_place_adds;
     d["out_of_place_adds"] = c.out_of_place_adds;
     d["window_fusions"] = c.window_fusions;
+    d["placed_gradients"] = c.placed_gradients;
     return d;
   });
 }

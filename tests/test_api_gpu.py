@@ -388,6 +388,54 @@ def test_autograd_layernorm_chain_on_views(sp, view):
         assert err <= 1e-6 * np.sqrt(rows * cols) * scale * 8, f"{name}: {err} vs scale {scale}"
 
 
+@pytest.mark.parametrize("norm", ["layer_norm", "rms_norm"])
+def test_autograd_norm_gradient_written_into_base(sp, norm):
+    """A fused norm whose input is a chain of narrows writes that input's
+    gradient straight into the gradient of the chain's base, whose border the
+    engine zeroes first; the base's gradient is handed down the chain and
+    delivered where the chain would have embedded it.  Against the same norm
+    on an exact copy of x (x.contiguous() of the strided view, x * 1.0 of the
+    contiguous one), whose dense gradient the chain embeds: every
+    gradient bit-exact, including the base's second contribution added in
+    the same order."""
+    layer = norm == "layer_norm"
+    shape = (70, 300) if layer else (70, 256)
+    base_np = normal(101, shape)
+    rng = np.random.default_rng(102)
+    w_np = rng.uniform(0.5, 1.5, 256).astype(F32)
+    b_np = rng.uniform(-0.1, 0.1, 256).astype(F32)
+    G_np = normal(103, (60, 256))
+    H_np = normal(104, shape)
+
+    def run(copy):
+        base = hip_tensor(sp, base_np, True)
+        w = hip_tensor(sp, w_np, True)
+        b = hip_tensor(sp, b_np, True)
+        x = base.narrow(0, 5, 60)
+        if layer:
+            x = x.narrow(1, 20, 256)  # rows 300 apart, read in place
+        if copy:  # an exact copy with a node of its own
+            x = x.contiguous() if layer else sp.multiply_scalar(x, 1.0)
+        y = sp.layer_norm(x, w, b, 1e-5) if layer else sp.rms_norm(x, w, 1e-5)
+        loss = sp.add(weighted_sum(sp, y, hip_tensor(sp, G_np)),
+                      weighted_sum(sp, base, hip_tensor(sp, H_np)))
+        before = sp.autograd_counters()
+        loss.backward()
+        after = sp.autograd_counters()
+        grads = [host(sp, base.grad()), host(sp, w.grad())] + ([host(sp, b.grad())] if layer else [])
+        return grads, after["placed_gradients"] - before["placed_gradients"]
+
+    placed, count = run(copy=False)
+    embedded, count_copy = run(copy=True)
+    assert count == 1 and count_copy == 0
+    for got, want, name in zip(placed, embedded, ["base", "weight", "bias"]):
+        assert_bitexact(got, want, f"{norm} {name}")
+    box = (slice(5, 65), slice(20, 276)) if layer else (slice(5, 65), slice(None))
+    outside = np.ones(shape, bool)
+    outside[box] = False
+    assert_bitexact(placed[0][outside], H_np[outside], "border holds only the second term")
+
+
 def test_autograd_narrow_chains_embed_once(sp):
     """A chain of narrows is embedded into its base once: each narrow whose
     input is a narrow with no other consumer hands its gradient down with

@@ -236,6 +236,13 @@ def test_box_embed(hip, dtype, extents, box):
     hip.call("spar_hip_launch_box_embed", out.ptr, src.ptr, len(extents),
              *[a.ctypes.data for a in arrays], np.dtype(dtype).itemsize, 0)
     assert_bitexact(out.to_numpy(dtype, want.shape), want, "box embed")
+    # input null: only the zeros around the box; the box keeps what it held
+    hip.call("spar_hip_launch_fill", out.ptr, want.size, tag(dtype), 7.0, 0)
+    hip.call("spar_hip_launch_box_embed", out.ptr, None, len(extents),
+             *[a.ctypes.data for a in arrays], np.dtype(dtype).itemsize, 0)
+    border = np.zeros(extents, dtype)
+    border[tuple(slice(start, start + length) for start, length in box)] = 7.0
+    assert_bitexact(out.to_numpy(dtype, want.shape), border, "box border")
 
 
 def test_box_embed_rejects_bad_arguments(hip):
@@ -253,6 +260,9 @@ def test_box_embed_rejects_bad_arguments(hip):
     assert call((4, 4, 4, 4, 4), (1,) * 5, (2,) * 5) == 1     # five boxed axes
     assert call((1 << 16, 1 << 16), (0, 0), (1, 1)) == 1      # more than 2^31 - 1 elements
     assert call((4, 8), (1, 2), (2, 3)) == 0
+    arrays = [np.array(v, dtype=np.uint64) for v in ((4, 8), (0, 2), (0, 3))]
+    assert lib.spar_hip_launch_box_embed(p, None, 2, *[a.ctypes.data for a in arrays], 4,
+                                         0).code == 1  # empty box, border only
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -164,7 +164,7 @@ def test_norm_backward_kernel(hip, dtype, center):
         x, w, b, g = data(rows, n, dtype, 200 + index)
         _, _, _, (dx_in, mu, d) = forward_device(hip, x, w, b, center, dtype)
         dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
-        hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
+        hip.call("spar_hip_launch_norm_backward", dx.ptr, n, dw.ptr, db.ptr if center else None,
                  dev(hip, g).ptr, dx_in.ptr, n, 1, dev(hip, w).ptr, mu.ptr if center else None,
                  d.ptr, rows, n, int(center), tag(dtype), 0)
         tx = R.RTensor.of(x, requires_grad=True)
@@ -209,16 +209,18 @@ def test_norm_entry_points_reject_bad_arguments(hip):
     for args in bad:
         assert lib.spar_hip_launch_norm_forward(*args).code == 1, args
     backward_bad = [
-        (p, p, None, p, p, 8, 1, p, p, p, 4, 8, 1, 0, 0),  # LayerNorm without a bias gradient
-        (p, p, p, p, p, 6, 1, p, p, p, 4, 8, 1, 0, 0),     # rows overlap
-        (p, p, p, p, p, 1, 3, p, p, p, 4, 8, 1, 0, 0),     # columns overlap
-        (p, p, p, p, p, 8, 2, p, p, p, 4, 8, 1, 0, 0),     # neither layout
+        (p, 8, p, None, p, p, 8, 1, p, p, p, 4, 8, 1, 0, 0),  # LayerNorm without a bias gradient
+        (p, 8, p, p, p, p, 6, 1, p, p, p, 4, 8, 1, 0, 0),     # rows overlap
+        (p, 8, p, p, p, p, 1, 3, p, p, p, 4, 8, 1, 0, 0),     # columns overlap
+        (p, 8, p, p, p, p, 8, 2, p, p, p, 4, 8, 1, 0, 0),     # neither layout
+        (p, 7, p, p, p, p, 8, 1, p, p, p, 4, 8, 1, 0, 0),     # dx rows overlap
+        (p, 3, p, p, p, p, 1, 4, p, p, p, 4, 8, 1, 0, 0),     # dx columns overlap
     ]
     for args in backward_bad:
         assert lib.spar_hip_launch_norm_backward(*args).code == 1, args
     # zero rows: parameter gradients are zero, nothing else is touched
     dw, db = out_buf(hip, 8, F32), out_buf(hip, 8, F32)
-    hip.call("spar_hip_launch_norm_backward", None, dw.ptr, db.ptr, None, None, 8, 1, p, None,
+    hip.call("spar_hip_launch_norm_backward", None, 8, dw.ptr, db.ptr, None, None, 8, 1, p, None,
              None, 0, 8, 1, 0, 0)
     assert not dw.to_numpy(F32, (8,)).any() and not db.to_numpy(F32, (8,)).any()
 
@@ -393,7 +395,7 @@ def test_norm_row_stride_matches_contiguous(hip, dtype, center, rows, n, pitch, 
     outs = []
     for source, stride in ((x_dev.ptr, n), (wide_dev.address(first * item), pitch)):
         dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
-        hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
+        hip.call("spar_hip_launch_norm_backward", dx.ptr, n, dw.ptr, db.ptr if center else None,
                  dev(hip, g).ptr, source, stride, 1, dev(hip, w).ptr, mu.ptr if center else None,
                  d.ptr, rows, n, int(center), tag(dtype), 0)
         outs.append([dx.to_numpy(dtype, (rows, n)), dw.to_numpy(dtype, (n,))] +
@@ -453,6 +455,62 @@ def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
 
 @pytest.mark.parametrize("dtype", [F32, F64])
 @pytest.mark.parametrize("center", [True, False])
+@pytest.mark.parametrize("layout,rows,n,stride,first", [
+    ("rows", 64, 2048, 2304, 256),   # a block of a wider gradient, 16-byte aligned
+    ("rows", 37, 300, 309, 5),       # unaligned rows: scalar stores
+    ("columns", 256, 512, 320, 64),  # q columns further apart than rows
+    ("columns", 37, 300, 41, 3),     # unaligned
+])
+def test_norm_backward_strided_input_gradient(hip, dtype, center, layout, rows, n, stride,
+                                              first):
+    """dx written into a wider buffer: rows `stride` apart (row layout) or
+    element (p, q) at first + p + q * stride (column layout).  The block holds
+    exactly the values of the packed write (same kernels, same order), and
+    every element around it keeps the sentinel it was filled with."""
+    x, w, b, g = data(rows, n, dtype, 900 + rows + n)
+    _, _, _, (x_dev, mu, d) = forward_device(hip, x, w, b, center, dtype)
+    item = np.dtype(dtype).itemsize
+    if layout == "rows":
+        source, row_stride, column_stride, packed_stride = x_dev.ptr, n, 1, n
+        size = first + (rows - 1) * stride + n
+    else:
+        store = np.zeros(n * rows, dtype)
+        store.reshape(n, rows)[:, :] = x.T
+        source, row_stride, column_stride, packed_stride = dev(hip, store).ptr, 1, rows, rows
+        size = first + rows + (n - 1) * stride
+    g_dev, w_dev = dev(hip, g), dev(hip, w)
+    sentinel = np.full(size, -7.25, dtype)
+    wide = dev(hip, sentinel)
+    # the packed write starts at the same offset, so both take the same
+    # (vector or scalar) kernel and sum in the same order
+    packed = out_buf(hip, first + rows * n, dtype)
+    dws = []
+    for dx_ptr, dx_stride in ((packed.address(first * item), packed_stride),
+                              (wide.address(first * item), stride)):
+        dw, db = out_buf(hip, n, dtype), out_buf(hip, n, dtype)
+        hip.call("spar_hip_launch_norm_backward", dx_ptr, dx_stride,
+                 dw.ptr, db.ptr if center else None, g_dev.ptr, source, row_stride,
+                 column_stride, w_dev.ptr, mu.ptr if center else None, d.ptr, rows, n,
+                 int(center), tag(dtype), 0)
+        dws.append(dw.to_numpy(dtype, (n,)))
+    flat = packed.to_numpy(dtype, (first + rows * n,))[first:]
+    got = wide.to_numpy(dtype, (size,))
+    written = np.zeros(size, bool)
+    p_idx, q_idx = np.meshgrid(np.arange(rows), np.arange(n), indexing="ij")
+    if layout == "rows":
+        where = first + p_idx * stride + q_idx
+        want = flat.reshape(rows, n)
+    else:
+        where = first + p_idx + q_idx * stride
+        want = flat.reshape(n, rows).T
+    written[where.ravel()] = True
+    assert_bitexact(got[where], want, f"strided dx {layout}")
+    assert np.all(got[~written] == dtype(-7.25)), "elements around the block were written"
+    assert_bitexact(dws[1], dws[0], "d weight")
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
 @pytest.mark.parametrize("rows,n,pitch,first", [
     (512, 1024, 512, 0),     # a transposed contiguous matrix: whole tiles
     (200, 520, 264, 4),      # a transposed block of a wider matrix: partial tiles
@@ -479,7 +537,8 @@ def test_norm_backward_column_layout(hip, dtype, center, rows, n, pitch, first):
     for source, row_stride, column_stride in ((x_dev.ptr, n, 1),
                                               (store_dev.address(first * item), 1, pitch)):
         dx, dw, db = out_buf(hip, rows * n, dtype), out_buf(hip, n, dtype), out_buf(hip, n, dtype)
-        hip.call("spar_hip_launch_norm_backward", dx.ptr, dw.ptr, db.ptr if center else None,
+        hip.call("spar_hip_launch_norm_backward", dx.ptr, n if column_stride == 1 else rows,
+                 dw.ptr, db.ptr if center else None,
                  g_dev.ptr, source, row_stride, column_stride, w_dev.ptr,
                  mu.ptr if center else None, d.ptr, rows, n, int(center), tag(dtype), 0)
         got = dx.to_numpy(dtype, (rows * n,))
