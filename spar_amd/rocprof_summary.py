@@ -314,7 +314,7 @@ def summarize_suite(raw: Path, out: Path, section: str) -> None:
         "Generated (from the repository root) by",
         "",
         f"    python3 -m spar_amd.rocprof_summary suite --section {section} "
-        f"--raw gpurun_out/suite_prof_{section} --out profiles",
+        f"--raw {raw} --out profiles",
         "",
         "which runs",
         "",
@@ -457,7 +457,7 @@ def summarize_traffic(raw: Path, out: Path) -> None:
         "Generated (from the repository root) by",
         "",
         f"    python3 -m spar_amd.rocprof_summary traffic --section {section} "
-        f"--raw gpurun_out/traffic_{section} --out profiles",
+        f"--raw {raw} --out profiles",
         "",
         f"which runs two counter passes per op, for example (op `{ops[0]}`):",
         "",
