@@ -481,9 +481,7 @@ struct BoxGeometry {
   uint32_t in_stride[kMaxBoxAxes];  // input elements per step along the axis
 };
 
-// BORDER: write only the zeros outside the box (input unused), leaving the
-// box to a producer that writes it in place.
-template <typename E, bool VEC, int R, bool BORDER>
+template <typename E, bool VEC, int R>
 __global__ void __launch_bounds__(kThreads)
     box_embed_kernel(E* output, const E* input, uint64_t groups, BoxGeometry box) {
   constexpr int G = VEC ? static_cast<int>(16 / sizeof(E)) : 1;
@@ -503,20 +501,51 @@ __global__ void __launch_bounds__(kThreads)
       inside = inside && c >= box.start[a] && c - box.start[a] < box.length[a];
       from += (c - box.start[a]) * box.in_stride[a];
     }
-    if constexpr (BORDER) {
-      if (!inside) {
-        if constexpr (VEC) {
-          *reinterpret_cast<V*>(output + element) = V{};
-        } else {
-          output[element] = E(0);
-        }
-      }
-    } else if constexpr (VEC) {
+    if constexpr (VEC) {
       V value{};
       if (inside) value = stream_load(reinterpret_cast<const V*>(input + from));
       *reinterpret_cast<V*>(output + element) = value;
     } else {
       output[element] = inside ? input[from] : E(0);
+    }
+  }
+}
+
+// Only the zeros around a box, which a producer writes in place: a
+// workgroup per row of the last axis (rows decoded once, not per element).
+// A row inside the box on every outer axis gets its two margins along the
+// last axis, any other row all of it.  VEC: 16-byte groups (the last axis's
+// extent, start and length are multiples of G).
+template <typename E, bool VEC, int R>
+__global__ void __launch_bounds__(kThreads)
+    box_border_kernel(E* output, uint64_t rows, BoxGeometry box) {
+  constexpr uint32_t G = VEC ? static_cast<uint32_t>(16 / sizeof(E)) : 1;
+  using V = typename Vec16<E>::type;
+  const uint32_t extent = box.extent[R - 1].divisor / G;
+  const uint32_t first = box.start[R - 1] / G;
+  const uint32_t last = first + box.length[R - 1] / G;
+  for (uint64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    uint32_t rest = static_cast<uint32_t>(row);
+    bool inside = true;
+#pragma unroll
+    for (int a = R - 2; a >= 0; --a) {
+      const uint32_t outer = box.extent[a].div(rest);
+      const uint32_t c = rest - outer * box.extent[a].divisor;
+      rest = outer;
+      inside = inside && c >= box.start[a] && c - box.start[a] < box.length[a];
+    }
+    E* base = output + row * box.extent[R - 1].divisor;
+    // the groups [0, first) and [last, extent) of an inside row, all others'
+    const uint32_t gap_begin = inside ? first : extent;
+    const uint32_t gap_end = inside ? last : extent;
+    const uint32_t zeros = extent - (gap_end - gap_begin);
+    for (uint32_t k = threadIdx.x; k < zeros; k += kThreads) {
+      const uint32_t g = k < gap_begin ? k : k + (gap_end - gap_begin);
+      if constexpr (VEC) {
+        reinterpret_cast<V*>(base)[g] = V{};
+      } else {
+        base[g] = E(0);
+      }
     }
   }
 }
@@ -536,8 +565,6 @@ void launch_box_embed(E* output, const E* input, int rank, const uint64_t* exten
     in_stride *= static_cast<uint32_t>(lengths[a]);
   }
   const int last = rank - 1;
-  // (with input null, border only, every 16-byte group lies wholly inside
-  // or outside the box under the same conditions)
   const bool vec = aligned16(output) && aligned16(input) && extents[last] % G == 0 &&
                    starts[last] % G == 0 && lengths[last] % G == 0;
   const uint64_t groups = vec ? count / G : count;
@@ -549,27 +576,44 @@ void launch_box_embed(E* output, const E* input, int rank, const uint64_t* exten
     kernel<<<static_cast<uint32_t>(blocks), kThreads, 0, guard.stream>>>(output, input, groups,
                                                                           box);
   };
-  auto with_rank = [&](auto vec_tag, auto border_tag) {
-    constexpr bool VEC = decltype(vec_tag)::value;
-    constexpr bool BORDER = decltype(border_tag)::value;
-    switch (rank) {
-      case 1: launch(box_embed_kernel<E, VEC, 1, BORDER>); break;
-      case 2: launch(box_embed_kernel<E, VEC, 2, BORDER>); break;
-      case 3: launch(box_embed_kernel<E, VEC, 3, BORDER>); break;
-      default: launch(box_embed_kernel<E, VEC, 4, BORDER>); break;
-    }
-  };
-  auto with_border = [&](auto vec_tag) {
-    if (input == nullptr) {
-      with_rank(vec_tag, std::true_type{});
+  if (input == nullptr) {
+    // border only: a workgroup per row of the last axis
+    const uint64_t rows = count / extents[last];
+    uint64_t row_blocks = rows < cap ? rows : cap;
+    if (row_blocks == 0) row_blocks = 1;
+    auto border = [&](auto kernel) {
+      kernel<<<static_cast<uint32_t>(row_blocks), kThreads, 0, guard.stream>>>(output, rows,
+                                                                                box);
+    };
+    auto border_rank = [&](auto vec_tag) {
+      constexpr bool VEC = decltype(vec_tag)::value;
+      switch (rank) {
+        case 1: border(box_border_kernel<E, VEC, 1>); break;
+        case 2: border(box_border_kernel<E, VEC, 2>); break;
+        case 3: border(box_border_kernel<E, VEC, 3>); break;
+        default: border(box_border_kernel<E, VEC, 4>); break;
+      }
+    };
+    if (vec) {
+      border_rank(std::true_type{});
     } else {
-      with_rank(vec_tag, std::false_type{});
+      border_rank(std::false_type{});
+    }
+    return;
+  }
+  auto with_rank = [&](auto vec_tag) {
+    constexpr bool VEC = decltype(vec_tag)::value;
+    switch (rank) {
+      case 1: launch(box_embed_kernel<E, VEC, 1>); break;
+      case 2: launch(box_embed_kernel<E, VEC, 2>); break;
+      case 3: launch(box_embed_kernel<E, VEC, 3>); break;
+      default: launch(box_embed_kernel<E, VEC, 4>); break;
     }
   };
   if (vec) {
-    with_border(std::true_type{});
+    with_rank(std::true_type{});
   } else {
-    with_border(std::false_type{});
+    with_rank(std::false_type{});
   }
 }
 
