@@ -669,11 +669,14 @@ bool launch_vec_tiled(T* out, const T* a, const T* b, const MultiView& view, int
   tg.tiles_p.init(static_cast<uint32_t>(tiles_p));
   tg.tiles_q.init(static_cast<uint32_t>(tiles_q));
   tg.tile_count = static_cast<uint32_t>(tiles);
-  // One workgroup per resident slot (two per CU with one staged operand, one
-  // with two), each walking tiles.  Without an occupancy answer the view
-  // takes another kernel (same values).
+  // Three workgroups per resident slot (two slots per CU with one staged
+  // operand, one with two), each walking tiles: the workgroups beyond the
+  // resident ones start as others finish.  On x^T - mu for x [8192, 4096]
+  // float32 (2048 tiles) one per slot took 48.8-49.5 us, three 47.0-48.0
+  // and four to eight no less.  Without an occupancy answer the view takes
+  // another kernel (same values).
   auto launch = [&](auto kernel) {
-    const uint64_t slots = resident_blocks(kernel, kThreads, guard);
+    const uint64_t slots = 3 * resident_blocks(kernel, kThreads, guard);
     if (slots == 0) return false;
     kernel<<<static_cast<uint32_t>(tiles < slots ? tiles : slots), kThreads, 0, guard.stream>>>(
         out, a, b, tg, f);
