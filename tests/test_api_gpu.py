@@ -389,7 +389,8 @@ def test_autograd_layernorm_chain_on_views(sp, view):
 
 
 @pytest.mark.parametrize("norm", ["layer_norm", "rms_norm"])
-def test_autograd_norm_gradient_written_into_base(sp, norm):
+@pytest.mark.parametrize("computed", [False, True])
+def test_autograd_norm_gradient_written_into_base(sp, norm, computed):
     """A fused norm whose input is a chain of narrows writes that input's
     gradient straight into the gradient of the chain's base, whose border the
     engine zeroes first; the base's gradient is handed down the chain and
@@ -397,7 +398,8 @@ def test_autograd_norm_gradient_written_into_base(sp, norm):
     on an exact copy of x (x.contiguous() of the strided view, x * 1.0 of the
     contiguous one), whose dense gradient the chain embeds: every
     gradient bit-exact, including the base's second contribution added in
-    the same order."""
+    the same order.  `computed`: the chain starts on base * 2 instead of the
+    leaf, so the placed gradient feeds that product's rule."""
     layer = norm == "layer_norm"
     shape = (70, 300) if layer else (70, 256)
     base_np = normal(101, shape)
@@ -411,7 +413,8 @@ def test_autograd_norm_gradient_written_into_base(sp, norm):
         base = hip_tensor(sp, base_np, True)
         w = hip_tensor(sp, w_np, True)
         b = hip_tensor(sp, b_np, True)
-        x = base.narrow(0, 5, 60)
+        top = sp.multiply_scalar(base, 2.0) if computed else base
+        x = top.narrow(0, 5, 60)
         if layer:
             x = x.narrow(1, 20, 256)  # rows 300 apart, read in place
         if copy:  # an exact copy with a node of its own
@@ -433,6 +436,8 @@ def test_autograd_norm_gradient_written_into_base(sp, norm):
     box = (slice(5, 65), slice(20, 276)) if layer else (slice(5, 65), slice(None))
     outside = np.ones(shape, bool)
     outside[box] = False
+    # outside the box the first term's gradient is zero (through the product
+    # too), so only the second term's remains
     assert_bitexact(placed[0][outside], H_np[outside], "border holds only the second term")
 
 
