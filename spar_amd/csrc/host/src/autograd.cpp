@@ -35,6 +35,7 @@
 // an incoming view.  The view rules return dense gradients themselves
 // (transpose's is made contiguous); the reductions return their gradient as
 // a stride-0 broadcast view, which the rules that follow read in place.
+#include <algorithm>
 #include <atomic>
 #include <unordered_map>
 
@@ -381,6 +382,14 @@ class Sweep final {
       throw std::logic_error{"Backward rule returned an incorrect number of gradients"};
     }
     if (placed) {
+      // the narrow hands on `buffer` at its turn, so the rule's first
+      // contribution must be the destination it wrote, not another tensor
+      const Tensor& first{contributions.front()};
+      if (TensorInternals::storage(first) != TensorInternals::storage(placed->buffer) ||
+          first.storage_offset() != placed->destination.storage_offset() ||
+          !std::ranges::equal(first.strides(), placed->destination.strides())) {
+        throw std::logic_error{"Placed backward rule did not return its destination"};
+      }
       placed_[placed->slot] = std::move(placed->buffer);
       g_placed_gradients.fetch_add(1, std::memory_order_relaxed);
     }
