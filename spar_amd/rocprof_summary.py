@@ -72,7 +72,7 @@ CLASSES = {
 COPY_PATTERN = r"CopyOp"
 CALIBRATION_BYTES = 512 << 20
 
-TRACE_ARGS = ["--no-cpu-baseline", "--steps", "20"]
+TRACE_ARGS = ["--no-cpu-baseline", "--no-suite", "--steps", "20"]
 LOOP_ARGS = ["--profile-loop", "2"]
 STATS_FILE = "kernel_stats_x32x1024x4096.md"
 TRAFFIC_FILE = "hbm_traffic_x32x1024x4096.md"
