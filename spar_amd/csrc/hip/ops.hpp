@@ -234,26 +234,27 @@ __device__ __forceinline__ NormalTail normal_tail(double a) {
 }
 
 // GELU of a float32 from the tail table at `table` (global memory or an LDS
-// copy: the same values, so the same bits), pieces STRIDE doubles apart.  No branches and no patched
-// results: x is clamped to [-15, 15] inside the product, where Q(15) = 3.7e-51
-// already makes GELU round to -0 below -15 and to x above 15, and +inf stays
-// +inf (inf - 15 Q(15)).  Below 0 the product gains x - x, which is 0 for a
-// finite x and NaN for -inf, as (0.5 x) erfc(-x / sqrt 2) is; NaN inputs
-// take the x >= 0 form and propagate through it.
+// copy: the same values, so the same bits), pieces STRIDE doubles apart.
+// With a = |x| clamped to 15 and q = Q(a), GELU is x - a q for x >= 0 and
+// -a q (that is x Q(|x|)) below 0: one fused multiply-add, -a q + base, with
+// base = x above 0 and x - x below (0 for a finite x, NaN for -inf, as
+// (0.5 x) erfc(-x / sqrt 2) is).  The clamp (exact at +-15) and base are
+// formed in float32, so only the table lookup, the Horner steps and that
+// multiply-add run in double.  No branches and no patched results: Q(15) =
+// 3.7e-51 already makes GELU round to -0 below -15 and to x above 15, +inf
+// stays +inf (inf - 15 Q(15)), NaN propagates through base, and -0 gives -0.
 template <int STRIDE = kGeluStride>
 __device__ __forceinline__ float gelu_float(float value, const double* table) {
-  const double x = value;
-  const double clamped = fmin(fmax(x, -kGeluTailLimit), kGeluTailLimit);
-  const double a = __builtin_fabs(clamped);
+  constexpr float kLimit = static_cast<float>(kGeluTailLimit);
+  const double a = __builtin_fabs(static_cast<double>(fminf(fmaxf(value, -kLimit), kLimit)));
   const double g = a * __builtin_fma(kGeluBeta, a, kGeluAlpha);
   const double* c = table + static_cast<int>(g) * STRIDE;
   const double t = __builtin_amdgcn_fract(g);
   double q = c[kGeluDegree];
 #pragma unroll
   for (int k = kGeluDegree - 1; k >= 0; --k) q = __builtin_fma(q, t, c[k]);
-  const double negative = clamped * q + (x - x);
-  const double positive = __builtin_fma(-clamped, q, x);
-  return static_cast<float>(x < 0.0 ? negative : positive);
+  const float base = value < 0.0f ? value - value : value;
+  return static_cast<float>(__builtin_fma(-a, q, static_cast<double>(base)));
 }
 
 // The derivative: |x| is clamped to 15 and the results outside [-15, 15]
