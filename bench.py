@@ -15,12 +15,16 @@ with upstream gradient G ~ N(0,1).  Every op runs through the backend's C ABI
 `value` is the step's algorithmic HBM bytes (each distinct input byte read
 once, each output byte written once, broadcast operands at their stored size)
 divided by the measured time, in GB/s (1e9 B/s).  One JSON line is printed.
-Its `suite` key holds every op of the other configurations (C1, C3, C4, C5
-and the optimizer kernels), each timed steady state, with the HBM traffic per
-launch that the committed rocprof summaries measured, and per configuration a
-roofline record for its dominant op.  `--suite` also prints one JSON line per
-op; `--suite-op CONFIG/OP --profile-launches K` runs only that op, K times,
-for the counter passes that write those summaries.
+Its `suite` key holds every op of the other configurations (C1, the same ops
+on [8192, 8192] as C1L, C3, C4, C5 and the optimizer kernels), each timed
+steady state, as a compact [ms, fraction of peak, L2-fabric traffic MB, CPU
+GB/s] array: the traffic per launch that the committed rocprof summaries
+measured, and Spar's CPU path (the oracle's 1-thread C loops) timed on a
+bounded sample of the same inputs in the same run.  Each configuration also
+carries a roofline record for its dominant op and its CPU baseline.
+`--suite` also prints one JSON line per op with the cold timings;
+`--suite-op CONFIG/OP --profile-launches K` runs only that op, K times, for
+the counter passes that write those summaries.
 """
 from __future__ import annotations
 
@@ -54,7 +58,7 @@ def parse():
     p.add_argument("--suite", action="store_true",
                    help="also print one JSON line per suite op")
     p.add_argument("--suite-only", default=None,
-                   help="comma-separated suite sections to run (C1,C3,C4,C5,optim)")
+                   help="comma-separated suite sections to run (C1,C1L,C3,C4,C5,optim)")
     p.add_argument("--no-suite", action="store_true", help="leave the suite out of the line")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-loop", type=int, default=0,
@@ -160,7 +164,7 @@ def time_ops(hip, ops, reps=20, warmup=3):
     return times
 
 
-def cpu_baseline(hip, work: Workload, sample_batch=16, repeats=3):
+def cpu_baseline(hip, work: Workload, sample_batch=8, repeats=3):
     """The oracle (a 1-thread C restatement of Spar's CPU loops) on the first
     `sample_batch` batch rows of the same device inputs."""
     import oracle.ops as O
@@ -195,12 +199,11 @@ def cpu_baseline(hip, work: Workload, sample_batch=16, repeats=3):
         "cores": 1,
         "kind": "port",
         "cpu_model": model,
-        "sample": (f"the five ops of the step on the first {sample_batch} of {B} batch rows "
-                   f"(x[{sample_batch},{T},{C}], half the step's bytes, scaled by its own bytes), "
-                   f"the oracle's C loops (-O2 -ffp-contract=off) on 1 core of {model} "
-                   f"({os.cpu_count()} logical CPUs visible), median of {repeats} runs of "
-                   f"{sum(per_rep) / repeats:.2f} s"),
-        "seconds_per_step_sample": round(seconds, 4),
+        "sample": (f"the step's 5 ops on batch rows 0-{sample_batch - 1} of {B} "
+                   f"(x[{sample_batch},{T},{C}]), GB/s from the sample's own bytes; oracle C "
+                   f"loops (-O2 -ffp-contract=off), 1 thread, {os.cpu_count()} logical CPUs "
+                   f"visible, median of {repeats}"),
+        "s": round(seconds, 4),
     }
 
 
@@ -295,16 +298,15 @@ def main():
     for name, kernel, _ in ops:
         mean_ms = times[name]
         gbps = nbytes[name] / (mean_ms * 1e-3) / 1e9
-        per_op[name] = {"kernel": kernel, "ms": round(mean_ms, 5), "GB/s": round(gbps, 1),
-                        "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": nbytes[name]}
+        per_op[name] = [round(mean_ms, 5), round(gbps / HBM_PEAK_GBPS, 4)]
         kernel_time[kernel] = kernel_time.get(kernel, 0.0) + mean_ms
         kernel_bytes[kernel] = kernel_bytes.get(kernel, 0) + nbytes[name]
     dominant = max(kernel_time, key=kernel_time.get)
     launches = sum(1 for _, k, _ in ops if k == dominant)
     achieved = kernel_bytes[dominant] / (kernel_time[dominant] * 1e-3) / 1e9
     # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # (python3 -m spar_amd.rocprof_summary run ...), null until profiled.
-    from spar_amd.rocprof_summary import TRAFFIC_FILE, read_traffic
+    # (python3 rocprof_summary.py run ...), null until profiled.
+    from rocprof_summary import TRAFFIC_FILE, read_traffic
 
     traffic = read_traffic(ROOT / "profiles" / TRAFFIC_FILE).get(dominant)
     roofline = {
@@ -342,7 +344,7 @@ def main():
         "frac_of_peak": round(value / HBM_PEAK_GBPS, 4),
         "elements_per_s": round(5 * work.n / (ms_per_step * 1e-3), 1),
         "wall_s": round(wall, 4),
-        "per_op": per_op,
+        "per_op": per_op,  # op: [ms per launch, fraction of 8 TB/s]
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:
@@ -350,8 +352,10 @@ def main():
     suite = None
     if not args.no_suite:
         del work
-        suite = Suite(hip)
+        suite = Suite(hip, cpu=not args.no_cpu_baseline)
         suite.run(None if args.suite_only is None else args.suite_only.split(","))
+        result["suite_format"] = ("op: [ms per launch, fraction of 8 TB/s, L2-fabric MB per "
+                                  "launch, CPU path GB/s]; rooflines hbm-bound, peak 8000 GB/s")
         result["suite"] = suite.summary()
     print(json.dumps(result), flush=True)
     if args.suite and suite is not None:
@@ -365,34 +369,35 @@ MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 
 # The suite's configurations, their workloads and their ops, in run order.
 SUITE_WORKLOADS = {
-    "C1": "contiguous fp32 elementwise on [4096, 4096] a, b ~ N(0,1)",
-    "C3": "axis reductions on [8192, 8192] ~ N(0,1); full reductions of 2^28 ~ U(-1,1)",
-    "C4": "row softmax / log-softmax (and cross entropy) on logits [8192, 32768] ~ N(0, 2)",
-    "C5": "LayerNorm chain through the Tensor API on [4096, 8192] views: a transposed "
-          "[8192, 4096] base and a block of a [4608, 9216] base",
-    "optim": "AdamW, gradient-norm summary and scaling over 124,439,808 fp32 parameters",
+    "C1": "a, b [4096,4096] ~ N(0,1)",
+    "C1L": "a, b [8192,8192] ~ N(0,1)",
+    "C3": "X [8192,8192] ~ N(0,1); v [2^28] ~ U(-1,1)",
+    "C4": "logits [8192,32768] ~ N(0,2); composed CE (cross entropy) against fused CE bytes",
+    "C5": "LayerNorm (LN) through the Tensor API on [4096,8192] views of a [8192,4096] base "
+          "(transposed) and a [4608,9216] base (sliced); LN ops against the fused minimum "
+          "(fwd: x in, y out; bwd: x, G in, dx out); the LN backwards timed cold",
+    "optim": "124,439,808 fp32 parameters; AdamW with double inner math",
 }
 SUITE_OPS = {
     "C1": ["a+b", "a*b", "gelu(a)", "exp(a)"],
+    "C1L": ["a+b", "a*b", "gelu(a)", "exp(a)"],
     "C3": [f"{op} axis {axis}" for axis in (1, 0) for op in ("sum", "mean", "max", "argmax")]
           + [f"full {op} 2^28" for op in ("sum", "mean", "max")],
     "C4": ["softmax forward", "softmax backward", "log_softmax forward", "log_softmax backward",
-           "cross_entropy forward (fused)", "cross_entropy backward (fused)",
-           "cross_entropy forward (composed, vs fused bytes)",
-           "cross_entropy backward (composed, vs fused bytes)"],
+           "CE forward fused", "CE backward fused", "CE forward composed",
+           "CE backward composed"],
     "C5": [f"{op} {view}" for view in ("transposed", "sliced")
            for op in ("mu=mean(x,1)", "xc=x-mu", "square(xc)", "var=mean(sq,1)", "xhat=xc/sd",
                       "xhat*gamma", "+beta", "y*G", "sum(y*G)")]
-          + [f"{op} {view} (vs fused minimum)" for view in ("transposed", "sliced")
-             for op in ("forward chain", "backward chain", "fused layer_norm forward",
-                        "fused layer_norm backward")],
-    "optim": ["adamw step (fp32, double math)", "gradient norm summary",
-              "scale gradients in place"],
+          + [f"{op} {view}" for view in ("transposed", "sliced")
+             for op in ("LN forward chain", "LN backward chain", "fused LN forward",
+                        "fused LN backward")],
+    "optim": ["adamw step", "grad norm summary", "scale in place"],
 }
 # Ops measured against a minimum other than their own bytes (the fused
 # minimum of the C5 chain, the fused cross entropy's bytes): reported, but
 # never a configuration's roofline op.
-SUITE_REFERENCE_ONLY = ("composed", "chain", "fused layer_norm")
+SUITE_REFERENCE_ONLY = ("composed", "chain", "fused LN")
 
 
 def rotation(set_bytes):
@@ -421,18 +426,20 @@ class Suite:
     cold only.
 
     With `profile=(config, op, launches)` only that op runs, `launches`
-    times, each launch preceded by a marker dispatch (a 16-byte
-    spar_hip_touch) and the last one followed by another, so a counter pass
-    can attribute the dispatches between markers to the op (a prepare step,
-    such as building a fresh graph, runs before its marker)."""
+    times, each launch between an opening and a closing marker dispatch (a
+    16-byte spar_hip_touch), so a counter pass attributes to the op exactly
+    the dispatches inside each marker pair; a prepare step, such as building
+    a fresh graph, runs between a closing marker and the next opening one."""
 
-    def __init__(self, hip, reps=20, warmup=3, profile=None):
+    def __init__(self, hip, reps=20, warmup=3, profile=None, cpu=False):
         self.hip = hip
         self.reps = reps
         self.warmup = warmup
         self.profile = profile
+        self.with_cpu = cpu and profile is None
         self.lines = []
         self.results = {}
+        self.cpu = {}
         self.profile_bytes = None
         self.flush = hip.DeviceBuffer(512 << 20)
         hip.call("spar_hip_zero", self.flush.ptr, self.flush.nbytes, 0)
@@ -454,10 +461,10 @@ class Suite:
             hip.synchronize()
             for k in range(self.profile[2]):
                 if prepare is not None:
-                    prepare()
-                hip.call("spar_hip_touch", self.sink.ptr, 16, 0, 0)  # marker: a launch starts
+                    prepare()  # outside any window: its dispatches are not the op's
+                hip.call("spar_hip_touch", self.sink.ptr, 16, 0, 0)  # marker: the launch opens
                 launches[k % len(launches)]()
-            hip.call("spar_hip_touch", self.sink.ptr, 16, 0, 0)  # marker: the last one ended
+                hip.call("spar_hip_touch", self.sink.ptr, 16, 0, 0)  # marker: the launch closes
             hip.synchronize()
             return
         for _ in range(self.warmup):
@@ -486,6 +493,7 @@ class Suite:
             self.stop.record()
             ms = self.start.elapsed_ms(self.stop) / count
             line["timing"] = f"steady, {len(launches)} rotated sets"
+            line["sets"] = len(launches)
         else:
             ms = cold
             line["timing"] = "cold"
@@ -498,30 +506,60 @@ class Suite:
         self.lines.append(line)
         self.results.setdefault(config, {})[name] = line
 
+    def cpu_baseline(self, config, sample, ops, repeats=3):
+        """Spar's CPU path, as the oracle restates it (1-thread C loops built
+        -O2 -ffp-contract=off over logical indices), on a bounded sample of
+        this configuration's inputs copied from the device: `ops` is a list
+        of (op name, the sample's algorithmic bytes, callable).  Each op is
+        timed per run; the median over `repeats` runs gives each op's GB/s
+        and, over all ops, the configuration's."""
+        if not self.with_cpu:
+            return
+        per_op = {name: [] for name, _, _ in ops}
+        for _ in range(repeats):
+            for name, _, fn in ops:
+                t0 = time.perf_counter()
+                fn()
+                per_op[name].append(time.perf_counter() - t0)
+        seconds = {name: statistics.median(times) for name, times in per_op.items()}
+        total_s = sum(seconds.values())
+        total_bytes = sum(nbytes for _, nbytes, _ in ops)
+        self.cpu[config] = {
+            "GB/s": round(total_bytes / total_s / 1e9, 3), "s": round(total_s, 3),
+            "sample": sample,
+            "ops": {name: round(nbytes / seconds[name] / 1e9, 3) for name, nbytes, _ in ops}}
+
     def summary(self):
-        """Per configuration: every op's steady-state figures with its HBM
-        traffic per launch from the committed counter summary (null where
-        none was measured), and the roofline record of its dominant op (the
-        longest op measured against its own bytes)."""
-        from spar_amd.rocprof_summary import read_op_traffic, suite_traffic_file
+        """Per configuration, compactly: each op as [ms per launch, fraction
+        of 8 TB/s, L2-fabric MB per launch from the committed counter summary
+        (null where none was measured), the CPU path's GB/s on its sample
+        (null where it has none)]; the roofline record of the configuration's
+        dominant op (the longest op measured against its own bytes); and the
+        CPU baseline."""
+        from rocprof_summary import read_op_traffic, suite_traffic_file
 
         out = {}
         for config, ops in self.results.items():
             traffic = read_op_traffic(ROOT / "profiles" / suite_traffic_file(config))
+            cpu = self.cpu.get(config, {})
+            cpu_ops = cpu.get("ops", {})
             entry = {"workload": SUITE_WORKLOADS[config], "ops": {}}
             for name, line in ops.items():
-                entry["ops"][name] = {key: line[key] for key in ("ms", "GB/s", "frac", "bytes",
-                                                                 "timing")}
-                entry["ops"][name]["traffic"] = traffic.get(name)
+                moved = traffic.get(name)
+                entry["ops"][name] = [line["ms"], line["frac"],
+                                      None if moved is None else round(moved / 1e6, 1),
+                                      cpu_ops.get(name)]
+                if line["timing"] != "cold":
+                    entry["sets"] = line["sets"]
             own = {name: line for name, line in ops.items()
                    if not any(tag in name for tag in SUITE_REFERENCE_ONLY)}
             if own:
                 name = max(own, key=lambda op: own[op]["ms"])
                 line = own[name]
-                entry["roofline"] = {"op": name, "bound": "hbm", "achieved": line["GB/s"],
-                                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": line["frac"],
-                                     "bytes_per_launch": line["bytes"],
-                                     "avg_launch_ms": line["ms"], "traffic": traffic.get(name)}
+                entry["roofline"] = {"op": name, "achieved": line["GB/s"], "frac": line["frac"],
+                                     "bytes_per_launch": line["bytes"], "traffic": traffic.get(name)}
+            if cpu:
+                entry["cpu_baseline"] = {key: cpu[key] for key in ("GB/s", "s", "sample")}
             out[config] = entry
         return out
 
@@ -547,16 +585,16 @@ class Suite:
             hip.call("spar_hip_random_uniform", buf.ptr, n, F, seed, low, high, 0)
             return buf
 
-        def c1():
-            # C1: contiguous elementwise on [4096, 4096]; set 0 carries the
+        def elementwise(config, side, cpu_rows):
+            # Contiguous elementwise on [side, side]; set 0 carries the
             # benchmark seeds, the other sets only rotate the cache.
-            n = 4096 * 4096
+            n = side * side
             sets = [(normal(n, 1 + 100 * k), normal(n, 2 + 100 * k), hip.DeviceBuffer(n * 4))
                     for k in range(rotation(12 * n))]
             for name, op in (("a+b", hip.ADD), ("a*b", hip.MULTIPLY)):
-                measure("C1", name, 12 * n, [lambda a=a, b=b, out=out, op=op: hip.call(
+                measure(config, name, 12 * n, [lambda a=a, b=b, out=out, op=op: hip.call(
                     "spar_hip_launch_binary", out.ptr, a.ptr, b.ptr, n, F, op, 0) for a, b, out in sets], n)
-            measure("C1", "gelu(a)", 8 * n, [lambda a=a, out=out: hip.call(
+            measure(config, "gelu(a)", 8 * n, [lambda a=a, out=out: hip.call(
                 "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.GELU, 0) for a, _, out in sets], n)
             # exp(clip(a, -10, 10)): the clip is the identity on these draws (checked here)
             peak = hip.DeviceBuffer(8)
@@ -564,10 +602,27 @@ class Suite:
                 hip.call("spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.NEGATE, 0)
                 for source in (a, out):  # max(a) and max(-a)
                     hip.call("spar_hip_launch_reduction", peak.ptr, source.ptr, n, F, hip.MAX, 0)
-                    assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "C1 draw exceeds the clip range"
-            measure("C1", "exp(a)", 8 * n, [lambda a=a, out=out: hip.call(
+                    assert peak.to_numpy(np.float32, (1,))[0] <= 10.0, "draw exceeds the clip range"
+            measure(config, "exp(a)", 8 * n, [lambda a=a, out=out: hip.call(
                 "spar_hip_launch_unary", out.ptr, a.ptr, n, F, hip.EXP, 0) for a, _, out in sets], n)
+            if self.with_cpu:
+                import oracle.ops as O
+
+                a = sets[0][0].to_numpy(np.float32, (side, side))[:cpu_rows].copy()
+                b = sets[0][1].to_numpy(np.float32, (side, side))[:cpu_rows].copy()
+                m = a.size
+                self.cpu_baseline(config, f"rows 0-{cpu_rows - 1} of {side}", [
+                    ("a+b", 12 * m, lambda: O.binary(a, b, "add")),
+                    ("a*b", 12 * m, lambda: O.binary(a, b, "multiply")),
+                    ("gelu(a)", 8 * m, lambda: O.unary(a, "gelu")),
+                    ("exp(a)", 8 * m, lambda: O.unary(a, "exp"))])
             del sets
+
+        def c1():
+            elementwise("C1", 4096, 4096)
+
+        def c1l():
+            elementwise("C1L", 8192, 1024)
 
         def c3():
             # C3: axis reductions on [8192, 8192] and a full reduction of 2^28
@@ -582,6 +637,21 @@ class Suite:
                         lambda x=x, out=out, code=code, axis=axis: hip.call(
                             "spar_hip_launch_axis_reduction", out.ptr, x.ptr, 2, u([R, R]), u([R, 1]), 0,
                             1 << axis, F, code, 0) for x, out in sets], n)
+            cpu_ops = []
+            if self.with_cpu:
+                import oracle.ops as O
+
+                # axis reductions of rows 0-1023: over axis 1, 1024 rows of 8192; over
+                # axis 0, the block's 8192 columns of 1024
+                block = sets[0][0].to_numpy(np.float32, (R, R))[:1024].copy()
+                m = block.size
+                for axis in (1, 0):
+                    cpu_ops += [
+                        (f"sum axis {axis}", 4 * m, lambda axis=axis: O.axis_sum(block, [axis])),
+                        (f"mean axis {axis}", 4 * m,
+                         lambda axis=axis: O.scalar(O.axis_sum(block, [axis]), "divide", block.shape[axis])),
+                        (f"max axis {axis}", 4 * m, lambda axis=axis: O.axis_max(block, [axis])),
+                        (f"argmax axis {axis}", 4 * m, lambda axis=axis: O.axis_max(block, [axis]))]
             del sets
             n = 1 << 28
             sets = [(uniform(n, 4 + 100 * k, -1.0, 1.0), hip.DeviceBuffer(8))
@@ -590,6 +660,12 @@ class Suite:
                 measure("C3", f"full {name} 2^28", 4 * n + 4, [lambda v=v, out=out, name=name: hip.call(
                     "spar_hip_launch_reduction", out.ptr, v.ptr, n, F, codes[name], 0)
                     for v, out in sets], n)
+            if self.with_cpu:
+                head = sets[0][0].to_numpy(np.float32, (n,))[:1 << 24].copy()
+                cpu_ops += [(f"full {name} 2^28", 4 * head.size,
+                             lambda name=name: O.full_reduce(head, name)) for name in ("sum", "mean", "max")]
+                self.cpu_baseline("C3", "axis ops: rows 0-1023 of 8192; full ops: the first 2^24 "
+                                  "elements", cpu_ops)
             del sets
 
         def c4():
@@ -615,6 +691,22 @@ class Suite:
                 measure("C4", f"{label} backward", 12 * n + 4 * rows, [lambda s=s, log=log: hip.call(
                     "spar_hip_launch_probability_backward", s.dx.ptr, s.grad.ptr, s.probs.ptr,
                     s.undefined.ptr, rows, V, 1, F, log, 0) for s in sets], n)
+            if self.with_cpu:
+                import oracle.ops as O
+
+                k = 128  # rows 0-127
+                logits = sets[0].logits.to_numpy(np.float32, (rows, V))[:k].copy()
+                grad = sets[0].grad.to_numpy(np.float32, (rows, V))[:k].copy()
+                probs, undefined = O.softmax_axis(logits, 1)
+                log_probs, log_undefined = O.log_softmax(logits, 1)
+                m = logits.size
+                self.cpu_baseline("C4", f"softmax family on rows 0-{k - 1} of {rows}", [
+                    ("softmax forward", 8 * m + 4 * k, lambda: O.softmax_axis(logits, 1)),
+                    ("softmax backward", 12 * m + 4 * k,
+                     lambda: O.softmax_axis_backward(grad, probs, undefined, 1)),
+                    ("log_softmax forward", 8 * m + 4 * k, lambda: O.log_softmax(logits, 1)),
+                    ("log_softmax backward", 12 * m + 4 * k,
+                     lambda: O.log_softmax_backward(grad, log_probs, log_undefined, 1))])
             # C4 as a loss: cross entropy over the same logits, fused (one read of the
             # logits forward; one read and one write backward) and composed as the
             # reference runs it (log_softmax, NLL gather; zero fill, NLL scatter,
@@ -627,7 +719,7 @@ class Suite:
             invalid = hip.DeviceBuffer(4)
             loss_grad = uniform(rows, 10, 0.5, 1.5)
             small = rows * (8 + 4 * 4)  # targets read; loss, max, log-sum, flag written
-            measure("C4", "cross_entropy forward (fused)", 4 * n + small, [lambda s=s: hip.call(
+            measure("C4", "CE forward fused", 4 * n + small, [lambda s=s: hip.call(
                 "spar_hip_launch_cross_entropy_forward", losses.ptr, row_max.ptr, row_log_sum.ptr,
                 s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows, V, 0, F, hip.INT64, 0, 0)
                 for s in sets], n)
@@ -637,7 +729,7 @@ class Suite:
                 hip.call("spar_hip_launch_cross_entropy_forward", losses.ptr, s.row_max.ptr,
                          s.row_log_sum.ptr, s.undefined.ptr, invalid.ptr, s.logits.ptr, targets.ptr, rows,
                          V, 0, F, hip.INT64, 0, 0)
-            measure("C4", "cross_entropy backward (fused)", 8 * n + rows * 24, [lambda s=s: hip.call(
+            measure("C4", "CE backward fused", 8 * n + rows * 24, [lambda s=s: hip.call(
                 "spar_hip_launch_cross_entropy_backward", s.dx.ptr, loss_grad.ptr, s.logits.ptr,
                 s.row_max.ptr, s.row_log_sum.ptr, s.undefined.ptr, targets.ptr, rows, V, 0, F,
                 hip.INT64, 0, 0) for s in sets], n)
@@ -656,9 +748,9 @@ class Suite:
                          s.undefined.ptr, rows, V, 1, F, 1, 0)
 
             # reported against the fused kernels' bytes, so the ratio is the speed-up
-            measure("C4", "cross_entropy forward (composed, vs fused bytes)", 4 * n + small,
+            measure("C4", "CE forward composed", 4 * n + small,
                     [lambda s=s: composed_forward(s) for s in sets], n)
-            measure("C4", "cross_entropy backward (composed, vs fused bytes)", 8 * n + rows * 24,
+            measure("C4", "CE backward composed", 8 * n + rows * 24,
                     [lambda s=s: composed_backward(s) for s in sets], n)
             del sets, targets, losses, row_max, row_log_sum, invalid, loss_grad
 
@@ -735,7 +827,7 @@ class Suite:
                 # Whole forward, then backward.  Both are reported against the fused
                 # minimum: forward reads x and G once (the loss is a scalar);
                 # backward reads x and G and writes dx (gamma, beta grads are small).
-                measure("C5", f"forward chain {label} (vs fused minimum)", 2 * T,
+                measure("C5", f"LN forward chain {label}", 2 * T,
                         [lambda k=k: forward(view_of(label, k), Gs[k]) for k in range(count)], n)
                 losses = []
 
@@ -744,12 +836,12 @@ class Suite:
                         leaf.zero_grad()
                     losses[:] = [forward(view_of(label), Gs[0])]
 
-                measure("C5", f"backward chain {label} (vs fused minimum)", 3 * T,
+                measure("C5", f"LN backward chain {label}", 3 * T,
                         lambda: losses[0].backward(), n, prepare=prepare)
 
                 # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
                 # first made contiguous, inside the timed op.
-                measure("C5", f"fused layer_norm forward {label} (vs fused minimum)", 2 * T,
+                measure("C5", f"fused LN forward {label}", 2 * T,
                         [lambda k=k: spar.layer_norm(view_of(label, k), gamma, beta, 1e-5)
                          for k in range(count)], n)
 
@@ -759,9 +851,50 @@ class Suite:
                     y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
                     losses[:] = [spar.sum(spar.multiply(y, Gs[0]), None, False)]
 
-                measure("C5", f"fused layer_norm backward {label} (vs fused minimum)", 3 * T,
+                measure("C5", f"fused LN backward {label}", 3 * T,
                         lambda: losses[0].backward(), n, prepare=prepare_fused)
                 del losses
+            if self.with_cpu:
+                import oracle.reference as R
+
+                # The same chain on the reference's CPU path for rows 0-255 of each
+                # view: the transposed view of columns 0-255 of the base, and the
+                # block of rows 256-511 of the sliced base's first 512 rows.
+                k = 256
+                cpu_device = spar.Device.cpu()
+
+                def host(t):
+                    return np.ascontiguousarray(t.to(cpu_device).numpy())
+
+                g_host, b_host = host(gamma), host(beta)
+                G_host = host(Gs[0])[:k].copy()
+                blocks = {"transposed": host(bases["transposed"][0])[:, :k].copy(),
+                          "sliced": host(bases["sliced"][0])[:256 + k].copy()}
+                cpu_ops, graphs = [], {}
+                for label, block in blocks.items():
+                    leaves = [R.RTensor.of(block, True), R.RTensor.of(g_host, True),
+                              R.RTensor.of(b_host, True)]
+                    G_r = R.RTensor.of(G_host)
+
+                    def cpu_forward(label=label, leaves=leaves, G_r=G_r):
+                        for leaf in leaves:
+                            leaf.meta.leaf_grad = None
+                        base, w, b = leaves
+                        x = base.transpose(0, 1) if label == "transposed" else \
+                            base.narrow(0, 256, k).narrow(1, 512, cols)
+                        mu = R.mean(x, [1], True)
+                        xc = R.subtract(x, mu)
+                        var = R.mean(R.square(xc), [1], True)
+                        xhat = R.divide(xc, R.sqrt(R.add_scalar(var, 1e-5)))
+                        y = R.add(R.multiply(xhat, w), b)
+                        graphs[label] = R.sum(R.multiply(y, G_r), None, False)
+
+                    T_s = 4 * k * cols
+                    cpu_ops += [(f"LN forward chain {label}", 2 * T_s, cpu_forward),
+                                (f"LN backward chain {label}", 3 * T_s,
+                                 lambda label=label: graphs[label].backward())]
+                self.cpu_baseline("C5", f"the LN chain, forward and backward, on rows 0-{k - 1} "
+                                  f"of each view", cpu_ops)
 
         def optim():
             # Optimizer: one AdamW step, the gradient-norm summary and the clip scaling
@@ -772,18 +905,27 @@ class Suite:
                      normal(n, 83 + 100 * k, 1e-3), uniform(n, 84 + 100 * k, 0.0, 1e-5),
                      hip.DeviceBuffer(64)) for k in range(count)]
             c1, c2 = 1.0 - 0.9 ** 1000, 1.0 - 0.95 ** 1000
-            measure("optim", "adamw step (fp32, double math)", 28 * n, [
+            measure("optim", "adamw step", 28 * n, [
                 lambda p=p, g=g, m=m, v=v: hip.call(
                     "spar_hip_launch_adamw", p.ptr, g.ptr, m.ptr, v.ptr, n, F, 3e-4, 0.9, 0.95, 1e-8, 0.1,
                     c1, c2, 0) for p, g, m, v, _ in sets], n)
-            measure("optim", "gradient norm summary", 4 * n, [lambda g=g, summary=summary: hip.call(
+            measure("optim", "grad norm summary", 4 * n, [lambda g=g, summary=summary: hip.call(
                 "spar_hip_launch_gradient_norm_summary", summary.ptr, g.ptr, n, F, 0)
                 for _, g, _, _, summary in sets], n)
-            measure("optim", "scale gradients in place", 8 * n, [lambda g=g: hip.call(
+            measure("optim", "scale in place", 8 * n, [lambda g=g: hip.call(
                 "spar_hip_launch_scale_in_place", g.ptr, n, F, 1.0, 0) for _, g, _, _, _ in sets], n)
+            if self.with_cpu:
+                import oracle.ops as O
+
+                k = 1 << 24  # parameters 0 to 2^24 - 1
+                p, g, m, v = (buf.to_numpy(np.float32, (n,))[:k].copy() for buf in sets[0][:4])
+                self.cpu_baseline("optim", f"parameters 0 to 2^24 - 1 of {n:,}", [
+                    ("adamw step", 28 * k, lambda: O.adamw(p, g, m, v, 3e-4, 0.9, 0.95, 1e-8, 0.1, c1, c2)),
+                    ("grad norm summary", 4 * k, lambda: O.SumSquares().add(g)),
+                    ("scale in place", 8 * k, lambda: O.scale(g, 1.0))])
             del sets
 
-        return {"C1": c1, "C3": c3, "C4": c4, "C5": c5, "optim": optim}
+        return {"C1": c1, "C1L": c1l, "C3": c3, "C4": c4, "C5": c5, "optim": optim}
 
 
 if __name__ == "__main__":

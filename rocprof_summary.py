@@ -2,7 +2,7 @@
 markdown summaries: per-kernel durations, and HBM bytes per dispatch from the
 FETCH_SIZE / WRITE_SIZE counters.
 
-    python3 -m spar_amd.rocprof_summary run --raw DIR --out DIR
+    python3 rocprof_summary.py run --raw DIR --out DIR
 
 runs, as child processes (this process never touches the GPU):
 
@@ -21,13 +21,13 @@ for its roofline ``traffic`` field.
 
 ``summarize`` regenerates the markdown from an existing raw directory.
 
-    python3 -m spar_amd.rocprof_summary suite --section optim --raw DIR --out DIR
+    python3 rocprof_summary.py suite --section optim --raw DIR --out DIR
 
 profiles one ``bench.py --suite-only SECTION`` run with ``--kernel-trace
 --stats`` and runs the same command without a profiler, then writes a
 per-kernel duration table next to the suite's own event-timed lines.
 
-    python3 -m spar_amd.rocprof_summary traffic --section C3 --raw DIR --out DIR
+    python3 rocprof_summary.py traffic --section C3 --raw DIR --out DIR
 
 measures every op of a suite section alone (``bench.py --suite-op
 SECTION/OP --profile-launches 4``): one ``--pmc FETCH_SIZE`` and one ``--pmc
@@ -59,7 +59,7 @@ import subprocess
 import sys
 from pathlib import Path
 
-ROOT = Path(__file__).resolve().parent.parent
+ROOT = Path(__file__).resolve().parent
 
 # bench.py's kernel classes: a regex over the demangled kernel name, and
 # whether dispatches of that kernel count as launches of the class (helper
@@ -266,6 +266,7 @@ def summarize(raw: Path, out: Path) -> None:
 # Suite sections: the workload each one times, for the summary's name and title.
 SUITE_WORKLOADS = {
     "C1": ("c1_4096x4096", "C1 contiguous elementwise on [4096, 4096] fp32"),
+    "C1L": ("c1l_8192x8192", "C1L contiguous elementwise on [8192, 8192] fp32"),
     "C3": ("c3_8192x8192", "C3 axis reductions on [8192, 8192] and full reductions of 2^28 fp32"),
     "C4": ("c4_8192x32768", "C4 softmax, log-softmax and cross entropy on [8192, 32768] fp32"),
     "C5": ("c5_4096x8192", "C5 LayerNorm chain and fused layer_norm on [4096, 8192] fp32 views"),
@@ -313,7 +314,7 @@ def summarize_suite(raw: Path, out: Path, section: str) -> None:
         "",
         "Generated (from the repository root) by",
         "",
-        f"    python3 -m spar_amd.rocprof_summary suite --section {section} "
+        f"    python3 rocprof_summary.py suite --section {section} "
         f"--raw {raw} --out profiles",
         "",
         "which runs",
@@ -353,7 +354,8 @@ def read_traffic(path: Path):
     return found
 
 
-SUITE_FILES = {"C1": "c1_4096x4096", "C3": "c3_8192x8192", "C4": "c4_8192x32768",
+SUITE_FILES = {"C1": "c1_4096x4096", "C1L": "c1l_8192x8192", "C3": "c3_8192x8192",
+               "C4": "c4_8192x32768",
                "C5": "c5_4096x8192", "optim": "optim_124439808"}
 MARKER = r"touch_kernel"
 GENERATORS = r"normal_kernel<|uniform_f32_kernel|uniform_kernel<"
@@ -385,16 +387,23 @@ def dispatches(path: Path):
     return [by_id[k] for k in sorted(by_id)]
 
 
-def op_window(rows):
-    """Dispatches between the first and the last marker, markers excluded,
-    and the calibration copy (the last dispatch)."""
+def op_window(rows, launches=None):
+    """The dispatches inside each (opening, closing) marker pair, markers
+    excluded, and the calibration copy (the last dispatch).  Markers come in
+    pairs, one pair per launch; whatever runs between a closing marker and
+    the next opening one (a fresh graph's forward, say) is left out."""
     marks = [i for i, (_, name, _) in enumerate(rows) if re.search(MARKER, name)]
-    if len(marks) < 2:
-        raise SystemExit("expected marker dispatches around the op")
+    if len(marks) < 2 or len(marks) % 2:
+        raise SystemExit(f"expected marker pairs around each launch, found {len(marks)} markers")
+    if launches is not None and len(marks) != 2 * launches:
+        raise SystemExit(f"expected {2 * launches} markers for {launches} launches, "
+                         f"found {len(marks)}")
     copy = rows[-1]
     if not re.search(COPY_PATTERN, copy[1]):
         raise SystemExit(f"last dispatch is not the calibration copy: {copy[1]}")
-    window = [row for row in rows[marks[0] + 1:marks[-1]] if not re.search(MARKER, row[1])]
+    window = []
+    for opening, closing in zip(marks[0::2], marks[1::2]):
+        window += rows[opening + 1:closing]
     return window, copy
 
 
@@ -451,12 +460,12 @@ def summarize_traffic(raw: Path, out: Path) -> None:
     section, ops, launches = plan["section"], plan["ops"], plan["launches"]
     cal_kib = CALIBRATION_BYTES / 1024
     lines = [
-        f"# HBM traffic per launch: bench.py suite section {section}, "
+        f"# L2-fabric (HBM + Infinity Cache) traffic per launch: bench.py suite section {section}, "
         f"{SUITE_WORKLOADS[section][1]}",
         "",
         "Generated (from the repository root) by",
         "",
-        f"    python3 -m spar_amd.rocprof_summary traffic --section {section} "
+        f"    python3 rocprof_summary.py traffic --section {section} "
         f"--raw {raw} --out profiles",
         "",
         f"which runs two counter passes per op, for example (op `{ops[0]}`):",
@@ -464,21 +473,28 @@ def summarize_traffic(raw: Path, out: Path) -> None:
         "    " + plan["commands"]["op00_fetch_size"],
         "    " + plan["commands"]["op00_write_size"],
         "",
-        f"Each pass runs the op alone {launches} times between marker dispatches and ends with",
-        "a plain contiguous copy of 512 MiB; each pass's FETCH_SIZE and WRITE_SIZE are",
-        "scaled by 512 MiB over the copy's reading, and the dispatches between the",
-        "markers (random generators excluded) are summed and divided by the launches.",
+        f"Each pass runs the op alone {launches} times, each launch between an opening and a",
+        "closing marker dispatch, and ends with a plain contiguous copy of 512 MiB; each",
+        "pass's FETCH_SIZE and WRITE_SIZE are scaled by 512 MiB over the copy's reading, and",
+        "the dispatches inside the marker pairs (random generators excluded) are summed and",
+        "divided by the launches.  Work a launch needs first (a fresh graph's forward for a",
+        "backward) runs outside the pairs and is not counted.",
         "",
-        "| op | kernels per launch | FETCH_SIZE scale | HBM read MB | HBM write MB | "
-        "HBM MB per launch | algorithmic MB | ratio |",
+        "What the counters see: FETCH_SIZE and WRITE_SIZE count the L2's traffic to and from",
+        "the data fabric, that is HBM plus Infinity Cache (MALL) hits; gfx950 exposes no",
+        "counter that separates the two.  For a kernel that re-reads data from the Infinity",
+        "Cache the figures below are L2-fabric bytes, an upper bound on its HBM bytes.",
+        "",
+        "| op | kernels per launch | FETCH_SIZE scale | L2-fabric read MB | L2-fabric write MB | "
+        "L2-fabric MB per launch | algorithmic MB | ratio |",
         "|---|---|---|---|---|---|---|---|",
     ]
     results = []
     for k, op in enumerate(ops):
         fetch_rows = dispatches(raw / f"op{k:02d}_fetch_size" / f"op{k:02d}_fetch_size_counter_collection.csv")
         write_rows = dispatches(raw / f"op{k:02d}_write_size" / f"op{k:02d}_write_size_counter_collection.csv")
-        fwin, fcopy = op_window(fetch_rows)
-        wwin, wcopy = op_window(write_rows)
+        fwin, fcopy = op_window(fetch_rows, launches)
+        wwin, wcopy = op_window(write_rows, launches)
         f_scale = cal_kib / fcopy[2]["FETCH_SIZE"]
         w_scale = cal_kib / wcopy[2]["WRITE_SIZE"]
         fwin = [r for r in fwin if not re.search(GENERATORS, r[1])]
@@ -494,10 +510,11 @@ def summarize_traffic(raw: Path, out: Path) -> None:
         lines.append(f"| {op} | {'<br>'.join('`' + n + '`' for n in kernels)} | {f_scale:.3f} | "
                      f"{read / 1e6:.1f} | {write / 1e6:.1f} | {(read + write) / 1e6:.1f} | "
                      f"{alg_mb} | {ratio} |")
-    lines += ["", "HBM bytes per launch of each op (bench.py reads these lines):", ""]
+    lines += ["", "L2-fabric bytes per launch of each op (bench.py reads these lines as the op's",
+              "traffic):", ""]
     lines += [f"- op_hbm_bytes_per_launch[{op}] = {value}" for op, value in results]
     req = dispatches(raw / "requests" / "requests_counter_collection.csv")
-    rwin, rcopy = op_window(req)
+    rwin, rcopy = op_window(req, launches)
 
     def request_bytes(c):
         return 32 * c["TCC_EA0_RDREQ_32B_sum"] + 64 * c["TCC_EA0_RDREQ_64B_sum"] + \
