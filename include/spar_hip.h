@@ -449,6 +449,23 @@ struct SparHipStatus spar_hip_launch_norm_backward(
     const void* mean, const void* denominator, uint64_t rows,
     uint64_t extent, int center, int dtype, int device);
 
+/* The same backward with the output gradient given as a product: dy[i] =
+ * output_gradient_scale[0] * output_gradient[i], output_gradient_scale one
+ * element of `dtype` in device memory, each product formed in the kernels
+ * with the single rounding (and operand order) of the multiply op.  This is
+ * the gradient a product y * c hands y when c needs no gradient and the
+ * product's own gradient is one value broadcast, as in loss = sum(y * c):
+ * the reference's autograd materialises dy with a multiply kernel
+ * (src/ops/elementwise.cpp:159-166, then K1 of cuda_kernels.cu) before the
+ * normalisation's backward reads it; here no dy is written.  Returns status
+ * 1 for a NULL scale with rows > 0. */
+struct SparHipStatus spar_hip_launch_norm_backward_scaled(
+    void* input_gradient, uint64_t input_gradient_stride, void* weight_gradient,
+    void* bias_gradient, const void* output_gradient, const void* output_gradient_scale,
+    const void* input, uint64_t input_row_stride, uint64_t input_column_stride,
+    const void* weight, const void* mean, const void* denominator, uint64_t rows,
+    uint64_t extent, int center, int dtype, int device);
+
 /* --------------------------------------------- cross entropy (log-softmax + NLL) */
 
 /* Sets *invalid_target (host memory) to 1 if any of `count` class indices

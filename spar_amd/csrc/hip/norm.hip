@@ -148,6 +148,27 @@ __device__ __forceinline__ void norm_store(T* row, const T (&y)[E], uint64_t n) 
   }
 }
 
+// An output gradient handed over as factor x one value (the gradient of a
+// product whose other operand needs none, fed a single value broadcast): dy
+// = value * factor for each present element, with the one rounding the
+// product op gives it and the value on the left as the product op has it;
+// absent (zero) elements stay zero.
+template <typename T, int THREADS, int E, bool VEC, bool FULL>
+__device__ __forceinline__ void norm_scale(T (&g)[E], T value, uint64_t n) {
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    if (FULL || norm_column<T, THREADS, VEC>(j) < n) g[j] = value * g[j];
+  }
+}
+
+template <typename T, typename V>
+__device__ __forceinline__ V scale_granule(T value, V v) {
+  V out;
+#pragma unroll
+  for (int k = 0; k < Vec16<T>::width; ++k) vec_set<T>(out, k, value * vec_get<T>(v, k));
+  return out;
+}
+
 // q / d for many q and one d: q0 = q * (1 / d) corrected by one residual
 // step through a fused multiply-add (Markstein), within one ulp of the IEEE
 // quotient and equal to it in almost all cases.
@@ -578,9 +599,12 @@ __global__ void __launch_bounds__(kApplyThreads)
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     norm_backward_kernel(T* dx, uint64_t dx_stride, T* partial_weight, T* partial_bias,
-                         const T* dy, const T* in, uint64_t in_stride, const T* weight,
-                         const T* mean, const T* denominator, uint64_t rows, uint64_t n) {
+                         const T* dy, const T* dy_scale, const T* in, uint64_t in_stride,
+                         const T* weight, const T* mean, const T* denominator, uint64_t rows,
+                         uint64_t n) {
   const T count = static_cast<T>(n);
+  const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
+  const T value = scaled ? *dy_scale : T(1);
   T acc_w[E];
   T acc_b[CENTER ? E : 1];
 #pragma unroll
@@ -594,6 +618,7 @@ __global__ void __launch_bounds__(THREADS)
     T g[E];
     norm_load<T, THREADS, E, VEC, FULL>(x, in + r * in_stride, n);
     norm_load<T, THREADS, E, VEC, FULL>(g, dy + r * n, n);
+    if (scaled) norm_scale<T, THREADS, E, VEC, FULL>(g, value, n);
     const T mu = CENTER ? mean[r] : T(0);
     const Divisor<T> divide(denominator[r]);
     T sum_g = T(0);
@@ -651,10 +676,12 @@ __global__ void __launch_bounds__(THREADS)
 template <typename T, int THREADS, int E, bool CENTER, bool VEC, bool FULL, bool NT>
 __global__ void __launch_bounds__(THREADS)
     norm_backward_pipelined_kernel(T* dx, uint64_t dx_stride, T* partial_weight,
-                                   T* partial_bias, const T* dy, const T* in, uint64_t in_stride,
-                                   const T* weight, const T* mean, const T* denominator,
-                                   uint64_t rows, uint64_t n) {
+                                   T* partial_bias, const T* dy, const T* dy_scale, const T* in,
+                                   uint64_t in_stride, const T* weight, const T* mean,
+                                   const T* denominator, uint64_t rows, uint64_t n) {
   const T count = static_cast<T>(n);
+  const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
+  const T value = scaled ? *dy_scale : T(1);
   T acc_w[E];
   T acc_b[CENTER ? E : 1];
   T w[E];
@@ -674,6 +701,7 @@ __global__ void __launch_bounds__(THREADS)
   if (r < rows) {
     norm_load<T, THREADS, E, VEC, FULL>(x, in + r * in_stride, n);
     norm_load<T, THREADS, E, VEC, FULL>(g, dy + r * n, n);
+    if (scaled) norm_scale<T, THREADS, E, VEC, FULL>(g, value, n);
   }
   for (; r < rows; r += gridDim.x) {
     const T mu = CENTER ? mean[r] : T(0);
@@ -696,6 +724,7 @@ __global__ void __launch_bounds__(THREADS)
     if (next < rows) {
       norm_load<T, THREADS, E, VEC, FULL>(next_x, in + next * in_stride, n);
       norm_load<T, THREADS, E, VEC, FULL>(next_g, dy + next * n, n);
+      if (scaled) norm_scale<T, THREADS, E, VEC, FULL>(next_g, value, n);
     }
     if constexpr (CENTER) {
       norm_block_sum2<T, THREADS>(sum_g, sum_gx);
@@ -845,7 +874,8 @@ constexpr int kWholeTiles = 2;
 template <typename T, bool CENTER, int MODE, bool CACHED>
 __global__ void __launch_bounds__(kApplyThreads)
     norm_backward_columns_sums_kernel(T* row_partial, T* partial_weight, T* partial_bias,
-                                      const T* dy, const T* in, uint64_t pitch, const T* weight,
+                                      const T* dy, const T* dy_scale, const T* in,
+                                      uint64_t pitch, const T* weight,
                                       const T* mean, const T* denominator, uint64_t rows,
                                       uint64_t n, uint32_t tiles_q, uint32_t splits,
                                       uint32_t split_tiles) {
@@ -899,6 +929,8 @@ __global__ void __launch_bounds__(kApplyThreads)
   const uint64_t lane_offset = static_cast<uint64_t>(threadIdx.x % G) * W +
                                static_cast<uint64_t>(threadIdx.x / G) * n;
   const uint64_t load_step = static_cast<uint64_t>(kApplyThreads / G) * n;
+  const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
+  const T value = scaled ? *dy_scale : T(1);
   V staged[kLoads];
   auto load_tile = [&](uint64_t q0) {
     if constexpr (VEC) {
@@ -914,7 +946,7 @@ __global__ void __launch_bounds__(kApplyThreads)
             WHOLE ||
             (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
         const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
-        staged[it] = present ? v : V{};
+        staged[it] = present ? (scaled ? scale_granule<T>(value, v) : v) : V{};
       }
     } else {
 #pragma unroll
@@ -926,7 +958,10 @@ __global__ void __launch_bounds__(kApplyThreads)
         if (pr < rows) {
 #pragma unroll
           for (int k = 0; k < W; ++k) {
-            if (q + k < n) vec_set<T>(v, k, dy[pr * n + q + k]);
+            if (q + k < n) {
+              const T element = dy[pr * n + q + k];
+              vec_set<T>(v, k, scaled ? value * element : element);
+            }
           }
         }
         staged[it] = v;
@@ -1123,8 +1158,8 @@ __global__ void __launch_bounds__(kCombineThreads)
 
 template <typename T, bool CENTER, int MODE, bool NT>
 __global__ void __launch_bounds__(kApplyThreads)
-    norm_backward_columns_apply_kernel(T* dx, uint64_t dx_stride, const T* dy, const T* in,
-                                       uint64_t pitch,
+    norm_backward_columns_apply_kernel(T* dx, uint64_t dx_stride, const T* dy,
+                                       const T* dy_scale, const T* in, uint64_t pitch,
                                        const T* weight, const T* mean, const T* denominator,
                                        const T* row_means, uint64_t rows, uint64_t n,
                                        FastDiv tiles_p, FastDiv tiles_q, uint32_t tile_count) {
@@ -1149,6 +1184,8 @@ __global__ void __launch_bounds__(kApplyThreads)
     p0 = static_cast<uint64_t>(tp) * TP;
     q0 = static_cast<uint64_t>(tq) * TQ;
   };
+  const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
+  const T value = scaled ? *dy_scale : T(1);
   V staged[kLoads];
   // Staged dy granules: q offset (lane % G) W, p offsets lane / G + it *
   // kApplyThreads / G.
@@ -1167,7 +1204,7 @@ __global__ void __launch_bounds__(kApplyThreads)
             WHOLE ||
             (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
         const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
-        staged[it] = present ? v : V{};
+        staged[it] = present ? (scaled ? scale_granule<T>(value, v) : v) : V{};
       }
     } else {
 #pragma unroll
@@ -1179,7 +1216,10 @@ __global__ void __launch_bounds__(kApplyThreads)
         if (p < rows) {
 #pragma unroll
           for (int k = 0; k < W; ++k) {
-            if (q + k < n) vec_set<T>(v, k, dy[p * n + q + k]);
+            if (q + k < n) {
+              const T element = dy[p * n + q + k];
+              vec_set<T>(v, k, scaled ? value * element : element);
+            }
           }
         }
         staged[it] = v;
@@ -1428,6 +1468,7 @@ struct NormBackwardArgs {
   void* dweight;
   void* dbias;
   const void* dy;
+  const void* dy_scale;  // null, or one element: dy = *dy_scale * dy[i]
   const void* input;
   uint64_t input_stride;
   const void* weight;
@@ -1475,6 +1516,7 @@ hipError_t backward_columns_as(const NormBackwardArgs& a, uint64_t pitch, int de
   T* partial_bias = CENTER ? partial_weight + tiles_p * a.n : nullptr;
   T* means = piece(partial_weight, column_partials * sizeof(T));
   const T* dy = static_cast<const T*>(a.dy);
+  const T* dy_scale = static_cast<const T*>(a.dy_scale);
   const T* in = static_cast<const T*>(a.input);
   const T* weight = static_cast<const T*>(a.weight);
   const T* mean = static_cast<const T*>(a.mean);
@@ -1483,13 +1525,15 @@ hipError_t backward_columns_as(const NormBackwardArgs& a, uint64_t pitch, int de
   if (a.rows * a.n * sizeof(T) <= kCacheReuseBytes) {
     norm_backward_columns_sums_kernel<T, CENTER, MODE, true>
         <<<sums_grid, kApplyThreads, 0, guard.stream>>>(
-            row_partial, partial_weight, partial_bias, dy, in, pitch, weight, mean, denominator,
+            row_partial, partial_weight, partial_bias, dy, dy_scale, in, pitch, weight, mean,
+            denominator,
             a.rows, a.n, static_cast<uint32_t>(tiles_q), static_cast<uint32_t>(splits),
             static_cast<uint32_t>(split_tiles));
   } else {
     norm_backward_columns_sums_kernel<T, CENTER, MODE, false>
         <<<sums_grid, kApplyThreads, 0, guard.stream>>>(
-            row_partial, partial_weight, partial_bias, dy, in, pitch, weight, mean, denominator,
+            row_partial, partial_weight, partial_bias, dy, dy_scale, in, pitch, weight, mean,
+            denominator,
             a.rows, a.n, static_cast<uint32_t>(tiles_q), static_cast<uint32_t>(splits),
             static_cast<uint32_t>(split_tiles));
   }
@@ -1512,8 +1556,8 @@ hipError_t backward_columns_as(const NormBackwardArgs& a, uint64_t pitch, int de
     uint64_t slots = resident_blocks(kernel, kApplyThreads, guard);
     if (slots == 0) slots = 2 * cus;
     kernel<<<static_cast<uint32_t>(tiles < slots ? tiles : slots), kApplyThreads, 0,
-             guard.stream>>>(static_cast<T*>(a.dx), a.dx_stride, dy, in, pitch, weight, mean,
-                             denominator, means, a.rows, a.n, divide_p, divide_q,
+             guard.stream>>>(static_cast<T*>(a.dx), a.dx_stride, dy, dy_scale, in, pitch,
+                             weight, mean, denominator, means, a.rows, a.n, divide_p, divide_q,
                              static_cast<uint32_t>(tiles));
   });
   error = hipGetLastError();
@@ -1561,7 +1605,7 @@ hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard&
   with_policy(stream, [&](auto nt) {
     kernel_for(nt)<<<static_cast<uint32_t>(grid), THREADS, 0, guard.stream>>>(
         static_cast<T*>(a.dx), a.dx_stride, partial_weight, partial_bias,
-        static_cast<const T*>(a.dy),
+        static_cast<const T*>(a.dy), static_cast<const T*>(a.dy_scale),
         static_cast<const T*>(a.input), a.input_stride, static_cast<const T*>(a.weight),
         static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n);
   });
@@ -1730,11 +1774,15 @@ extern "C" SparHipStatus spar_hip_launch_norm_forward(void* output, void* mean, 
   return finish(guard);
 }
 
-extern "C" SparHipStatus spar_hip_launch_norm_backward(
-    void* input_gradient, uint64_t input_gradient_stride, void* weight_gradient,
-    void* bias_gradient, const void* output_gradient, const void* input,
-    uint64_t input_row_stride, uint64_t input_column_stride, const void* weight, const void* mean,
-    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device) {
+namespace {
+
+SparHipStatus norm_backward(void* input_gradient, uint64_t input_gradient_stride,
+                            void* weight_gradient, void* bias_gradient,
+                            const void* output_gradient, const void* output_gradient_scale,
+                            const void* input, uint64_t input_row_stride,
+                            uint64_t input_column_stride, const void* weight, const void* mean,
+                            const void* denominator, uint64_t rows, uint64_t extent, int center,
+                            int dtype, int device) {
   // The forward's two layouts.  dx takes the input's layout: rows
   // input_gradient_stride apart (row layout), or dx[p + q * stride] (column
   // layout; stride == rows packs it).
@@ -1765,11 +1813,11 @@ extern "C" SparHipStatus spar_hip_launch_norm_backward(
     if (status.code == 0 && center) status = spar_hip_zero(bias_gradient, bytes, device);
     return status;
   }
-  const NormBackwardArgs a{input_gradient, input_gradient_stride, weight_gradient,
-                           bias_gradient,  output_gradient,       input,
-                           input_row_stride, weight,              mean,
-                           denominator,    rows,                  extent,
-                           center != 0};
+  const NormBackwardArgs a{input_gradient,   input_gradient_stride, weight_gradient,
+                           bias_gradient,    output_gradient,       output_gradient_scale,
+                           input,            input_row_stride,      weight,
+                           mean,             denominator,           rows,
+                           extent,           center != 0};
   if (column_layout) {
     const bool vec = aligned_rows(output_gradient, extent, width) && extent % width == 0 &&
                      aligned_rows(weight, extent, width) &&
@@ -1836,4 +1884,29 @@ extern "C" SparHipStatus spar_hip_launch_norm_backward(
   if (!handled) return invalid();
   if (error != hipSuccess) return runtime(error);
   return finish(guard);
+}
+
+}  // namespace
+
+extern "C" SparHipStatus spar_hip_launch_norm_backward(
+    void* input_gradient, uint64_t input_gradient_stride, void* weight_gradient,
+    void* bias_gradient, const void* output_gradient, const void* input,
+    uint64_t input_row_stride, uint64_t input_column_stride, const void* weight, const void* mean,
+    const void* denominator, uint64_t rows, uint64_t extent, int center, int dtype, int device) {
+  return norm_backward(input_gradient, input_gradient_stride, weight_gradient, bias_gradient,
+                       output_gradient, nullptr, input, input_row_stride, input_column_stride,
+                       weight, mean, denominator, rows, extent, center, dtype, device);
+}
+
+extern "C" SparHipStatus spar_hip_launch_norm_backward_scaled(
+    void* input_gradient, uint64_t input_gradient_stride, void* weight_gradient,
+    void* bias_gradient, const void* output_gradient, const void* output_gradient_scale,
+    const void* input, uint64_t input_row_stride, uint64_t input_column_stride,
+    const void* weight, const void* mean, const void* denominator, uint64_t rows,
+    uint64_t extent, int center, int dtype, int device) {
+  if (output_gradient_scale == nullptr && rows != 0) return invalid();
+  return norm_backward(input_gradient, input_gradient_stride, weight_gradient, bias_gradient,
+                       output_gradient, output_gradient_scale, input, input_row_stride,
+                       input_column_stride, weight, mean, denominator, rows, extent, center,
+                       dtype, device);
 }

@@ -252,10 +252,28 @@ struct PlacedBackward final {
   std::function<std::vector<Tensor>(const Tensor& gradient, const Tensor& destination)> rule;
 };
 
+/// A third form of a backward rule, for ops whose kernels can take their
+/// output gradient as a product factor x value, `value` a one-element tensor
+/// (the value of a gradient broadcast from one element): the rule forms each
+/// value * factor[i] itself, with the one rounding and the operand order of
+/// the multiply op, so its results are those of the plain rule on the
+/// materialised product.  `destination` is null, or the destination the
+/// engine offers as for PlacedBackward (accepted by its `accepts`).
+using ScaledBackward = std::function<std::vector<Tensor>(
+    const Tensor& factor, const Tensor& value, const Tensor* destination)>;
+
 void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
                       BackwardFunction backward);
 void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
                       BackwardFunction backward, PlacedBackward placed);
+/// Gives the operation recorded for `output` its scaled form.
+void set_scaled_backward(Tensor& output, ScaledBackward scaled);
+/// Marks the operation recorded for `output` as a product whose one tracked
+/// input's gradient is the output gradient times `factor` (the other
+/// operand, of the input's shape): when that gradient is one value broadcast
+/// and the input's producer has a scaled form, the engine hands that
+/// producer (factor, value) instead of running this operation's rule.
+void set_product_factor(Tensor& output, Tensor factor);
 void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward);
 [[nodiscard]] bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept;
 
@@ -263,9 +281,10 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
 /// gradients copied because their storage was shared, gradient
 /// accumulations done in place or out of place, narrows whose gradient was
 /// handed to the narrow below them unembedded (a chain of narrows is
-/// embedded once), and gradients a rule wrote straight into the gradient of
-/// a narrow chain's base (no embedding pass at all).  The engine never
-/// copies an intermediate gradient.
+/// embedded once), gradients a rule wrote straight into the gradient of
+/// a narrow chain's base (no embedding pass at all), and product gradients
+/// handed to a scaled rule as factor and value (no product pass).  The
+/// engine never copies an intermediate gradient.
 struct AutogradCounters final {
   std::uint64_t backward_calls;
   std::uint64_t leaf_copies;
@@ -273,6 +292,7 @@ struct AutogradCounters final {
   std::uint64_t out_of_place_adds;
   std::uint64_t window_fusions;
   std::uint64_t placed_gradients;
+  std::uint64_t scaled_gradients;
 };
 [[nodiscard]] AutogradCounters autograd_counters() noexcept;
 

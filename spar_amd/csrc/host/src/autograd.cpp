@@ -24,6 +24,14 @@
 //      that gradient straight into the box of a buffer shaped like the
 //      chain's base, its border zeroed; the buffer travels down the same
 //      chain and is delivered at the same turn, with the same values.
+//   6. A product whose one tracked input x receives value * factor (the
+//      output gradient is one value broadcast, the factor the other
+//      operand), where x's producer has a scaled form and this is the only
+//      gradient x receives, hands that producer (factor, value) at x's own
+//      turn; its kernels form value * factor[i] with the product's one
+//      rounding and operand order, so x's producer computes what it would
+//      from the materialised product, and every identity still receives its
+//      gradients in the same order.
 // Given identical contributions, the gradients are therefore identical to
 // the reference's.  The reference also cloned each contribution
 // (autograd.cpp:145, :244), which copied values into a dense tensor.  Here a
@@ -54,6 +62,7 @@ std::atomic<std::uint64_t> g_in_place_adds{0};
 std::atomic<std::uint64_t> g_out_of_place_adds{0};
 std::atomic<std::uint64_t> g_window_fusions{0};
 std::atomic<std::uint64_t> g_placed_gradients{0};
+std::atomic<std::uint64_t> g_scaled_gradients{0};
 
 GradInput input_of(const Tensor& parent) {
   return GradInput{TensorInternals::grad_state(parent), parent.shape(), parent.dtype(),
@@ -96,6 +105,23 @@ void record_operation(Tensor& output, std::vector<Tensor> requiring_parents,
   TensorInternals::grad_state(output)->producer->placed = std::move(placed);
 }
 
+void set_scaled_backward(Tensor& output, ScaledBackward scaled) {
+  const auto& state{TensorInternals::grad_state(output)};
+  if (state == nullptr || state->producer == nullptr) {
+    throw std::logic_error{"A scaled backward form needs a recorded operation"};
+  }
+  state->producer->scaled = std::move(scaled);
+}
+
+void set_product_factor(Tensor& output, Tensor factor) {
+  const auto& state{TensorInternals::grad_state(output)};
+  if (state == nullptr || state->producer == nullptr || state->producer->inputs.size() != 1) {
+    throw std::logic_error{"A product factor needs an operation with one tracked input"};
+  }
+  if (factor.requires_grad()) throw std::logic_error{"A product factor must be detached"};
+  state->producer->product_factor = std::move(factor);
+}
+
 void record_transfer_operation(Tensor& output, Tensor requiring_parent, BackwardFunction backward) {
   if (!requiring_parent.requires_grad()) {
     throw std::logic_error{"Cannot record a transfer from a non-requiring parent"};
@@ -113,7 +139,7 @@ void record_transfer_operation(Tensor& output, Tensor requiring_parent, Backward
 AutogradCounters autograd_counters() noexcept {
   return AutogradCounters{g_backward_calls.load(), g_leaf_copies.load(), g_in_place_adds.load(),
                           g_out_of_place_adds.load(), g_window_fusions.load(),
-                          g_placed_gradients.load()};
+                          g_placed_gradients.load(), g_scaled_gradients.load()};
 }
 
 bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept {
@@ -224,6 +250,16 @@ class Sweep final {
         continue;
       }
       if (!state.producer->window.empty() && narrow_chain(position, gradient, box)) continue;
+      if (scale_[position].has_value()) {
+        Tensor value{std::move(*scale_[position])};
+        scale_[position].reset();
+        propagate(*state.producer, std::move(gradient), &value);
+        continue;
+      }
+      if (state.producer->product_factor.has_value() &&
+          hand_scaled(*state.producer, gradient)) {
+        continue;
+      }
       propagate(*state.producer, std::move(gradient));
     }
   }
@@ -257,6 +293,7 @@ class Sweep final {
     pending_.resize(order_.size());
     deferred_.resize(order_.size());
     placed_.resize(order_.size());
+    scale_.resize(order_.size());
     incoming_.assign(order_.size(), 0);
     for (const GradState* state : order_) {
       if (state->producer == nullptr) continue;
@@ -329,6 +366,40 @@ class Sweep final {
     accumulate(order_[position]->producer->inputs.front(), std::move(buffer));
   }
 
+  // Contract, point 6: the product `function` (one tracked input x, whose
+  // gradient is `gradient` times the product factor) hands x's producer the
+  // factor and `gradient`'s one value when `gradient` is that value
+  // broadcast, the producer has a scaled form, and x receives nothing else.
+  // Returns false when the product's own rule should run instead.
+  bool hand_scaled(const GradFunction& function, const Tensor& gradient) {
+    const GradInput& input{function.inputs.front()};
+    const Tensor& factor{*function.product_factor};
+    const auto found{slot_.find(input.identity.get())};
+    if (found == slot_.end()) return false;
+    const std::size_t next{found->second};
+    const GradFunction* consumer{order_[next]->producer.get()};
+    if (consumer == nullptr || !consumer->scaled || incoming_[next] != 1 ||
+        pending_[next].has_value() || placed_[next].has_value() || !deferred_[next].empty() ||
+        !consumer->window.empty()) {
+      return false;
+    }
+    if (!gradient.device().is_hip() || gradient.numel() == 0 || gradient.shape() != input.shape ||
+        gradient.dtype() != input.dtype || gradient.device() != input.device ||
+        factor.shape() != input.shape || factor.dtype() != input.dtype ||
+        factor.device() != input.device || !factor.is_contiguous()) {
+      return false;
+    }
+    for (std::size_t k{0}; k < gradient.rank(); ++k) {
+      if (gradient.shape()[k] != 1 && gradient.strides()[k] != 0) return false;  // not one value
+    }
+    Tensor value{gradient.detach()};  // its first element, at the gradient's own offset
+    for (std::size_t k{0}; k < value.rank(); ++k) value = value.narrow(k, 0, 1);
+    pending_[next] = factor;
+    scale_[next] = std::move(value);
+    g_scaled_gradients.fetch_add(1, std::memory_order_relaxed);
+    return true;
+  }
+
   struct Placement {
     std::size_t slot;    // the first input's identity (the top narrow)
     Tensor buffer;       // the chain base's gradient, border zeroed
@@ -373,11 +444,16 @@ class Sweep final {
     return Placement{found->second, std::move(buffer), std::move(destination)};
   }
 
-  // Runs one operation's rule and hands each input its gradient.
-  void propagate(const GradFunction& function, Tensor gradient) {
+  // Runs one operation's rule and hands each input its gradient.  With
+  // `value`, `gradient` is the factor of a product gradient handed over by
+  // hand_scaled and the scaled form runs.
+  void propagate(const GradFunction& function, Tensor gradient, const Tensor* value = nullptr) {
     std::optional<Placement> placed{placement(function)};
-    std::vector<Tensor> contributions{placed ? function.placed.rule(gradient, placed->destination)
-                                             : function.rule(gradient)};
+    std::vector<Tensor> contributions{
+        value != nullptr
+            ? function.scaled(gradient, *value, placed ? &placed->destination : nullptr)
+        : placed ? function.placed.rule(gradient, placed->destination)
+                 : function.rule(gradient)};
     if (contributions.size() != function.inputs.size()) {
       throw std::logic_error{"Backward rule returned an incorrect number of gradients"};
     }
@@ -461,6 +537,9 @@ class Sweep final {
   // per identity: the gradient of its narrow chain's base, when a rule wrote
   // this identity's gradient into it (the pending gradient is then a view)
   std::vector<std::optional<Tensor>> placed_;
+  // per identity: the one value its pending gradient (then a product
+  // factor) is to be multiplied by, when a product handed it over scaled
+  std::vector<std::optional<Tensor>> scale_;
 };
 
 }  // namespace

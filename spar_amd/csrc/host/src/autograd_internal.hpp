@@ -46,6 +46,11 @@ struct GradFunction final {
   /// Optional: the rule's form that writes inputs[0]'s gradient into a
   /// destination the engine provides (empty functions when absent).
   PlacedBackward placed;
+  /// Optional: the rule's form that takes its gradient as factor x value.
+  ScaledBackward scaled;
+  /// Set for a product with one tracked input: the other operand, which
+  /// times the output gradient is that input's gradient.
+  std::optional<Tensor> product_factor;
 };
 
 struct GradState final {

@@ -181,28 +181,57 @@ struct SavedNorm {
 
 // The backward kernels with dx written at `dx` (rows `dx_stride` elements
 // apart in the row layout; element (p, q) at dx[p + q * dx_stride] in the
-// column layout); `dx_view` is the gradient handed to autograd for x.
-std::vector<Tensor> norm_backward(const SavedNorm& saved, const Tensor& gradient, void* dx,
-                                  std::size_t dx_stride, const Tensor& dx_view) {
+// column layout); `dx_view` is the gradient handed to autograd for x.  With
+// `scale` (one element), the output gradient is *scale * gradient, each
+// product formed in the kernels.
+std::vector<Tensor> norm_backward(const SavedNorm& saved, const Tensor& gradient,
+                                  const Tensor* scale, void* dx, std::size_t dx_stride,
+                                  const Tensor& dx_view) {
   const Tensor dy{gradient.is_contiguous() ? gradient.detach() : gradient.detach().contiguous()};
   Tensor dw{saved.weight_shape, saved.x.dtype(), saved.x.device()};
   std::optional<Tensor> db;
   if (saved.center) db.emplace(saved.weight_shape, saved.x.dtype(), saved.x.device());
-  hip::check(spar_hip_launch_norm_backward(
-                 dx, dx_stride, HipTensorAccess::mutable_data(dw),
-                 saved.center ? HipTensorAccess::mutable_data(*db) : nullptr,
-                 HipTensorAccess::data(dy), first_element(saved.x), saved.row_stride,
-                 saved.column_stride, HipTensorAccess::data(saved.w),
-                 saved.center ? HipTensorAccess::data(*saved.mean_rows) : nullptr,
-                 HipTensorAccess::data(saved.denominator), saved.rows, saved.extent,
-                 saved.center ? 1 : 0, hip::dtype_tag(saved.x.dtype()),
-                 saved.x.device().index()),
-             std::string{saved.name} + " backward", saved.x.device());
+  void* dbias{saved.center ? HipTensorAccess::mutable_data(*db) : nullptr};
+  const void* mean{saved.center ? HipTensorAccess::data(*saved.mean_rows) : nullptr};
+  const int dtype{hip::dtype_tag(saved.x.dtype())};
+  const SparHipStatus status{
+      scale == nullptr
+          ? spar_hip_launch_norm_backward(
+                dx, dx_stride, HipTensorAccess::mutable_data(dw), dbias, HipTensorAccess::data(dy),
+                first_element(saved.x), saved.row_stride, saved.column_stride,
+                HipTensorAccess::data(saved.w), mean, HipTensorAccess::data(saved.denominator),
+                saved.rows, saved.extent, saved.center ? 1 : 0, dtype, saved.x.device().index())
+          : spar_hip_launch_norm_backward_scaled(
+                dx, dx_stride, HipTensorAccess::mutable_data(dw), dbias, HipTensorAccess::data(dy),
+                first_element(*scale), first_element(saved.x), saved.row_stride,
+                saved.column_stride, HipTensorAccess::data(saved.w), mean,
+                HipTensorAccess::data(saved.denominator), saved.rows, saved.extent,
+                saved.center ? 1 : 0, dtype, saved.x.device().index())};
+  hip::check(status, std::string{saved.name} + " backward", saved.x.device());
   std::vector<Tensor> contributions;
   if (saved.grad_x) contributions.push_back(dx_view);
   if (saved.grad_w) contributions.push_back(dw);
   if (saved.grad_b) contributions.push_back(*db);
   return contributions;
+}
+
+// The backward rule in all its forms: dx into a fresh gradient (in x's
+// layout: packed columns for an input read in the column layout, so that
+// the gradient of a transposed view is the transpose of a contiguous block
+// passed on without a copy; contiguous for one read in rows), or into the
+// engine's `destination`; the output gradient `gradient`, or *scale *
+// gradient.
+std::vector<Tensor> norm_rule(const SavedNorm& saved, const Tensor& gradient, const Tensor* scale,
+                              const Tensor* destination) {
+  if (destination != nullptr) {
+    void* first{const_cast<void*>(first_element(*destination))};
+    return norm_backward(saved, gradient, scale, first, *uniform_row_stride(*destination),
+                         *destination);
+  }
+  const bool columns{saved.column_stride != 1};
+  PackedColumns dx{input_gradient(saved.x, columns)};
+  return norm_backward(saved, gradient, scale, HipTensorAccess::mutable_data(dx.storage),
+                       columns ? saved.rows : saved.extent, dx.view);
 }
 
 Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, double epsilon,
@@ -246,15 +275,14 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
         x.source.detach(), x.row_stride, x.column_stride, w.detach(), mean_rows, denominator,
         rows, extent, center, grad_x, grad_w, grad_b, weight.shape(), name})};
     detail::BackwardFunction rule{[saved](const Tensor& gradient) {
-      // An input read in the column layout gets its gradient in that layout,
-      // packed (the gradient of a transposed view is then the transpose of a
-      // contiguous block, passed on without a copy); one read in rows gets a
-      // contiguous gradient.
-      const bool columns{saved->column_stride != 1};
-      PackedColumns dx{input_gradient(saved->x, columns)};
-      return norm_backward(*saved, gradient, HipTensorAccess::mutable_data(dx.storage),
-                           columns ? saved->rows : saved->extent, dx.view);
+      return norm_rule(*saved, gradient, nullptr, nullptr);
     }};
+    // The output gradient of loss = sum(y * c) is c times one value: the
+    // kernels take (c, value) and form the products themselves.
+    detail::ScaledBackward scaled{
+        [saved](const Tensor& factor, const Tensor& value, const Tensor* destination) {
+          return norm_rule(*saved, factor, &value, destination);
+        }};
     if (!grad_x || x.column_stride != 1) {
       detail::record_operation(output, std::move(parents), std::move(rule));
     } else {
@@ -269,12 +297,11 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
                    uniform_row_stride(destination).has_value();
           },
           [saved](const Tensor& gradient, const Tensor& destination) {
-            void* first{const_cast<void*>(first_element(destination))};
-            return norm_backward(*saved, gradient, first, *uniform_row_stride(destination),
-                                 destination);
+            return norm_rule(*saved, gradient, nullptr, &destination);
           }};
       detail::record_operation(output, std::move(parents), std::move(rule), std::move(placed));
     }
+    detail::set_scaled_backward(output, std::move(scaled));
   }
   return output;
 }

@@ -232,6 +232,14 @@ Tensor multiply(const Tensor& a, const Tensor& b) {
           if (grad_b) contributions.push_back(multiply_then_reduce(gradient, *saved_a, shape_b));
           return contributions;
         });
+    // One tracked operand of the output's shape: its gradient is the output
+    // gradient times the other operand, with no reduction, which a scaled
+    // rule downstream can take as (other operand, value).
+    const Tensor& factor{grad_a ? b : a};
+    if (grad_a != grad_b && (grad_a ? shape_a : shape_b) == output_shape &&
+        factor.shape() == output_shape && factor.is_contiguous()) {
+      detail::set_product_factor(output, grad_a ? *saved_b : *saved_a);
+    }
   }
   return output;
 }

@@ -338,6 +338,7 @@ PYBIND11_MODULE(_spar, m) {
     d["out_of_place_adds"] = c.out_of_place_adds;
     d["window_fusions"] = c.window_fusions;
     d["placed_gradients"] = c.placed_gradients;
+    d["scaled_gradients"] = c.scaled_gradients;
     return d;
   });
 }

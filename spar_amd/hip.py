@@ -107,6 +107,8 @@ SIGNATURES = {
                                      _I],
     "spar_hip_launch_norm_backward": [_P, _U64, _P, _P, _P, _P, _U64, _U64, _P, _P, _P, _U64,
                                       _U64, _I, _I, _I],
+    "spar_hip_launch_norm_backward_scaled": [_P, _U64, _P, _P, _P, _P, _P, _U64, _U64, _P, _P,
+                                             _P, _U64, _U64, _I, _I, _I],
     "spar_hip_validate_targets": [ctypes.POINTER(ctypes.c_int32), _P, _U64, _U64, _I, _I],
     "spar_hip_launch_nll_forward": [_P, _P, _P, _U64, _U64, _U64, _I, _I, _I, _I],
     "spar_hip_launch_nll_backward": [_P, _P, _P, _U64, _U64, _U64, _I, _I, _I, _I],
