@@ -145,74 +145,62 @@ uint32_t scalar_grid(uint64_t count, const DeviceGuard& guard) {
   return static_cast<uint32_t>(blocks);
 }
 
-// GELU of contiguous float32 with the tail table in LDS (ops.hpp).  A
-// single-wave workgroup per tile would copy the 9 KiB table for every 2 KiB
-// tile, so this kernel runs one 512-lane workgroup per resident slot, each
-// copying the table once and then walking whole tiles of two 16-byte vectors
-// per lane, without bounds checks; the leftover vectors and elements come
-// after.  On 4096 x 4096 (steady state, MI355X): 33.0 us with the direct
-// double evaluation in the single-wave kernel, 24.6 us here; a plain copy
-// took 24.5 us in a persistent loop like this one and 22.0 us in the
-// single-wave kernel.
+// GELU of contiguous float32 with the tail table in LDS (ops.hpp): one
+// workgroup per chunk of kGeluVectors 16-byte vectors per lane.  A workgroup
+// issues its table reads, then its chunk's loads, copies the table to LDS
+// while the loads fly, and then computes and stores vector by vector; it
+// exits with its stores in flight.  The last chunk is partial (per-vector
+// bounds), and workgroup 0 also takes the count % 4 trailing elements.
+//
+// Inputs of kGeluChunkedFrom elements or more take this kernel; smaller ones
+// the persistent one below.  On [8192, 8192] the persistent grid-stride loop
+// measured worse: within its loop the compiler waits for all outstanding
+// vector memory operations (s_waitcnt vmcnt(0)), the previous tile's stores
+// included, at the top of each iteration, so a plain copy in that loop
+// reached 73% of HBM bandwidth against 80-81% for one chunk per workgroup,
+// and GELU 69-72% against 72-74% here.  On [4096, 4096] the chunks' table
+// copies (18 KiB per 32 KiB chunk) weigh more: 62% here against 68% for the
+// persistent loop, which copies the table once per workgroup.
 constexpr int kGeluThreads = 512;
-constexpr int kGeluVectors = 2;
-// The table's pieces sit 10 doubles (80 bytes) apart in LDS, not 8 as in
-// global memory: 16-byte reads of random pieces by the lanes of a wave then
-// start on 16 different groups of 4 banks instead of 4, fewer of them
-// collide.  With the next tile's loads issued before the current tile is
-// computed, long back-to-back runs over N(0, 1) inputs on 4096 x 4096 took
-// 26-28 us per launch against 28-31 us (the clock drops in such runs); short
-// bursts stay at 24.5 us either way.
-constexpr int kGeluLdsStride = 10;
+constexpr int kGeluVectors = 4;
+// The table's pieces keep their global layout in LDS, two 16-byte units
+// apart (18 KiB); padding them to three units measured no faster.
+constexpr int kGeluLdsStride = 2;
 
 template <bool NT>
 __global__ void __launch_bounds__(kGeluThreads)
     gelu_table_kernel(float* out, const float* in, uint64_t count) {
-  __shared__ double table[kGeluPieces * kGeluLdsStride];
-  for (int k = threadIdx.x; k < kGeluPieces * kGeluStride; k += kGeluThreads) {
-    table[(k / kGeluStride) * kGeluLdsStride + k % kGeluStride] = kGeluTable[k];
+  __shared__ f64x2 table[kGeluPieces * kGeluLdsStride];
+  const f64x2* units = reinterpret_cast<const f64x2*>(kGeluTable);  // two per piece
+  constexpr int kUnits = kGeluPieces * 2;
+  constexpr int kUnitsPerLane = (kUnits + kGeluThreads - 1) / kGeluThreads;
+  f64x2 staged[kUnitsPerLane];
+#pragma unroll
+  for (int j = 0; j < kUnitsPerLane; ++j) {
+    const int k = j * kGeluThreads + threadIdx.x;
+    staged[j] = units[k < kUnits ? k : 0];
   }
-  __syncthreads();
   const uint64_t vectors = count / 4;
-  constexpr uint64_t kTile = static_cast<uint64_t>(kGeluThreads) * kGeluVectors;
-  const uint64_t whole = vectors / kTile;
+  const uint64_t first = static_cast<uint64_t>(blockIdx.x) * kGeluThreads * kGeluVectors +
+                         threadIdx.x;
   const f32x4* src = reinterpret_cast<const f32x4*>(in);
   f32x4* dst = reinterpret_cast<f32x4*>(out);
   f32x4 r[kGeluVectors];
-  if (blockIdx.x < whole) {
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kTile + threadIdx.x;
 #pragma unroll
-    for (int u = 0; u < kGeluVectors; ++u) r[u] = stream_load(src + base + u * kGeluThreads);
+  for (int u = 0; u < kGeluVectors; ++u) {
+    const uint64_t i = first + static_cast<uint64_t>(u) * kGeluThreads;
+    r[u] = i < vectors ? stream_load(src + i) : f32x4{};
   }
-  for (uint64_t t = blockIdx.x; t < whole; t += gridDim.x) {
-    const uint64_t base = t * kTile + threadIdx.x;
-    const uint64_t next = t + gridDim.x;
-    // the next tile's loads fly while this tile is computed and stored
-    f32x4 ahead[kGeluVectors];
-    if (next < whole) {
 #pragma unroll
-      for (int u = 0; u < kGeluVectors; ++u) {
-        ahead[u] = stream_load(src + next * kTile + threadIdx.x + u * kGeluThreads);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kGeluVectors; ++u) {
-      f32x4 o;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = gelu_float<kGeluLdsStride>(r[u][k], table);
-      store_vector<NT>(dst + base + u * kGeluThreads, o);
-    }
-#pragma unroll
-    for (int u = 0; u < kGeluVectors; ++u) r[u] = ahead[u];
+  for (int j = 0; j < kUnitsPerLane; ++j) {
+    const int k = j * kGeluThreads + threadIdx.x;
+    if (k < kUnits) table[(k / 2) * kGeluLdsStride + k % 2] = staged[j];
   }
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kGeluThreads;
-  for (uint64_t i = whole * kTile + static_cast<uint64_t>(blockIdx.x) * kGeluThreads + threadIdx.x;
-       i < vectors; i += stride) {
-    const f32x4 r = src[i];
-    f32x4 o;
+  __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = gelu_float<kGeluLdsStride>(r[k], table);
-    dst[i] = o;
+  for (int u = 0; u < kGeluVectors; ++u) {
+    const uint64_t i = first + static_cast<uint64_t>(u) * kGeluThreads;
+    if (i < vectors) store_vector<NT>(dst + i, gelu_float4<kGeluLdsStride>(r[u], table));
   }
   if (blockIdx.x == 0) {
     const uint64_t i = vectors * 4 + threadIdx.x;
@@ -220,14 +208,78 @@ __global__ void __launch_bounds__(kGeluThreads)
   }
 }
 
+// The same GELU as one workgroup per resident slot, each copying the table
+// once and then walking whole tiles of two vectors per lane with the next
+// tile's loads in flight; leftover vectors and elements come after.  The
+// same operations on each element, so the same bits.
+constexpr int kGeluLoopVectors = 2;
+
+template <bool NT>
+__global__ void __launch_bounds__(kGeluThreads)
+    gelu_table_persistent_kernel(float* out, const float* in, uint64_t count) {
+  __shared__ f64x2 table[kGeluPieces * kGeluLdsStride];
+  const f64x2* units = reinterpret_cast<const f64x2*>(kGeluTable);
+  for (int k = threadIdx.x; k < kGeluPieces * 2; k += kGeluThreads) {
+    table[(k / 2) * kGeluLdsStride + k % 2] = units[k];
+  }
+  __syncthreads();
+  const uint64_t vectors = count / 4;
+  constexpr uint64_t kTile = static_cast<uint64_t>(kGeluThreads) * kGeluLoopVectors;
+  const uint64_t whole = vectors / kTile;
+  const f32x4* src = reinterpret_cast<const f32x4*>(in);
+  f32x4* dst = reinterpret_cast<f32x4*>(out);
+  f32x4 r[kGeluLoopVectors];
+  if (blockIdx.x < whole) {
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kTile + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kGeluLoopVectors; ++u) r[u] = stream_load(src + base + u * kGeluThreads);
+  }
+  for (uint64_t t = blockIdx.x; t < whole; t += gridDim.x) {
+    const uint64_t base = t * kTile + threadIdx.x;
+    const uint64_t next = t + gridDim.x;
+    f32x4 ahead[kGeluLoopVectors];
+    if (next < whole) {
+#pragma unroll
+      for (int u = 0; u < kGeluLoopVectors; ++u) {
+        ahead[u] = stream_load(src + next * kTile + threadIdx.x + u * kGeluThreads);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kGeluLoopVectors; ++u) {
+      store_vector<NT>(dst + base + u * kGeluThreads, gelu_float4<kGeluLdsStride>(r[u], table));
+    }
+#pragma unroll
+    for (int u = 0; u < kGeluLoopVectors; ++u) r[u] = ahead[u];
+  }
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kGeluThreads;
+  for (uint64_t i = whole * kTile + static_cast<uint64_t>(blockIdx.x) * kGeluThreads + threadIdx.x;
+       i < vectors; i += stride) {
+    dst[i] = gelu_float4<kGeluLdsStride>(src[i], table);
+  }
+  if (blockIdx.x == 0) {
+    const uint64_t i = vectors * 4 + threadIdx.x;
+    if (i < count) out[i] = gelu_float<kGeluLdsStride>(in[i], table);
+  }
+}
+
+constexpr uint64_t kGeluChunkedFrom = uint64_t{1} << 25;
+
 void launch_gelu_table(float* out, const float* in, uint64_t count, const DeviceGuard& guard) {
   with_policy(stream_output(count * sizeof(float)), [&](auto nt) {
-    const auto kernel = gelu_table_kernel<decltype(nt)::value>;
+    constexpr bool NT = decltype(nt)::value;
+    if (count >= kGeluChunkedFrom) {
+      constexpr uint64_t kChunk = static_cast<uint64_t>(kGeluThreads) * kGeluVectors;
+      const uint64_t chunks = (count / 4 + kChunk - 1) / kChunk;
+      gelu_table_kernel<NT><<<static_cast<uint32_t>(chunks), kGeluThreads, 0, guard.stream>>>(
+          out, in, count);
+      return;
+    }
+    const auto kernel = gelu_table_persistent_kernel<NT>;
     // Workgroups are independent: an unknown occupancy (0) takes two per CU.
     uint64_t slots = resident_blocks(kernel, kGeluThreads, guard);
     if (slots == 0) slots = static_cast<uint64_t>(guard.multiprocessors) * 2;
-    const uint64_t tiles = (count / 4 + kGeluThreads * kGeluVectors - 1) /
-                           (static_cast<uint64_t>(kGeluThreads) * kGeluVectors);
+    constexpr uint64_t kTile = static_cast<uint64_t>(kGeluThreads) * kGeluLoopVectors;
+    const uint64_t tiles = (count / 4 + kTile - 1) / kTile;
     const uint64_t grid = tiles == 0 ? 1 : tiles < slots ? tiles : slots;
     kernel<<<static_cast<uint32_t>(grid), kGeluThreads, 0, guard.stream>>>(out, in, count);
   });

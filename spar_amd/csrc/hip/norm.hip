@@ -800,6 +800,23 @@ __global__ void __launch_bounds__(kCombineThreads)
   }
 }
 
+// The weight and bias partials in one launch: groups [0, groups) of the
+// weight, then the bias's, each summed as norm_combine_kernel sums it.
+template <typename T>
+__global__ void __launch_bounds__(kCombineThreads)
+    norm_combine_pair_kernel(T* out_weight, const T* partial_weight, T* out_bias,
+                             const T* partial_bias, uint64_t parts, uint64_t n) {
+  __shared__ T lds[kCombineWaves][kWave];
+  const uint64_t groups = (n + kWave - 1) / kWave;
+  for (uint64_t group = blockIdx.x; group < 2 * groups; group += gridDim.x) {
+    if (group < groups) {
+      combine_group<T>(out_weight, partial_weight, parts, n, group, lds);
+    } else {
+      combine_group<T>(out_bias, partial_bias, parts, n, group - groups, lds);
+    }
+  }
+}
+
 // ------------------------------------- backward, rows down storage columns
 //
 // The backward over the forward's column layout, x[p][q] = in[p + q * pitch],
@@ -1609,12 +1626,14 @@ hipError_t backward_as(const NormBackwardArgs& a, int device, const DeviceGuard&
         static_cast<const T*>(a.input), a.input_stride, static_cast<const T*>(a.weight),
         static_cast<const T*>(a.mean), static_cast<const T*>(a.denominator), a.rows, a.n);
   });
-  const uint32_t combine_grid = grid_for((a.n + kWave - 1) / kWave);
-  norm_combine_kernel<T><<<combine_grid, kCombineThreads, 0, guard.stream>>>(
-      static_cast<T*>(a.dweight), partial_weight, grid, a.n);
+  const uint64_t groups = (a.n + kWave - 1) / kWave;
   if constexpr (CENTER) {
-    norm_combine_kernel<T><<<combine_grid, kCombineThreads, 0, guard.stream>>>(
-        static_cast<T*>(a.dbias), partial_bias, grid, a.n);
+    norm_combine_pair_kernel<T><<<grid_for(2 * groups), kCombineThreads, 0, guard.stream>>>(
+        static_cast<T*>(a.dweight), partial_weight, static_cast<T*>(a.dbias), partial_bias, grid,
+        a.n);
+  } else {
+    norm_combine_kernel<T><<<grid_for(groups), kCombineThreads, 0, guard.stream>>>(
+        static_cast<T*>(a.dweight), partial_weight, grid, a.n);
   }
   error = hipGetLastError();
   scratch_release(scratch, device);  // stream-ordered reuse

@@ -161,10 +161,11 @@ __device__ __forceinline__ double gelu_derivative_double(double x) {
 //
 // GELU reads Q(a) = 0.5 erfc(a / sqrt 2), 0 <= a <= 15, from a table of
 // piecewise polynomials (gelu_table.hpp, fit_gelu_table.py): the piece is
-// i = floor(g) for g = 2a + a^2/2, and a degree-6 polynomial in fract(g)
-// gives Q to 1.0e-8 relative, about 23 VALU instructions per element against
-// about 50 for an exp and a global polynomial.  The contiguous kernel holds
-// the table in LDS; other layouts read it from global memory.
+// i = floor(g) for g = 4 (2a + a^2/2), and with t = fract(g),
+// Q = scale (1 + t (c1 + t (d2 + t (d3 + t d4)))) to 9.9e-9 relative, the
+// d terms in float32 and the rest in double: about 21 VALU instructions and
+// 32 bytes of table per element.  The contiguous kernel holds the table in
+// LDS; other layouts read it from global memory.
 //
 // The derivative needs the density exp(-a^2/2) as well, and keeps the
 // direct evaluation: the normal upper tail Q(a) is exp(-a^2/2) * M(a) with
@@ -234,27 +235,75 @@ __device__ __forceinline__ NormalTail normal_tail(double a) {
 }
 
 // GELU of a float32 from the tail table at `table` (global memory or an LDS
-// copy: the same values, so the same bits), pieces STRIDE doubles apart.
-// With a = |x| clamped to 15 and q = Q(a), GELU is x - a q for x >= 0 and
-// -a q (that is x Q(|x|)) below 0: one fused multiply-add, -a q + base, with
-// base = x above 0 and x - x below (0 for a finite x, NaN for -inf, as
-// (0.5 x) erfc(-x / sqrt 2) is).  The clamp (exact at +-15) and base are
-// formed in float32, so only the table lookup, the Horner steps and that
-// multiply-add run in double.  No branches and no patched results: Q(15) =
-// 3.7e-51 already makes GELU round to -0 below -15 and to x above 15, +inf
-// stays +inf (inf - 15 Q(15)), NaN propagates through base, and -0 gives -0.
-template <int STRIDE = kGeluStride>
-__device__ __forceinline__ float gelu_float(float value, const double* table) {
+// copy: the same values, so the same bits), pieces STRIDE 16-byte units
+// apart: unit 0 holds (scale, c1) as doubles, unit 1 (d2, d3, d4, pad) as
+// floats.  With a = |x| clamped to 15 and q = Q(a), GELU is x - a q for
+// x >= 0 and -a q (that is x Q(|x|)) below 0: one fused multiply-add,
+// -a q + base, with base = x above 0 and x - x below (0 for a finite x, NaN
+// for -inf, as (0.5 x) erfc(-x / sqrt 2) is).  The clamp (exact at +-15) and
+// base are formed in float32, as is the polynomial's d part; the table
+// lookup, the last two Horner steps, the scaling and that multiply-add run in
+// double.  No branches and no patched results: Q(15) = 3.7e-51 already makes
+// GELU round to -0 below -15 and to x above 15, +inf stays +inf
+// (inf - 15 Q(15)), NaN propagates through base, and -0 gives -0.  Simulated
+// on the CPU over all 2^32 float32 inputs (fmaf, fma and conversions as the
+// GPU rounds them), every result is within 1 ulp of the double definition.
+static_assert(sizeof(GeluPiece) == 32, "a GELU piece is two 16-byte units");
+
+template <int STRIDE = 2>
+__device__ __forceinline__ float gelu_float(float value, const f64x2* table) {
   constexpr float kLimit = static_cast<float>(kGeluTailLimit);
-  const double a = __builtin_fabs(static_cast<double>(fminf(fmaxf(value, -kLimit), kLimit)));
-  const double g = a * __builtin_fma(kGeluBeta, a, kGeluAlpha);
-  const double* c = table + static_cast<int>(g) * STRIDE;
+  // median of three: a NaN gives NaN or a bound, either of which indexes a
+  // piece in range (v_cvt_i32_f64 maps NaN to 0), and base carries the NaN
+  const double a = __builtin_fabs(static_cast<double>(__builtin_amdgcn_fmed3f(value, -kLimit, kLimit)));
+  const double g = a * __builtin_fma(kGeluBeta, a, kGeluAlpha);  // 0 <= g <= 570
+  // piece index < 2^24: a full-rate 24-bit multiply, not the quarter-rate 32-bit one
+  const f64x2* piece = table + __umul24(static_cast<uint32_t>(static_cast<int>(g)), STRIDE);
+  const f64x2 high = piece[0];
+  const f32x4 low = *reinterpret_cast<const f32x4*>(piece + 1);
   const double t = __builtin_amdgcn_fract(g);
-  double q = c[kGeluDegree];
-#pragma unroll
-  for (int k = kGeluDegree - 1; k >= 0; --k) q = __builtin_fma(q, t, c[k]);
+  const float tf = static_cast<float>(t);
+  const float p = __builtin_fmaf(__builtin_fmaf(low[2], tf, low[1]), tf, low[0]);
+  const double q =
+      high[0] * __builtin_fma(__builtin_fma(static_cast<double>(p), t, high[1]), t, 1.0);
   const float base = value < 0.0f ? value - value : value;
   return static_cast<float>(__builtin_fma(-a, q, static_cast<double>(base)));
+}
+
+// gelu_float of four values with their piece reads issued together, so the
+// LDS latency is paid once per group rather than per element.  The same
+// operations on each value, so the same bits.
+template <int STRIDE = 2>
+__device__ __forceinline__ f32x4 gelu_float4(f32x4 value, const f64x2* table) {
+  constexpr float kLimit = static_cast<float>(kGeluTailLimit);
+  double a[4];
+  double g[4];
+  const f64x2* piece[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    a[k] = __builtin_fabs(static_cast<double>(__builtin_amdgcn_fmed3f(value[k], -kLimit, kLimit)));
+    g[k] = a[k] * __builtin_fma(kGeluBeta, a[k], kGeluAlpha);
+    piece[k] = table + __umul24(static_cast<uint32_t>(static_cast<int>(g[k])), STRIDE);
+  }
+  f64x2 high[4];
+  f32x4 low[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    high[k] = piece[k][0];
+    low[k] = *reinterpret_cast<const f32x4*>(piece[k] + 1);
+  }
+  f32x4 out;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const double t = __builtin_amdgcn_fract(g[k]);
+    const float tf = static_cast<float>(t);
+    const float p = __builtin_fmaf(__builtin_fmaf(low[k][2], tf, low[k][1]), tf, low[k][0]);
+    const double q =
+        high[k][0] * __builtin_fma(__builtin_fma(static_cast<double>(p), t, high[k][1]), t, 1.0);
+    const float base = value[k] < 0.0f ? value[k] - value[k] : value[k];
+    out[k] = static_cast<float>(__builtin_fma(-a[k], q, static_cast<double>(base)));
+  }
+  return out;
 }
 
 // The derivative: |x| is clamped to 15 and the results outside [-15, 15]
@@ -277,7 +326,9 @@ __device__ __forceinline__ float gelu_derivative_float(float value) {
 template <typename F> struct VectorsPerLane { static constexpr int value = 1; };
 
 struct GeluOp {
-  __device__ __forceinline__ float operator()(float x) const { return gelu_float(x, kGeluTable); }
+  __device__ __forceinline__ float operator()(float x) const {
+    return gelu_float(x, reinterpret_cast<const f64x2*>(kGeluTable));
+  }
   __device__ __forceinline__ double operator()(double x) const { return gelu_double(x); }
 };
 

@@ -136,6 +136,29 @@ def test_gelu_float32_sweep(hip):
     assert not bad.any(), f"gelu' sweep: {int(bad.sum())} outside the bound, e.g. x={x[finite][bad][:3]}"
 
 
+def test_gelu_chunked_kernel_sweep(hip):
+    """Contiguous float32 inputs of 2^25 elements or more take the one-chunk-
+    per-workgroup GELU kernel, smaller ones the persistent one.  Every 128th
+    float32 bit pattern (2^25 inputs, every exponent and both signs) plus a
+    ragged tail of 7 elements through the chunked kernel: within 1 ulp of the
+    double definition, and the same bits as the persistent kernel gives on
+    the first 2^24 + 3 of them."""
+    bits = (np.arange(1 << 25, dtype=np.uint64) * 128 + 45).astype(np.uint32)
+    x = np.concatenate([bits.view(F32), np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -15.0,
+                                                  15.0], F32)])
+    n = x.size
+    assert n >= 1 << 25 and n % 4 == 3
+    d = dev(hip, x)
+    out = out_buf(hip, (n,), F32)
+    hip.call("spar_hip_launch_unary", out.ptr, d.ptr, n, 0, hip.GELU, 0)
+    chunked = out.to_numpy(F32, (n,))
+    assert_ulp(chunked, ref.unary(x, "gelu"), 1, "gelu chunked sweep")
+    m = (1 << 24) + 3
+    small = out_buf(hip, (m,), F32)
+    hip.call("spar_hip_launch_unary", small.ptr, d.ptr, m, 0, hip.GELU, 0)
+    assert_bitexact(small.to_numpy(F32, (m,)), chunked[:m], "gelu persistent vs chunked")
+
+
 def test_exp_clipped_config_range(hip):
     # exp over N(0,1) clipped to [-10, 10], the elementwise benchmark input
     x = np.clip(np.random.default_rng(5).standard_normal(1 << 20), -10, 10).astype(F32)
