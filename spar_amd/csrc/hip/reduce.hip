@@ -371,6 +371,32 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// Short rows (n <= kNarrowRow): one lane per row, scanning its n elements in
+// index order with the exact rule, so a sum is the CPU loop's in-order sum
+// and a max / argmax keeps the first maximum and the first NaN.  The row
+// kernel would give every such row a whole workgroup and a block-wide
+// combine, about a microsecond per row whatever its length.
+constexpr uint64_t kNarrowRow = 32;
+
+template <typename T, Kind K, int NIN>
+__global__ void __launch_bounds__(kThreads)
+    narrow_row_kernel(const T* a, const T* b, uint64_t rows, uint64_t n, uint64_t stride,
+                      RowMap map, Sink<T> sink) {
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * kThreads;
+  for (uint64_t row = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; row < rows;
+       row += step) {
+    const uint64_t base = row_offset(map, row);
+    ScanAcc<T, K> scan;
+    scan.init();
+    for (uint64_t i = 0; i < n; ++i) {
+      scan.add(load_value<T, NIN>(a, b, base + i * stride), static_cast<uint32_t>(i));
+    }
+    Acc<T, K> acc = scan.finish(0);
+    if (n > 0) acc.seal(0);  // a row of only -inf: its first element
+    sink_write<T, K>(sink, row, acc, 0);
+  }
+}
+
 // Second pass after row splits: one block per output reduces its `parts`
 // consecutive partials with a fixed tree.
 template <typename T, Kind K>
@@ -1006,6 +1032,11 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     const uint64_t rows = plan.outputs;
     const uint64_t n = plan.red_extents[0];
     const RowMap map = make_row_map(plan, plan.kept_rank);
+    if (n <= kNarrowRow) {
+      narrow_row_kernel<T, K, NIN><<<grid_for((rows + kThreads - 1) / kThreads), kThreads, 0,
+                                     guard.stream>>>(a, b, rows, n, 1, map, final_sink());
+      return hipSuccess;
+    }
     bool vec = n % W == 0 && plan.offset % W == 0 && aligned16(a) && (NIN == 1 || aligned16(b));
     for (int k = 0; k < plan.kept_rank; ++k) {
       if (plan.kept_strides[k] % W != 0) vec = false;

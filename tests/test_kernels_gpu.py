@@ -549,6 +549,42 @@ def test_axis_reductions_3d(hip, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 2, 3, 7, 16, 32, 33])
+def test_short_row_reductions_exact(hip, dtype, n):
+    """Rows of at most 32 contiguous elements take one lane per row, scanning
+    in index order: sum, mean, max and argmax equal the oracle's in-order
+    loops bit for bit (rows of 33 take the workgroup kernel: sum and mean
+    within red(n)).  Rows hold NaNs, infinities, all -inf rows and ties; the
+    rows are read in place from a block of a wider tensor and from a
+    permuted view whose reduced axis is the contiguous one."""
+    rows = 5000
+    rng = np.random.default_rng(n)
+    wide = np.round(rng.standard_normal((rows, n + 5)) * 4).astype(dtype) / dtype(4)
+    wide[7, :] = -np.inf
+    wide[11, min(2, n - 1)] = np.nan
+    wide[13, 0] = np.inf
+    wide[17, n // 2] = np.nan
+    wide[17, n - 1] = np.inf
+    block = wide[:, 2:2 + n]
+    cube = np.ascontiguousarray(wide[: 4000].reshape(40, 100, n + 5)[:, :, :n])
+    views = [(wide, block, [1], "block"), (cube, cube.transpose(1, 0, 2), [2], "permuted")]
+    for base, view, axes, name in views:
+        what = f"short rows n={n} {name}"
+        s = ref.axis_sum(view, axes)
+        mean_ref = ref.scalar(s, "divide", float(n))
+        if n <= 32:
+            assert_bitexact(axis_reduce(hip, base, view, axes, "sum", dtype), s, what + " sum")
+            assert_bitexact(axis_reduce(hip, base, view, axes, "mean", dtype), mean_ref,
+                            what + " mean")
+        else:
+            norm = np.sqrt(ref.axis_sum((view.astype(np.float64) ** 2), axes))
+            assert_red(axis_reduce(hip, base, view, axes, "sum", dtype), s, n, norm, what)
+        mx, am = ref.axis_max(view, axes)
+        assert_bitexact(axis_reduce(hip, base, view, axes, "max", dtype), mx, what + " max")
+        assert_bitexact(axis_reduce(hip, base, view, axes, "argmax", dtype), am, what + " argmax")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("shape,axes", [((300, 2048), [0]), ((3, 200, 1100), [1]),
                                         ((2, 70, 4096), [0, 1]), ((5000, 1024), [0])])
 def test_column_reductions_wide_rows(hip, dtype, shape, axes):
