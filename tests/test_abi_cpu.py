@@ -87,8 +87,13 @@ def test_module_binding_compiles_and_calls_the_abi():
     module with spar_hip.h in its global module fragment, as Spar's backend
     modules include the CUDA header (src/backend/cuda_ops.cppm:1-5); build()
     compiles it with clang++ --precompile and links a consumer that imports
-    it.  The consumer calls launchers through the module: an empty launch
-    succeeds and an invalid dtype becomes std::invalid_argument."""
+    it.  The module wraps every in-scope function of the reference's
+    spar.cuda_ops (cuda_ops.cppm:33-65: binary, scalar, unary, reduction,
+    row_reduction, probability forward and backward, fill_from_device_scalar,
+    validate_targets, nll forward and backward, gradient_norm_summary,
+    scale_in_place, adamw_update); the consumer drives each through its
+    host-only paths: empty launches succeed, invalid arguments become
+    std::invalid_argument, the module's own checks std::logic_error."""
     import subprocess
 
     binary = ROOT / "spar_amd" / "lib" / "spar_hip_module_check"
@@ -96,3 +101,12 @@ def test_module_binding_compiles_and_calls_the_abi():
     run = subprocess.run([str(binary)], capture_output=True, text=True, timeout=60)
     assert run.returncode == 0, run.stdout + run.stderr
     assert "empty launch ok, invalid dtype rejected" in run.stdout
+    assert ", 0 failed;" in run.stdout
+    lines = [line for line in run.stdout.splitlines() if line.startswith(("ok", "FAIL"))]
+    assert lines and all(line.startswith("ok") for line in lines), run.stdout
+    wrappers = {line.split()[1].rstrip(",:") for line in lines}
+    assert wrappers == {"binary", "scalar", "unary", "reduction", "row_reduction",
+                        "probability_forward", "probability_backward",
+                        "fill_from_device_scalar", "validate_targets", "nll_forward",
+                        "nll_backward", "gradient_norm_summary", "scale_in_place",
+                        "adamw_update"}, wrappers
