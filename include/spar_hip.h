@@ -136,6 +136,12 @@ struct SparHipNormSummary {
  * spar::detail::cuda::validate_device, cuda_runtime.cppm:109-120). */
 struct SparHipStatus spar_hip_device_count(int* count);
 
+/* Compute units (CUs) of `device`, as the launchers size their grids and
+ * split their reductions (256 on MI355X).  A reduction's partial results,
+ * and so whether spar_hip_launch_axis_reduction_no_alloc can take it,
+ * depend on this count.  No reference counterpart. */
+struct SparHipStatus spar_hip_multiprocessor_count(int* count, int device);
+
 /* Caching device allocator: size-classed free lists over hipMalloc, reuse is
  * stream-ordered on the backend's single stream.  Replaces cuda::allocate /
  * cuda::deallocate (cuda_runtime.cppm:121-159).  bytes == 0 yields NULL. */

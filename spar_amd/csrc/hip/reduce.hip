@@ -947,15 +947,15 @@ uint32_t grid_for(uint64_t blocks) {
 // caching allocator supplies them for the duration of the launch; otherwise
 // they are carved from the caller's fixed region of `capacity` bytes (values
 // first, then 32-bit indices at the next 256-byte boundary), and a plan that
-// needs more is refused with kWorkspaceExceeded before anything is launched.
+// needs more is refused before anything is launched: run_plan sets
+// `exceeded` and returns hipErrorInvalidValue.  The flag, not the error
+// code, tells the caller it was the capacity check, so a real error from
+// the runtime is never reported as a refusal.
 struct Workspace {
   void* fixed = nullptr;
   uint64_t capacity = 0;
+  mutable bool exceeded = false;
 };
-
-// Returned by run_plan when the fixed workspace is too small; no kernel of
-// the reduction has been enqueued.
-constexpr hipError_t kWorkspaceExceeded = hipErrorOutOfMemory;
 
 uint64_t align256(uint64_t bytes) { return (bytes + 255) / 256 * 256; }
 
@@ -987,7 +987,10 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     if (workspace.fixed != nullptr) {
       const uint64_t value_bytes = align256(slots * sizeof(T));
       const uint64_t needed = value_bytes + (indexed ? slots * sizeof(uint32_t) : 0);
-      if (needed > workspace.capacity) return kWorkspaceExceeded;
+      if (needed > workspace.capacity) {
+        workspace.exceeded = true;  // nothing enqueued
+        return hipErrorInvalidValue;
+      }
       values = workspace.fixed;
       indices = indexed ? static_cast<unsigned char*>(workspace.fixed) + value_bytes : nullptr;
     } else {
@@ -1258,7 +1261,7 @@ SparHipStatus execute_with(const Plan& plan, const void* a, const void* b, int n
                 ? dispatch_plan<double, 1>(plan, a, b, output, operation, device, guard, workspace)
                 : dispatch_plan<double, 2>(plan, a, b, output, operation, device, guard, workspace);
   }
-  if (error == kWorkspaceExceeded && workspace.fixed != nullptr) {
+  if (workspace.exceeded) {
     return {SPAR_HIP_STATUS_WORKSPACE_EXCEEDED, static_cast<int>(hipErrorInvalidValue)};
   }
   if (error != hipSuccess) return runtime(error);

@@ -228,6 +228,14 @@ extern "C" SparHipStatus spar_hip_device_count(int* count) {
   return error == hipSuccess ? ok() : runtime(error);
 }
 
+extern "C" SparHipStatus spar_hip_multiprocessor_count(int* count, int device) {
+  if (count == nullptr) return invalid();
+  DeviceGuard guard;
+  if (enter(device, guard) != hipSuccess) return runtime(guard.error);
+  *count = guard.multiprocessors;
+  return ok();
+}
+
 extern "C" SparHipStatus spar_hip_allocate(void** pointer, uint64_t bytes, int device) {
   if (pointer == nullptr) return invalid();
   *pointer = nullptr;

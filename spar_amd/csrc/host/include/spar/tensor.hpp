@@ -240,15 +240,25 @@ void swap_storage_payloads(Tensor& original, Tensor& staged) noexcept;
 
 using BackwardFunction = std::function<std::vector<Tensor>(const Tensor&)>;
 
+/// The layout of a destination the engine would offer a placed rule: its
+/// shape, element strides, dtype and device, described before any storage
+/// for it exists.
+struct PlacedLayout final {
+  const Shape& shape;
+  std::span<const Shape::stride_type> strides;
+  DType dtype;
+  Device device;
+};
+
 /// A second form of a backward rule, for ops that can write their first
 /// parent's gradient into storage the engine provides: when that parent is a
 /// chain of narrowed views, the engine offers a view of the gradient of the
 /// chain's base (its border already zero) instead of embedding the gradient
 /// afterwards.  `accepts` says whether `rule` can write into a destination
-/// of that layout; `rule` then returns the contributions with the
-/// destination, written, in the first parent's place.
+/// of that layout, before the engine allocates it; `rule` then returns the
+/// contributions with the destination, written, in the first parent's place.
 struct PlacedBackward final {
-  std::function<bool(const Tensor& destination)> accepts;
+  std::function<bool(const PlacedLayout& destination)> accepts;
   std::function<std::vector<Tensor>(const Tensor& gradient, const Tensor& destination)> rule;
 };
 
@@ -295,5 +305,10 @@ struct AutogradCounters final {
   std::uint64_t scaled_gradients;
 };
 [[nodiscard]] AutogradCounters autograd_counters() noexcept;
+/// Process-wide: whether backward() hands gradients down narrow chains,
+/// writes them in place into a chain's base and hands products over as
+/// factor and value (on by default).  Off, every rule runs in its plain
+/// form; the gradients are the same bits either way, which tests check.
+void set_autograd_hand_overs(bool enabled) noexcept;
 
 }  // namespace spar::detail

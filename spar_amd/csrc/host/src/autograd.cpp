@@ -63,6 +63,10 @@ std::atomic<std::uint64_t> g_out_of_place_adds{0};
 std::atomic<std::uint64_t> g_window_fusions{0};
 std::atomic<std::uint64_t> g_placed_gradients{0};
 std::atomic<std::uint64_t> g_scaled_gradients{0};
+// Whether backward() may take the hand-overs of contract points 5 and 6
+// (narrow chains, placed gradients, scaled products); without them every
+// rule runs in its plain form, which the contract says gives the same bits.
+std::atomic<bool> g_hand_overs{true};
 
 GradInput input_of(const Tensor& parent) {
   return GradInput{TensorInternals::grad_state(parent), parent.shape(), parent.dtype(),
@@ -140,6 +144,10 @@ AutogradCounters autograd_counters() noexcept {
   return AutogradCounters{g_backward_calls.load(), g_leaf_copies.load(), g_in_place_adds.load(),
                           g_out_of_place_adds.load(), g_window_fusions.load(),
                           g_placed_gradients.load(), g_scaled_gradients.load()};
+}
+
+void set_autograd_hand_overs(bool enabled) noexcept {
+  g_hand_overs.store(enabled, std::memory_order_relaxed);
 }
 
 bool shares_autograd_identity(const Tensor& left, const Tensor& right) noexcept {
@@ -228,7 +236,10 @@ void zero_border(Tensor& buffer, const std::vector<WindowAxis>& box) {
 // The sweep state of one backward() call.
 class Sweep final {
  public:
-  explicit Sweep(GradState* loss) { order_from(loss); }
+  explicit Sweep(GradState* loss)
+      : hand_overs_{g_hand_overs.load(std::memory_order_relaxed)} {
+    order_from(loss);
+  }
 
   void run(GradState* loss, Tensor seed) {
     pending_[slot_.at(loss)] = std::move(seed);
@@ -250,13 +261,14 @@ class Sweep final {
         continue;
       }
       if (!state.producer->window.empty() && narrow_chain(position, gradient, box)) continue;
+      // (with the hand-overs off no box, placed buffer or scale is ever set)
       if (scale_[position].has_value()) {
         Tensor value{std::move(*scale_[position])};
         scale_[position].reset();
         propagate(*state.producer, std::move(gradient), &value);
         continue;
       }
-      if (state.producer->product_factor.has_value() &&
+      if (hand_overs_ && state.producer->product_factor.has_value() &&
           hand_scaled(*state.producer, gradient)) {
         continue;
       }
@@ -337,7 +349,7 @@ class Sweep final {
       composed[k].length = box[k].length;
     }
     if (slot_.find(input.identity.get()) == slot_.end()) return true;  // no longer tracked
-    const auto next{chain_parent(position)};
+    const auto next{hand_overs_ ? chain_parent(position) : std::nullopt};
     if (next && gradient.device().is_hip() && gradient.is_contiguous()) {
       pending_[*next] = std::move(gradient);
       deferred_[*next] = std::move(composed);
@@ -412,7 +424,8 @@ class Sweep final {
   // base's shape.  The buffer of that shape is made here, its border zeroed
   // once the rule accepts the box's layout.
   std::optional<Placement> placement(const GradFunction& function) {
-    if (!function.placed.rule || !function.placed.accepts || function.inputs.empty()) {
+    if (!hand_overs_ || !function.placed.rule || !function.placed.accepts ||
+        function.inputs.empty()) {
       return std::nullopt;
     }
     const GradInput& input{function.inputs.front()};
@@ -434,12 +447,25 @@ class Sweep final {
       box = std::move(composed);
       position = *next;
     }
-    Tensor buffer{order_[position]->producer->inputs.front().shape, input.dtype, input.device};
+    // The box of a contiguous buffer shaped like the chain's base: the box's
+    // lengths with the base's contiguous strides.  The rule judges that
+    // layout before the buffer is allocated.
+    const Shape& base_shape{order_[position]->producer->inputs.front().shape};
+    const std::vector<Shape::stride_type> base_strides{base_shape.contiguous_strides()};
+    std::vector<Shape::dimension_type> lengths;
+    for (const WindowAxis& axis : box) {
+      lengths.push_back(static_cast<Shape::dimension_type>(axis.length));
+    }
+    const Shape box_shape{std::move(lengths)};
+    if (box_shape.numel() == 0 ||
+        !function.placed.accepts(PlacedLayout{box_shape, base_strides, input.dtype, input.device})) {
+      return std::nullopt;
+    }
+    Tensor buffer{base_shape, input.dtype, input.device};
     Tensor destination{buffer};
     for (std::size_t k{0}; k < box.size(); ++k) {
       destination = destination.narrow(k, box[k].start, box[k].length);
     }
-    if (destination.numel() == 0 || !function.placed.accepts(destination)) return std::nullopt;
     zero_border(buffer, box);
     return Placement{found->second, std::move(buffer), std::move(destination)};
   }
@@ -527,6 +553,7 @@ class Sweep final {
 
   static constexpr std::size_t kUnplaced = static_cast<std::size_t>(-1);
 
+  bool hand_overs_;
   std::vector<GradState*> order_;
   std::unordered_map<const GradState*, std::size_t> slot_;
   std::vector<std::optional<Tensor>> pending_;

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <memory>
 #include <optional>
+#include <span>
 #include <stdexcept>
 #include <string>
 
@@ -77,25 +78,30 @@ struct Rows {
   std::size_t column_stride;  // elements between neighbours in a row
 };
 
-std::optional<std::size_t> uniform_row_stride(const Tensor& input) {
-  const std::size_t rank{input.rank()};
-  if (input.strides()[rank - 1] != 1 && input.shape()[rank - 1] != 1) return std::nullopt;
+std::optional<std::size_t> uniform_row_stride(const Shape& shape,
+                                              std::span<const Shape::stride_type> strides) {
+  const std::size_t rank{shape.rank()};
+  if (strides[rank - 1] != 1 && shape[rank - 1] != 1) return std::nullopt;
   std::optional<std::size_t> stride;
   std::size_t inner_rows{1};  // rows spanned by the axes inside the current one
   for (std::size_t axis{rank - 1}; axis-- > 0;) {
-    const auto extent{static_cast<std::size_t>(input.shape()[axis])};
+    const auto extent{static_cast<std::size_t>(shape[axis])};
     if (extent == 1) continue;
     if (!stride) {
-      stride = input.strides()[axis];
-    } else if (input.strides()[axis] != *stride * inner_rows) {
+      stride = strides[axis];
+    } else if (strides[axis] != *stride * inner_rows) {
       return std::nullopt;
     }
     inner_rows *= extent;
   }
-  const auto extent{static_cast<std::size_t>(input.shape()[rank - 1])};
+  const auto extent{static_cast<std::size_t>(shape[rank - 1])};
   if (!stride) return extent;  // one row
   if (*stride < extent) return std::nullopt;
   return stride;
+}
+
+std::optional<std::size_t> uniform_row_stride(const Tensor& input) {
+  return uniform_row_stride(input.shape(), input.strides());
 }
 
 std::optional<std::size_t> column_stride_of(const Tensor& input) {
@@ -290,11 +296,11 @@ Tensor fused(const Tensor& input, const Tensor& weight, const Tensor* bias, doub
       // block of a wider gradient whose rows are a uniform stride apart (the
       // gradient of a narrowed view's base).
       detail::PlacedBackward placed{
-          [saved](const Tensor& destination) {
-            return destination.device() == saved->x.device() &&
-                   destination.dtype() == saved->x.dtype() &&
-                   destination.shape() == saved->x.shape() &&
-                   uniform_row_stride(destination).has_value();
+          [saved](const detail::PlacedLayout& destination) {
+            return destination.device == saved->x.device() &&
+                   destination.dtype == saved->x.dtype() &&
+                   destination.shape == saved->x.shape() &&
+                   uniform_row_stride(destination.shape, destination.strides).has_value();
           },
           [saved](const Tensor& gradient, const Tensor& destination) {
             return norm_rule(*saved, gradient, nullptr, &destination);

@@ -329,6 +329,7 @@ PYBIND11_MODULE(_spar, m) {
   });
   m.def("synchronize", &spar::synchronize, py::arg("device") = Device::hip(0));
   m.def("hip_device_count", &spar::hip_device_count);
+  m.def("set_autograd_hand_overs", &spar::detail::set_autograd_hand_overs, py::arg("enabled"));
   m.def("autograd_counters", [] {
     const auto c = spar::detail::autograd_counters();
     py::dict d;

@@ -66,6 +66,7 @@ _U64P = ctypes.POINTER(ctypes.c_uint64)
 # norm_max_extent)
 SIGNATURES = {
     "spar_hip_device_count": [ctypes.POINTER(ctypes.c_int)],
+    "spar_hip_multiprocessor_count": [ctypes.POINTER(ctypes.c_int), _I],
     "spar_hip_allocate": [ctypes.POINTER(ctypes.c_void_p), _U64, _I],
     "spar_hip_deallocate": [_P, _I],
     "spar_hip_empty_cache": [_I],
@@ -172,6 +173,12 @@ def u64_array(values) -> ctypes.Array:
 
 def dtype_tag(dtype) -> int:
     return _DTYPE_TAGS[np.dtype(dtype)]
+
+
+def multiprocessor_count(device: int = 0) -> int:
+    count = ctypes.c_int(0)
+    call("spar_hip_multiprocessor_count", ctypes.byref(count), device)
+    return count.value
 
 
 def device_count() -> int:

@@ -109,17 +109,24 @@ def test_no_alloc_layouts(hip, op):
 
 
 def test_no_alloc_refuses_plans_beyond_the_workspace(hip):
-    # float32 argmax over axis 0 of [32, 255*4096]: 255 column blocks of 4096
-    # on 256 CUs split the 32 rows in two, so the partials take
-    # 2 * 1,044,480 * (4 + 4) = 16,711,680 bytes > 8 MiB.  The call must
-    # return SPAR_HIP_STATUS_WORKSPACE_EXCEEDED and enqueue nothing.
-    cols = 255 * 4096
+    # float32 argmax over axis 0 of [32, (cus - 1) * 4096]: cus - 1 column
+    # blocks of 4096 columns, one short of one block per CU, so the planner
+    # splits the 32 rows in two, and the partials take 2 * cols values and
+    # 2 * cols 32-bit indices (values rounded up to 256 bytes).  With more
+    # than 128 CUs that exceeds the workspace, and the call must return
+    # SPAR_HIP_STATUS_WORKSPACE_EXCEEDED and enqueue nothing.
+    cus = hip.multiprocessor_count(0)
+    cols = (cus - 1) * 4096
     rows = 32
+    partial_bytes = -(-2 * cols * 4 // 256) * 256 + 2 * cols * 4
+    if partial_bytes <= WORKSPACE_BYTES:
+        pytest.skip(f"{cus} CUs: a [32, {cols}] argmax's partials fit the workspace")
+    # MI355X: 256 CUs, 16,711,680 bytes of partials against 8 MiB
     x = normal(hip, rows * cols, 35, np.float32)
     out = hip.DeviceBuffer(cols * 8)
     sentinel = np.full(cols, -7, np.int64)
     hip.call("spar_hip_copy_host_to_device", out.ptr, sentinel.ctypes.data, sentinel.nbytes, 0)
-    say("no_alloc ARGMAX [32, 1044480] axis 0 (expected refusal)")
+    say(f"no_alloc ARGMAX [32, {cols}] axis 0 (expected refusal)")
     status = hip.status_of("spar_hip_launch_axis_reduction_no_alloc", out.ptr, x.ptr, 2,
                            hip.u64_array([rows, cols]), hip.u64_array([cols, 1]), 0, 1,
                            hip.FLOAT32, hip.ARGMAX, 0)
