@@ -701,13 +701,15 @@ __global__ void __launch_bounds__(THREADS)
   if (r < rows) {
     norm_load<T, THREADS, E, VEC, FULL>(x, in + r * in_stride, n);
     norm_load<T, THREADS, E, VEC, FULL>(g, dy + r * n, n);
-    if (scaled) norm_scale<T, THREADS, E, VEC, FULL>(g, value, n);
   }
   for (; r < rows; r += gridDim.x) {
     const T mu = CENTER ? mean[r] : T(0);
     const Divisor<T> divide(denominator[r]);
     T sum_g = T(0);
     T sum_gx = T(0);
+    // The scale is applied here, where the row is consumed: applied when
+    // the next row's loads are issued it would wait for them at once.
+    if (scaled) norm_scale<T, THREADS, E, VEC, FULL>(g, value, n);
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       const bool in_row = FULL || norm_column<T, THREADS, VEC>(j) < n;
@@ -724,7 +726,6 @@ __global__ void __launch_bounds__(THREADS)
     if (next < rows) {
       norm_load<T, THREADS, E, VEC, FULL>(next_x, in + next * in_stride, n);
       norm_load<T, THREADS, E, VEC, FULL>(next_g, dy + next * n, n);
-      if (scaled) norm_scale<T, THREADS, E, VEC, FULL>(next_g, value, n);
     }
     if constexpr (CENTER) {
       norm_block_sum2<T, THREADS>(sum_g, sum_gx);
@@ -948,6 +949,13 @@ __global__ void __launch_bounds__(kApplyThreads)
   const uint64_t load_step = static_cast<uint64_t>(kApplyThreads / G) * n;
   const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
   const T value = scaled ? *dy_scale : T(1);
+  // Staged granules stay as loaded; the scale is applied when they go to
+  // LDS, where the loads have to be waited for anyway (applied at load time
+  // it would wait for the next tile's loads at once).  Bit `it` of
+  // staged_present marks a granule that exists (absent ones hold zero and
+  // must stay zero whatever the scale).
+  static_assert(kLoads <= 32, "presence bits");
+  uint32_t staged_present = 0;
   V staged[kLoads];
   auto load_tile = [&](uint64_t q0) {
     if constexpr (VEC) {
@@ -957,13 +965,15 @@ __global__ void __launch_bounds__(kApplyThreads)
       const T* at = dy + p0 * n + q0 + lane_offset;
       const bool q_present = q0 + static_cast<uint64_t>(threadIdx.x % G) * W < n;
       const uint64_t first_p = p0 + threadIdx.x / G;
+      staged_present = 0;
 #pragma unroll
       for (int it = 0; it < kLoads; ++it) {
         const bool present =
             WHOLE ||
             (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
         const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
-        staged[it] = present ? (scaled ? scale_granule<T>(value, v) : v) : V{};
+        staged[it] = present ? v : V{};
+        staged_present |= present ? 1U << it : 0U;
       }
     } else {
 #pragma unroll
@@ -997,7 +1007,9 @@ __global__ void __launch_bounds__(kApplyThreads)
     for (int it = 0; it < kLoads; ++it) {
       const int index = it * kApplyThreads + threadIdx.x;
       const int row = index / G;
-      lds[row][(index % G) ^ ((row / W) & 7)] = staged[it];
+      V v = staged[it];
+      if (VEC && scaled && ((staged_present >> it) & 1U)) v = scale_granule<T>(value, v);
+      lds[row][(index % G) ^ ((row / W) & 7)] = v;
     }
     // the tile's weight, one granule per lane of the first TQ / W
     if (threadIdx.x < TQ / W) {
@@ -1203,6 +1215,13 @@ __global__ void __launch_bounds__(kApplyThreads)
   };
   const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
   const T value = scaled ? *dy_scale : T(1);
+  // Staged granules stay as loaded; the scale is applied when they go to
+  // LDS, where the loads have to be waited for anyway (applied at load time
+  // it would wait for the next tile's loads at once).  Bit `it` of
+  // staged_present marks a granule that exists (absent ones hold zero and
+  // must stay zero whatever the scale).
+  static_assert(kLoads <= 32, "presence bits");
+  uint32_t staged_present = 0;
   V staged[kLoads];
   // Staged dy granules: q offset (lane % G) W, p offsets lane / G + it *
   // kApplyThreads / G.
@@ -1215,13 +1234,15 @@ __global__ void __launch_bounds__(kApplyThreads)
       const T* at = dy + p0 * n + q0 + lane_offset;
       const bool q_present = q0 + static_cast<uint64_t>(threadIdx.x % G) * W < n;
       const uint64_t first_p = p0 + threadIdx.x / G;
+      staged_present = 0;
 #pragma unroll
       for (int it = 0; it < kLoads; ++it) {
         const bool present =
             WHOLE ||
             (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
         const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
-        staged[it] = present ? (scaled ? scale_granule<T>(value, v) : v) : V{};
+        staged[it] = present ? v : V{};
+        staged_present |= present ? 1U << it : 0U;
       }
     } else {
 #pragma unroll
@@ -1260,7 +1281,9 @@ __global__ void __launch_bounds__(kApplyThreads)
     for (int it = 0; it < kLoads; ++it) {
       const int index = it * kApplyThreads + threadIdx.x;
       const int row = index / G;
-      lds[row][(index % G) ^ ((row / W) & 7)] = staged[it];
+      V v = staged[it];
+      if (VEC && scaled && ((staged_present >> it) & 1U)) v = scale_granule<T>(value, v);
+      lds[row][(index % G) ^ ((row / W) & 7)] = v;
     }
     __syncthreads();
     // This tile's x, weight and row statistics, issued before the next
