@@ -145,24 +145,25 @@ uint32_t scalar_grid(uint64_t count, const DeviceGuard& guard) {
   return static_cast<uint32_t>(blocks);
 }
 
-// GELU of contiguous float32 with the tail table in LDS (ops.hpp): one
-// workgroup per chunk of kGeluVectors 16-byte vectors per lane.  A workgroup
-// issues its table reads, then its chunk's loads, copies the table to LDS
-// while the loads fly, and then computes and stores vector by vector; it
-// exits with its stores in flight.  The last chunk is partial (per-vector
-// bounds), and workgroup 0 also takes the count % 4 trailing elements.
-//
-// Inputs of kGeluChunkedFrom elements or more take this kernel; smaller ones
-// the persistent one below.  On [8192, 8192] the persistent grid-stride loop
-// measured worse: within its loop the compiler waits for all outstanding
-// vector memory operations (s_waitcnt vmcnt(0)), the previous tile's stores
-// included, at the top of each iteration, so a plain copy in that loop
-// reached 73% of HBM bandwidth against 80-81% for one chunk per workgroup,
-// and GELU 69-72% against 72-74% here.  On [4096, 4096] the chunks' table
-// copies (18 KiB per 32 KiB chunk) weigh more: 62% here against 68% for the
-// persistent loop, which copies the table once per workgroup.
+// GELU of contiguous float32 with the tail table in LDS (ops.hpp).  One
+// 512-lane workgroup per CU copies the table to LDS once and walks tiles of
+// kGeluLoopVectors 16-byte vectors per lane, t = blockIdx.x, + gridDim.x, ...
+// with two register sets used in turn: the loads of tile t + gridDim.x are
+// issued before tile t is computed and stored, and no register is copied from
+// one set to the other.  A loop that moved the prefetched set into the
+// working set at the end of each iteration made the wave wait for those
+// loads there, so the prefetch overlapped nothing: on [8192, 8192] N(0,1)
+// that loop measured 73.1% of HBM bandwidth and a single-chunk-per-workgroup
+// form (which copies the table per 32 KiB chunk) 73.2%; this one 75.1-76.1%,
+// on [4096, 4096] 63.8% (chunks) against 69.9%.  A prefetch past the last
+// whole tile reads the last whole tile again (every path issues the same
+// loads, so the compiler's wait counts stay exact); it is not stored.
+// Leftover vectors and the count % 4 trailing elements come after the loop.
+// On the same inputs a plain copy in this loop reaches 78.5% and in
+// single-wave workgroups 83%: the LDS table is what keeps GELU in the loop
+// (read from global memory instead, GELU took 150 us on [8192, 8192]).
 constexpr int kGeluThreads = 512;
-constexpr int kGeluVectors = 4;
+constexpr int kGeluLoopVectors = 2;
 // The table's pieces keep their global layout in LDS, two 16-byte units
 // apart (18 KiB); padding them to three units measured no faster.
 constexpr int kGeluLdsStride = 2;
@@ -172,116 +173,67 @@ __global__ void __launch_bounds__(kGeluThreads)
     gelu_table_kernel(float* out, const float* in, uint64_t count) {
   __shared__ f64x2 table[kGeluPieces * kGeluLdsStride];
   const f64x2* units = reinterpret_cast<const f64x2*>(kGeluTable);  // two per piece
-  constexpr int kUnits = kGeluPieces * 2;
-  constexpr int kUnitsPerLane = (kUnits + kGeluThreads - 1) / kGeluThreads;
-  f64x2 staged[kUnitsPerLane];
-#pragma unroll
-  for (int j = 0; j < kUnitsPerLane; ++j) {
-    const int k = j * kGeluThreads + threadIdx.x;
-    staged[j] = units[k < kUnits ? k : 0];
-  }
-  const uint64_t vectors = count / 4;
-  const uint64_t first = static_cast<uint64_t>(blockIdx.x) * kGeluThreads * kGeluVectors +
-                         threadIdx.x;
-  const f32x4* src = reinterpret_cast<const f32x4*>(in);
-  f32x4* dst = reinterpret_cast<f32x4*>(out);
-  f32x4 r[kGeluVectors];
-#pragma unroll
-  for (int u = 0; u < kGeluVectors; ++u) {
-    const uint64_t i = first + static_cast<uint64_t>(u) * kGeluThreads;
-    r[u] = i < vectors ? stream_load(src + i) : f32x4{};
-  }
-#pragma unroll
-  for (int j = 0; j < kUnitsPerLane; ++j) {
-    const int k = j * kGeluThreads + threadIdx.x;
-    if (k < kUnits) table[(k / 2) * kGeluLdsStride + k % 2] = staged[j];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int u = 0; u < kGeluVectors; ++u) {
-    const uint64_t i = first + static_cast<uint64_t>(u) * kGeluThreads;
-    if (i < vectors) store_vector<NT>(dst + i, gelu_float4<kGeluLdsStride>(r[u], table));
-  }
-  if (blockIdx.x == 0) {
-    const uint64_t i = vectors * 4 + threadIdx.x;
-    if (i < count) out[i] = gelu_float<kGeluLdsStride>(in[i], table);
-  }
-}
-
-// The same GELU as one workgroup per resident slot, each copying the table
-// once and then walking whole tiles of two vectors per lane with the next
-// tile's loads in flight; leftover vectors and elements come after.  The
-// same operations on each element, so the same bits.
-constexpr int kGeluLoopVectors = 2;
-
-template <bool NT>
-__global__ void __launch_bounds__(kGeluThreads)
-    gelu_table_persistent_kernel(float* out, const float* in, uint64_t count) {
-  __shared__ f64x2 table[kGeluPieces * kGeluLdsStride];
-  const f64x2* units = reinterpret_cast<const f64x2*>(kGeluTable);
   for (int k = threadIdx.x; k < kGeluPieces * 2; k += kGeluThreads) {
     table[(k / 2) * kGeluLdsStride + k % 2] = units[k];
   }
-  __syncthreads();
   const uint64_t vectors = count / 4;
   constexpr uint64_t kTile = static_cast<uint64_t>(kGeluThreads) * kGeluLoopVectors;
   const uint64_t whole = vectors / kTile;
-  const f32x4* src = reinterpret_cast<const f32x4*>(in);
-  f32x4* dst = reinterpret_cast<f32x4*>(out);
-  f32x4 r[kGeluLoopVectors];
-  if (blockIdx.x < whole) {
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kTile + threadIdx.x;
+  const f32x4* src = reinterpret_cast<const f32x4*>(in) + threadIdx.x;
+  f32x4* dst = reinterpret_cast<f32x4*>(out) + threadIdx.x;
+  f32x4 a[kGeluLoopVectors];
+  f32x4 b[kGeluLoopVectors];
+  auto load = [&](f32x4(&r)[kGeluLoopVectors], uint64_t tile) {
+    const f32x4* at = src + (tile < whole ? tile : whole - 1) * kTile;
 #pragma unroll
-    for (int u = 0; u < kGeluLoopVectors; ++u) r[u] = stream_load(src + base + u * kGeluThreads);
-  }
-  for (uint64_t t = blockIdx.x; t < whole; t += gridDim.x) {
-    const uint64_t base = t * kTile + threadIdx.x;
-    const uint64_t next = t + gridDim.x;
-    f32x4 ahead[kGeluLoopVectors];
-    if (next < whole) {
-#pragma unroll
-      for (int u = 0; u < kGeluLoopVectors; ++u) {
-        ahead[u] = stream_load(src + next * kTile + threadIdx.x + u * kGeluThreads);
-      }
-    }
+    for (int u = 0; u < kGeluLoopVectors; ++u) r[u] = stream_load(at + u * kGeluThreads);
+  };
+  auto emit = [&](const f32x4(&r)[kGeluLoopVectors], uint64_t tile) {
+    f32x4* at = dst + tile * kTile;
 #pragma unroll
     for (int u = 0; u < kGeluLoopVectors; ++u) {
-      store_vector<NT>(dst + base + u * kGeluThreads, gelu_float4<kGeluLdsStride>(r[u], table));
+      store_vector<NT>(at + u * kGeluThreads, gelu_float4<kGeluLdsStride>(r[u], table));
     }
-#pragma unroll
-    for (int u = 0; u < kGeluLoopVectors; ++u) r[u] = ahead[u];
+  };
+  uint64_t t = blockIdx.x;
+  if (t < whole) load(a, t);  // uniform over the workgroup
+  __syncthreads();            // the table is in LDS
+  if (t < whole) {
+    while (true) {
+      const uint64_t t1 = t + gridDim.x;
+      load(b, t1);
+      emit(a, t);
+      if (t1 >= whole) break;
+      const uint64_t t2 = t1 + gridDim.x;
+      load(a, t2);
+      emit(b, t1);
+      if (t2 >= whole) break;
+      t = t2;
+    }
   }
+  const f32x4* rest = reinterpret_cast<const f32x4*>(in);
+  f32x4* rest_out = reinterpret_cast<f32x4*>(out);
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kGeluThreads;
   for (uint64_t i = whole * kTile + static_cast<uint64_t>(blockIdx.x) * kGeluThreads + threadIdx.x;
        i < vectors; i += stride) {
-    dst[i] = gelu_float4<kGeluLdsStride>(src[i], table);
+    rest_out[i] = gelu_float4<kGeluLdsStride>(rest[i], table);
   }
   if (blockIdx.x == 0) {
     const uint64_t i = vectors * 4 + threadIdx.x;
     if (i < count) out[i] = gelu_float<kGeluLdsStride>(in[i], table);
   }
 }
-
-constexpr uint64_t kGeluChunkedFrom = uint64_t{1} << 25;
 
 void launch_gelu_table(float* out, const float* in, uint64_t count, const DeviceGuard& guard) {
   with_policy(stream_output(count * sizeof(float)), [&](auto nt) {
     constexpr bool NT = decltype(nt)::value;
-    if (count >= kGeluChunkedFrom) {
-      constexpr uint64_t kChunk = static_cast<uint64_t>(kGeluThreads) * kGeluVectors;
-      const uint64_t chunks = (count / 4 + kChunk - 1) / kChunk;
-      gelu_table_kernel<NT><<<static_cast<uint32_t>(chunks), kGeluThreads, 0, guard.stream>>>(
-          out, in, count);
-      return;
-    }
-    const auto kernel = gelu_table_persistent_kernel<NT>;
-    // Workgroups are independent: an unknown occupancy (0) takes two per CU.
-    uint64_t slots = resident_blocks(kernel, kGeluThreads, guard);
-    if (slots == 0) slots = static_cast<uint64_t>(guard.multiprocessors) * 2;
+    // one workgroup per CU (two or four per CU measured 1-3% slower)
     constexpr uint64_t kTile = static_cast<uint64_t>(kGeluThreads) * kGeluLoopVectors;
     const uint64_t tiles = (count / 4 + kTile - 1) / kTile;
+    const uint64_t slots = static_cast<uint64_t>(guard.multiprocessors);
     const uint64_t grid = tiles == 0 ? 1 : tiles < slots ? tiles : slots;
-    kernel<<<static_cast<uint32_t>(grid), kGeluThreads, 0, guard.stream>>>(out, in, count);
+    gelu_table_kernel<NT><<<static_cast<uint32_t>(grid), kGeluThreads, 0, guard.stream>>>(
+        out, in, count);
   });
 }
 

@@ -136,13 +136,12 @@ def test_gelu_float32_sweep(hip):
     assert not bad.any(), f"gelu' sweep: {int(bad.sum())} outside the bound, e.g. x={x[finite][bad][:3]}"
 
 
-def test_gelu_chunked_kernel_sweep(hip):
-    """Contiguous float32 inputs of 2^25 elements or more take the one-chunk-
-    per-workgroup GELU kernel, smaller ones the persistent one.  Every 128th
-    float32 bit pattern (2^25 inputs, every exponent and both signs) plus a
-    ragged tail of 7 elements through the chunked kernel: within 1 ulp of the
-    double definition, and the same bits as the persistent kernel gives on
-    the first 2^24 + 3 of them."""
+def test_gelu_large_sweep(hip):
+    """Every 128th float32 bit pattern (2^25 inputs, every exponent and both
+    signs) plus a ragged tail of 7 elements through the contiguous GELU kernel
+    (32 tiles per workgroup, then the leftover vectors and elements): within 1
+    ulp of the double definition, and the same bits as a call on the first
+    2^24 + 3 of them, whose tiles and leftovers fall elsewhere."""
     bits = (np.arange(1 << 25, dtype=np.uint64) * 128 + 45).astype(np.uint32)
     x = np.concatenate([bits.view(F32), np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -15.0,
                                                   15.0], F32)])
@@ -151,12 +150,12 @@ def test_gelu_chunked_kernel_sweep(hip):
     d = dev(hip, x)
     out = out_buf(hip, (n,), F32)
     hip.call("spar_hip_launch_unary", out.ptr, d.ptr, n, 0, hip.GELU, 0)
-    chunked = out.to_numpy(F32, (n,))
-    assert_ulp(chunked, ref.unary(x, "gelu"), 1, "gelu chunked sweep")
+    full = out.to_numpy(F32, (n,))
+    assert_ulp(full, ref.unary(x, "gelu"), 1, "gelu large sweep")
     m = (1 << 24) + 3
     small = out_buf(hip, (m,), F32)
     hip.call("spar_hip_launch_unary", small.ptr, d.ptr, m, 0, hip.GELU, 0)
-    assert_bitexact(small.to_numpy(F32, (m,)), chunked[:m], "gelu persistent vs chunked")
+    assert_bitexact(small.to_numpy(F32, (m,)), full[:m], "gelu shorter call")
 
 
 def test_exp_clipped_config_range(hip):
@@ -180,7 +179,8 @@ def test_unaligned_pointers_take_scalar_path(hip):
     assert_bitexact(got, ref.binary(a[1:], b[1:], "add"), "unaligned add")
 
 
-@pytest.mark.parametrize("n", [1, 3, 1027, 4099, 2 * 512 * 2 * 4 + 13, 1 << 20])
+@pytest.mark.parametrize("n", [1, 3, 1027, 4099, 2 * 512 * 2 * 4 + 13, 1 << 20, 257 * 4096 + 3,
+                               3 * 256 * 4096 + 23])
 def test_gelu_layouts_agree(hip, n):
     """GELU float32 reads its tail table from LDS in the contiguous kernel
     (whole tiles, leftover vectors, leftover elements) and from global memory
