@@ -829,13 +829,13 @@ __global__ void __launch_bounds__(kCombineThreads)
 // dx:
 //
 //  1. norm_backward_columns_sums_kernel.  Tiles of 32 W values of p by 32 W
-//     values of q in the transposed frame: dy goes through LDS (XOR swizzle,
-//     the next tile's dy in flight while the current one is used) and x is
-//     read along p, before that prefetch.  A workgroup owns one p tile and a
-//     run of q tiles (a split of q); each lane keeps one granule of W rows
-//     for the run and the sums of g = dy * w and g * xhat over its columns,
-//     which at the end the 8 lanes of each granule add (two per wave by a
-//     lane exchange, then the waves in order through LDS).  Per block of W
+//     values of q in the transposed frame: dy goes through LDS (XOR swizzle)
+//     and x is read along p; the next tile's x, dy and weight are in flight
+//     while the current tile is used.  A workgroup owns one p tile and a run
+//     of q tiles (a split of q); each lane keeps one granule of W rows for
+//     the run and the sums of g = dy * w and g * xhat over its columns, which
+//     at the end the lanes of each granule add (two per wave by a lane
+//     exchange, then the waves in order through LDS).  Per block of W
 //     columns the lane's partials of dy * xhat and dy over its rows are
 //     added across the 32 lanes of its half wave (the tile's p) by a
 //     butterfly.  Results: [2, splits, rows] row sums and [tiles_p, n]
@@ -853,6 +853,10 @@ __global__ void __launch_bounds__(kCombineThreads)
 // the sums pass reads x with cached loads and the apply pass finds it there.
 // lanes that share one p granule (and take every kBackwardGroups-th q granule)
 constexpr int kBackwardGroups = kApplyThreads / kApplyGranules;
+// Lanes of a sums-pass workgroup: at 512 a lane's share of a 128 x 128
+// float32 tile (8 dy granules, 2 blocks of x) leaves room for a second x set,
+// so every tile's x is loaded one tile ahead.
+constexpr int kSumsThreads = 512;
 
 // Butterfly reduce-scatter over the 32 lanes of a half wave: on entry each
 // lane holds NV values (NV divides 32), on exit lane c holds in v[0] the sum
@@ -889,8 +893,8 @@ constexpr int kScalarTiles = 0;
 constexpr int kVectorTiles = 1;
 constexpr int kWholeTiles = 2;
 
-template <typename T, bool CENTER, int MODE, bool CACHED>
-__global__ void __launch_bounds__(kApplyThreads)
+template <typename T, bool CENTER, int MODE, bool CACHED, int THREADS>
+__global__ void __launch_bounds__(THREADS)
     norm_backward_columns_sums_kernel(T* row_partial, T* partial_weight, T* partial_bias,
                                       const T* dy, const T* dy_scale, const T* in,
                                       uint64_t pitch, const T* weight,
@@ -904,12 +908,12 @@ __global__ void __launch_bounds__(kApplyThreads)
   constexpr int G = kApplyGranules;
   constexpr int TP = G * W;
   constexpr int TQ = G * W;
-  constexpr int kLoads = TP * G / kApplyThreads;             // dy granules staged per lane
-  constexpr int kBlocks = (TP / W) * G / kApplyThreads;      // W x W blocks per lane
-  constexpr int kGroups = kBackwardGroups;
-  constexpr int kValues = W * 2;                              // column partials per block
-  constexpr int kWaves = kApplyThreads / kWave;
-  static_assert(kApplyThreads % G == 0 && kGroups * (TP / W) == kApplyThreads, "lane layout");
+  constexpr int kLoads = TP * G / THREADS;             // dy granules staged per lane
+  constexpr int kBlocks = (TP / W) * G / THREADS;      // W x W blocks per lane
+  constexpr int kGroups = THREADS / G;                 // lanes that share one p granule
+  constexpr int kValues = W * 2;                       // column partials per block
+  constexpr int kWaves = THREADS / kWave;
+  static_assert(THREADS % G == 0 && kGroups * (TP / W) == THREADS, "lane layout");
   static_assert(TP / W == 32 && 32 % kValues == 0, "half-wave reduce-scatter");
   static_assert(kWaves * (TP / W) * 2 * W * sizeof(T) <= sizeof(V) * TP * G, "row sums fit");
   __shared__ V lds[TP][G];
@@ -943,10 +947,10 @@ __global__ void __launch_bounds__(kApplyThreads)
     sum_gx[i] = T(0);
   }
   // Staged dy granules: q offset (lane % G) W, p offsets lane / G + it *
-  // kApplyThreads / G.
+  // THREADS / G.
   const uint64_t lane_offset = static_cast<uint64_t>(threadIdx.x % G) * W +
                                static_cast<uint64_t>(threadIdx.x / G) * n;
-  const uint64_t load_step = static_cast<uint64_t>(kApplyThreads / G) * n;
+  const uint64_t load_step = static_cast<uint64_t>(THREADS / G) * n;
   const bool scaled = dy_scale != nullptr;  // dy = *dy_scale * factor
   const T value = scaled ? *dy_scale : T(1);
   // Staged granules stay as loaded; the scale is applied when they go to
@@ -970,7 +974,7 @@ __global__ void __launch_bounds__(kApplyThreads)
       for (int it = 0; it < kLoads; ++it) {
         const bool present =
             WHOLE ||
-            (q_present && first_p + static_cast<uint64_t>(it) * (kApplyThreads / G) < rows);
+            (q_present && first_p + static_cast<uint64_t>(it) * (THREADS / G) < rows);
         const V v = stream_load(reinterpret_cast<const V*>(present ? at + it * load_step : dy));
         staged[it] = present ? v : V{};
         staged_present |= present ? 1U << it : 0U;
@@ -978,7 +982,7 @@ __global__ void __launch_bounds__(kApplyThreads)
     } else {
 #pragma unroll
       for (int it = 0; it < kLoads; ++it) {
-        const int index = it * kApplyThreads + threadIdx.x;
+        const int index = it * THREADS + threadIdx.x;
         const uint64_t pr = p0 + index / G;
         const uint64_t q = q0 + static_cast<uint64_t>(index % G) * W;
         V v{};
@@ -997,126 +1001,165 @@ __global__ void __launch_bounds__(kApplyThreads)
   };
   // The run starts at a tile rotated by the p tile, so that workgroups side
   // by side read different q.
-  uint32_t offset = tp % run;
-  load_tile(static_cast<uint64_t>(first_tile + offset) * TQ);
-  for (uint32_t step = 0; step < run; ++step) {
-    const uint64_t q0 = static_cast<uint64_t>(first_tile + offset) * TQ;
-    offset = offset + 1 == run ? 0 : offset + 1;
+  const uint32_t start = tp % run;
+  auto tile_q0 = [&](uint32_t step) {
+    const uint32_t o = start + step < run ? start + step : start + step - run;
+    return static_cast<uint64_t>(first_tile + o) * TQ;
+  };
+  // The tile's weight, staged in a register like dy and written to LDS with
+  // it by the first TQ / W lanes.  Every lane loads granule lane % (TQ / W)
+  // (vector tiles: unconditionally, absent granules from the first element
+  // and zeroed), so no wave branches around the load.
+  V staged_weight{};
+  auto load_weight = [&](uint64_t q0) {
+    const uint64_t q = q0 + static_cast<uint64_t>(threadIdx.x % (TQ / W)) * W;
+    if constexpr (VEC) {
+      const bool present = WHOLE || q < n;
+      const V wv = *reinterpret_cast<const V*>(present ? weight + q : weight);
+      staged_weight = present ? wv : V{};
+    } else {
+      V wv{};
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        if (q + k < n) vec_set<T>(wv, k, weight[q + k]);
+      }
+      staged_weight = wv;
+    }
+  };
+  // x of the tile at q0: [block][q offset], W values of p each
+  auto load_x = [&](V(&x)[kBlocks][W], uint64_t q0) {
+    const uint64_t first_q = q0 + static_cast<uint64_t>(g0) * W;
+      if constexpr (VEC) {
+        const T* at = in + p + first_q * pitch;
+  #pragma unroll
+        for (int it = 0; it < kBlocks; ++it) {
+          const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
+          const bool present = WHOLE || (p < rows && q < n);
+  #pragma unroll
+          for (int k = 0; k < W; ++k) {
+            const V* source = reinterpret_cast<const V*>(
+                present ? at + (static_cast<uint64_t>(it) * kGroups * W + k) * pitch : in);
+            const V v = CACHED ? *source : stream_load(source);
+            x[it][k] = present ? v : V{};
+          }
+        }
+      } else {
+  #pragma unroll
+        for (int it = 0; it < kBlocks; ++it) {
+          const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
+  #pragma unroll
+          for (int k = 0; k < W; ++k) {
+            x[it][k] = q + k < n ? load_column_group<T, false>(in, p, q + k, pitch, rows) : V{};
+          }
+        }
+      }
+  };
+  // One tile: dy (staged) and the weight to LDS, then (PREFETCH) the next
+  // tile's x, dy and weight issued, then this tile's sums from x (loaded one
+  // tile ago) and LDS.  Two x register sets are used in turn (x, x_next), so
+  // no register is copied between tiles: a copy would make the wave wait for
+  // the next tile's loads right after issuing them.  The prefetch is a
+  // compile-time choice, the last tile's body being the only one without:
+  // behind a run-time test the compiler counts the loads of the path that
+  // skips it, and the sums would wait for the next tile's first loads.
+  auto body = [&](V(&x)[kBlocks][W], V(&x_next)[kBlocks][W], uint32_t step, auto prefetch) {
+    const uint64_t q0 = tile_q0(step);
     __syncthreads();  // the previous tile's LDS readers are done
 #pragma unroll
     for (int it = 0; it < kLoads; ++it) {
-      const int index = it * kApplyThreads + threadIdx.x;
+      const int index = it * THREADS + threadIdx.x;
       const int row = index / G;
       V v = staged[it];
       if (VEC && scaled && ((staged_present >> it) & 1U)) v = scale_granule<T>(value, v);
       lds[row][(index % G) ^ ((row / W) & 7)] = v;
     }
-    // the tile's weight, one granule per lane of the first TQ / W
-    if (threadIdx.x < TQ / W) {
-      const uint64_t q = q0 + static_cast<uint64_t>(threadIdx.x) * W;
-      V wv{};
-      if constexpr (VEC) {
-        if (WHOLE || q < n) wv = *reinterpret_cast<const V*>(weight + q);
-      } else {
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-          if (q + k < n) vec_set<T>(wv, k, weight[q + k]);
-        }
-      }
-      tile_weight[threadIdx.x] = wv;
-    }
+    if (threadIdx.x < TQ / W) tile_weight[threadIdx.x] = staged_weight;
     __syncthreads();
-    // This tile's x, issued before the next tile's dy loads (the wait counter
-    // retires vector loads in issue order).
+    if constexpr (decltype(prefetch)::value) {
+      const uint64_t next_q0 = tile_q0(step + 1);
+      load_x(x_next, next_q0);
+      load_tile(next_q0);
+      load_weight(next_q0);
+    }
     const uint64_t first_q = q0 + static_cast<uint64_t>(g0) * W;
-    V x[kBlocks][W];  // [block][q offset], W values of p each
-    if constexpr (VEC) {
-      const T* at = in + p + first_q * pitch;
-#pragma unroll
+      // Column partials, block by block: value k * 2 + s is the sum over the
+      // lane's W rows of dy * xhat (s = 0) or dy (s = 1) at q row k of the
+      // block, then over the 32 lanes of the half wave (the tile's p), after
+      // which lane c holds value c / (32 / kValues).  Absent rows and columns
+      // hold zero dy and add nothing.
+  #pragma unroll
       for (int it = 0; it < kBlocks; ++it) {
-        const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
-        const bool present = WHOLE || (p < rows && q < n);
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-          const V* source = reinterpret_cast<const V*>(
-              present ? at + (static_cast<uint64_t>(it) * kGroups * W + k) * pitch : in);
-          const V v = CACHED ? *source : stream_load(source);
-          x[it][k] = present ? v : V{};
-        }
-      }
-    } else {
-#pragma unroll
-      for (int it = 0; it < kBlocks; ++it) {
-        const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-          x[it][k] = q + k < n ? load_column_group<T, false>(in, p, q + k, pitch, rows) : V{};
-        }
-      }
-    }
-    if (step + 1 < run) load_tile(static_cast<uint64_t>(first_tile + offset) * TQ);
-    // Column partials, block by block: value k * 2 + s is the sum over the
-    // lane's W rows of dy * xhat (s = 0) or dy (s = 1) at q row k of the
-    // block, then over the 32 lanes of the half wave (the tile's p), after
-    // which lane c holds value c / (32 / kValues).  Absent rows and columns
-    // hold zero dy and add nothing.
-#pragma unroll
-    for (int it = 0; it < kBlocks; ++it) {
-      const int g = g0 + it * kGroups;
-      T grad[W][W];  // [p offset][q offset]
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        const V block = lds[c * W + i][g ^ (c & 7)];
-#pragma unroll
-        for (int k = 0; k < W; ++k) grad[i][k] = vec_get<T>(block, k);
-      }
-      const V wv = tile_weight[g];  // zero past the last column
-      T column[kValues];
-      T block_g[W];
-      T block_gx[W];
-#pragma unroll
-      for (int k = 0; k < W; ++k) {
-        T dw = T(0);
-        T db = T(0);
-#pragma unroll
+        const int g = g0 + it * kGroups;
+        T grad[W][W];  // [p offset][q offset]
+  #pragma unroll
         for (int i = 0; i < W; ++i) {
-          const Divisor<T> divide(d[i], r[i]);
-          const T xhat = divide(vec_get<T>(x[it][k], i) - mu[i]);
-          dw += grad[i][k] * xhat;
-          if constexpr (CENTER) db += grad[i][k];
-          const T gw = grad[i][k] * vec_get<T>(wv, k);
-          if (k == 0) {
-            block_g[i] = gw;
-            block_gx[i] = gw * xhat;
-          } else {
-            block_g[i] += gw;
-            block_gx[i] += gw * xhat;
+          const V block = lds[c * W + i][g ^ (c & 7)];
+  #pragma unroll
+          for (int k = 0; k < W; ++k) grad[i][k] = vec_get<T>(block, k);
+        }
+        const V wv = tile_weight[g];  // zero past the last column
+        T column[kValues];
+        T block_g[W];
+        T block_gx[W];
+  #pragma unroll
+        for (int k = 0; k < W; ++k) {
+          T dw = T(0);
+          T db = T(0);
+  #pragma unroll
+          for (int i = 0; i < W; ++i) {
+            const Divisor<T> divide(d[i], r[i]);
+            const T xhat = divide(vec_get<T>(x[it][k], i) - mu[i]);
+            dw += grad[i][k] * xhat;
+            if constexpr (CENTER) db += grad[i][k];
+            const T gw = grad[i][k] * vec_get<T>(wv, k);
+            if (k == 0) {
+              block_g[i] = gw;
+              block_gx[i] = gw * xhat;
+            } else {
+              block_g[i] += gw;
+              block_gx[i] += gw * xhat;
+            }
           }
+          column[k * 2] = dw;
+          column[k * 2 + 1] = db;
         }
-        column[k * 2] = dw;
-        column[k * 2 + 1] = db;
-      }
-      // The row sums gather the block's W columns first.  The empty asm
-      // pins each sum here: otherwise the compiler sinks these adds to the
-      // loop's end and keeps the block's xhat and g * w live until then.
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        if constexpr (CENTER) {
-          sum_g[i] += block_g[i];
-          asm volatile("" : "+v"(sum_g[i]));
+        // The row sums gather the block's W columns first.  The empty asm
+        // pins each sum here: otherwise the compiler sinks these adds to the
+        // loop's end and keeps the block's xhat and g * w live until then.
+  #pragma unroll
+        for (int i = 0; i < W; ++i) {
+          if constexpr (CENTER) {
+            sum_g[i] += block_g[i];
+            asm volatile("" : "+v"(sum_g[i]));
+          }
+          sum_gx[i] += block_gx[i];
+          asm volatile("" : "+v"(sum_gx[i]));
         }
-        sum_gx[i] += block_gx[i];
-        asm volatile("" : "+v"(sum_gx[i]));
+        half_wave_reduce_scatter<T, kValues>(column, c);
+        constexpr int kLanesPerValue = 32 / kValues;
+        const int j = c / kLanesPerValue;
+        const int s = j % 2;
+        const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W + j / 2;
+        if (c % kLanesPerValue == 0 && (WHOLE || q < n) && (CENTER || s == 0)) {
+          (s == 0 ? partial_weight : partial_bias)[static_cast<uint64_t>(tp) * n + q] = column[0];
+        }
       }
-      half_wave_reduce_scatter<T, kValues>(column, c);
-      constexpr int kLanesPerValue = 32 / kValues;
-      const int j = c / kLanesPerValue;
-      const int s = j % 2;
-      const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W + j / 2;
-      if (c % kLanesPerValue == 0 && (WHOLE || q < n) && (CENTER || s == 0)) {
-        (s == 0 ? partial_weight : partial_bias)[static_cast<uint64_t>(tp) * n + q] = column[0];
-      }
-    }
+  };
+  V xa[kBlocks][W];
+  V xb[kBlocks][W];
+  load_x(xa, tile_q0(0));
+  load_tile(tile_q0(0));
+  load_weight(tile_q0(0));
+  uint32_t step = 0;
+  for (; step + 2 < run; step += 2) {
+    body(xa, xb, step, Policy<true>{});
+    body(xb, xa, step + 1, Policy<true>{});
+  }
+  if (step + 1 < run) {
+    body(xa, xb, step, Policy<true>{});
+    body(xb, xa, step + 1, Policy<false>{});
+  } else {
+    body(xa, xb, step, Policy<false>{});
   }
   // The row sums over the run: lanes c and c + 32 of a wave, then the waves
   // in order through LDS.
@@ -1136,7 +1179,7 @@ __global__ void __launch_bounds__(kApplyThreads)
     }
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < 2 * TP; t += kApplyThreads) {
+  for (int t = threadIdx.x; t < 2 * TP; t += THREADS) {
     const int s = t / TP;
     const int pl = t % TP;
     const uint64_t row = p0 + pl;
@@ -1563,15 +1606,15 @@ hipError_t backward_columns_as(const NormBackwardArgs& a, uint64_t pitch, int de
   const T* denominator = static_cast<const T*>(a.denominator);
   const uint32_t sums_grid = static_cast<uint32_t>(tiles_p * splits);
   if (a.rows * a.n * sizeof(T) <= kCacheReuseBytes) {
-    norm_backward_columns_sums_kernel<T, CENTER, MODE, true>
-        <<<sums_grid, kApplyThreads, 0, guard.stream>>>(
+    norm_backward_columns_sums_kernel<T, CENTER, MODE, true, kSumsThreads>
+        <<<sums_grid, kSumsThreads, 0, guard.stream>>>(
             row_partial, partial_weight, partial_bias, dy, dy_scale, in, pitch, weight, mean,
             denominator,
             a.rows, a.n, static_cast<uint32_t>(tiles_q), static_cast<uint32_t>(splits),
             static_cast<uint32_t>(split_tiles));
   } else {
-    norm_backward_columns_sums_kernel<T, CENTER, MODE, false>
-        <<<sums_grid, kApplyThreads, 0, guard.stream>>>(
+    norm_backward_columns_sums_kernel<T, CENTER, MODE, false, kSumsThreads>
+        <<<sums_grid, kSumsThreads, 0, guard.stream>>>(
             row_partial, partial_weight, partial_bias, dy, dy_scale, in, pitch, weight, mean,
             denominator,
             a.rows, a.n, static_cast<uint32_t>(tiles_q), static_cast<uint32_t>(splits),
