@@ -1031,11 +1031,11 @@ __global__ void __launch_bounds__(THREADS)
     const uint64_t first_q = q0 + static_cast<uint64_t>(g0) * W;
       if constexpr (VEC) {
         const T* at = in + p + first_q * pitch;
-  #pragma unroll
+#pragma unroll
         for (int it = 0; it < kBlocks; ++it) {
           const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
           const bool present = WHOLE || (p < rows && q < n);
-  #pragma unroll
+#pragma unroll
           for (int k = 0; k < W; ++k) {
             const V* source = reinterpret_cast<const V*>(
                 present ? at + (static_cast<uint64_t>(it) * kGroups * W + k) * pitch : in);
@@ -1044,10 +1044,10 @@ __global__ void __launch_bounds__(THREADS)
           }
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int it = 0; it < kBlocks; ++it) {
           const uint64_t q = first_q + static_cast<uint64_t>(it) * kGroups * W;
-  #pragma unroll
+#pragma unroll
           for (int k = 0; k < W; ++k) {
             x[it][k] = q + k < n ? load_column_group<T, false>(in, p, q + k, pitch, rows) : V{};
           }
@@ -1087,25 +1087,25 @@ __global__ void __launch_bounds__(THREADS)
       // block, then over the 32 lanes of the half wave (the tile's p), after
       // which lane c holds value c / (32 / kValues).  Absent rows and columns
       // hold zero dy and add nothing.
-  #pragma unroll
+#pragma unroll
       for (int it = 0; it < kBlocks; ++it) {
         const int g = g0 + it * kGroups;
         T grad[W][W];  // [p offset][q offset]
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < W; ++i) {
           const V block = lds[c * W + i][g ^ (c & 7)];
-  #pragma unroll
+#pragma unroll
           for (int k = 0; k < W; ++k) grad[i][k] = vec_get<T>(block, k);
         }
         const V wv = tile_weight[g];  // zero past the last column
         T column[kValues];
         T block_g[W];
         T block_gx[W];
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < W; ++k) {
           T dw = T(0);
           T db = T(0);
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < W; ++i) {
             const Divisor<T> divide(d[i], r[i]);
             const T xhat = divide(vec_get<T>(x[it][k], i) - mu[i]);
@@ -1126,7 +1126,7 @@ __global__ void __launch_bounds__(THREADS)
         // The row sums gather the block's W columns first.  The empty asm
         // pins each sum here: otherwise the compiler sinks these adds to the
         // loop's end and keeps the block's xhat and g * w live until then.
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < W; ++i) {
           if constexpr (CENTER) {
             sum_g[i] += block_g[i];
