@@ -61,6 +61,15 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 
+
+def shown(path: Path) -> str:
+    """A path as the profile headers print it: relative to the repository
+    root when it lies inside it (the raw directories of a GPU run do)."""
+    try:
+        return str(path.relative_to(ROOT))
+    except ValueError:
+        return str(path)
+
 # bench.py's kernel classes: a regex over the demangled kernel name, and
 # whether dispatches of that kernel count as launches of the class (helper
 # kernels such as the partial-sum combine add traffic but no launch).
@@ -315,7 +324,7 @@ def summarize_suite(raw: Path, out: Path, section: str) -> None:
         "Generated (from the repository root) by",
         "",
         f"    python3 rocprof_summary.py suite --section {section} "
-        f"--raw {raw} --out profiles",
+        f"--raw {shown(raw)} --out profiles",
         "",
         "which runs",
         "",
@@ -466,7 +475,7 @@ def summarize_traffic(raw: Path, out: Path) -> None:
         "Generated (from the repository root) by",
         "",
         f"    python3 rocprof_summary.py traffic --section {section} "
-        f"--raw {raw} --out profiles",
+        f"--raw {shown(raw)} --out profiles",
         "",
         f"which runs two counter passes per op, for example (op `{ops[0]}`):",
         "",
