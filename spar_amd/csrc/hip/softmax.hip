@@ -284,15 +284,41 @@ __device__ __forceinline__ T block_max_first(T value, int32_t index) {
   return best;
 }
 
+template <typename T>
+__device__ __forceinline__ T value_max(T a, T b) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_fmaxf(a, b);
+  } else {
+    return __builtin_fmax(a, b);
+  }
+}
+
+// Block-wide maximum by value (maxNum: NaN operands are skipped), for a
+// reduction that runs once per kernel (no guard barrier).
+template <typename T, int THREADS>
+__device__ __forceinline__ T block_max_value(T value) {
+  constexpr int kWavesPerBlock = THREADS / kWave;
+  __shared__ T lds_value[kWavesPerBlock];
+#pragma unroll
+  for (int mask = kWave / 2; mask > 0; mask >>= 1) {
+    value = value_max(value, __shfl_xor(value, mask, kWave));
+  }
+  if (threadIdx.x % kWave == 0) lds_value[threadIdx.x / kWave] = value;
+  exchange_barrier();
+  T best = lds_value[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) best = value_max(best, lds_value[w]);
+  return best;
+}
+
 // Forward over rows held in registers, one row per workgroup (the launcher
 // splits the rows into grids of at most kMaxGrid workgroups).  With no row
 // loop nothing is hoisted across rows, so a lane needs E + ~30 VGPRs and
 // several workgroups share a CU: while one reduces or stores, the others'
-// loads are in flight.  The per-lane maximum tracks the register slot j
-// (an immediate) and turns it into a column once, after the scan.
+// loads are in flight.
 //
-// The fast path keeps no NaN or infinity bookkeeping: with m the
-// first-occurrence maximum over the non-NaN elements, S = sum exp(x - m) is
+// The fast path keeps no NaN or infinity bookkeeping: with m the maximum
+// over the non-NaN elements, S = sum exp(x - m) is
 // NaN exactly when the slice is undefined (a NaN element gives NaN - m; a +inf
 // maximum gives inf - inf; an all -inf slice gives -inf - -inf), and is
 // otherwise finite (1 <= S <= n).  Undefined rows, which are rare, reload the
@@ -315,20 +341,19 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(ro
   // adds an exact +0 to the sum for every m that leaves the row defined.
   T x[E];
   load_row<T, THREADS, E, VEC, FULL>(x, in + r * n, live, -positive_infinity<T>());
-  // Lane maximum: columns reach a lane in increasing order of j, so a later
-  // element wins only if it is strictly larger.
+  // The row maximum over the non-NaN elements, by value only (IEEE maxNum,
+  // one v_max per element, which skips NaNs as the CPU's strict `>` scan
+  // does).  Which element is the first maximum does not matter here: the
+  // value is the same, and when it is a zero of either sign the results are
+  // too (x - m is the same nonzero value for x != 0 and a zero for x = +-0,
+  // whose exp is 1; for log-softmax a zero x - m meets log S = 0 only when
+  // S = 1, that is when the maximum is the row's only zero, and then m is
+  // that element).
   T lane_max = -positive_infinity<T>();
-  int lane_slot = E;
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
-    const bool take = x[j] > lane_max;
-    lane_max = take ? x[j] : lane_max;
-    lane_slot = take ? j : lane_slot;
-  }
-  const int32_t lane_index =
-      lane_slot == E ? INT32_MAX : static_cast<int32_t>(column_of<T, THREADS, VEC>(lane_slot));
+  for (int j = 0; j < E; ++j) lane_max = value_max(lane_max, x[j]);
   // Each block reduction below runs once per kernel: no guard barriers.
-  const T maximum = block_max_first<T, THREADS, false>(lane_max, lane_index);
+  const T maximum = block_max_value<T, THREADS>(lane_max);
   // The results overwrite x in place so one row costs E registers per lane.
   T local = T(0);
 #pragma unroll
