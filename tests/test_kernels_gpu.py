@@ -926,6 +926,36 @@ def test_softmax_special_long_rows(hip, dtype, extent):
         assert_ulp(got, want, 2, f"special long rows {extent} log={log}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("extent", [7, 1000, 32768])
+def test_softmax_zero_maximum_bits(hip, dtype, extent):
+    """Rows whose maximum is a signed zero, alone or beside the other zero
+    (with -inf or very negative values elsewhere, so that S can be exactly
+    1): the register-row forward takes the maximum by value, whichever zero
+    it meets, and must give the oracle's first-occurrence results bit for
+    bit, zero signs included."""
+    inf = np.inf
+    x = np.full((6, extent), -inf, dtype=dtype)
+    x[0, 0] = -0.0
+    x[1, :] = -200.0 if dtype == F32 else -1000.0  # exp underflows to +0
+    x[1, extent - 1] = -0.0
+    x[2, 1] = -0.0
+    x[2, extent - 1] = 0.0
+    x[3, 0] = 0.0
+    x[3, extent // 2] = -0.0
+    x[4, :] = -1e30
+    x[4, 3] = -0.0
+    x[5, 2] = 0.0
+    rows = x.shape[0]
+    for log in (False, True):
+        got, und = softmax_device(hip, x, rows, extent, 1, log, dtype)
+        want, und_ref = (ref.log_softmax(x, 1) if log else ref.softmax_axis(x, 1))
+        assert not und_ref.any() and not und.any()
+        bits = np.uint32 if dtype == F32 else np.uint64
+        assert np.array_equal(got.view(bits), want.astype(dtype).view(bits)), \
+            f"zero maximum rows, extent {extent} log={log}"
+
+
 def test_softmax_rows_beyond_one_grid(hip):
     """More rows than one launch grid holds (2^20): the rows go out in
     several grids at shifted offsets."""
