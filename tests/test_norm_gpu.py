@@ -518,6 +518,10 @@ def test_norm_backward_strided_input_gradient(hip, dtype, center, layout, rows, 
     (8, 8192, 8, 0),         # few rows, long rows: one p tile, many q splits
     (1000, 12, 1000, 0),     # many rows, short rows: one q tile
     (3, 5, 7, 1),            # tiny and ragged
+    # long columns ending in a partial p tile, x within the sums pass's cache
+    # budget (float32 4800) or over it (the others)
+    (4800, 8192, 4800, 0),
+    (5280, 8192, 5280, 0),
 ])
 def test_norm_backward_column_layout(hip, dtype, center, rows, n, pitch, first):
     """The backward over rows that run down storage columns writes dx packed
