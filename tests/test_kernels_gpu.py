@@ -739,8 +739,12 @@ def test_max_argmax_ties_nan_signed_zero(hip):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("n", [1, 5, 1000, 1 << 16, 3 * (1 << 18) + 7])
+@pytest.mark.parametrize("n", [1, 5, 1000, 1 << 16, 3 * (1 << 18) + 7, 1 << 20,
+                               4 * (5 * 512 * 256 + 77), 1 << 25])
 def test_full_reduction(hip, dtype, n):
+    """Full sum, mean, max and argmax.  Long vector-aligned rows take the
+    interleaved sum (several loop trips and a remainder for the middle
+    sizes); the others the split scan."""
     x = (np.random.default_rng(24).random(n) * 2 - 1).astype(dtype)
     dx = dev(hip, x)
     out = out_buf(hip, (1,), np.int64)
