@@ -371,45 +371,82 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// Sum (or mean) of one long contiguous row, interleaved: block b's lanes
+// One long contiguous row (a full reduction), interleaved: block b's lanes
 // take the 16-byte vectors b * kThreads + lane, then every gridDim.x *
 // kThreads vectors after, four loads in flight, so that at any moment the
-// whole grid reads one contiguous window of the row.  Per lane the four load
-// slots accumulate separately and are added in slot order; the block's sum
-// goes to partial b (combined in block order by combine_rows_kernel).  On 2^25
-// float32 elements, 512 such blocks and the combine took 22.8 us against 25.1
-// us for 2048 blocks each scanning a contiguous 64 KiB segment, and on 2^28
-// 155 us against 160 us.  The row's start and length are multiples of W.
+// whole grid reads one contiguous window of the row.  Each lane's four load
+// slots keep their own accumulators, each fed in increasing index order
+// (max/argmax indices are the elements' own, below kMaxScanRange), merged in
+// slot order; the block's result goes to partial b (combined by
+// combine_rows_kernel).  A lane that saw a NaN rescans its elements in index
+// order with the exact rule, as row_kernel does.  On 2^25 float32 elements
+// the sum over 512 such blocks and the combine took 22.8 us against 25.1 us
+// for 2048 blocks each scanning a contiguous 64 KiB segment, and on 2^28
+// 156-162 us against 172 us on the same box.  The row's start and length
+// are multiples of W.
 constexpr uint64_t kInterleavedBlocksPerCu = 2;
 
-template <typename T, int NIN>
+template <typename T, Kind K, int NIN>
 __global__ void __launch_bounds__(kThreads)
-    interleaved_sum_kernel(const T* a, const T* b, uint64_t base, uint64_t n, Sink<T> sink) {
-  using V = typename Vec16<T>::type;
+    interleaved_row_kernel(const T* a, const T* b, uint64_t base, uint64_t n, Sink<T> sink) {
   constexpr int W = Vec16<T>::width;
   const uint64_t vectors = n / W;
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
-  V acc[4];
+  const uint64_t first = static_cast<uint64_t>(blockIdx.x) * kThreads;
+  ScanAcc<T, K> scan[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) acc[u] = V{};
-  uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  for (int u = 0; u < 4; ++u) scan[u].init();
+  bool unordered = false;
+  uint64_t i = first + threadIdx.x;
   for (; i + 3 * stride < vectors; i += 4 * stride) {
-    V v[4];
+    typename Vec16<T>::type v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) v[u] = load_vector<T, NIN>(a, b, base + (i + u * stride) * W);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u] = acc[u] + v[u];
-  }
-  for (; i < vectors; i += stride) acc[0] = acc[0] + load_vector<T, NIN>(a, b, base + i * W);
-  Acc<T, Kind::Sum> lane;
-  lane.value = T(0);
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t element = static_cast<uint32_t>((i + u * stride) * W);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-#pragma unroll
-    for (int k = 0; k < W; ++k) lane.value += vec_get<T>(acc[u], k);
+      for (int k = 0; k < W; ++k) {
+        scan[u].add_ordered(vec_get<T>(v[u], k), element + k);
+        if constexpr (K == Kind::Max) {
+          if (u % 2 == 1) {
+            unordered |= __builtin_isunordered(vec_get<T>(v[u], k), vec_get<T>(v[u - 1], k));
+          }
+        }
+      }
+    }
   }
-  const Acc<T, Kind::Sum> total = block_reduce<T, Kind::Sum>(lane);
-  if (threadIdx.x == 0) sink_write<T, Kind::Sum>(sink, blockIdx.x, total, 0);
+  for (; i < vectors; i += stride) {
+    const auto v = load_vector<T, NIN>(a, b, base + i * W);
+    const uint32_t element = static_cast<uint32_t>(i * W);
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      scan[0].add_ordered(vec_get<T>(v, k), element + k);
+      if constexpr (K == Kind::Max) unordered |= __builtin_isunordered(vec_get<T>(v, k), T(0));
+    }
+  }
+  if constexpr (K == Kind::Max) {
+    if (unordered) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) scan[u].init();
+      for (uint64_t j = first + threadIdx.x; j < vectors; j += stride) {
+        const auto v = load_vector<T, NIN>(a, b, base + j * W);
+        const uint32_t element = static_cast<uint32_t>(j * W);
+#pragma unroll
+        for (int k = 0; k < W; ++k) scan[0].add(vec_get<T>(v, k), element + k);
+      }
+    }
+  }
+  Acc<T, K> acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc[u] = scan[u].finish(0);
+  acc[0].merge(acc[1]);
+  acc[2].merge(acc[3]);
+  acc[0].merge(acc[2]);
+  Acc<T, K> total = block_reduce<T, K>(acc[0]);
+  // a block that saw only -inf answers with its first element
+  total.seal(static_cast<int64_t>(first * W));
+  if (threadIdx.x == 0) sink_write<T, K>(sink, blockIdx.x, total, 0);
 }
 
 // Short rows (n <= kNarrowRow): one lane per row, scanning its n elements in
@@ -1097,19 +1134,18 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
     }
     const uint64_t range_splits = (n + kMaxScanRange / 2 - 1) / (kMaxScanRange / 2);
     if (splits < range_splits) splits = range_splits;
-    // A full sum or mean of a long contiguous row: interleaved blocks.
-    if constexpr (K == Kind::Sum) {
-      if (rows == 1 && vec && splits > 1) {
-        uint64_t blocks = static_cast<uint64_t>(cus) * kInterleavedBlocksPerCu;
-        if (blocks > splits) blocks = splits;
-        const uint64_t base = map.offset;  // row 0
-        return with_partials(blocks, [&](const Sink<T>& partial) {
-          interleaved_sum_kernel<T, NIN><<<static_cast<uint32_t>(blocks), kThreads, 0,
-                                           guard.stream>>>(a, b, base, n, partial);
-          combine_rows_kernel<T, K><<<1, kThreads, 0, guard.stream>>>(
-              partial.values, partial.partial_indices, 1, blocks, 0, final_sink());
-        });
-      }
+    // A full reduction of a long contiguous row: interleaved blocks.
+    if (rows == 1 && vec && splits > 1 && n < kMaxScanRange) {
+      uint64_t blocks = static_cast<uint64_t>(cus) * kInterleavedBlocksPerCu;
+      if (blocks > splits) blocks = splits;
+      const uint64_t base = map.offset;  // row 0
+      return with_partials(blocks, [&](const Sink<T>& partial) {
+        interleaved_row_kernel<T, K, NIN><<<static_cast<uint32_t>(blocks), kThreads, 0,
+                                            guard.stream>>>(a, b, base, n, partial);
+        // partial b's index is the element's own: segment 0
+        combine_rows_kernel<T, K><<<1, kThreads, 0, guard.stream>>>(
+            partial.values, partial.partial_indices, 1, blocks, 0, final_sink());
+      });
     }
     uint64_t segment = (n + splits - 1) / splits;
     if (vec) segment = (segment + W - 1) / W * W;

@@ -739,6 +739,41 @@ def test_max_argmax_ties_nan_signed_zero(hip):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1 << 20, 4 * (5 * 512 * 256 + 77)])
+def test_full_max_argmax_special(hip, dtype, n):
+    """Full max and argmax of long rows (the interleaved scan, whose lanes
+    take vectors a grid apart): a maximum repeated in other workgroups and
+    lanes, NaNs (the first wins), a -0 maximum ahead of a +0, +inf twice and
+    a -inf row with one late NaN, each against the oracle's in-order scan."""
+    rng = np.random.default_rng(n)
+    cases = []
+    x = rng.uniform(-1, 1, n).astype(dtype)
+    x[[n // 7, n // 3, n - 5]] = dtype(2.5)           # repeated maximum
+    cases.append(x)
+    x = rng.uniform(-1, 1, n).astype(dtype)
+    x[[n // 2, n // 9]] = np.nan                      # two NaNs: index n // 9 first
+    cases.append(x)
+    x = np.full(n, -1.0, dtype=dtype)
+    x[1001] = -0.0
+    x[n - 1000] = 0.0                                 # -0 first: max is -0 at 1001
+    cases.append(x)
+    x = rng.uniform(-1, 1, n).astype(dtype)
+    x[[4099, 3 * n // 4]] = np.inf
+    cases.append(x)
+    x = np.full(n, -np.inf, dtype=dtype)
+    x[n - 3] = np.nan
+    cases.append(x)
+    out = out_buf(hip, (1,), np.int64)
+    for k, x in enumerate(cases):
+        mx, am = ref.axis_max(x.reshape(1, n), [1])
+        d = dev(hip, x)
+        hip.call("spar_hip_launch_reduction", out.ptr, d.ptr, n, tag(dtype), hip.MAX, 0)
+        assert_bitexact(out.to_numpy(dtype, (1,)), mx.reshape(1), f"full max case {k}")
+        hip.call("spar_hip_launch_reduction", out.ptr, d.ptr, n, tag(dtype), hip.ARGMAX, 0)
+        assert out.to_numpy(np.int64, (1,))[0] == int(am.reshape(-1)[0]), f"full argmax case {k}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n", [1, 5, 1000, 1 << 16, 3 * (1 << 18) + 7, 1 << 20,
                                4 * (5 * 512 * 256 + 77), 1 << 25])
 def test_full_reduction(hip, dtype, n):
