@@ -813,6 +813,7 @@ def test_row_reduction(hip, dtype):
     ((4, 64, 96), (96,)), ((4, 64, 96), (4, 1, 96)), ((4, 64, 96), (64, 1)),
     ((4, 64, 96), (1, 64, 96)), ((4, 64, 96), (4, 64, 96)), ((4, 64, 96), ()),
     ((3, 1, 5), (1, 5)), ((2048, 36), (36,)),
+    ((512, 4096), ()),   # a long full reduction: the interleaved scan, sum and product
 ])
 def test_broadcast_reduce_and_product(hip, dtype, gshape, oshape):
     g = inputs(26, int(np.prod(gshape)), dtype, with_specials=False).reshape(gshape)
