@@ -862,14 +862,27 @@ __global__ void __launch_bounds__(kThreads)
 // Second pass after column splits.  A 1024-lane block holds 16 / P groups of
 // P waves; each group owns 64 columns of one outer index, its wave p combines
 // splits p, p + P, ... in order, and the group's P results are combined by a
-// fixed LDS tree, so the result is deterministic.  P grows with the number
-// of splits: few splits need no split parallelism, and a block of 16 waves
-// on one column range would then be mostly idle.
+// fixed tree, so the result is deterministic.  P grows with the number of
+// splits: few splits need no split parallelism, and a block of 16 waves on
+// one column range would then be mostly idle.
+//
+// The combine is short (a few microseconds after the split pass), so its
+// latency chain is what it costs:
+//   * a wave issues a batch of B partials at once.  EXACT launches have
+//     splits a multiple of P x B, so no load has a bounds test and slots step
+//     by the uniform P x inner from the batch's first (one 64-bit add per
+//     address); other split counts test each slot.  After the 256-split pass
+//     over [8192, 4096] (steady state, back to back) the pass plus combine
+//     took 26.3 us with two batches of 8 tested loads and about 24.3 us with
+//     one exact batch of 16: a bounds test per load kept the batch from going
+//     out back to back (the compiler branches around each load).
+//   * after one barrier the group's first wave reads the P results from LDS
+//     and evaluates the tree in registers: the same pairs in the same order
+//     as a tree through LDS with a barrier per level, so the same bits.
 constexpr int kCombineThreads = 1024;
 constexpr int kCombineWaves = kCombineThreads / kWave;
-constexpr int kCombineBatch = 8;
 
-template <typename T, Kind K, int P, bool INDEX = true>
+template <typename T, Kind K, int P, int B, bool EXACT, bool INDEX>
 __global__ void __launch_bounds__(kCombineThreads)
     combine_columns_kernel(const T* part_values, const uint32_t* part_indices, uint64_t outer,
                            uint64_t splits, uint64_t segment, uint64_t inner, Sink<T> sink) {
@@ -881,6 +894,7 @@ __global__ void __launch_bounds__(kCombineThreads)
   const int p = wave % P;
   const uint64_t ranges = (inner + kWave - 1) / kWave;  // 64-column ranges per outer index
   const uint64_t blocks = outer * ((ranges + kGroups - 1) / kGroups);
+  const uint64_t step = static_cast<uint64_t>(P) * inner;  // slots between a wave's partials
   for (uint64_t block = blockIdx.x; block < blocks; block += gridDim.x) {
     const uint64_t range = block * kGroups + group;  // over outer x ranges, ranges padded
     const uint64_t o = range / (((ranges + kGroups - 1) / kGroups) * kGroups);
@@ -890,35 +904,39 @@ __global__ void __launch_bounds__(kCombineThreads)
     Acc<T, K> acc;
     acc.init();
     if (valid) {
-      // Batches of kCombineBatch partials: every load of a batch is issued
-      // before the first merge, so a lane waits for one batch at a time.
-      for (uint64_t s0 = p; s0 < splits; s0 += P * kCombineBatch) {
-        Acc<T, K> part[kCombineBatch];
+      for (uint64_t s0 = p; s0 < splits; s0 += static_cast<uint64_t>(P) * B) {
+        Acc<T, K> part[B];
+        const uint64_t first = (o * splits + s0) * inner + i;
 #pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) {
+        for (int j = 0; j < B; ++j) {
           const uint64_t s = s0 + static_cast<uint64_t>(j) * P;
-          if (s < splits) {
+          if (EXACT || s < splits) {
             part[j] = partial_read<T, K, INDEX>(part_values, part_indices,
-                                                (o * splits + s) * inner + i, s, segment);
+                                                first + static_cast<uint64_t>(j) * step, s,
+                                                segment);
           } else {
             part[j].init();
           }
         }
 #pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) acc.merge(part[j]);
+        for (int j = 0; j < B; ++j) acc.merge(part[j]);
       }
     }
     if constexpr (P > 1) {
-      __syncthreads();
+      if (block != blockIdx.x) __syncthreads();  // the previous range's readers are done
       lds[wave][lane] = acc;
       __syncthreads();
+      if (p == 0) {
+        // Level `half` merges result q + half into result q, q < half.
+        Acc<T, K> tree[P];
 #pragma unroll
-      for (int half = P / 2; half > 0; half /= 2) {
-        if (p < half) {
-          acc.merge(lds[wave + half][lane]);
-          lds[wave][lane] = acc;
+        for (int q = 0; q < P; ++q) tree[q] = lds[wave + q][lane];
+#pragma unroll
+        for (int half = P / 2; half > 0; half /= 2) {
+#pragma unroll
+          for (int q = 0; q < half; ++q) tree[q].merge(tree[q + half]);
         }
-        __syncthreads();
+        acc = tree[0];
       }
     }
     if (p == 0 && valid) sink_write<T, K>(sink, o * inner + i, acc, 0);
@@ -1260,14 +1278,29 @@ hipError_t run_plan(const Plan& plan, const T* a, const T* b, void* output, int 
                  guard.stream>>>(partial.values, partial.partial_indices, outer, splits, segment,
                                  inner, final_sink());
       };
+      // Waves per column range P and batch B: the exact kernels when the
+      // splits are a multiple of P x B (256 and 128 splits over wide rows,
+      // 8 for C2's per-batch sums), tested loads otherwise.
       auto combine_all = [&](auto index) {
         constexpr bool INDEX = decltype(index)::value;
         if (splits >= 128) {
-          combine(combine_columns_kernel<T, K, 16, INDEX>, 1);
+          if (splits % 256 == 0) {
+            combine(combine_columns_kernel<T, K, 16, 16, true, INDEX>, 1);
+          } else if (splits % 128 == 0) {
+            combine(combine_columns_kernel<T, K, 16, 8, true, INDEX>, 1);
+          } else {
+            combine(combine_columns_kernel<T, K, 16, 16, false, INDEX>, 1);
+          }
         } else if (splits >= 16) {
-          combine(combine_columns_kernel<T, K, 4, INDEX>, 4);
+          if (splits % 32 == 0) {
+            combine(combine_columns_kernel<T, K, 4, 8, true, INDEX>, 4);
+          } else {
+            combine(combine_columns_kernel<T, K, 4, 16, false, INDEX>, 4);
+          }
+        } else if (splits % 8 == 0) {
+          combine(combine_columns_kernel<T, K, 1, 8, true, INDEX>, 16);
         } else {
-          combine(combine_columns_kernel<T, K, 1, INDEX>, 16);
+          combine(combine_columns_kernel<T, K, 1, 16, false, INDEX>, 16);
         }
       };
       if constexpr (K == Kind::Max) {
