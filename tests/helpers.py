@@ -97,7 +97,8 @@ def assert_red(got, want, n: int, norm, what: str = "") -> None:
     bound = red_bound(n, want, np.asarray(norm, dtype=np.float64))
     gn, wn = np.isnan(got), np.isnan(want)
     assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
-    ok = gn | (np.abs(got - want) <= bound) | (got == want)
+    with np.errstate(invalid="ignore"):  # inf - inf where both are the same infinity
+        ok = gn | (np.abs(got - want) <= bound) | (got == want)
     if not ok.all():
         i = np.flatnonzero(~ok.ravel())[0]
         raise AssertionError(

@@ -671,6 +671,26 @@ def test_max_argmax_column_strips(hip, case):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows", [4096, 2048, 2400, 1024, 600, 160, 128])
+def test_column_combine_split_counts(hip, dtype, rows):
+    """Sum, mean, max and argmax over axis 0 of [rows, 4096]: the column pass
+    takes one workgroup per CU, so it splits the rows into min(CUs, rows / 16)
+    ranges (float32 on a 256-CU device: 256, 128, 150, 64, 37, 10 and 8), and
+    the combine meets every batch form: 16 x 16, 16 x 8, 4 x 8 and 1 x 8
+    without bounds tests, and tested loads for the other counts.  Values are
+    quantised so that maxima tie across splits; one column holds NaNs and one
+    is all -inf."""
+    cols = 4096
+    x = np.round(inputs(36, rows * cols, dtype, with_specials=False) * 8) / 8
+    x = x.astype(dtype).reshape(rows, cols)
+    x[rows // 3, 11] = np.nan
+    x[rows - 1, 11] = np.nan
+    x[:, 12] = -np.inf
+    x[:, 13] = 0.5
+    check_axis(hip, x, x, [0], dtype, f"split counts [{rows}, {cols}]")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows", [8192, 700])
 def test_column_max_value_only_across_splits(hip, dtype, rows):
     """A max without argmax over wide rows keeps no indices: ties between
