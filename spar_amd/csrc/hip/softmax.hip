@@ -827,25 +827,28 @@ __global__ void __launch_bounds__(kEntropyThreads)
     }
     T m = -positive_infinity<T>();
     T s = T(0);
-    for (uint64_t base = static_cast<uint64_t>(threadIdx.x) * W; base < classes;
-         base += kStep * U) {
-      T x[U * W];
+    // Batch `start` (the same for every lane) covers columns [start, start +
+    // kStep * U): lane l reads W columns at start + l * W + u * kStep.  Whole
+    // batches load without bounds tests, so their U loads go out back to
+    // back (behind a test per load the compiler branched around each load
+    // and waited in the middle of the batch); a partial last batch pads
+    // with -inf.
+    const uint64_t lane_column = static_cast<uint64_t>(threadIdx.x) * W;
+    constexpr uint64_t kBatch = kStep * U;
+    auto load_whole = [&](T (&x)[U * W], uint64_t start) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const uint64_t c = base + u * kStep;
-        if (c < classes) {
-          if constexpr (VEC) {
-            const V v = stream_load(reinterpret_cast<const V*>(row + c));
+        const uint64_t c = start + lane_column + u * kStep;
+        if constexpr (VEC) {
+          const V v = stream_load(reinterpret_cast<const V*>(row + c));
 #pragma unroll
-            for (int k = 0; k < W; ++k) x[u * W + k] = vec_get<T>(v, k);
-          } else {
-            x[u] = row[c];
-          }
+          for (int k = 0; k < W; ++k) x[u * W + k] = vec_get<T>(v, k);
         } else {
-#pragma unroll
-          for (int k = 0; k < W; ++k) x[u * W + k] = -positive_infinity<T>();
+          x[u] = row[c];
         }
       }
+    };
+    auto update = [&](const T (&x)[U * W]) {
       T top = m;
 #pragma unroll
       for (int j = 0; j < U * W; ++j) top = fmax_of(top, x[j]);
@@ -862,6 +865,57 @@ __global__ void __launch_bounds__(kEntropyThreads)
       }
       s = rescaled(s, m, top) + batch;
       m = top;
+    };
+    // Whole batches through two register sets used in turn: batch k + 1
+    // loads while batch k is reduced, with the last one or two peeled so
+    // that every load in the loop is unconditional.
+    const uint64_t whole = classes / kBatch;
+    uint64_t start = 0;
+    if (whole > 0) {
+      T xa[U * W];
+      T xb[U * W];
+      load_whole(xa, 0);
+      uint64_t k = 0;
+      for (; k + 2 < whole; k += 2) {
+        load_whole(xb, start + kBatch);
+        __builtin_amdgcn_sched_barrier(0);
+        update(xa);
+        load_whole(xa, start + 2 * kBatch);
+        __builtin_amdgcn_sched_barrier(0);
+        update(xb);
+        start += 2 * kBatch;
+      }
+      if (k + 1 < whole) {
+        load_whole(xb, start + kBatch);
+        __builtin_amdgcn_sched_barrier(0);
+        update(xa);
+        update(xb);
+        start += 2 * kBatch;
+      } else {
+        update(xa);
+        start += kBatch;
+      }
+    }
+    // A partial last batch pads with -inf.
+    if (start < classes) {
+      T x[U * W];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint64_t c = start + lane_column + u * kStep;
+        if (c < classes) {
+          if constexpr (VEC) {
+            const V v = stream_load(reinterpret_cast<const V*>(row + c));
+#pragma unroll
+            for (int k = 0; k < W; ++k) x[u * W + k] = vec_get<T>(v, k);
+          } else {
+            x[u] = row[c];
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < W; ++k) x[u * W + k] = -positive_infinity<T>();
+        }
+      }
+      update(x);
     }
     block_online<T, kEntropyThreads>(m, s);
     const T maximum = m;
