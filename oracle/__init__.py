@@ -6,7 +6,8 @@ ctypes and adds numpy helpers.  `oracle.reference` restates the host-side
 tensor logic (views, broadcast, autograd) in Python on top of these loops.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import
-this package, always as the checker; the product (spar_amd/) never does.
+this package, always as the reference results are compared with; the
+product (spar_amd/) never does.
 """
 from __future__ import annotations
 

@@ -1,6 +1,6 @@
 /*
  * spar_oracle.c — CPU restatement of Spar's CPU path for the elementwise,
- * broadcast and reduction ops.  TEST INFRASTRUCTURE ONLY: it is the checker
+ * broadcast and reduction ops.  TEST INFRASTRUCTURE ONLY: it is the reference
  * that tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg compare
  * the HIP backend against.  Nothing in spar_amd/ links or calls it.
  *

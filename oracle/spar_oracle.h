@@ -1,7 +1,8 @@
 /*
  * spar_oracle.h — CPU restatement of Spar's CPU path (see spar_oracle.c).
  * TEST INFRASTRUCTURE ONLY: used by tests/, smoke() and bench.py's CPU
- * baseline as the checker; the product never links it.
+ * baseline as the reference results are compared with; the product never
+ * links it.
  */
 #ifndef SPAR_ORACLE_H
 #define SPAR_ORACLE_H
