@@ -234,7 +234,13 @@ def summarize(raw: Path, out: Path) -> None:
     f_scale = cal_kib / fetch_copy
     w_scale = cal_kib / write_copy
     lines = [
-        "# HBM traffic per dispatch: bench.py --profile-loop 2, x[32,1024,4096] fp32",
+        "# L2-fabric (HBM + Infinity Cache) traffic per dispatch: bench.py --profile-loop 2, "
+        "x[32,1024,4096] fp32",
+        "",
+        "FETCH_SIZE and WRITE_SIZE count what the L2 reads from and writes to the data",
+        "fabric, that is HBM plus Infinity Cache (MALL) hits; gfx950 exposes no counter",
+        "that tells the two apart.  This workload's 537 MB tensors rotate through more",
+        "than the 256 MB cache, so here the figures are close to HBM bytes.",
         "",
         "Commands (from the repository root), one counter per run:",
         "",
@@ -246,7 +252,7 @@ def summarize(raw: Path, out: Path) -> None:
         f"{write_copy:.0f} KiB per dispatch; every counter value below is scaled by "
         f"{f_scale:.4f} (fetch) and {w_scale:.4f} (write) to bytes.",
         "",
-        "| kernel | class | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB per dispatch |",
+        "| kernel | class | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | L2-fabric MB per dispatch |",
         "|---|---|---|---|---|---|",
     ]
     class_bytes = collections.defaultdict(float)
@@ -262,8 +268,9 @@ def summarize(raw: Path, out: Path) -> None:
             class_bytes[cls] += per * len(values)
             if counts:
                 class_launches[cls] += len(values)
-    lines += ["", "HBM bytes per launch of each bench.py kernel class (all dispatches of the",
-              "class over its launches):", ""]
+    lines += ["", "L2-fabric bytes per launch of each bench.py kernel class (all dispatches",
+              "of the class over its launches; bench.py reads these lines as its roofline's",
+              "traffic):", ""]
     for cls in CLASSES:
         if class_launches[cls]:
             lines.append(f"- hbm_bytes_per_launch[{cls}] = "
