@@ -675,7 +675,7 @@ def test_max_argmax_column_strips(hip, case):
 def test_column_combine_split_counts(hip, dtype, rows):
     """Sum, mean, max and argmax over axis 0 of [rows, 4096]: the column pass
     takes one workgroup per CU, so it splits the rows into min(CUs, rows / 16)
-    ranges (float32 on a 256-CU device: 256, 128, 150, 64, 37, 10 and 8), and
+    ranges (float32 on a 256-CU device: 256, 128, 150, 64, 36, 10 and 8), and
     the combine meets every batch form: 16 x 16, 16 x 8, 4 x 8 and 1 x 8
     without bounds tests, and tested loads for the other counts.  Values are
     quantised so that maxima tie across splits; one column holds NaNs and one
@@ -688,6 +688,21 @@ def test_column_combine_split_counts(hip, dtype, rows):
     x[:, 12] = -np.inf
     x[:, 13] = 0.5
     check_axis(hip, x, x, [0], dtype, f"split counts [{rows}, {cols}]")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("outer,rows", [(2, 2048), (3, 1400), (5, 512)])
+def test_column_combine_outer_indices(hip, dtype, outer, rows):
+    """The same reductions over axis 1 of [outer, rows, 4096]: every outer
+    index has its own splits (float32 on a 256-CU device: 128, 83 and 32 per
+    outer index), so the combine's outer-index arithmetic meets exact and
+    tested batches alike."""
+    cols = 4096
+    x = np.round(inputs(37 + outer, outer * rows * cols, dtype, with_specials=False) * 8) / 8
+    x = x.astype(dtype).reshape(outer, rows, cols)
+    x[outer - 1, rows // 2, 17] = np.nan
+    x[0, :, 18] = -np.inf
+    check_axis(hip, x, x, [1], dtype, f"outer {outer} x [{rows}, {cols}]")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
