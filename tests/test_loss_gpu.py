@@ -86,8 +86,13 @@ def check(got_loss, want_loss, got_dx, want_dx, x, per_row_targets, reduction, d
 @pytest.mark.parametrize("dtype", [F32, F64])
 @pytest.mark.parametrize("reduction", ["none", "sum", "mean"])
 def test_cross_entropy_matches_oracle(sp, dtype, reduction):
+    """Class counts cover the fused forward's batch paths (float32 batches of
+    8192 classes per workgroup): none whole (1000, 4096), one whole batch
+    alone (8192) or with a partial tail (8292), two (16384), three with a
+    tail (32000), and odd counts that take scalar loads (5, 50257)."""
     rng = np.random.default_rng(80)
-    for rows, classes in [(1, 1), (3, 5), (64, 1000), (8, 4096), (4, 32000), (3, 50257)]:
+    for rows, classes in [(1, 1), (3, 5), (64, 1000), (8, 4096), (3, 8192), (2, 8292),
+                          (2, 16384), (4, 32000), (3, 50257)]:
         x = (rng.standard_normal((rows, classes)) * 2).astype(dtype)
         t = rng.integers(0, classes, rows).astype(np.int64 if rows % 2 else np.int32)
         got, want, gdx, wdx = run_both(sp, x, t, reduction)
