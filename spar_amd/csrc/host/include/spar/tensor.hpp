@@ -218,6 +218,15 @@ template <typename T>
   return tensor;
 }
 
+/// A gradient that reaches a broadcast parent of its own shape is passed on
+/// as it is, with no copy (the default).  The reference instead adds it into
+/// a zeroed buffer (tensor.cpp:597-632), which turns each -0.0 element into
+/// +0.0.  With exact zero signs on, such a gradient is re-added to +0.0 the
+/// same way (one scalar-add pass), so gradients carry the reference's bits
+/// including the signs of zeros.  The setting is process-wide.
+void set_exact_gradient_zero_signs(bool enabled) noexcept;
+[[nodiscard]] bool exact_gradient_zero_signs() noexcept;
+
 }  // namespace spar
 
 namespace spar::detail {

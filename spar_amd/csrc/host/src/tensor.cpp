@@ -6,6 +6,7 @@
 // view op here is one call of make_view(), which builds the view and records
 // the gradient rule; every device transfer and gather goes through the C ABI
 // (include/spar_hip.h).
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -483,6 +484,16 @@ Tensor ones(Shape shape, DType dtype, Device device) {
   return full_value(std::move(shape), dtype, 1.0, device);
 }
 
+namespace {
+std::atomic<bool> exact_zero_signs{false};
+}  // namespace
+
+void set_exact_gradient_zero_signs(bool enabled) noexcept {
+  exact_zero_signs.store(enabled, std::memory_order_relaxed);
+}
+
+bool exact_gradient_zero_signs() noexcept { return exact_zero_signs.load(std::memory_order_relaxed); }
+
 }  // namespace spar
 
 namespace spar::detail {
@@ -583,9 +594,10 @@ Shape broadcast_shape(const Shape& left, const Shape& right) {
 
 // Sums a gradient over the axes its parent was broadcast along (the role of
 // tensor.cpp:572-632).  A gradient that already has the parent's shape is
-// returned as is (the reference re-accumulated it into a zeroed buffer);
-// otherwise one deterministic device reduction reads the gradient in place,
-// contiguous or not.
+// returned as is (the reference re-accumulated it into a zeroed buffer), or
+// re-added to +0 when exact zero signs are on; otherwise one deterministic
+// device reduction reads the gradient in place, contiguous or not (its sums
+// start from +0, as the reference's do).
 Tensor reduce_gradient_to_shape(const Tensor& gradient, const Shape& original_shape) {
   if (!is_floating(gradient.dtype())) {
     throw std::logic_error{"Broadcast gradient reduction requires a floating dtype"};
@@ -595,7 +607,12 @@ Tensor reduce_gradient_to_shape(const Tensor& gradient, const Shape& original_sh
         "Gradient shape cannot be reduced to the requested broadcast parent shape"};
   }
   require_hip(gradient, "reduce_gradient_to_shape");
-  if (gradient.shape() == original_shape) return gradient.detach();
+  if (gradient.shape() == original_shape) {
+    if (!exact_gradient_zero_signs()) return gradient.detach();
+    // g + (+0), read in place whatever its strides (a sum's gradient is a
+    // stride-0 view): -0 + +0 = +0, every other value unchanged.
+    return add(gradient.detach(), zeros(Shape{}, gradient.dtype(), gradient.device()));
+  }
   Tensor result{original_shape, gradient.dtype(), gradient.device()};
   // Reduced: the leading axes the parent lacks, and its extent-1 axes that
   // the gradient spans.

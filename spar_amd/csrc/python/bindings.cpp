@@ -180,6 +180,8 @@ PYBIND11_MODULE(_spar, m) {
         py::arg("shape"), py::arg("dtype"), py::arg("random"), py::arg("mean") = 0.0,
         py::arg("stddev") = 1.0, py::arg("device") = Device::cpu());
 
+  m.def("set_exact_gradient_zero_signs", &spar::set_exact_gradient_zero_signs, py::arg("enabled"));
+  m.def("exact_gradient_zero_signs", &spar::exact_gradient_zero_signs);
   m.def("zeros", [](const std::vector<std::int64_t>& s, DType d, Device dev) { return spar::zeros(to_shape(s), d, dev); },
         py::arg("shape"), py::arg("dtype"), py::arg("device") = Device::cpu());
   m.def("ones", [](const std::vector<std::int64_t>& s, DType d, Device dev) { return spar::ones(to_shape(s), d, dev); },

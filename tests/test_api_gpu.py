@@ -286,6 +286,42 @@ def test_autograd_elementwise_chain_bitexact_grads(sp):
         assert_bitexact(gd, gr, f"grad {i}")
 
 
+def test_exact_gradient_zero_signs(sp):
+    """A gradient that reaches a parent of its own shape is passed on as is by
+    default, so a -0.0 element stays -0.0, where the reference adds it into a
+    zeroed buffer (tensor.cpp:597-632) and gets +0.0.  With exact zero signs
+    on, every gradient equals the oracle's bit for bit, zero signs included:
+    d a = 1 * w and d w = 1 * a hold -0.0 where w or a do, and subtract's
+    negated gradient turns +0.0 into -0.0."""
+    a = normal(40, (8, 16))
+    w = normal(41, (8, 16))
+    c = normal(43, (8, 16))
+    w[0, :4] = -0.0
+    w[1, :4] = 0.0
+    a[2, :3] = -0.0
+    bias = normal(42, (16,))
+
+    def build(lib, t):
+        y = lib.subtract(lib.add(lib.multiply(t[0], t[1]), t[2]), lib.multiply(t[3], t[1]))
+        return lib.sum(y)
+
+    arrays = [a, w, bias, c]
+    assert not sp.exact_gradient_zero_signs()
+    _, _, gd, gr = run_both(sp, build, arrays)
+    assert np.signbit(gd[0][0, :4]).all() and not np.signbit(gr[0][0, :4]).any()
+    sp.set_exact_gradient_zero_signs(True)
+    try:
+        assert sp.exact_gradient_zero_signs()
+        loss_d, loss_r, gd, gr = run_both(sp, build, arrays)
+        for i, (got, want) in enumerate(zip(gd, gr)):
+            assert_bitexact(got, want, f"grad {i} with exact zero signs")
+        # d a = 1 * w and d c = -1 * w at the zeros of w: +0.0 throughout
+        for got in (gd[0][:2, :4], gd[3][:2, :4]):
+            assert np.all(got == 0) and not np.signbit(got).any()
+    finally:
+        sp.set_exact_gradient_zero_signs(False)
+
+
 def test_autograd_unary_chain(sp):
     x = normal(15, (8, 32))
     w = normal(16, (8, 32))
