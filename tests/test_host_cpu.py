@@ -127,6 +127,18 @@ def test_autograd_flags_on_cpu_tensors():
     assert not d.requires_grad
 
 
+def test_exact_gradient_zero_signs_setting():
+    """Off by default (the zero-copy pass-through of same-shape gradients);
+    the process-wide switch turns on and back off."""
+    assert not spar.exact_gradient_zero_signs()
+    spar.set_exact_gradient_zero_signs(True)
+    try:
+        assert spar.exact_gradient_zero_signs()
+    finally:
+        spar.set_exact_gradient_zero_signs(False)
+    assert not spar.exact_gradient_zero_signs()
+
+
 def test_cpu_transfers_and_factories():
     x = np.random.default_rng(0).standard_normal((5, 6)).astype(np.float32)
     t = cpu(x)
