@@ -422,8 +422,10 @@ class Suite:
       launch itself leaves dirty in the cache, which flatters ordinary stores
       against non-temporal ones.
 
-    Ops that need a fresh graph per launch (the backward chains) are timed
-    cold only.
+    Ops that need a fresh graph per launch (the backwards) are timed in
+    steady state over graphs built beforehand on the rotated sets, each
+    launch clearing its leaves' gradients on the host first (no device work)
+    so that it writes fresh gradients as a cold launch does.
 
     With `profile=(config, op, launches)` only that op runs, `launches`
     times, each launch between an opening and a closing marker dispatch (a
@@ -449,7 +451,12 @@ class Suite:
     def wanted(self, config, name):
         return self.profile is None or (config, name) == self.profile[:2]
 
-    def measure(self, config, name, nbytes, launches, elements, prepare=None):
+    def measure(self, config, name, nbytes, launches, elements, prepare=None, build_runs=None):
+        """`prepare`, when given, runs before each cold launch (outside its
+        events): work the launch needs first, such as building a fresh graph.
+        `build_runs(count)`, when given, returns `count` launches that are
+        ready to run back to back (their graphs built beforehand, over the
+        rotated sets), so that such an op is also timed in steady state."""
         assert name in SUITE_OPS[config], (config, name)
         if not self.wanted(config, name):
             return
@@ -494,6 +501,17 @@ class Suite:
             ms = self.start.elapsed_ms(self.stop) / count
             line["timing"] = f"steady, {len(launches)} rotated sets"
             line["sets"] = len(launches)
+        elif build_runs is not None:
+            runs, sets = build_runs(self.reps)
+            hip.synchronize()
+            self.start.record()
+            for run in runs:
+                run()
+            self.stop.record()
+            ms = self.start.elapsed_ms(self.stop) / len(runs)
+            del runs
+            line["timing"] = f"steady, {sets} rotated sets, graphs built beforehand"
+            line["sets"] = sets
         else:
             ms = cold
             line["timing"] = "cold"
@@ -836,8 +854,23 @@ class Suite:
                         leaf.zero_grad()
                     losses[:] = [forward(view_of(label), Gs[0])]
 
+                def backward_runs(make_loss, runs):
+                    # `runs` losses built over the rotated sets in turn; each run
+                    # clears its leaves' gradients (host only: no device work) so
+                    # that every backward writes fresh gradients, as a cold one does.
+                    built = [(k % count, make_loss(k % count)) for k in range(runs)]
+
+                    def run(k, loss):
+                        for leaf in (gamma, beta, bases[label][k]):
+                            leaf.zero_grad()
+                        loss.backward()
+
+                    return [lambda k=k, loss=loss: run(k, loss) for k, loss in built], count
+
                 measure("C5", f"LN backward chain {label}", 3 * T,
-                        lambda: losses[0].backward(), n, prepare=prepare)
+                        lambda: losses[0].backward(), n, prepare=prepare,
+                        build_runs=lambda runs: backward_runs(
+                            lambda k: forward(view_of(label, k), Gs[k]), runs))
 
                 # The same LayerNorm fused (spar.layer_norm); a non-contiguous view is
                 # first made contiguous, inside the timed op.
@@ -851,8 +884,13 @@ class Suite:
                     y = spar.layer_norm(view_of(label), gamma, beta, 1e-5)
                     losses[:] = [spar.sum(spar.multiply(y, Gs[0]), None, False)]
 
+                def fused_loss(k):
+                    y = spar.layer_norm(view_of(label, k), gamma, beta, 1e-5)
+                    return spar.sum(spar.multiply(y, Gs[k]), None, False)
+
                 measure("C5", f"fused LN backward {label}", 3 * T,
-                        lambda: losses[0].backward(), n, prepare=prepare_fused)
+                        lambda: losses[0].backward(), n, prepare=prepare_fused,
+                        build_runs=lambda runs: backward_runs(fused_loss, runs))
                 del losses
             if self.with_cpu:
                 import oracle.reference as R
