@@ -705,6 +705,41 @@ def test_column_combine_outer_indices(hip, dtype, outer, rows):
     check_axis(hip, x, x, [1], dtype, f"outer {outer} x [{rows}, {cols}]")
 
 
+def random_reduction_case(rng):
+    """A random view of a random base and a random set of reduced axes: rank 1
+    to 4, extents 1 to 300 (views up to 4 M elements), the view's axes
+    permuted and each narrowed at a random offset."""
+    rank = int(rng.integers(1, 5))
+    while True:
+        shape = [int(rng.choice([1, 2, 3, 7, 16, 33, 64, 100, 256, 300])) for _ in range(rank)]
+        if int(np.prod(shape)) <= (4 << 20):
+            break
+    base_shape = [e + int(rng.integers(0, 3)) for e in shape]
+    starts = [int(rng.integers(0, b - e + 1)) for b, e in zip(base_shape, shape)]
+    order = [int(a) for a in rng.permutation(rank)]
+    count = int(rng.integers(1, rank + 1))
+    axes = sorted(int(a) for a in rng.choice(rank, count, replace=False))
+    return base_shape, starts, shape, order, axes
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_random_axis_reductions(hip, dtype):
+    """Sum, mean, max and argmax of 60 random views and axis sets against the
+    oracle: every planner path (row, column, column strip, interleaved, narrow
+    and generic kernels, with and without splits) on layouts nobody chose.
+    Values are quantised so that maxima tie."""
+    rng = np.random.default_rng(90 if dtype == F32 else 91)
+    for case in range(60):
+        base_shape, starts, shape, order, axes = random_reduction_case(rng)
+        size = int(np.prod(base_shape))
+        base = (np.round(inputs(1000 + case, size, dtype, with_specials=False) * 4) / 4)
+        base = base.astype(dtype).reshape(base_shape)
+        window = tuple(slice(s0, s0 + e) for s0, e in zip(starts, shape))
+        view = base[window].transpose(order)
+        check_axis(hip, base, view, axes, dtype,
+                   f"case {case}: base {base_shape} view {list(view.shape)} axes {axes}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows", [8192, 700])
 def test_column_max_value_only_across_splits(hip, dtype, rows):
