@@ -414,6 +414,41 @@ def test_strided_binary_broadcasts(hip, dtype, op):
         assert_bitexact(got, want, f"{name} {op} x")
 
 
+def random_binary_operand(rng, shape, dtype, seed):
+    """A view that broadcasts to `shape`: leading axes sometimes dropped, some
+    axes of extent 1, stored in a random axis order inside a larger base and
+    narrowed at random offsets."""
+    lead = int(rng.integers(0, len(shape))) if rng.random() < 0.3 else 0
+    vshape = [1 if rng.random() < 0.25 else e for e in shape[lead:]]
+    order = [int(a) for a in rng.permutation(len(vshape))]
+    stored = [vshape[a] for a in order]
+    base_shape = [e + int(rng.integers(0, 3)) for e in stored]
+    base = inputs(seed, int(np.prod(base_shape)), dtype).reshape(base_shape)
+    starts = [int(rng.integers(0, b - e + 1)) for b, e in zip(base_shape, stored)]
+    window = base[tuple(slice(s0, s0 + e) for s0, e in zip(starts, stored))]
+    return base, window.transpose(np.argsort(order))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_random_strided_binary(hip, dtype):
+    """Every binary op over 50 random pairs of broadcasting views (rank 1-4,
+    permuted, narrowed, extent-1 and missing axes) against the oracle, bit for
+    bit, with IEEE special values among the inputs."""
+    rng = np.random.default_rng(92 if dtype == F32 else 93)
+    ops = sorted(hip.BINARY_OPS)
+    for case in range(50):
+        rank = int(rng.integers(1, 5))
+        while True:
+            shape = [int(rng.choice([1, 2, 3, 7, 16, 33, 64, 100, 130, 256])) for _ in range(rank)]
+            if int(np.prod(shape)) <= (2 << 20):
+                break
+        lb, lv = random_binary_operand(rng, shape, dtype, 2000 + 2 * case)
+        rb, rv = random_binary_operand(rng, shape, dtype, 2001 + 2 * case)
+        op = ops[int(rng.integers(0, len(ops)))]
+        got, want = strided_binary(hip, lb, lv, rb, rv, op, dtype)
+        assert_bitexact(got, want, f"case {case}: {list(lv.shape)} {op} {list(rv.shape)}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_strided_binary_views(hip, dtype):
     base = inputs(17, 200 * 130, dtype).reshape(200, 130)
