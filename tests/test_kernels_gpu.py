@@ -1136,6 +1136,48 @@ def test_softmax_inner_axis(hip, dtype, shape, axis):
     assert np.all(err <= bound)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_random_softmax_shapes(hip, dtype):
+    """Softmax and log-softmax, forward and backward, over 30 random
+    [outer, extent, inner] shapes (extents around the row kernels' register
+    sizes and past the longest one, inner slices of 1 to 17) against the
+    oracle within the derived bounds."""
+    rng = np.random.default_rng(94 if dtype == F32 else 95)
+    extents = [1, 2, 5, 63, 64, 65, 255, 256, 1000, 1024, 3000, 8193, 16385, 32769, 40000]
+    for case in range(30):
+        while True:
+            outer = int(rng.integers(1, 200))
+            extent = int(rng.choice(extents))
+            inner = int(rng.choice([1, 1, 1, 2, 3, 17]))
+            if outer * extent * inner <= (2 << 20):
+                break
+        shape = (outer, extent, inner)
+        what = f"case {case}: {list(shape)}"
+        x = (inputs(3000 + case, outer * extent * inner, dtype, with_specials=False)
+             * dtype(2)).reshape(shape)
+        g = inputs(4000 + case, x.size, dtype, with_specials=False).reshape(shape)
+        for log in (False, True):
+            got, und = softmax_device(hip, x, outer, extent, inner, log, dtype)
+            if log:
+                want, und_ref = ref.log_softmax(x, 1)
+                log_softmax_tolerance_check(got, want, extent, dtype, what + " log fwd")
+                back = ref.log_softmax_backward(g, want, und_ref, 1)
+            else:
+                want, und_ref = ref.softmax_axis(x, 1)
+                softmax_tolerance_check(got, want, extent, dtype, what + " fwd")
+                back = ref.softmax_axis_backward(g, want, und_ref, 1)
+            assert np.array_equal(und, und_ref.astype(np.int32).ravel()), what
+            out = out_buf(hip, shape, dtype)
+            hip.call("spar_hip_launch_probability_backward", out.ptr, dev(hip, g).ptr,
+                     dev(hip, want).ptr, dev(hip, und_ref.astype(np.int32)).ptr, outer, extent,
+                     inner, tag(dtype), int(log), 0)
+            err = np.abs(out.to_numpy(dtype, shape).astype(np.float64) - back)
+            bound = np.moveaxis(softmax_backward_bound(np.moveaxis(g, 1, -1),
+                                                       np.moveaxis(want, 1, -1), extent, dtype,
+                                                       log), -1, 1)
+            assert np.all(err <= bound), f"{what} backward log={log}"
+
+
 # ---------------------------------------------------------------- random
 
 @pytest.mark.parametrize("dtype", DTYPES)
