@@ -423,6 +423,29 @@ def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
     statistics around a shift in double, the row kernel in T, so the two agree
     within the statistics' rounding: y within the row tolerance, mean and d
     within a few ulp of the row's scale."""
+    check_column_layout(hip, dtype, center, rows, n, pitch, first)
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+@pytest.mark.parametrize("center", [True, False])
+def test_random_norm_column_layout(hip, dtype, center):
+    """The column-layout forward over 20 random (rows, n, pitch, offset)
+    layouts: partial tiles, pitches that are and are not multiples of the
+    vector width, every split count the launcher picks."""
+    rng = np.random.default_rng(96 + int(center) + (2 if dtype == F64 else 0))
+    for case in range(20):
+        while True:
+            rows = int(rng.integers(1, 700))
+            n = int(rng.integers(1, 3000))
+            if rows * n <= (1 << 20):
+                break
+        pitch = rows + int(rng.integers(0, 40))
+        first = int(rng.integers(0, 8))
+        check_column_layout(hip, dtype, center, rows, n, pitch, first,
+                            f"case {case}: rows {rows} n {n} pitch {pitch} first {first}")
+
+
+def check_column_layout(hip, dtype, center, rows, n, pitch, first, what="column layout"):
     x, w, b, g = data(rows, n, dtype, 500 + rows + n)
     store = np.zeros(first + n * pitch, dtype)
     store[first:].reshape(n, pitch)[:, :rows] = x.T
@@ -435,14 +458,14 @@ def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
     hip.call("spar_hip_launch_norm_forward", y.ptr, mu.ptr if center else None, d.ptr,
              store_dev.address(first * item), 1, pitch, dev(hip, w).ptr,
              dev(hip, b).ptr if center else None, rows, n, EPSILON, int(center), tag(dtype), 0)
-    assert_rows(y.to_numpy(dtype, (rows, n)), y_ref, n, dtype, "column layout y")
+    assert_rows(y.to_numpy(dtype, (rows, n)), y_ref, n, dtype, what + " y")
     eps = np.finfo(dtype).eps
     scale = np.max(np.abs(x.astype(np.float64)), axis=1)
     got_d = d.to_numpy(dtype, (rows,)).astype(np.float64)
-    assert np.all(np.abs(got_d - d_ref) <= 8 * eps * np.sqrt(n) * d_ref), "column layout d"
+    assert np.all(np.abs(got_d - d_ref) <= 8 * eps * np.sqrt(n) * d_ref), what + " d"
     if center:
         got_mu = mu.to_numpy(dtype, (rows,)).astype(np.float64)
-        assert np.all(np.abs(got_mu - mu_ref) <= 8 * eps * np.sqrt(n) * scale), "column layout mean"
+        assert np.all(np.abs(got_mu - mu_ref) <= 8 * eps * np.sqrt(n) * scale), what + " mean"
     # and against float64 statistics computed here
     x64 = x.astype(np.float64)
     mean64 = x64.mean(axis=1) if center else np.zeros(rows)
@@ -450,7 +473,7 @@ def test_norm_column_layout(hip, dtype, center, rows, n, pitch, first):
     # float32: the double sums are exact to well below an ulp of T; float64:
     # they carry their own rounding, a random walk over the row
     allowance = 4.0 if dtype == F32 else 8.0 * np.sqrt(n)
-    assert np.all(np.abs(got_d - d64) <= allowance * eps * d64), "column layout d vs float64"
+    assert np.all(np.abs(got_d - d64) <= allowance * eps * d64), what + " d vs float64"
 
 
 @pytest.mark.parametrize("dtype", [F32, F64])
