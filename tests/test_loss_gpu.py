@@ -119,6 +119,29 @@ def test_language_model_cross_entropy(sp, reduction):
     assert not gdx[:, -1].any() and not np.signbit(gdx[:, -1]).any(), "last position: +0"
 
 
+@pytest.mark.parametrize("dtype", [F32, F64])
+def test_random_cross_entropy_shapes(sp, dtype):
+    """Plain and language-model cross entropy over 16 random shapes each
+    (batches of 1 to 6 sequences of 1 to 40 positions, 2 to 20000 classes,
+    int32 and int64 targets, every reduction) against the oracle."""
+    rng = np.random.default_rng(97 if dtype == F32 else 98)
+    for case in range(16):
+        batch, sequence = int(rng.integers(1, 7)), int(rng.integers(1, 41))
+        classes = int(rng.choice([2, 3, 17, 1000, 4097, 8192, 8193, 20000]))
+        reduction = ["none", "sum", "mean"][case % 3]
+        x = (rng.standard_normal((batch, sequence, classes)) * 2).astype(dtype)
+        t = rng.integers(0, classes, (batch, sequence)).astype(np.int64 if case % 2 else np.int32)
+        what = f"case {case}: [{batch}, {sequence}, {classes}] {reduction}"
+        got, want, gdx, wdx = run_both(sp, x, t, reduction)
+        check(got, want, gdx, wdx, x, t.astype(np.int64), reduction, dtype, what)
+        if sequence < 2:
+            continue  # a language model needs a next token
+        got, want, gdx, wdx = run_both(sp, x, t, reduction, language_model=True)
+        check(got, want, gdx[:, :-1], wdx[:, :-1], x[:, :-1], t[:, 1:].astype(np.int64),
+              reduction, dtype, what + " language model")
+        assert not gdx[:, -1].any() and not np.signbit(gdx[:, -1]).any(), what + " last position"
+
+
 def test_cross_entropy_undefined_rows(sp):
     """Rows with NaN, +inf or only -inf follow log-softmax's special cases:
     the loss is NaN, -(-log k) or inf as the oracle gives, and the gradient
