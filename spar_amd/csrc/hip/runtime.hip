@@ -100,7 +100,11 @@ hipError_t allocate_on(DeviceState* state, void** pointer, uint64_t bytes) {
   hipError_t error = hipMalloc(&block, size);
   if (error == hipErrorOutOfMemory || error == hipErrorMemoryAllocation) {
     (void)hipGetLastError();
-    release_cached(state);
+    const hipError_t released = release_cached(state);
+    if (released != hipSuccess) {
+      (void)hipGetLastError();
+      return released;
+    }
     error = hipMalloc(&block, size);
   }
   if (error != hipSuccess) {
