@@ -527,6 +527,163 @@ def test_autograd_narrow_chains_embed_once(sp):
     assert_bitexact(gd[0], gr[0], "base through a product and two narrows")
 
 
+GRAPH_SHAPE = (6, 8, 8)
+GRAPH_LEAVES = [(10, 12, 11), GRAPH_SHAPE, (8, 9, 8)]
+
+
+def random_graph(seed, steps=24):
+    """A random recipe over three leaves: view chains (narrow, transpose)
+    from the larger leaves down to GRAPH_SHAPE, scaled copies of whole
+    leaves that are then narrowed (a chain that ends on a computed tensor),
+    views shared by several chains, and exact elementwise arithmetic
+    (add, subtract, multiply, divide by 1 + y*y, negate, square, scalar
+    scale and shift) on GRAPH_SHAPE nodes, with tensors reused by several
+    consumers.  Unary and scalar ops take contiguous tensors only, as in
+    the reference (unary.cpp, elementwise.cpp), so they are applied to
+    leaves and computed nodes, never to views.  Every node that nothing
+    consumes is summed into the loss, so every leaf reaches it.  Returns
+    the recipe and the sink nodes.
+
+    Magnitudes are followed with float32 numpy values: a node above 64 is
+    scaled by 1/256 (an exact power of two) before it is used further."""
+    rng = np.random.default_rng(seed)
+    values = [normal(seed * 10 + k, s) for k, s in enumerate(GRAPH_LEAVES)]
+    shapes = [tuple(s) for s in GRAPH_LEAVES]
+    consumed = [False] * len(shapes)
+    dense = [True] * len(shapes)  # leaves and computed nodes are contiguous
+    recipe = []
+
+    def emit(step, value):
+        for i in step[1:]:
+            if isinstance(i, tuple):  # node references are tagged ("n", index)
+                consumed[i[1]] = True
+        recipe.append(step)
+        values.append(value.astype(F32))
+        shapes.append(tuple(value.shape))
+        consumed.append(False)
+        dense.append(step[0] not in ("narrow", "transpose"))
+        node = len(values) - 1
+        if np.max(np.abs(values[node])) > 64:
+            return emit(("scale", ("n", node), 1.0 / 256.0), values[node] * F32(1.0 / 256.0))
+        return node
+
+    def view_step(i):
+        shape = shapes[i]
+        narrowable = [a for a in range(3) if shape[a] > GRAPH_SHAPE[a]]
+        if rng.random() < 0.2 and shape[1] >= 8 and shape[2] >= 8:
+            return emit(("transpose", ("n", i)), np.swapaxes(values[i], 1, 2))
+        axis = int(rng.choice(narrowable))
+        length = int(rng.integers(GRAPH_SHAPE[axis], shape[axis]))
+        start = int(rng.integers(0, shape[axis] - length + 1))
+        index = [slice(None)] * 3
+        index[axis] = slice(start, start + length)
+        return emit(("narrow", ("n", i), axis, start, length), values[i][tuple(index)])
+
+    def chain_to_shape(i):
+        while shapes[i] != GRAPH_SHAPE:
+            i = view_step(i)
+        return i
+
+    for leaf in (0, 2):
+        chain_to_shape(leaf)
+    for _ in range(steps):
+        pick = rng.random()
+        ready = [i for i, s in enumerate(shapes) if s == GRAPH_SHAPE]
+        large = [i for i, s in enumerate(shapes) if s != GRAPH_SHAPE]
+        if pick < 0.25 and large:
+            i = int(rng.choice(large))
+            if rng.random() < 0.3 and i in (0, 2):
+                c = float(rng.choice([0.5, -2.0, 3.0]))
+                i = emit(("scale", ("n", i), c), values[i] * F32(c))
+            chain_to_shape(view_step(i) if shapes[i] != GRAPH_SHAPE else i)
+        elif pick < 0.5 and any(dense[i] for i in ready):
+            i = int(rng.choice([i for i in ready if dense[i]]))
+            kind = str(rng.choice(["negate", "square", "scale", "shift"]))
+            if kind == "negate":
+                emit(("negate", ("n", i)), -values[i])
+            elif kind == "square":
+                emit(("square", ("n", i)), values[i] * values[i])
+            elif kind == "scale":
+                c = float(rng.choice([0.75, -1.5, 2.0]))
+                emit(("scale", ("n", i), c), values[i] * F32(c))
+            else:
+                c = float(rng.choice([0.25, -1.0]))
+                emit(("shift", ("n", i), c), values[i] + F32(c))
+        else:
+            i, j = (int(k) for k in rng.choice(ready, 2))
+            kind = str(rng.choice(["add", "subtract", "multiply", "divide"]))
+            if kind == "divide":
+                square = ("square", ("n", j)) if dense[j] else ("multiply", ("n", j), ("n", j))
+                sq = emit(square, values[j] * values[j])
+                j = emit(("shift", ("n", sq), 1.0), values[sq] + F32(1.0))
+            op = {"add": np.add, "subtract": np.subtract, "multiply": np.multiply,
+                  "divide": np.divide}[kind]
+            emit((kind, ("n", i), ("n", j)), op(values[i], values[j]))
+    sinks = [i for i, s in enumerate(shapes) if s == GRAPH_SHAPE and not consumed[i]]
+    return recipe, sinks
+
+
+def replay_graph(lib, leaves, recipe, sinks):
+    """Builds the recipe on `lib` and returns the sum of its sinks."""
+    nodes = list(leaves)
+    for step in recipe:
+        kind = step[0]
+        x = nodes[step[1][1]]
+        if kind == "narrow":
+            nodes.append(x.narrow(step[2], step[3], step[4]))
+        elif kind == "transpose":
+            nodes.append(x.transpose(1, 2))
+        elif kind == "scale":
+            nodes.append(lib.multiply_scalar(x, step[2]))
+        elif kind == "shift":
+            nodes.append(lib.add_scalar(x, step[2]))
+        elif kind in ("negate", "square"):
+            nodes.append(getattr(lib, kind)(x))
+        else:
+            nodes.append(getattr(lib, kind)(x, nodes[step[2][1]]))
+    total = nodes[sinks[0]]
+    for i in sinks[1:]:
+        total = lib.add(total, nodes[i])
+    return total
+
+
+@pytest.mark.parametrize("exact_signs", [False, True])
+def test_random_autograd_graphs(sp, exact_signs):
+    """Sixteen random graphs (random_graph) run through the engine and
+    through the oracle's engine, which follows autograd.cpp:201-265 one
+    node at a time.  Every op on the way is exact IEEE arithmetic or a
+    view, so the leaf gradients agree bit for bit when exact zero signs
+    are on, and in value (+0 and -0 taken as equal) by default; the loss
+    is a full sum, compared with its red bound.  The graphs exercise the
+    engine's narrow-chain hand-down, gradients placed into a base, shared
+    intermediate views, chains that end on a computed tensor and the
+    accumulation order of reused tensors."""
+    sp.set_exact_gradient_zero_signs(exact_signs)
+    before = sp.autograd_counters()["window_fusions"]
+    try:
+        for seed in range(300, 316):
+            recipe, sinks = random_graph(seed)
+            arrays = [normal(seed * 10 + k, s) for k, s in enumerate(GRAPH_LEAVES)]
+            arrays.append(normal(seed * 10 + 7, GRAPH_SHAPE))
+
+            def build(lib, t, recipe=recipe, sinks=sinks):
+                return weighted_sum(lib, replay_graph(lib, t[:3], recipe, sinks), t[3])
+
+            loss_d, loss_r, gd, gr = run_both(sp, build, arrays)
+            total = replay_graph(R, [R.RTensor.of(a) for a in arrays[:3]], recipe, sinks).numpy()
+            terms = total.astype(np.float64) * arrays[3]
+            assert_red(loss_d, loss_r, terms.size, np.sqrt(np.sum(terms ** 2)), f"seed {seed} loss")
+            for k, (got, want) in enumerate(zip(gd, gr)):
+                what = f"seed {seed} ({len(recipe)} steps) grad {k}"
+                if exact_signs:
+                    assert_bitexact(got, want, what)
+                else:
+                    assert_bitexact(got + F32(0), want + F32(0), what)
+        assert sp.autograd_counters()["window_fusions"] > before, "no narrow chain was handed down"
+    finally:
+        sp.set_exact_gradient_zero_signs(False)
+
+
 def test_autograd_api_errors(sp):
     x = hip_tensor(sp, normal(1, (3,)), requires_grad=True)
     y = sp.multiply(x, x)
