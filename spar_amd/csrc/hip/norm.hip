@@ -858,28 +858,106 @@ constexpr int kBackwardGroups = kApplyThreads / kApplyGranules;
 // so every tile's x is loaded one tile ahead.
 constexpr int kSumsThreads = 512;
 
+// Lane exchanges within a half wave, on 32-bit words (a double as two).
+// swap_rows: v_permlane16_swap, which swaps the odd 16-lane rows of its first
+// operand with the even rows of its second: for lanes c < 16 of a half wave
+// `second` becomes the first operand of lane c + 16, for lanes c >= 16
+// `first` becomes the second operand of lane c - 16.
+// mirror<CTRL>: a DPP move within 16-lane rows, lane c reading lane
+// 15 - c (row_mirror, 0x140), within 8-lane halves 7 - c (row_half_mirror,
+// 0x141), or c ^ 2 and c ^ 1 within quads (quad_perm 0x4E and 0xB1).
+__device__ __forceinline__ void swap_rows(uint32_t& first, uint32_t& second) {
+  const auto swapped = __builtin_amdgcn_permlane16_swap(first, second, false, false);
+  first = swapped[0];
+  second = swapped[1];
+}
+
+template <typename T>
+__device__ __forceinline__ void swap_rows(T& first, T& second) {
+  if constexpr (sizeof(T) == 4) {
+    uint32_t a = __builtin_bit_cast(uint32_t, first);
+    uint32_t b = __builtin_bit_cast(uint32_t, second);
+    swap_rows(a, b);
+    first = __builtin_bit_cast(T, a);
+    second = __builtin_bit_cast(T, b);
+  } else {
+    static_assert(sizeof(T) == 8, "32- or 64-bit values");
+    const uint64_t a = __builtin_bit_cast(uint64_t, first);
+    const uint64_t b = __builtin_bit_cast(uint64_t, second);
+    uint32_t a0 = static_cast<uint32_t>(a), a1 = static_cast<uint32_t>(a >> 32);
+    uint32_t b0 = static_cast<uint32_t>(b), b1 = static_cast<uint32_t>(b >> 32);
+    swap_rows(a0, b0);
+    swap_rows(a1, b1);
+    first = __builtin_bit_cast(T, (static_cast<uint64_t>(a1) << 32) | a0);
+    second = __builtin_bit_cast(T, (static_cast<uint64_t>(b1) << 32) | b0);
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t mirror_word(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL, typename T>
+__device__ __forceinline__ T mirror(T x) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, mirror_word<CTRL>(__builtin_bit_cast(uint32_t, x)));
+  } else {
+    const uint64_t a = __builtin_bit_cast(uint64_t, x);
+    const uint64_t lo = mirror_word<CTRL>(static_cast<uint32_t>(a));
+    const uint64_t hi = mirror_word<CTRL>(static_cast<uint32_t>(a >> 32));
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+
 // Butterfly reduce-scatter over the 32 lanes of a half wave: on entry each
 // lane holds NV values (NV divides 32), on exit lane c holds in v[0] the sum
 // over the 32 lanes of value c * NV / 32, the 32 / NV lanes that share it
-// alike.  Step b pairs lanes c and c ^ b; while more than one value is left
-// the lane with bit b set keeps the upper half, after that both add.
+// alike.  Step b pairs lane c with a lane whose bit b differs: c ^ 16 (a row
+// swap), then 15 - c, 7 - c, c ^ 2 and c ^ 1 within rows (DPP moves, no
+// LDS); the partners' offsets 16, 15, 7, 2, 1 span all 32 lanes, so after
+// the five steps every lane's value covers the half wave once.  While more
+// than one value is left the lane with bit b set keeps the upper half,
+// after that both add.  The row swap exchanges a pair of values at once: a
+// lane of the lower row gets its partner's lower value in `upper_half`'s
+// place, a lane of the upper row the partner's upper value in `lower`'s, so
+// one add gives each lane its kept half.
 template <typename T, int NV, int B = 16>
 __device__ __forceinline__ void half_wave_reduce_scatter(T (&v)[NV], int c) {
   if constexpr (B >= 1) {
+    constexpr int kCtrl = B == 8 ? 0x140 : B == 4 ? 0x141 : B == 2 ? 0x4E : 0xB1;
     if constexpr (NV > 1) {
       constexpr int kHalf = NV / 2;
-      const bool upper = (c & B) != 0;
       T kept[kHalf];
+      if constexpr (B == 16) {
 #pragma unroll
-      for (int j = 0; j < kHalf; ++j) {
-        const T send = upper ? v[j] : v[j + kHalf];
-        const T keep = upper ? v[j + kHalf] : v[j];
-        kept[j] = keep + __shfl_xor(send, B);
+        for (int j = 0; j < kHalf; ++j) {
+          T lower = v[j];
+          T upper_half = v[j + kHalf];
+          swap_rows(lower, upper_half);
+          kept[j] = lower + upper_half;
+        }
+      } else {
+        const bool upper = (c & B) != 0;
+#pragma unroll
+        for (int j = 0; j < kHalf; ++j) {
+          const T send = upper ? v[j] : v[j + kHalf];
+          const T keep = upper ? v[j + kHalf] : v[j];
+          kept[j] = keep + mirror<kCtrl>(send);
+        }
       }
       half_wave_reduce_scatter<T, kHalf, B / 2>(kept, c);
       v[0] = kept[0];
     } else {
-      v[0] = v[0] + __shfl_xor(v[0], B);
+      if constexpr (B == 16) {
+        T own = v[0];
+        T other = v[0];
+        swap_rows(own, other);
+        v[0] = own + other;
+      } else {
+        v[0] = v[0] + mirror<kCtrl>(v[0]);
+      }
       half_wave_reduce_scatter<T, 1, B / 2>(v, c);
     }
   }
